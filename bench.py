@@ -1,0 +1,349 @@
+"""MoE expert-layer benchmark on one MI355X.
+
+Headline (the JSON `value`): T=8 speculative-verify MoE layer with Zipf(1.1)
+expert popularity -- HBM GB/s on the unique expert weight bytes a step
+touches.  A step is one sparse MoE block over 8 tokens: softmax/top-k on the
+drawn logits, bucketing, routed SwiGLU experts, shared expert, ordered
+combine.  Steps rotate over the resident layers so the touched experts are
+not Infinity-Cache resident; the steps run as HIP-graph replays.
+
+Also reported under "configs": T=1 decode layer with the router (latency and
+GB/s), the raw expert gather at T in {1,4,8,16}, the 40-layer decode chain
+with RMSNorm + residual at T=1 and T=16, and the T=2048 prefill (TFLOPS).
+
+`roofline` is for the gate/up kernel of the headline step, timed with HIP
+events around its launches; `cpu_baseline` is the reference CPU expert
+kernel (edge35b/cpu_experts.c built from source into oracle/_ref) on the
+host's cores over a bounded sample of the same routes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from lightreason_amd import _native  # noqa: E402
+from lightreason_amd.moe import (EXPERT_BYTES, EXPERT_ELEMENTS, HIDDEN, INNER, LayerWeights, Workspace,  # noqa: E402
+                                 gather, moe_layer)
+from lightreason_amd.synthetic import SyntheticModel  # noqa: E402
+
+METRIC = "MoE layer µs + HBM GB/s vs peak at T=1,8; prefill BF16 TFLOPS at T=2048"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+PAIR_FLOP = 2 * 3 * INNER * HIDDEN  # one (token, expert) SwiGLU pair
+SHARED_BYTES = EXPERT_BYTES + 2 * HIDDEN
+ROUTER_BYTES = 256 * HIDDEN * 2
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bf16_from_f64(values: np.ndarray, device) -> torch.Tensor:
+    f32 = np.ascontiguousarray(values, dtype=np.float32)
+    bits = f32.view(np.uint32).astype(np.uint64)
+    b = (((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+    return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def zipf_logits(tokens: int, seed: int, s: float = 1.1) -> np.ndarray:
+    """L[t, e] = -s ln(rank_e) + Gumbel[t, e]: top-8 of a row is a Zipf(s)
+    draw of 8 distinct experts (Gumbel-top-k)."""
+    rng = np.random.default_rng(seed)
+    ranks = rng.permutation(256) + 1
+    return -s * np.log(ranks)[None, :] + rng.gumbel(size=(tokens, 256))
+
+
+def timed_replays(graph, replays: int) -> float:
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop)
+
+
+def capture(fn):
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return graph
+
+
+class Case:
+    """One workload: per-layer static inputs and outputs, run as one graph
+    that steps through the layers in order."""
+
+    def __init__(self, model, tokens, *, logits=None, norm=False, chain=False, layers=None):
+        self.model = model
+        self.tokens = tokens
+        self.layer_ids = list(range(len(model.layers))) if layers is None else layers
+        device = model.device
+        self.ws = Workspace(device, tokens)
+        self.x = [model.hidden(tokens, step=100 + i) for i in self.layer_ids]
+        self.out = [torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=device) for _ in self.layer_ids]
+        self.idx = [torch.empty((tokens, 8), dtype=torch.int64, device=device) for _ in self.layer_ids]
+        self.logits = logits
+        self.chain = chain
+        self.layers = []
+        for i in self.layer_ids:
+            base = model.layers[i]
+            self.layers.append(LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None}))
+
+    def run(self):
+        for j, layer in enumerate(self.layers):
+            x = self.out[j - 1] if (self.chain and j > 0) else self.x[j]
+            moe_layer(x, layer, out=self.out[j], indices=self.idx[j],
+                      logits_in=None if self.logits is None else self.logits[j], workspace=self.ws)
+
+    def unique_counts(self) -> list[int]:
+        self.run()
+        torch.cuda.synchronize()
+        return [len(set(i.cpu().numpy().ravel().tolist())) for i in self.idx]
+
+
+def bench_case(case: Case, replays: int, warmup: int) -> float:
+    """Milliseconds per graph replay (one pass over the case's layers)."""
+    graph = capture(case.run)
+    for _ in range(warmup):
+        graph.replay()
+    return timed_replays(graph, replays) / replays
+
+
+def kernel_time(case: Case, stage: int, passes: int) -> tuple[float, int]:
+    """Average duration (ms) of one stage's launches over eager passes."""
+    case.run()
+    torch.cuda.synchronize()
+    _native.timing_enable(stage, passes * len(case.layers) + 8)
+    for _ in range(passes):
+        case.run()
+    total, launches = _native.timing_collect(stage)
+    _native.timing_enable(0)
+    return total / max(launches, 1), launches
+
+
+def cpu_baseline(model, case: Case, uniques, budget_s: float = 12.0) -> dict:
+    """The reference CPU expert kernel (oracle/_ref/libcpu_experts.so, built
+    from edge35b/cpu_experts.c) on the headline routes: expert_block_rows over
+    the 64 (token, expert) rows of a layer, all threads of this process's
+    CPU share.  GB/s on the same unique-expert bytes as the GPU figure."""
+    from oracle import oracle as O
+
+    ref = O.reference()
+    kind = "reference"
+    if ref is None:
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": kind,
+                "sample": "reference CPU kernel not built (oracle/Makefile needs the reference source)"}
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    samples, total_bytes, total_s, calls = 0, 0, 0.0, 0
+    started = time.perf_counter()
+    for j, layer in enumerate(case.layer_ids):
+        if time.perf_counter() - started > budget_s:
+            break
+        idx = case.idx[j].cpu().numpy()
+        x = case.x[j].cpu().view(torch.int16).numpy().view(np.uint16)
+        experts = sorted(set(idx.ravel().tolist()))
+        host = {}
+        for e in experts:
+            row = model.bank.bank[layer, e].cpu().view(torch.int16).numpy().view(np.uint16)
+            host[e] = (np.ascontiguousarray(row[:2 * INNER * HIDDEN]), np.ascontiguousarray(row[2 * INNER * HIDDEN:]))
+        gu = [host[e][0] for e in idx.ravel().tolist()]
+        dn = [host[e][1] for e in idx.ravel().tolist()]
+        tok = np.repeat(np.arange(idx.shape[0], dtype=np.int32), idx.shape[1])
+        O.reference_expert_block_rows(gu, dn, x, tok, threads)  # warm the pages
+        t0 = time.perf_counter()
+        reps = 0
+        while reps < 3 or time.perf_counter() - t0 < 1.0:
+            O.reference_expert_block_rows(gu, dn, x, tok, threads)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        total_s += dt
+        total_bytes += uniques[j] * EXPERT_BYTES
+        samples += 1
+        calls += reps
+    gbs = total_bytes / total_s / 1e9 if total_s else None
+    return {"value": round(gbs, 2) if gbs else None, "unit": "GB/s", "cores": threads, "kind": kind,
+            "ms_per_layer": round(1e3 * total_s / max(samples, 1), 3),
+            "sample": f"{samples} layers of the T=8 Zipf routes (64 rows each, {calls} timed calls), "
+                      f"expert_block_rows with {threads} OpenMP threads; routed experts only "
+                      "(the reference CPU path has no router, combine or shared expert)"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=400, help="timed headline steps (layer calls)")
+    parser.add_argument("--warmup", type=int, default=40)
+    parser.add_argument("--layers", type=int, default=40, help="resident layers (40 = the whole model)")
+    parser.add_argument("--seed", type=int, default=2026)
+    parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--skip-prefill", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(multi-GPU sharding is a design note only)", file=sys.stderr)
+        return 2
+    device = torch.device("cuda:0")
+    _native.device_check()
+    t0 = time.perf_counter()
+    model = SyntheticModel(layers=args.layers, device=device, seed=args.seed, shared=True, norm="normal")
+    torch.cuda.synchronize()
+    log(f"[bench] {args.layers} layers resident ({model.bank.nbytes / 2**30:.1f} GiB experts) "
+        f"in {time.perf_counter() - t0:.1f}s")
+    L = args.layers
+    replays = max(1, args.steps // L)
+    warm = max(1, args.warmup // L)
+    configs = {}
+
+    # ---- headline: T=8 Zipf verify ----
+    logits = [bf16_from_f64(zipf_logits(8, args.seed * 1000 + l), device) for l in range(L)]
+    c2 = Case(model, 8, logits=logits)
+    uniques = c2.unique_counts()
+    ms = bench_case(c2, replays, warm)
+    ms_step = ms / L
+    bytes_step = (np.mean(uniques) * EXPERT_BYTES + SHARED_BYTES)
+    gbs = bytes_step / (ms_step * 1e-3) / 1e9
+    log(f"[bench] C2 T=8 zipf: {ms_step * 1e3:.1f} us/layer, U={np.mean(uniques):.1f}, {gbs:.0f} GB/s")
+    gate_ms, launches = kernel_time(c2, _native.STAGE_GATE_UP, passes=max(2, replays))
+    down_ms, _ = kernel_time(c2, _native.STAGE_DOWN, passes=max(2, replays))
+    gate_bytes = (np.mean(uniques) + 1) * (2 * INNER * HIDDEN * 2) + (8 * 8 + 8) * (HIDDEN * 2 + INNER * 2)
+    gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
+    log(f"[bench] C2 gate/up kernel {gate_ms * 1e3:.1f} us ({gate_gbs:.0f} GB/s), down {down_ms * 1e3:.1f} us")
+    configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2), unique_experts=round(float(np.mean(uniques)), 2),
+                                        gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
+                                        gateup_us=round(gate_ms * 1e3, 2), down_us=round(down_ms * 1e3, 2))
+
+    # ---- C0: T=1 decode layer with the router ----
+    c0 = Case(model, 1)
+    ms0 = bench_case(c0, replays, warm) / L
+    b0 = 8 * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES
+    configs["c0_decode_t1"] = dict(us_per_layer=round(ms0 * 1e3, 2), gbs=round(b0 / (ms0 * 1e-3) / 1e9, 1),
+                                   frac_hbm=round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+    log(f"[bench] C0 T=1: {ms0 * 1e3:.1f} us/layer, {configs['c0_decode_t1']['gbs']} GB/s")
+
+    # ---- C1: raw expert gather ----
+    gather_res = {}
+    ptrs = model.bank.tables.cpu()
+    staging = torch.empty((128, EXPERT_ELEMENTS), dtype=torch.bfloat16, device=device)
+    for T in (1, 4, 8, 16):
+        rng = np.random.default_rng(T)
+        per_layer = []
+        for l in range(L):
+            sel = sorted(set(np.concatenate([rng.choice(256, 8, replace=False) for _ in range(T)]).tolist()))
+            per_layer.append(sel)
+        descs = [torch.stack([ptrs[l][:, 0], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1)[None]
+                 .contiguous().to(device) for l in range(L)]
+        srcs = [torch.tensor(s + [0] * (128 - len(s)), dtype=torch.int32, device=device) for s in per_layer]
+        dst = torch.arange(128, dtype=torch.int32, device=device)
+        counts = [torch.tensor([len(s)], device=device) for s in per_layer]
+        dests = torch.tensor([staging.data_ptr()], device=device)
+        sizes = torch.tensor([EXPERT_BYTES], device=device)
+        max_copies = max(len(s) for s in per_layer)
+
+        def run_gather():
+            for l in range(L):
+                gather(descs[l], dests, sizes, srcs[l], dst, counts[l], max_copies=max_copies, experts=256, stripes=48)
+
+        msg = bench_case(type("G", (), {"run": staticmethod(run_gather)})(), replays, warm) / L
+        u = float(np.mean([len(s) for s in per_layer]))
+        moved = 2 * u * EXPERT_BYTES
+        gather_res[f"t{T}"] = dict(unique=round(u, 1), us=round(msg * 1e3, 2), gbs_moved=round(moved / (msg * 1e-3) / 1e9, 1))
+    configs["c1_gather"] = gather_res
+    log(f"[bench] C1 gather: {gather_res}")
+    del staging
+
+    # ---- C3: 40-layer chain with RMSNorm + residual ----
+    for T in (1, 16):
+        c3 = Case(model, T, norm=True, chain=True)
+        u3 = c3.unique_counts()
+        ms3 = bench_case(c3, max(2, replays // 2), 1)
+        b3 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u3)
+        configs[f"c3_chain_t{T}"] = dict(layers=L, ms_per_step=round(ms3, 4), gbs=round(b3 / (ms3 * 1e-3) / 1e9, 1),
+                                         frac_hbm=round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                         mean_unique=round(float(np.mean(u3)), 1))
+        log(f"[bench] C3 T={T}: {ms3:.3f} ms/step over {L} layers, {configs[f'c3_chain_t{T}']['gbs']} GB/s")
+
+    # ---- C4: T=2048 prefill with skewed routing ----
+    if not args.skip_prefill:
+        T = 2048
+        sigma_bias = 0.25
+        rng = np.random.default_rng(args.seed + 4)
+        layer_ids = list(range(min(L, 4)))
+        lg = []
+        for l in layer_ids:
+            x = model.hidden(T, step=100 + l).float()
+            base = (x @ model.layers[l].router.float().T).cpu().numpy()
+            lg.append(bf16_from_f64(base + rng.normal(0, sigma_bias, size=(1, 256)), device))
+        c4 = Case(model, T, logits=lg, layers=layer_ids)
+        idx_counts = []
+        c4.run()
+        torch.cuda.synchronize()
+        for i in c4.idx:
+            counts = np.bincount(i.cpu().numpy().ravel(), minlength=256)
+            idx_counts.append(counts)
+        ms4 = bench_case(c4, 3, 1) / len(layer_ids)
+        flops = (T * 8 + T) * PAIR_FLOP
+        hit = float(np.mean([(c > 0).sum() for c in idx_counts]))
+        skew = float(np.mean([c.max() / c.mean() for c in idx_counts]))
+        tflops = flops / (ms4 * 1e-3) / 1e12
+        configs["c4_prefill_t2048"] = dict(ms_per_layer=round(ms4, 3), tflops=round(tflops, 2),
+                                           frac_mfma=round(tflops / BF16_PEAK_TFLOPS, 4), experts_hit=hit,
+                                           max_over_mean=round(skew, 2), bias_sigma=sigma_bias,
+                                           flop_per_layer=flops, note="router GEMV excluded (logits given)")
+        log(f"[bench] C4 T=2048: {ms4:.3f} ms/layer, {tflops:.1f} TFLOPS, hit {hit}, max/mean {skew:.2f}")
+
+    cpu = {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference", "sample": "skipped"}
+    if not args.skip_cpu:
+        cpu = cpu_baseline(model, c2, uniques)
+        log(f"[bench] CPU baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": replays * L,
+        "warmup": warm * L,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded counter-based generator; Zipf(1.1) Gumbel-top-k logits)",
+        "config": {"workload": "T=8 speculative-verify MoE layer, 256 experts top-8, Zipf(1.1) routing, "
+                               "shared expert, HBM GB/s on unique expert bytes; steps rotate over resident layers",
+                   "tokens": 8, "hidden": HIDDEN, "experts": 256, "topk": 8, "inner": INNER,
+                   "layers_rotated": L, "mean_unique_experts": round(float(np.mean(uniques)), 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gateup_kernel", "avg_us": round(gate_ms * 1e3, 3), "launches": launches,
+                     "algorithmic_bytes": int(gate_bytes)},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

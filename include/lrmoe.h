@@ -1,0 +1,209 @@
+/*
+ * lrmoe.h -- C ABI of liblrmoe.so, the MI355X (gfx950) kernels for the MoE
+ * expert-layer hot path of the Qwen3.6-35B-A3B runner.
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers and sizes, no framework types;
+ *   - bf16 tensors are passed as uint16_t bit patterns, row-major, contiguous;
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is enqueued on
+ *     it and the call returns without a host synchronisation, so calls can be
+ *     captured into a HIP graph and replayed;
+ *   - the return value is 0 on success, a negative LRMOE_E_* code for misuse
+ *     detected on the host (nothing is launched), or a positive hipError_t;
+ *   - the library never allocates: scratch comes from a caller-provided
+ *     `workspace` of at least lrmoe_workspace_bytes(tokens) bytes, zeroed once
+ *     by the caller after allocation (its counters reset themselves), and used
+ *     by one stream at a time;
+ *   - route problems found on the device (an expert id outside [0, 256) or a
+ *     token routed twice to one expert) set bits in the int32 status word at
+ *     byte offset LRMOE_WS_STATUS_OFFSET of the workspace; the affected call
+ *     then writes zeros (plus the residual, where one is given) instead of
+ *     reading out of bounds.
+ *
+ * Fixed model shape: hidden 2048, 256 routed experts, top-8, expert
+ * intermediate 512, one shared expert with intermediate 512.  A routed
+ * expert's weights are gate_up [1024, 2048] (gate rows 0-511, up rows
+ * 512-1023) and down [2048, 512]; `expert_ptrs` is a device array of 256
+ * (gate_up, down) address pairs, so the expert banks can live anywhere in HBM
+ * (e.g. 40 layers x 256 experts in one allocation, the "packed pair" layout).
+ */
+#ifndef LRMOE_H
+#define LRMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LRMOE_HIDDEN 2048
+#define LRMOE_INNER 512
+#define LRMOE_EXPERTS 256
+#define LRMOE_TOPK 8
+
+#define LRMOE_OK 0
+#define LRMOE_E_ARG (-1)        /* null pointer, bad size or shape */
+#define LRMOE_E_WORKSPACE (-2)  /* workspace smaller than lrmoe_workspace_bytes(tokens) */
+#define LRMOE_E_DEVICE (-3)     /* current device is not gfx950 */
+
+#define LRMOE_WS_STATUS_OFFSET 4  /* int32 route status word in the workspace */
+#define LRMOE_STATUS_BAD_EXPERT 1
+#define LRMOE_STATUS_REPEATED_EXPERT 2
+#define LRMOE_STATUS_CODEC_ROW 4
+
+/* Library version string.  No reference counterpart. */
+const char *lrmoe_version(void);
+
+/* Human-readable text for a return code.  Replaces the status checks of
+ * edge35b/native_bf16_gather.py:25-29 (_checked) and packed_ada.py:10-12. */
+const char *lrmoe_error_string(int code);
+
+/* 0 when the current HIP device is gfx950, else LRMOE_E_DEVICE (or a
+ * hipError_t).  Replaces the capability gate of
+ * edge35b/native_bf16_gather.py:37-38 and packed_ada.py:17-18. */
+int lrmoe_device_check(void);
+
+/* Bytes of workspace a call with `tokens` tokens needs.  No reference
+ * counterpart (the reference allocates per call, e.g. block_experts.py:123-134). */
+size_t lrmoe_workspace_bytes(int tokens);
+
+/* Router: logits = bf16(x W^T) in a fixed fp32 reduction order, softmax over
+ * 256 experts in fp32, top-8 by (logit desc, id asc), renormalised in fp32,
+ * weights rounded to bf16; optionally RMSNorm (x*r)*(1+w) of `hidden` first
+ * (norm_weight != NULL) and the shared-expert gate bf16(sigmoid(bf16(x.w))).
+ * Exactly one of router_weight and logits_in is given: with logits_in
+ * [tokens, 256] bf16 the GEMV is skipped and top-k runs on those logits.
+ * Also leaves the route plan in the workspace.
+ * Replaces Transformers Qwen3_5MoeTopKRouter.forward (modeling_qwen3_5_moe.py,
+ * called from SparseMoeBlock.forward), whose outputs edge35b/expert_stream.py:383
+ * (_Layer.forward) receives; RMSNorm replaces Qwen3_5MoeRMSNorm.forward. */
+int lrmoe_route_topk(const uint16_t *hidden, int tokens, const uint16_t *router_weight,
+                     const uint16_t *logits_in, const uint16_t *norm_weight, float eps, const uint16_t *shared_expert_gate,
+                     uint16_t *logits_out, int64_t *indices_out, uint16_t *weights_out,
+                     uint16_t *shared_gate_out, uint16_t *normed_out, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/* Token-to-expert bucketing of indices [tokens, 8]: unique experts ascending
+ * (expert[0..unique)), pair offsets (offset[0..unique]), pairs in (expert asc,
+ * token asc) order (pair_token, pair_slot), and route_pair[t*8 + r] = pair of
+ * token t's r-th route in ascending expert order.  unique and status are
+ * single int32 device words.  Replaces edge35b/block_experts.py:102-121,
+ * fused_experts.py:47-54 (T=1 schedule), pipeline.py:59-76 (_routes) and
+ * packed_workers.cpp:102-113 (packed_plan), all of which run on the host after
+ * a device-to-host read of the indices. */
+int lrmoe_bucket(const int64_t *indices, int tokens, int32_t *expert, int32_t *offset,
+                 int32_t *pair_token, int32_t *pair_slot, int32_t *route_pair, int32_t *unique,
+                 int32_t *status, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Routed experts for given routes: out[t] = sum over t's routes in ascending
+ * expert order of bf16(y * w), y = SwiGLU expert output with cpu_experts.c's
+ * rounding points.  hidden [T,2048], indices [T,8] int64, weights [T,8] bf16.
+ * Replaces the experts forward the reference patches
+ * (edge35b/expert_stream.py:383-454 _Layer.forward, i.e. Transformers
+ * Qwen3_5MoeExperts.forward) and its modes fused_experts.fused_forward
+ * (fused_experts.py:40-70), block_experts.grouped_block (:89-139),
+ * pipeline.routed_forward (:79-110) and cpu_route.cpu_forward (:23-69). */
+int lrmoe_moe_experts(const uint16_t *hidden, int tokens, const int64_t *indices,
+                      const uint16_t *weights, const int64_t *expert_ptrs, uint16_t *out,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Whole sparse MoE block: router + top-k + bucketing, routed experts, ordered
+ * combine, shared expert scaled by its sigmoid gate.  With norm_weight:
+ * out = bf16(hidden + MoE(RMSNorm(hidden))) (the decoder layer's MLP half);
+ * without: out = MoE(hidden).  Shared expert pointers may all be NULL.
+ * Exactly one of router_weight and logits_in is given (see lrmoe_route_topk).
+ * indices_out / weights_out may be NULL.  Replaces Transformers
+ * Qwen3_5MoeSparseMoeBlock.forward + the residual add of
+ * Qwen3_5MoeDecoderLayer.forward, as driven by edge35b/expert_stream.py:457-526
+ * (patch_experts). */
+int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_weight,
+                    const uint16_t *logits_in, const int64_t *expert_ptrs, const uint16_t *shared_gate_proj,
+                    const uint16_t *shared_up_proj, const uint16_t *shared_down_proj,
+                    const uint16_t *shared_expert_gate, const uint16_t *norm_weight, float eps,
+                    uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* Raw BF16 row gather: for row < *count and bank b < banks, copy sizes[b]
+ * bytes from descriptors[(b*experts + src_ids[row])*3] to
+ * destinations[b] + dst_ids[row]*sizes[b]; a descriptor whose second field is
+ * >= 0 (a codec row) is skipped and LRMOE_STATUS_CODEC_ROW is or-ed into
+ * *status (may be NULL).  Grid (stripes, banks, max_copies).
+ * Replaces edge35b/bf16_gather_ada.cu:36-66 (gather_bf16 raw path) launched
+ * by native_bf16_gather.py:71-77 (NativeBf16Gather.copy), and the staging copy
+ * of scheduled_graph.py:14-26 (_stage). */
+int lrmoe_gather(const int64_t *descriptors, const int64_t *destinations, const int64_t *sizes,
+                 const int32_t *src_ids, const int32_t *dst_ids, const int64_t *count, int experts,
+                 int banks, int max_copies, int stripes, int32_t *status, void *stream);
+
+/* Batched matvec with the _matvec protocol: for e < experts and r < N,
+ * result[e*N + r] = bf16(sum_k W_e[r,k] x_e[k]), W_e = table[stride*e + column]
+ * (rows skipped when that address is 0 and stride != 3), x_e = x when
+ * shared_x else x + e*K.  K must be a multiple of 512.
+ * Replaces edge35b/fused_experts.py:8-24 (_matvec), launched at
+ * fused_experts.py:60,67, packed_hybrid.py:71-74, packed_native.py:49-52. */
+int lrmoe_matvec(const int64_t *table, const uint16_t *x, uint16_t *result, int K, int N, int column,
+                 int shared_x, int stride, int experts, void *stream);
+
+/* Ordered combine over the 8 table rows: out[h] = bf16 running sum of
+ * bf16(v_r[h] * router[table[stride*r + 2]]); v_r = hot[r] unless stride == 4,
+ * cold != NULL and table[4r + 3] >= 0, then cold[table[4r + 3]].
+ * Replaces edge35b/fused_experts.py:27-37 (_ordered_sum) and
+ * packed_hybrid.py:13-27 (_combine). */
+int lrmoe_ordered_sum(const int64_t *table, const uint16_t *hot, const uint16_t *cold,
+                      const uint16_t *router, uint16_t *out, int stride, void *stream);
+
+/* active[e*512 + r] = bf16(bf16(silu(bf16(g))) * bf16(u)) for the table rows
+ * whose gate_up address (table[stride*e]) is non-zero.
+ * Replaces edge35b/packed_ada.cu:13-40 (packed_gate_silu), loaded by
+ * packed_ada.py:15-66 (load_gate). */
+int lrmoe_gate_silu(const int64_t *table, const uint16_t *hidden, uint16_t *active, int stride,
+                    int experts, void *stream);
+
+/* Grouped projection with the _project protocol: for expert e < experts and
+ * route row r < 16, Y[(e*16 + r)*out + c] = bf16(sum_k X[row][k] W[c][k]),
+ * W = pointers[2e + down], row = e*16 + r (down) or routes[e*16 + r]
+ * (otherwise); routes < 0 read zeros.  in and out must be multiples of 256
+ * and 64.  Replaces edge35b/block_experts.py:12-28 (_project). */
+int lrmoe_project(const int64_t *pointers, const int32_t *routes, const uint16_t *X, uint16_t *Y,
+                  int in, int out, int down, int experts, void *stream);
+
+/* active[r][c] = bf16(bf16(silu(g)) * u), g = gates[r][c], u = gates[r][512 + c]
+ * for rows r < rows.  Replaces the torch act_fn(gate) * up between the two
+ * _project launches (edge35b/block_experts.py:131-132, fused_experts.py:61-62). */
+int lrmoe_swiglu_rows(const uint16_t *gates, uint16_t *active, int rows, void *stream);
+
+/* Per-token ordered combine through inverse [tokens][8][3] = (expert, row,
+ * slot): out[t][h] = bf16 running sum of bf16(v * router[t*8 + slot]),
+ * v = X[(expert*16 + row)][h], or cold[row][h] when hybrid and expert < 0.
+ * Replaces edge35b/block_experts.py:31-49 (_combine). */
+int lrmoe_block_combine(const int32_t *inverse, const uint16_t *X, const uint16_t *cold,
+                        const uint16_t *router, uint16_t *out, int tokens, int hybrid, void *stream);
+
+/* Synthetic bf16 ~N(0, sigma) from a counter-based generator: element i is a
+ * function of (seed, stream_id, first + i) only.  No reference counterpart
+ * (the reference draws torch.randn weights, probe_experts.py:69). */
+int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t stream_id,
+                           double sigma, int64_t first, void *stream);
+
+/* Measurement support, no reference counterpart (the reference brackets
+ * stages with CUDA events in Python, e.g. benchmark_packed_gather8.py:168-178).
+ * lrmoe_timing_enable(mask, launches) brackets every launch of the stages in
+ * `mask` (LRMOE_STAGE_* bits) with a pair of HIP events on its stream, room
+ * for `launches` launches per stage; mask 0 turns timing off.  Do not enable
+ * it while a stream is being captured.  lrmoe_timing_collect(stage, ...)
+ * synchronises on those events and returns the summed milliseconds and the
+ * launch count, then rewinds. */
+#define LRMOE_STAGE_ROUTE 1
+#define LRMOE_STAGE_GATE_UP 2
+#define LRMOE_STAGE_DOWN 4
+#define LRMOE_STAGE_COMBINE 8
+#define LRMOE_STAGE_GATHER 16
+int lrmoe_timing_enable(int mask, int launches);
+int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LRMOE_H */

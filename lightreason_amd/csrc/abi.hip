@@ -1,0 +1,240 @@
+// extern "C" entry points of liblrmoe.so (declared in include/lrmoe.h).
+// Host-side argument checks happen here; nothing is launched when they fail.
+#include <string.h>
+
+#include "lrmoe_internal.h"
+
+namespace {
+
+using lrmoe::Plan;
+using lrmoe::Workspace;
+
+constexpr int kMaxTokens = 1 << 16;
+
+hipStream_t as_stream(void* stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+int status_of(hipError_t err) { return err == hipSuccess ? LRMOE_OK : static_cast<int>(err); }
+
+// gfx950 check of the current device, cached per device ordinal.
+int check_device() {
+    static int verdict[64] = {0};  // 0 unknown, 1 ok, 2 wrong device
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return static_cast<int>(err);
+    if (device >= 0 && device < 64 && verdict[device] != 0) return verdict[device] == 1 ? LRMOE_OK : LRMOE_E_DEVICE;
+    hipDeviceProp_t prop;
+    err = hipGetDeviceProperties(&prop, device);
+    if (err != hipSuccess) return static_cast<int>(err);
+    const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    if (device >= 0 && device < 64) verdict[device] = ok ? 1 : 2;
+    return ok ? LRMOE_OK : LRMOE_E_DEVICE;
+}
+
+bool bad_tokens(int tokens) { return tokens < 0 || tokens > kMaxTokens; }
+
+}  // namespace
+
+extern "C" {
+
+const char* lrmoe_version(void) { return "lrmoe 0.1 gfx950"; }
+
+const char* lrmoe_error_string(int code) {
+    switch (code) {
+        case LRMOE_OK: return "ok";
+        case LRMOE_E_ARG: return "lrmoe: invalid argument (null pointer, size or shape)";
+        case LRMOE_E_WORKSPACE: return "lrmoe: workspace smaller than lrmoe_workspace_bytes(tokens)";
+        case LRMOE_E_DEVICE: return "lrmoe: the current HIP device is not gfx950 (MI355X)";
+        default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "lrmoe: unknown error";
+    }
+}
+
+int lrmoe_device_check(void) { return check_device(); }
+
+size_t lrmoe_workspace_bytes(int tokens) { return lrmoe::workspace_bytes(tokens); }
+
+int lrmoe_route_topk(const uint16_t* hidden, int tokens, const uint16_t* router_weight, const uint16_t* logits_in,
+                     const uint16_t* norm_weight, float eps, const uint16_t* shared_expert_gate, uint16_t* logits_out,
+                     int64_t* indices_out, uint16_t* weights_out, uint16_t* shared_gate_out, uint16_t* normed_out,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+    if (bad_tokens(tokens)) return LRMOE_E_ARG;
+    if (tokens > 0 && (!hidden || !indices_out || !weights_out || !workspace || (!router_weight == !logits_in)))
+        return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (workspace_bytes < lrmoe::workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    const Workspace ws = lrmoe::carve(workspace, tokens);
+    lrmoe::RouteArgs a{};
+    a.x = hidden;
+    a.norm = norm_weight;
+    a.eps = eps;
+    a.router = router_weight;
+    a.logits_in = logits_in;
+    a.shared_gate = shared_expert_gate;
+    a.tokens = tokens;
+    a.normed = normed_out ? normed_out : ws.normed;
+    a.logits = logits_out ? logits_out : ws.logits;
+    a.indices = indices_out;
+    a.weights = weights_out;
+    a.sg = shared_gate_out ? shared_gate_out : ws.sg;
+    a.plan = ws.plan;
+    a.ws = ws;
+    return status_of(lrmoe::launch_route(a, as_stream(stream)));
+}
+
+int lrmoe_bucket(const int64_t* indices, int tokens, int32_t* expert, int32_t* offset, int32_t* pair_token,
+                 int32_t* pair_slot, int32_t* route_pair, int32_t* unique, int32_t* status, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    if (bad_tokens(tokens)) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!indices || !expert || !offset || !pair_token || !pair_slot || !route_pair || !unique || !status)
+        return LRMOE_E_ARG;
+    if (tokens > 64 && (!workspace || workspace_bytes < lrmoe::workspace_bytes(tokens))) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    const Workspace ws = lrmoe::carve(workspace, tokens);
+    Plan plan{expert, offset, pair_token, pair_slot, route_pair, unique, status};
+    return status_of(lrmoe::launch_bucket(indices, tokens, ws, plan, as_stream(stream)));
+}
+
+int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices, const uint16_t* weights,
+                      const int64_t* expert_ptrs, uint16_t* out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    if (bad_tokens(tokens)) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!hidden || !indices || !weights || !expert_ptrs || !out || !workspace) return LRMOE_E_ARG;
+    if (workspace_bytes < lrmoe::workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    const Workspace ws = lrmoe::carve(workspace, tokens);
+    hipStream_t s = as_stream(stream);
+    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s);
+    if (err != hipSuccess) return status_of(err);
+    lrmoe::ExpertArgs a{};
+    a.x = hidden;
+    a.expert_ptrs = expert_ptrs;
+    a.weights = weights;
+    a.out = out;
+    a.tokens = tokens;
+    a.plan = ws.plan;
+    a.ws = ws;
+    return status_of(lrmoe::launch_experts(a, s));
+}
+
+int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_weight, const uint16_t* logits_in,
+                    const int64_t* expert_ptrs,
+                    const uint16_t* shared_gate_proj, const uint16_t* shared_up_proj,
+                    const uint16_t* shared_down_proj, const uint16_t* shared_expert_gate,
+                    const uint16_t* norm_weight, float eps, uint16_t* out, int64_t* indices_out,
+                    uint16_t* weights_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (bad_tokens(tokens)) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!hidden || !expert_ptrs || !out || !workspace || (!router_weight == !logits_in)) return LRMOE_E_ARG;
+    const bool any_shared = shared_gate_proj || shared_up_proj || shared_down_proj || shared_expert_gate;
+    const bool all_shared = shared_gate_proj && shared_up_proj && shared_down_proj && shared_expert_gate;
+    if (any_shared && !all_shared) return LRMOE_E_ARG;
+    if (workspace_bytes < lrmoe::workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    const Workspace ws = lrmoe::carve(workspace, tokens);
+    hipStream_t s = as_stream(stream);
+    lrmoe::RouteArgs r{};
+    r.x = hidden;
+    r.norm = norm_weight;
+    r.eps = eps;
+    r.router = router_weight;
+    r.logits_in = logits_in;
+    r.shared_gate = shared_expert_gate;
+    r.tokens = tokens;
+    r.normed = ws.normed;
+    r.logits = ws.logits;
+    r.indices = indices_out ? indices_out : ws.indices;
+    r.weights = weights_out ? weights_out : ws.weights;
+    r.sg = ws.sg;
+    r.plan = ws.plan;
+    r.ws = ws;
+    hipError_t err = lrmoe::launch_route(r, s);
+    if (err != hipSuccess) return status_of(err);
+    lrmoe::ExpertArgs a{};
+    a.x = norm_weight ? ws.normed : hidden;
+    a.expert_ptrs = expert_ptrs;
+    a.shared_gate_proj = shared_gate_proj;
+    a.shared_up_proj = shared_up_proj;
+    a.shared_down = shared_down_proj;
+    a.weights = r.weights;
+    a.sg = ws.sg;
+    a.residual = norm_weight ? hidden : nullptr;
+    a.out = out;
+    a.tokens = tokens;
+    a.plan = ws.plan;
+    a.ws = ws;
+    return status_of(lrmoe::launch_experts(a, s));
+}
+
+int lrmoe_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                 const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
+                 int max_copies, int stripes, int32_t* status, void* stream) {
+    if (!descriptors || !destinations || !sizes || !src_ids || !dst_ids || !count) return LRMOE_E_ARG;
+    if (experts <= 0 || banks <= 0 || banks > 65535 || max_copies < 0 || max_copies > 65535 || stripes <= 0 ||
+        stripes > 65535)
+        return LRMOE_E_ARG;
+    if (max_copies == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_gather(descriptors, destinations, sizes, src_ids, dst_ids, count, experts, banks,
+                                          max_copies, stripes, status, as_stream(stream)));
+}
+
+int lrmoe_matvec(const int64_t* table, const uint16_t* x, uint16_t* result, int K, int N, int column, int shared_x,
+                 int stride, int experts, void* stream) {
+    if (!table || !x || !result || K <= 0 || K % 512 != 0 || N <= 0 || experts <= 0 || experts > 65535 ||
+        stride < 2 || column < 0 || column >= stride)
+        return LRMOE_E_ARG;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_matvec(table, x, result, K, N, column, shared_x, stride, experts, as_stream(stream)));
+}
+
+int lrmoe_ordered_sum(const int64_t* table, const uint16_t* hot, const uint16_t* cold, const uint16_t* router,
+                      uint16_t* out, int stride, void* stream) {
+    if (!table || !hot || !router || !out || (stride != 3 && stride != 4)) return LRMOE_E_ARG;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_ordered_sum(table, hot, cold, router, out, stride, as_stream(stream)));
+}
+
+int lrmoe_gate_silu(const int64_t* table, const uint16_t* hidden, uint16_t* active, int stride, int experts,
+                    void* stream) {
+    if (!table || !hidden || !active || stride < 1 || experts <= 0 || experts > 65535) return LRMOE_E_ARG;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_gate_silu(table, hidden, active, stride, experts, as_stream(stream)));
+}
+
+int lrmoe_project(const int64_t* pointers, const int32_t* routes, const uint16_t* X, uint16_t* Y, int in, int out,
+                  int down, int experts, void* stream) {
+    if (!pointers || !routes || !X || !Y || in <= 0 || in % 256 != 0 || out <= 0 || out % 64 != 0 || experts < 0 ||
+        experts > 65535)
+        return LRMOE_E_ARG;
+    if (experts == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_project(pointers, routes, X, Y, in, out, down ? 1 : 0, experts, as_stream(stream)));
+}
+
+int lrmoe_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows, void* stream) {
+    if (!gates || !active || rows < 0) return LRMOE_E_ARG;
+    if (rows == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_swiglu_rows(gates, active, rows, as_stream(stream)));
+}
+
+int lrmoe_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
+                        uint16_t* out, int tokens, int hybrid, void* stream) {
+    if (!inverse || !X || !router || !out || bad_tokens(tokens) || (hybrid && !cold)) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_block_combine(inverse, X, cold, router, out, tokens, hybrid ? 1 : 0,
+                                                 as_stream(stream)));
+}
+
+int lrmoe_fill_normal_bf16(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
+                           int64_t first, void* stream) {
+    if (!out || count < 0) return LRMOE_E_ARG;
+    if (count == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_fill_normal(out, count, seed, stream_id, sigma, first, as_stream(stream)));
+}
+
+}  // extern "C"

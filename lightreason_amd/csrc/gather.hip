@@ -1,0 +1,110 @@
+// HBM-resident expert gather (raw BF16 rows) and the synthetic generator.
+//
+// Gather semantics: edge35b/bf16_gather_ada.cu:36-66 (raw path, base < 0) as
+// launched by edge35b/native_bf16_gather.py:71-77: for every copy row below
+// the device-resident *count, for every bank b, copy sizes[b] bytes from
+// descriptors[(b*experts + src_ids[row])*3 + 0] to
+// destinations[b] + dst_ids[row]*sizes[b].  The count stays on the device, so
+// a captured graph replays with new counts and descriptors.
+//
+// On MI355X every expert row is resident in HBM, so the copy is HBM->HBM.
+// Each workgroup owns one contiguous stripe of one row of one bank and moves
+// it with 16-byte loads, several in flight per lane, and 16-byte stores.
+#include "lrmoe_device.h"
+#include "lrmoe_internal.h"
+
+namespace lrmoe {
+namespace {
+
+constexpr int kGatherUnroll = 8;
+
+__global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors, const int64_t* destinations,
+                                                     const int64_t* sizes, const int32_t* src_ids,
+                                                     const int32_t* dst_ids, const int64_t* count, int experts,
+                                                     int32_t* status) {
+    const int stripe = blockIdx.x;
+    const int bank = blockIdx.y;
+    const int row = blockIdx.z;
+    if (row >= *count) return;
+    const int64_t* desc = descriptors + (static_cast<int64_t>(bank) * experts + src_ids[row]) * 3;
+    const u32x4* src = reinterpret_cast<const u32x4*>(desc[0]);
+    if (desc[1] >= 0) {
+        // A codec-packed row: not a raw BF16 row, so nothing is copied.
+        if (threadIdx.x == 0 && stripe == 0 && status != nullptr) atomicOr(status, kStatusCodecRow);
+        return;
+    }
+    const int64_t row_bytes = sizes[bank];
+    u32x4* dst = reinterpret_cast<u32x4*>(destinations[bank] + static_cast<int64_t>(dst_ids[row]) * row_bytes);
+    const int64_t units = row_bytes >> 4;
+    const int64_t per = (units + gridDim.x - 1) / gridDim.x;
+    const int64_t begin = stripe * per;
+    const int64_t end = begin + per < units ? begin + per : units;
+    const int64_t step = static_cast<int64_t>(blockDim.x) * kGatherUnroll;
+    int64_t i = begin + threadIdx.x;
+    for (; i + (kGatherUnroll - 1) * blockDim.x < end; i += step) {
+        u32x4 v[kGatherUnroll];
+#pragma unroll
+        for (int u = 0; u < kGatherUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * blockDim.x);
+#pragma unroll
+        for (int u = 0; u < kGatherUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * blockDim.x);
+    }
+    for (; i < end; i += blockDim.x) dst[i] = src[i];
+}
+
+// Counter-based synthetic bf16 ~N(0, sigma): h = splitmix64(key + index),
+// key = splitmix64(seed * 0x9E3779B97F4A7C15 + stream); Irwin-Hall sum of the
+// four 16-bit fields of h, centred and scaled to unit variance in double,
+// times sigma, rounded to float and then to bf16.  Integer and IEEE double
+// operations only, so any host can regenerate a tensor bit-for-bit.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(uint16_t* out, int64_t count, uint64_t key, double inv_std,
+                                                          double sigma, int64_t first) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const uint64_t h = splitmix64(key + static_cast<uint64_t>(first + i));
+        const int64_t s = static_cast<int64_t>(h & 0xffff) + static_cast<int64_t>((h >> 16) & 0xffff) +
+                          static_cast<int64_t>((h >> 32) & 0xffff) + static_cast<int64_t>(h >> 48);
+        const double z = (static_cast<double>(s) - 131070.0) * inv_std;
+        out[i] = static_cast<uint16_t>(f2bf(static_cast<float>(z * sigma)));
+    }
+}
+
+uint64_t host_splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                         const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
+                         int max_copies, int stripes, int32_t* status, hipStream_t stream) {
+    if (max_copies <= 0 || banks <= 0) return hipSuccess;
+    timing_mark(kStageGather, stream, true);
+    hipLaunchKernelGGL(gather_kernel, dim3(stripes, banks, max_copies), dim3(256), 0, stream, descriptors, destinations,
+                       sizes, src_ids, dst_ids, count, experts, status);
+    timing_mark(kStageGather, stream, false);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
+                              int64_t first, hipStream_t stream) {
+    if (count <= 0) return hipSuccess;
+    const uint64_t key = host_splitmix64(seed * 0x9E3779B97F4A7C15ull + stream_id);
+    const double inv_std = 1.0 / __builtin_sqrt(1431655765.0);
+    int64_t blocks = (count + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, out, count, key,
+                       inv_std, sigma, first);
+    return hipGetLastError();
+}
+
+}  // namespace lrmoe

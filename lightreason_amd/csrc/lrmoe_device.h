@@ -1,0 +1,142 @@
+// Device-side building blocks shared by the lrmoe kernels (gfx950 only).
+//
+// bf16 values travel as uint16 bit patterns.  Rounding to bf16 is
+// round-to-nearest-even on the fp32 bits, the same rule as
+// edge35b/cpu_experts.c:18-22 (to_bfloat), so every rounding point the
+// reference applies can be reproduced exactly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lrmoe {
+
+constexpr int kHidden = 2048;      // model hidden size
+constexpr int kInner = 512;        // expert intermediate size
+constexpr int kExperts = 256;      // routed experts per layer
+constexpr int kTopK = 8;           // routes per token
+constexpr int kWave = 64;          // CDNA wavefront width
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float value) {
+    const uint32_t bits = __float_as_uint(value);
+    return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float rbf(float value) { return bf2f(f2bf(value)); }
+
+// Low and high bf16 halves of a packed 32-bit word, as floats.
+__device__ __forceinline__ float lo_bf(uint32_t word) { return __uint_as_float(word << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t word) { return __uint_as_float(word & 0xffff0000u); }
+
+// exp(x): Cody-Waite reduction x = k ln2 + r, degree-7 Taylor polynomial for
+// exp(r) on |r| <= ln2/2 in Horner form, then two exact power-of-two scalings.
+// x < -87 gives 0 and x > 88.72283935546875 gives +inf, so every finite result
+// is a normal float.  Only IEEE mul/fma/rint are used, so the host oracle
+// reproduces it bit-for-bit.
+__device__ __forceinline__ float pow2i(int k) { return __uint_as_float(static_cast<uint32_t>(k + 127) << 23); }
+
+__device__ __forceinline__ float lr_exp(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -87.0f) return 0.0f;
+    const float k = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-k, 0x1.62e400p-1f, x);
+    r = __builtin_fmaf(-k, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ki = static_cast<int>(k);
+    const int k1 = ki / 2;
+    return (p * pow2i(k1)) * pow2i(ki - k1);
+}
+
+// The expert activation with cpu_experts.c:59-62 rounding points:
+// a = bf16(bf16(g / (1 + exp(-g))) * u) with g, u already bf16 values.
+__device__ __forceinline__ uint32_t swiglu_bf16(float gate, float up) {
+    const float silu = rbf(gate / (1.0f + lr_exp(-gate)));
+    return f2bf(silu * up);
+}
+
+// xor butterfly over the 64 lanes with offsets 1,2,4,...,32: the fixed
+// reduction order shared with the oracle for router and norm sums.
+__device__ __forceinline__ float wave_butterfly_sum(float value) {
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) value = value + __shfl_xor(value, offset, kWave);
+    return value;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t value) {
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(value), offset, kWave));
+        value = other > value ? other : value;
+    }
+    return value;
+}
+
+// Dot product of 8 bf16 weights (one 16-byte load) with 8 floats, as an
+// in-order fmaf chain onto acc.
+__device__ __forceinline__ float fma8(uint4 w, const float* x, float acc) {
+    acc = __builtin_fmaf(lo_bf(w.x), x[0], acc);
+    acc = __builtin_fmaf(hi_bf(w.x), x[1], acc);
+    acc = __builtin_fmaf(lo_bf(w.y), x[2], acc);
+    acc = __builtin_fmaf(hi_bf(w.y), x[3], acc);
+    acc = __builtin_fmaf(lo_bf(w.z), x[4], acc);
+    acc = __builtin_fmaf(hi_bf(w.z), x[5], acc);
+    acc = __builtin_fmaf(lo_bf(w.w), x[6], acc);
+    acc = __builtin_fmaf(hi_bf(w.w), x[7], acc);
+    return acc;
+}
+
+__device__ __forceinline__ void unpack8(uint4 w, float* out) {
+    out[0] = lo_bf(w.x); out[1] = hi_bf(w.x);
+    out[2] = lo_bf(w.y); out[3] = hi_bf(w.y);
+    out[4] = lo_bf(w.z); out[5] = hi_bf(w.z);
+    out[6] = lo_bf(w.w); out[7] = hi_bf(w.w);
+}
+
+// v_mfma_f32_16x16x32_bf16.  A is 16x32 (lane l holds row l%16, k-group l/16),
+// B is 32x16 (lane l holds column l%16, the same k-group), D is 16x16 with lane
+// l holding rows 4*(l/16)+i, i=0..3, of column l%16.  The k order inside a
+// group is irrelevant to the result as long as A and B use the same one.
+__device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+}
+
+// Coherent (agent scope) loads for data written by other workgroups of the
+// same launch, read after the completion counter says they are done.
+__device__ __forceinline__ uint32_t load_agent_u32(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Orderable key for top-k: bf16 logit (with -0 folded onto +0) in the high
+// 16 bits, 255 - expert id in the low 8 bits, so the maximum key is the
+// largest logit and, among equal logits, the lowest expert id.
+__device__ __forceinline__ uint32_t route_key(uint32_t bits, int expert) {
+    if (bits == 0x8000u) bits = 0;
+    const uint32_t ordered = (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
+    return (ordered << 8) | static_cast<uint32_t>(255 - expert);
+}
+
+__device__ __forceinline__ uint32_t key_bits(uint32_t key) {
+    const uint32_t ordered = key >> 8;
+    return (ordered & 0x8000u) ? (ordered & 0x7fffu) : (~ordered & 0xffffu);
+}
+
+}  // namespace lrmoe

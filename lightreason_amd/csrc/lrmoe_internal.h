@@ -1,0 +1,167 @@
+// Host/device shared definitions for the lrmoe library: status codes, the
+// workspace layout and the launch declarations each .hip file provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/lrmoe.h"
+
+namespace lrmoe {
+
+// Bits of the device status word (workspace control block).
+constexpr int32_t kStatusBadExpert = 1;     // expert id outside [0, 256)
+constexpr int32_t kStatusRepeatedExpert = 2;  // a token routes to one expert twice
+constexpr int32_t kStatusCodecRow = 4;      // gather met a codec descriptor (not a raw row)
+
+// Control block at the start of every workspace.  The route counter is reset
+// to zero by the workgroup that consumes it, so a zero-initialised workspace
+// stays valid across launches and graph replays.
+struct Control {
+    uint32_t route_counter;
+    int32_t status;
+    int32_t unique;
+    int32_t pad0;
+    uint32_t reserved[60];
+};
+
+// Route plan: unique experts ascending, per-expert (token, slot) pairs in
+// ascending token order, and per token the pair index of each of its routes
+// in ascending expert order.
+struct Plan {
+    int32_t* expert;      // [256]
+    int32_t* offset;      // [257]
+    int32_t* pair_token;  // [8T]
+    int32_t* pair_slot;   // [8T]
+    int32_t* route_pair;  // [T][8]
+    int32_t* unique;      // [1] (in the control block)
+    int32_t* status;      // [1] (in the control block)
+};
+
+// Carves one caller-provided device buffer into the per-call arrays.  The
+// layout depends only on `tokens`, so any buffer of at least
+// workspace_bytes(tokens) serves a call with that many tokens.
+struct Workspace {
+    Control* control;
+    uint16_t* logits;     // [T][256]
+    uint16_t* normed;     // [T][2048]
+    int64_t* indices;     // [T][8]
+    uint16_t* weights;    // [T][8]
+    uint16_t* sg;         // [T]
+    Plan plan;
+    uint16_t* act;        // [8T + T][512]: routed pairs, then shared rows
+    uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
+    uint32_t* counts;     // [256] prefill histogram
+    uint32_t* bitmaps;    // [256][words] prefill token bitmaps
+    uint32_t* word_prefix;  // [256][words]
+    int words;
+    size_t bytes;
+};
+
+inline size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
+
+inline Workspace carve(void* base, int tokens) {
+    Workspace ws{};
+    const size_t T = static_cast<size_t>(tokens > 0 ? tokens : 1);
+    const size_t P = 8 * T;
+    const int words = static_cast<int>((T + 31) / 32);
+    size_t offset = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = offset;
+        offset = align_up(offset + bytes, 256);
+        return static_cast<char*>(base) + at;
+    };
+    ws.control = reinterpret_cast<Control*>(take(sizeof(Control)));
+    ws.logits = reinterpret_cast<uint16_t*>(take(T * 256 * 2));
+    ws.normed = reinterpret_cast<uint16_t*>(take(T * 2048 * 2));
+    ws.indices = reinterpret_cast<int64_t*>(take(T * 8 * 8));
+    ws.weights = reinterpret_cast<uint16_t*>(take(T * 8 * 2));
+    ws.sg = reinterpret_cast<uint16_t*>(take(T * 2));
+    ws.plan.expert = reinterpret_cast<int32_t*>(take(256 * 4));
+    ws.plan.offset = reinterpret_cast<int32_t*>(take(257 * 4));
+    ws.plan.pair_token = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.plan.pair_slot = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.plan.route_pair = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.act = reinterpret_cast<uint16_t*>(take((P + T) * 512 * 2));
+    ws.y = reinterpret_cast<uint16_t*>(take((P + T) * 2048 * 2));
+    ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
+    ws.bitmaps = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
+    ws.word_prefix = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
+    ws.words = words;
+    ws.plan.unique = &ws.control->unique;
+    ws.plan.status = &ws.control->status;
+    ws.bytes = offset;
+    return ws;
+}
+
+inline size_t workspace_bytes(int tokens) { return carve(nullptr, tokens).bytes; }
+
+// Arguments of the router stage (decode and prefill share them).
+struct RouteArgs {
+    const uint16_t* x;            // [T][2048] layer input
+    const uint16_t* norm;         // [2048] RMSNorm weight, or null for no norm
+    float eps;
+    const uint16_t* router;       // [256][2048], or null when logits_in is given
+    const uint16_t* logits_in;    // [T][256] caller logits for top-k, or null
+    const uint16_t* shared_gate;  // [2048] shared_expert_gate weight, or null
+    int tokens;
+    uint16_t* normed;             // [T][2048] normalised input (when norm)
+    uint16_t* logits;             // [T][256]
+    int64_t* indices;             // [T][8]
+    uint16_t* weights;            // [T][8]
+    uint16_t* sg;                 // [T]
+    Plan plan;
+    Workspace ws;
+};
+
+// Expert stage arguments.  Experts are addressed through a per-layer table of
+// 256 (gate_up, down) device addresses; the shared expert through its three
+// projection pointers.
+struct ExpertArgs {
+    const uint16_t* x;            // [T][2048] expert input (normalised when the layer norms)
+    const int64_t* expert_ptrs;   // [256][2] gate_up [1024,2048] and down [2048,512] addresses
+    const uint16_t* shared_gate_proj;  // [512][2048] or null
+    const uint16_t* shared_up_proj;    // [512][2048]
+    const uint16_t* shared_down;       // [2048][512]
+    const uint16_t* weights;      // [T][8] routing weights by slot
+    const uint16_t* sg;           // [T] shared gate values
+    const uint16_t* residual;     // [T][2048] or null
+    uint16_t* out;                // [T][2048]
+    int tokens;
+    Plan plan;
+    Workspace ws;
+};
+
+// Optional per-stage timing: when a stage's bit is enabled, each launch of
+// that stage is bracketed by a pair of HIP events on its stream.
+enum Stage : int {
+    kStageRoute = 1,
+    kStageGateUp = 2,
+    kStageDown = 4,
+    kStageCombine = 8,
+    kStageGather = 16,
+};
+void timing_mark(int stage, hipStream_t stream, bool start);
+
+hipError_t launch_route(const RouteArgs& args, hipStream_t stream);
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream);
+hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                         const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
+                         int max_copies, int stripes, int32_t* status, hipStream_t stream);
+hipError_t launch_matvec(const int64_t* table, const uint16_t* x, uint16_t* result, int K, int N, int column,
+                         int shared_x, int stride, int experts, hipStream_t stream);
+hipError_t launch_ordered_sum(const int64_t* table, const uint16_t* hot, const uint16_t* cold, const uint16_t* router,
+                              uint16_t* out, int stride, hipStream_t stream);
+hipError_t launch_gate_silu(const int64_t* table, const uint16_t* hidden, uint16_t* active, int stride, int experts,
+                            hipStream_t stream);
+hipError_t launch_project(const int64_t* pointers, const int32_t* routes, const uint16_t* X, uint16_t* Y, int in,
+                          int out, int down, int experts, hipStream_t stream);
+hipError_t launch_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows, hipStream_t stream);
+hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
+                                uint16_t* out, int tokens, int hybrid, hipStream_t stream);
+hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
+hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
+                              int64_t first, hipStream_t stream);
+
+}  // namespace lrmoe

@@ -1,0 +1,445 @@
+// Router (softmax/top-k/renormalise) and route bucketing kernels.
+//
+// Semantics follow the Transformers Qwen3_5MoeTopKRouter.forward that the
+// reference patches around (modeling_qwen3_5_moe.py, called from
+// SparseMoeBlock.forward; edge35b/expert_stream.py:383-454 receives its
+// top_k_index / top_k_weights), and the reference's bucketing:
+// edge35b/fused_experts.py:47-54 (routes sorted by expert),
+// edge35b/block_experts.py:102-121 (experts ascending, tokens ascending,
+// inverse map per token), edge35b/pipeline.py:59-76.
+//
+// Router logits use one fixed fp32 reduction order so that indices are
+// reproducible bit-for-bit: lane l of a wave owns the 32 contiguous elements
+// [32l, 32l+32) of the 2048-long dot product and accumulates them in order
+// with fmaf from +0, then the 64 partials meet in an xor butterfly with
+// offsets 1,2,4,...,32.  Top-k ranks by (bf16 logit desc, expert id asc).
+#include "lrmoe_device.h"
+#include "lrmoe_internal.h"
+
+namespace lrmoe {
+namespace {
+
+constexpr int kTokTile = 16;     // tokens per router workgroup
+constexpr int kXStride = kHidden + 8;  // LDS row stride in bf16 (16-byte pad)
+
+// Stage up to 16 token rows of the router input into LDS, applying the
+// RMSNorm (x * r) * (1 + w) with r = 1/sqrt(sum(x^2)/2048 + eps) when `norm`
+// is given.  One wave per token; lane l owns elements [32l, 32l+32).
+__device__ void stage_tokens(uint16_t* xs, const uint16_t* x, const uint16_t* norm, float eps, int t0, int count,
+                             uint16_t* normed_out) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    for (int t = wave; t < count; t += 4) {
+        const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(t0 + t) * kHidden + 32 * lane);
+        uint4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = src[i];
+        if (norm != nullptr) {
+            float f[32];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) unpack8(v[i], f + 8 * i);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(f[j], f[j], acc);
+            const float mean = wave_butterfly_sum(acc) / static_cast<float>(kHidden);
+            const float r = 1.0f / __builtin_sqrtf(mean + eps);
+            const uint4* wsrc = reinterpret_cast<const uint4*>(norm + 32 * lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 w = wsrc[i];
+                float wf[8];
+                unpack8(w, wf);
+                uint32_t o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = f2bf((f[8 * i + j] * r) * (1.0f + wf[j]));
+                v[i] = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+            }
+            if (normed_out != nullptr) {
+                uint4* dst = reinterpret_cast<uint4*>(normed_out + static_cast<size_t>(t0 + t) * kHidden + 32 * lane);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[i] = v[i];
+            }
+        }
+        uint4* dst = reinterpret_cast<uint4*>(xs + t * kXStride + 32 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = v[i];
+    }
+}
+
+// Fixed-order dot of this lane's 32 weights with token row `t` in LDS.
+__device__ __forceinline__ float lane_dot(const float* w, const uint16_t* xs, int t, int lane) {
+    const uint4* row = reinterpret_cast<const uint4*>(xs + t * kXStride + 32 * lane);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float xf[8];
+        unpack8(row[i], xf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(w[8 * i + j], xf[j], acc);
+    }
+    return acc;
+}
+
+// Top-8 + softmax + renormalisation for token `t` by one wave.  Lane l holds
+// the logits of experts 4l..4l+3.  Writes indices (rank order) and weights;
+// returns this lane's chosen expert when lane < 8 (else -1).
+__device__ int topk_token(const uint16_t* logits_row, int64_t* indices_row, uint16_t* weights_row, bool coherent) {
+    const int lane = threadIdx.x & 63;
+    uint64_t packed;
+    if (coherent) {
+        packed = load_agent_u64(reinterpret_cast<const uint64_t*>(logits_row) + lane);
+    } else {
+        packed = reinterpret_cast<const uint64_t*>(logits_row)[lane];
+    }
+    uint32_t bits[4], keys[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
+        keys[j] = route_key(bits[j], 4 * lane + j) + 1u;  // +1 keeps 0 free as "taken"
+    }
+    uint32_t chosen[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        uint32_t mine = keys[0];
+#pragma unroll
+        for (int j = 1; j < 4; ++j) mine = keys[j] > mine ? keys[j] : mine;
+        const uint32_t best = wave_max_u32(mine);
+        chosen[k] = best - 1u;
+        const int expert = 255 - static_cast<int>((best - 1u) & 255u);
+        if ((expert >> 2) == lane) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) keys[j] = (j == (expert & 3)) ? 0u : keys[j];
+        }
+    }
+    const float top = bf2f(key_bits(chosen[0]));
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
+    const float total = wave_butterfly_sum(part);
+    float prob[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) prob[k] = lr_exp(bf2f(key_bits(chosen[k])) - top) / total;
+    float sum = prob[0];
+#pragma unroll
+    for (int k = 1; k < kTopK; ++k) sum = sum + prob[k];
+    int mine_expert = -1;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        if (lane == k) {
+            mine_expert = 255 - static_cast<int>(chosen[k] & 255u);
+            indices_row[k] = mine_expert;
+            weights_row[k] = static_cast<uint16_t>(f2bf(prob[k] / sum));
+        }
+    }
+    return mine_expert;
+}
+
+// Block-wide exclusive scan of one value per thread (256 threads).
+__device__ uint32_t block_exclusive_scan(uint32_t value, uint32_t* scratch, uint32_t* total) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    uint32_t inclusive = value;
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const uint32_t up = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset, kWave));
+        if (lane >= offset) inclusive += up;
+    }
+    if (lane == kWave - 1) scratch[wave] = inclusive;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += scratch[w];
+    if (total != nullptr) *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    __syncthreads();
+    return before + inclusive - value;
+}
+
+// Bucket <= 64 tokens held in LDS (ids[t*8 + r]) with one 256-thread
+// workgroup: thread e owns expert e.  `valid` must already be checked.
+__device__ void bucket_small(const int32_t* ids, int tokens, const Plan& plan) {
+    __shared__ uint32_t scan_scratch[4];
+    const int e = threadIdx.x;
+    uint32_t count = 0;
+    for (int i = 0; i < tokens * kTopK; ++i) count += (ids[i] == e) ? 1u : 0u;
+    uint32_t pairs_total = 0, unique_total = 0;
+    const uint32_t pair_offset = block_exclusive_scan(count, scan_scratch, &pairs_total);
+    const uint32_t rank = block_exclusive_scan(count ? 1u : 0u, scan_scratch, &unique_total);
+    if (count) {
+        plan.expert[rank] = e;
+        plan.offset[rank] = static_cast<int32_t>(pair_offset);
+        uint32_t k = 0;
+        for (int t = 0; t < tokens; ++t) {
+            for (int r = 0; r < kTopK; ++r) {
+                if (ids[t * kTopK + r] == e) {
+                    const int p = static_cast<int>(pair_offset + k++);
+                    plan.pair_token[p] = t;
+                    plan.pair_slot[p] = r;
+                    int order = 0;
+                    for (int q = 0; q < kTopK; ++q) order += (ids[t * kTopK + q] < e) ? 1 : 0;
+                    plan.route_pair[t * kTopK + order] = p;
+                }
+            }
+        }
+    }
+    if (e == 0) {
+        plan.offset[unique_total] = static_cast<int32_t>(pairs_total);
+        *plan.unique = static_cast<int32_t>(unique_total);
+    }
+}
+
+// Checks ids and returns the status bits for the whole set.
+__device__ int32_t validate_ids(const int32_t* ids, int tokens) {
+    __shared__ int32_t flags;
+    if (threadIdx.x == 0) flags = 0;
+    __syncthreads();
+    int32_t mine = 0;
+    for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
+        const int e = ids[i];
+        if (e < 0 || e >= kExperts) mine |= kStatusBadExpert;
+        const int t = i / kTopK;
+        for (int q = t * kTopK; q < i; ++q) mine |= (ids[q] == e) ? kStatusRepeatedExpert : 0;
+    }
+    if (mine) atomicOr(&flags, mine);
+    __syncthreads();
+    return flags;
+}
+
+// Logits for a tile of <= 16 tokens and 4*RPW router rows per workgroup
+// (RPW rows per wave), or the shared-expert gate (the last blockIdx.y, wave
+// 0).  With FUSED_TOPK (the whole call is one token tile), the last
+// workgroup to finish also runs top-k, renormalisation and bucketing.
+template <bool FUSED_TOPK, int RPW>
+__global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kTokTile * kXStride];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * kTokTile;
+    const int count = min(kTokTile, a.tokens - t0);
+    constexpr int kRowGroups = kExperts / (4 * RPW);
+
+    if (!FUSED_TOPK && blockIdx.x == 0 && blockIdx.y == 0) {
+        // Clear the prefill histogram and bitmaps; the top-k kernel that fills
+        // them runs after this launch on the same stream.
+        for (int i = threadIdx.x; i < kExperts; i += blockDim.x) a.ws.counts[i] = 0;
+        for (int i = threadIdx.x; i < kExperts * a.ws.words; i += blockDim.x) a.ws.bitmaps[i] = 0;
+        if (threadIdx.x == 0) *a.plan.status = 0;
+    }
+
+    // Issue this wave's router-row loads before staging the tokens.
+    const bool shared_row = blockIdx.y == kRowGroups;
+    const bool router_rows = !shared_row && a.router != nullptr;
+    uint4 wraw[RPW][4];
+    if (router_rows) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = (blockIdx.y * 4 + wave) * RPW + i;
+            const uint4* src = reinterpret_cast<const uint4*>(a.router + static_cast<size_t>(row) * kHidden + 32 * lane);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wraw[i][q] = src[q];
+        }
+    } else if (a.shared_gate != nullptr) {
+        const uint4* src = reinterpret_cast<const uint4*>(a.shared_gate + 32 * lane);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wraw[0][q] = src[q];
+    }
+
+    if (router_rows || (shared_row && a.shared_gate != nullptr) || (blockIdx.y == 0 && a.norm != nullptr)) {
+        stage_tokens(xs, a.x, a.norm, a.eps, t0, count, blockIdx.y == 0 ? a.normed : nullptr);
+    }
+    __syncthreads();
+
+    if (router_rows) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = (blockIdx.y * 4 + wave) * RPW + i;
+            float w[32];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) unpack8(wraw[i][q], w + 8 * q);
+            for (int t = 0; t < count; ++t) {
+                const float s = wave_butterfly_sum(lane_dot(w, xs, t, lane));
+                if (lane == 0) a.logits[static_cast<size_t>(t0 + t) * kExperts + row] = static_cast<uint16_t>(f2bf(s));
+            }
+        }
+    } else if (wave == 0 && a.shared_gate != nullptr) {
+        float w[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(wraw[0][q], w + 8 * q);
+        for (int t = 0; t < count; ++t) {
+            const float z = rbf(wave_butterfly_sum(lane_dot(w, xs, t, lane)));
+            if (lane == 0) a.sg[t0 + t] = static_cast<uint16_t>(f2bf(1.0f / (1.0f + lr_exp(-z))));
+        }
+    }
+
+    if constexpr (FUSED_TOPK) {
+        __shared__ uint32_t ticket;
+        __shared__ int32_t ids[kTokTile * kTopK];
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) ticket = atomicAdd(&a.ws.control->route_counter, 1u);
+        __syncthreads();
+        if (ticket != gridDim.x * gridDim.y - 1) return;
+        __threadfence();
+        const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
+        for (int t = wave; t < a.tokens; t += 4) {
+            const int expert = topk_token(logits + static_cast<size_t>(t) * kExperts, a.indices + t * kTopK,
+                                          a.weights + t * kTopK, true);
+            if (lane < kTopK) ids[t * kTopK + lane] = expert;
+        }
+        __syncthreads();
+        bucket_small(ids, a.tokens, a.plan);
+        if (threadIdx.x == 0) {
+            *a.plan.status = 0;
+            __hip_atomic_store(&a.ws.control->route_counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Prefill top-k: one wave per token; also records the expert histogram and
+// per-expert token bitmaps used by the bucketing kernels.
+__global__ __launch_bounds__(256) void topk_tokens(RouteArgs a) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= a.tokens) return;
+    const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
+    const int expert = topk_token(logits + static_cast<size_t>(t) * kExperts, a.indices + t * kTopK,
+                                  a.weights + t * kTopK, false);
+    if (lane < kTopK) {
+        atomicAdd(&a.ws.counts[expert], 1u);
+        atomicOr(&a.ws.bitmaps[expert * a.ws.words + (t >> 5)], 1u << (t & 31));
+    }
+}
+
+// Histogram + bitmaps from caller-provided indices (standalone bucketing of
+// more than 64 tokens), with validation.
+__global__ __launch_bounds__(256) void bucket_histogram(const int64_t* indices, int tokens, Workspace ws, Plan plan) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= tokens * kTopK) return;
+    const int t = i / kTopK;
+    const int64_t e = indices[i];
+    int32_t bad = 0;
+    if (e < 0 || e >= kExperts) bad |= kStatusBadExpert;
+    for (int q = t * kTopK; q < i; ++q) bad |= (indices[q] == e) ? kStatusRepeatedExpert : 0;
+    if (bad) {
+        atomicOr(plan.status, bad);
+        return;
+    }
+    atomicAdd(&ws.counts[e], 1u);
+    atomicOr(&ws.bitmaps[e * ws.words + (t >> 5)], 1u << (t & 31));
+}
+
+__global__ __launch_bounds__(256) void clear_histogram(Workspace ws, Plan plan) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0) *plan.status = 0;
+    if (i < kExperts) ws.counts[i] = 0;
+    for (int j = i; j < kExperts * ws.words; j += gridDim.x * blockDim.x) ws.bitmaps[j] = 0;
+}
+
+// Single workgroup: pair offsets and unique list from the histogram, and the
+// per-expert exclusive prefix of bitmap popcounts by 32-token word.
+__global__ __launch_bounds__(256) void bucket_scan(Workspace ws, Plan plan) {
+    __shared__ uint32_t scan_scratch[4];
+    const int e = threadIdx.x;
+    const int32_t status = *plan.status;
+    const uint32_t count = status ? 0u : ws.counts[e];
+    uint32_t pairs_total = 0, unique_total = 0;
+    const uint32_t pair_offset = block_exclusive_scan(count, scan_scratch, &pairs_total);
+    const uint32_t rank = block_exclusive_scan(count ? 1u : 0u, scan_scratch, &unique_total);
+    if (count) {
+        plan.expert[rank] = e;
+        plan.offset[rank] = static_cast<int32_t>(pair_offset);
+    }
+    uint32_t running = pair_offset;
+    for (int w = 0; w < ws.words; ++w) {
+        ws.word_prefix[e * ws.words + w] = running;
+        running += __popc(ws.bitmaps[e * ws.words + w]);
+    }
+    if (e == 0) {
+        plan.offset[unique_total] = static_cast<int32_t>(pairs_total);
+        *plan.unique = static_cast<int32_t>(unique_total);
+    }
+}
+
+// One thread per token: place its 8 routes.
+__global__ __launch_bounds__(256) void bucket_fill(const int64_t* indices, int tokens, Workspace ws, Plan plan) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tokens) return;
+    if (*plan.status) {
+        for (int r = 0; r < kTopK; ++r) plan.route_pair[t * kTopK + r] = -1;
+        return;
+    }
+    int ids[kTopK];
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) ids[r] = static_cast<int>(indices[t * kTopK + r]);
+    const uint32_t below = (1u << (t & 31)) - 1u;
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) {
+        const int e = ids[r];
+        const int word = e * ws.words + (t >> 5);
+        const int p = static_cast<int>(ws.word_prefix[word] + __popc(ws.bitmaps[word] & below));
+        plan.pair_token[p] = t;
+        plan.pair_slot[p] = r;
+        int order = 0;
+#pragma unroll
+        for (int q = 0; q < kTopK; ++q) order += (ids[q] < e) ? 1 : 0;
+        plan.route_pair[t * kTopK + order] = p;
+    }
+}
+
+// Standalone bucketing of <= 64 caller-provided tokens in one workgroup.
+__global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan) {
+    __shared__ int32_t ids[64 * kTopK];
+    for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
+        const int64_t e = indices[i];
+        ids[i] = (e < 0 || e >= kExperts) ? -1 : static_cast<int32_t>(e);
+    }
+    __syncthreads();
+    const int32_t status = validate_ids(ids, tokens);
+    if (status) {
+        if (threadIdx.x == 0) {
+            *plan.status = status;
+            *plan.unique = 0;
+            plan.offset[0] = 0;
+        }
+        for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) plan.route_pair[i] = -1;
+        return;
+    }
+    bucket_small(ids, tokens, plan);
+    if (threadIdx.x == 0) *plan.status = 0;
+}
+
+}  // namespace
+
+hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
+    if (a.tokens <= 0) return hipSuccess;
+    const int tiles = (a.tokens + kTokTile - 1) / kTokTile;
+    timing_mark(kStageRoute, stream, true);
+    if (a.tokens <= kTokTile) {
+        // Decode: one router row per wave, 64 workgroups + the shared gate.
+        hipLaunchKernelGGL((router_logits<true, 1>), dim3(1, kExperts / 4 + 1), dim3(256), 0, stream, a);
+        timing_mark(kStageRoute, stream, false);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((router_logits<false, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(topk_tokens, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, a.ws, a.plan);
+    hipLaunchKernelGGL(bucket_fill, dim3((a.tokens + 255) / 256), dim3(256), 0, stream, a.indices, a.tokens, a.ws,
+                       a.plan);
+    timing_mark(kStageRoute, stream, false);
+    return hipGetLastError();
+}
+
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream) {
+    if (tokens <= 0) return hipSuccess;
+    if (tokens <= 64) {
+        hipLaunchKernelGGL(bucket_small_kernel, dim3(1), dim3(256), 0, stream, indices, tokens, plan);
+        return hipGetLastError();
+    }
+    const int clear_blocks = min(64, (kExperts * ws.words + 255) / 256);
+    hipLaunchKernelGGL(clear_histogram, dim3(clear_blocks > 0 ? clear_blocks : 1), dim3(256), 0, stream, ws, plan);
+    hipLaunchKernelGGL(bucket_histogram, dim3((tokens * kTopK + 255) / 256), dim3(256), 0, stream, indices, tokens, ws,
+                       plan);
+    hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, ws, plan);
+    hipLaunchKernelGGL(bucket_fill, dim3((tokens + 255) / 256), dim3(256), 0, stream, indices, tokens, ws, plan);
+    return hipGetLastError();
+}
+
+}  // namespace lrmoe

@@ -1,0 +1,453 @@
+/*
+ * lro.c -- CPU oracle for the MoE expert-layer hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (lightreason_amd/) links,
+ * loads or calls this file; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, and only as the checker.
+ *
+ * It restates, in plain C with explicit fmaf() and no FP contraction, the
+ * arithmetic the reference performs on this path:
+ *
+ *   - expert SwiGLU arithmetic and its bf16 rounding points:
+ *       edge35b/cpu_experts.c:11-22 (from_bfloat / to_bfloat),
+ *       :29-41 (dot: two 8-lane FMA accumulators, then add + hadd tree),
+ *       :43-71 (expert_rows), :74-105 (expert_block_rows);
+ *   - the ordered bf16 combine: edge35b/fused_experts.py:27-37 (_ordered_sum),
+ *       edge35b/block_experts.py:31-49 (_combine), edge35b/cpu_route.py:66-68;
+ *   - route bucketing: edge35b/fused_experts.py:47-54 (T=1 schedule),
+ *       edge35b/block_experts.py:102-121 (experts ascending, tokens ascending,
+ *       inverse map per token in ascending-expert order);
+ *   - the router, shared expert, shared gate and RMSNorm of the third-party
+ *       Transformers Qwen3_5Moe classes the reference patches
+ *       (modeling_qwen3_5_moe.py: TopKRouter.forward, MLP.forward,
+ *       SparseMoeBlock.forward, RMSNorm.forward), called from
+ *       edge35b/expert_stream.py:383-454.
+ *
+ * The router GEMV, the softmax denominator and the RMSNorm sum of squares use
+ * one fixed fp32 reduction order (64 lane partials over contiguous chunks,
+ * then an xor butterfly with offsets 1,2,4,8,16,32) so that routing indices
+ * can be reproduced bit-exactly by the HIP kernels.  Top-k ties break toward
+ * the lower expert id.  exp() for softmax/sigmoid is lro_exp (Cody-Waite
+ * reduction plus a degree-7 Taylor polynomial), reproducible bit-for-bit on the
+ * device; the expert SiLU keeps libm expf, exactly as cpu_experts.c does.
+ *
+ * Build: oracle/Makefile (gcc -O3 -mavx2 -mfma -ffp-contract=off).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define LRO_HIDDEN 2048
+#define LRO_INNER 512
+#define LRO_EXPERTS 256
+#define LRO_TOPK 8
+
+/* ---- bf16 helpers: cpu_experts.c:11-22 ---------------------------------- */
+
+float lro_bf16_value(uint16_t value) {
+    uint32_t bits = (uint32_t)value << 16;
+    float result;
+    memcpy(&result, &bits, sizeof(result));
+    return result;
+}
+
+uint16_t lro_bf16_round(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, sizeof(bits));
+    return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+static inline float rbf(float value) { return lro_bf16_value(lro_bf16_round(value)); }
+
+/* ---- exp(): Cody-Waite reduction + degree-7 Taylor polynomial ------------ */
+/* x = k ln2 + r with k = rint(x log2 e); exp(r) by Horner on |r| <= ln2/2;
+ * result = p * 2^k applied as two exact power-of-two scalings.  Inputs below
+ * -87 return 0 and above 88.72283935546875 return +inf so every finite result
+ * is a normal float and no step depends on denormal handling. */
+static const float LRO_LOG2E = 0x1.715476p+0f;
+static const float LRO_LN2_HI = 0x1.62e400p-1f;
+static const float LRO_LN2_LO = 0x1.7f7d1cp-20f;
+static const float LRO_C7 = 0x1.a01a02p-13f; /* 1/5040 */
+static const float LRO_C6 = 0x1.6c16c2p-10f; /* 1/720 */
+static const float LRO_C5 = 0x1.111112p-7f;  /* 1/120 */
+static const float LRO_C4 = 0x1.555556p-5f;  /* 1/24 */
+static const float LRO_C3 = 0x1.555556p-3f;  /* 1/6 */
+
+static inline float pow2i(int k) {
+    uint32_t bits = (uint32_t)(k + 127) << 23;
+    float result;
+    memcpy(&result, &bits, sizeof(result));
+    return result;
+}
+
+float lro_exp(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    float k = rintf(x * LRO_LOG2E);
+    float r = fmaf(-k, LRO_LN2_HI, x);
+    r = fmaf(-k, LRO_LN2_LO, r);
+    float p = LRO_C7;
+    p = fmaf(p, r, LRO_C6);
+    p = fmaf(p, r, LRO_C5);
+    p = fmaf(p, r, LRO_C4);
+    p = fmaf(p, r, LRO_C3);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ki = (int)k;
+    int k1 = ki / 2;
+    int k2 = ki - k1;
+    return (p * pow2i(k1)) * pow2i(k2);
+}
+
+/* ---- synthetic generator ------------------------------------------------ */
+/* Counter-based: h = splitmix64(key + index), key = splitmix64(seed * phi +
+ * stream).  Irwin-Hall sum of the four 16-bit fields of h, centred and scaled
+ * to unit variance in double, times sigma, rounded to float then bf16 (RNE). */
+static inline uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void lro_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t stream,
+                          double sigma, int64_t first) {
+    const uint64_t key = splitmix64(seed * 0x9E3779B97F4A7C15ull + stream);
+    const double inv_std = 1.0 / sqrt(1431655765.0);
+    for (int64_t i = 0; i < count; ++i) {
+        uint64_t h = splitmix64(key + (uint64_t)(first + i));
+        int64_t s = (int64_t)(h & 0xffff) + (int64_t)((h >> 16) & 0xffff) +
+                    (int64_t)((h >> 32) & 0xffff) + (int64_t)(h >> 48);
+        double z = ((double)s - 131070.0) * inv_std;
+        out[i] = lro_bf16_round((float)(z * sigma));
+    }
+}
+
+/* ---- expert arithmetic: cpu_experts.c:29-105 ---------------------------- */
+
+/* cpu_experts.c:29-41: low/high 8-lane FMA accumulators over 16-element
+ * steps, lanes = low + high, (lanes[0:4] + lanes[4:8]), then two hadds. */
+float lro_expert_dot(const uint16_t *weights, const float *input, int width) {
+    float low[8] = {0}, high[8] = {0};
+    for (int i = 0; i < width; i += 16) {
+        for (int j = 0; j < 8; ++j) {
+            low[j] = fmaf(lro_bf16_value(weights[i + j]), input[i + j], low[j]);
+            high[j] = fmaf(lro_bf16_value(weights[i + 8 + j]), input[i + 8 + j], high[j]);
+        }
+    }
+    float lanes[8];
+    for (int j = 0; j < 8; ++j) lanes[j] = low[j] + high[j];
+    float s[4];
+    for (int j = 0; j < 4; ++j) s[j] = lanes[j] + lanes[j + 4];
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+/* One (expert, token) pair: cpu_experts.c:54-69 for a single expert.  gate and
+ * up are the two [512, 2048] halves (for routed experts up = gate + 512*2048),
+ * down is [2048, 512]; x is the token as floats; y receives 2048 bf16. */
+void lro_expert_pair(const uint16_t *gate, const uint16_t *up, const uint16_t *down,
+                     const float *x, uint16_t *y) {
+    float active[LRO_INNER];
+    for (int row = 0; row < LRO_INNER; ++row) {
+        float g = rbf(lro_expert_dot(gate + (size_t)row * LRO_HIDDEN, x, LRO_HIDDEN));
+        float u = rbf(lro_expert_dot(up + (size_t)row * LRO_HIDDEN, x, LRO_HIDDEN));
+        float silu = rbf(g / (1.0f + expf(-g)));
+        active[row] = rbf(silu * u);
+    }
+    for (int row = 0; row < LRO_HIDDEN; ++row) {
+        y[row] = lro_bf16_round(lro_expert_dot(down + (size_t)row * LRO_INNER, active, LRO_INNER));
+    }
+}
+
+static void to_floats(const uint16_t *x, float *out, int n) {
+    for (int i = 0; i < n; ++i) out[i] = lro_bf16_value(x[i]);
+}
+
+/* cpu_experts.c:43-71 (single-threaded restatement). */
+void lro_expert_rows(const uint16_t *const *gate_up, const uint16_t *const *down,
+                     const uint16_t *input, uint16_t *output, int experts) {
+    float hidden[LRO_HIDDEN];
+    to_floats(input, hidden, LRO_HIDDEN);
+    for (int e = 0; e < experts; ++e) {
+        lro_expert_pair(gate_up[e], gate_up[e] + (size_t)LRO_INNER * LRO_HIDDEN, down[e], hidden,
+                        output + (size_t)e * LRO_HIDDEN);
+    }
+}
+
+/* cpu_experts.c:74-105: row i uses input token token_ids[i]. */
+void lro_expert_block_rows(const uint16_t *const *gate_up, const uint16_t *const *down,
+                           const uint16_t *input, const int32_t *token_ids, uint16_t *output,
+                           int tokens, int experts) {
+    float *hidden = (float *)malloc(sizeof(float) * (size_t)tokens * LRO_HIDDEN);
+    for (int t = 0; t < tokens; ++t) to_floats(input + (size_t)t * LRO_HIDDEN, hidden + (size_t)t * LRO_HIDDEN, LRO_HIDDEN);
+    for (int e = 0; e < experts; ++e) {
+        lro_expert_pair(gate_up[e], gate_up[e] + (size_t)LRO_INNER * LRO_HIDDEN, down[e],
+                        hidden + (size_t)token_ids[e] * LRO_HIDDEN, output + (size_t)e * LRO_HIDDEN);
+    }
+    free(hidden);
+}
+
+/* ---- fixed-order reductions (router, shared gate, RMSNorm) -------------- */
+
+static float butterfly64(float *p) {
+    for (int offset = 1; offset < 64; offset <<= 1) {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ offset];
+        memcpy(p, q, sizeof(q));
+    }
+    return p[0];
+}
+
+/* Lane l of 64 owns elements [l*K/64, (l+1)*K/64) and accumulates them in
+ * ascending order with fmaf from +0; lane partials meet in butterfly64. */
+float lro_canon_dot(const uint16_t *weights, const float *x, int width) {
+    float p[64];
+    const int chunk = width / 64;
+    for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < chunk; ++j) acc = fmaf(lro_bf16_value(weights[l * chunk + j]), x[l * chunk + j], acc);
+        p[l] = acc;
+    }
+    return butterfly64(p);
+}
+
+/* Orderable 24-bit key: bf16 value (with -0 folded onto +0), then lower id. */
+static uint32_t route_key(uint16_t bits, int expert) {
+    if (bits == 0x8000) bits = 0;
+    uint32_t ordered = (bits & 0x8000) ? (uint32_t)(~bits & 0xffff) : (uint32_t)(bits | 0x8000);
+    return (ordered << 8) | (uint32_t)(255 - expert);
+}
+
+/* Router for one token: logits = bf16(x . Wr^T) (fixed order), softmax in fp32
+ * over 256 experts, top-8 by (logit desc, id asc), renormalised over the 8 in
+ * fp32 (sequential sum in rank order), weights rounded to bf16.  Indices are
+ * written in rank order, like torch.topk(sorted=True). */
+static void route_token(const float *x, const uint16_t *router, uint16_t *logits,
+                        int64_t *indices, uint16_t *weights) {
+    float value[LRO_EXPERTS];
+    for (int e = 0; e < LRO_EXPERTS; ++e) {
+        logits[e] = lro_bf16_round(lro_canon_dot(router + (size_t)e * LRO_HIDDEN, x, LRO_HIDDEN));
+        value[e] = lro_bf16_value(logits[e]);
+    }
+    int chosen[LRO_TOPK];
+    uint8_t taken[LRO_EXPERTS] = {0};
+    for (int k = 0; k < LRO_TOPK; ++k) {
+        uint32_t best = 0;
+        int best_e = -1;
+        for (int e = 0; e < LRO_EXPERTS; ++e) {
+            if (taken[e]) continue;
+            uint32_t key = route_key(logits[e], e);
+            if (best_e < 0 || key > best) {
+                best = key;
+                best_e = e;
+            }
+        }
+        taken[best_e] = 1;
+        chosen[k] = best_e;
+    }
+    const float top = value[chosen[0]];
+    float expo[LRO_EXPERTS];
+    for (int e = 0; e < LRO_EXPERTS; ++e) expo[e] = lro_exp(value[e] - top);
+    float p[64];
+    for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < 4; ++j) acc = acc + expo[4 * l + j];
+        p[l] = acc;
+    }
+    const float total = butterfly64(p);
+    float prob[LRO_TOPK];
+    for (int k = 0; k < LRO_TOPK; ++k) prob[k] = expo[chosen[k]] / total;
+    float sum = prob[0];
+    for (int k = 1; k < LRO_TOPK; ++k) sum = sum + prob[k];
+    for (int k = 0; k < LRO_TOPK; ++k) {
+        indices[k] = chosen[k];
+        weights[k] = lro_bf16_round(prob[k] / sum);
+    }
+}
+
+void lro_route(const uint16_t *x, const uint16_t *router, int tokens, uint16_t *logits,
+               int64_t *indices, uint16_t *weights) {
+    float hidden[LRO_HIDDEN];
+    for (int t = 0; t < tokens; ++t) {
+        to_floats(x + (size_t)t * LRO_HIDDEN, hidden, LRO_HIDDEN);
+        route_token(hidden, router, logits + (size_t)t * LRO_EXPERTS, indices + (size_t)t * LRO_TOPK,
+                    weights + (size_t)t * LRO_TOPK);
+    }
+}
+
+/* Shared-expert gate: sg = bf16(sigmoid(bf16(x . w_sg))) with the fixed
+ * reduction order and lro_exp. */
+void lro_shared_gate(const uint16_t *x, const uint16_t *gate_weight, int tokens, uint16_t *out) {
+    float hidden[LRO_HIDDEN];
+    for (int t = 0; t < tokens; ++t) {
+        to_floats(x + (size_t)t * LRO_HIDDEN, hidden, LRO_HIDDEN);
+        float z = rbf(lro_canon_dot(gate_weight, hidden, LRO_HIDDEN));
+        out[t] = lro_bf16_round(1.0f / (1.0f + lro_exp(-z)));
+    }
+}
+
+/* RMSNorm with the (1 + w) scale: n = bf16((x * r) * (1 + w)),
+ * r = 1 / sqrt(sum(x^2)/H + eps), sum(x^2) in the fixed order. */
+void lro_rmsnorm(const uint16_t *x, const uint16_t *weight, int tokens, float eps, uint16_t *out) {
+    float hidden[LRO_HIDDEN];
+    for (int t = 0; t < tokens; ++t) {
+        to_floats(x + (size_t)t * LRO_HIDDEN, hidden, LRO_HIDDEN);
+        float p[64];
+        for (int l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (int j = 0; j < LRO_HIDDEN / 64; ++j) {
+                float v = hidden[l * (LRO_HIDDEN / 64) + j];
+                acc = fmaf(v, v, acc);
+            }
+            p[l] = acc;
+        }
+        float mean = butterfly64(p) / (float)LRO_HIDDEN;
+        float r = 1.0f / sqrtf(mean + eps);
+        for (int i = 0; i < LRO_HIDDEN; ++i) {
+            out[(size_t)t * LRO_HIDDEN + i] =
+                lro_bf16_round((hidden[i] * r) * (1.0f + lro_bf16_value(weight[i])));
+        }
+    }
+}
+
+/* ---- bucketing ---------------------------------------------------------- */
+/* Unique experts ascending; per expert its (token, slot) pairs in ascending
+ * token order; route_pair[t*8 + r] = pair index of token t's r-th route in
+ * ascending-expert order.  Returns the unique count, or -1 for an
+ * out-of-range id, -2 for a token that repeats an expert. */
+int lro_bucket(const int64_t *indices, int tokens, int32_t *expert, int32_t *offset,
+               int32_t *pair_token, int32_t *pair_slot, int32_t *route_pair) {
+    int32_t count[LRO_EXPERTS] = {0};
+    for (int t = 0; t < tokens; ++t) {
+        for (int r = 0; r < LRO_TOPK; ++r) {
+            int64_t e = indices[t * LRO_TOPK + r];
+            if (e < 0 || e >= LRO_EXPERTS) return -1;
+            for (int q = 0; q < r; ++q) {
+                if (indices[t * LRO_TOPK + q] == e) return -2;
+            }
+            count[e] += 1;
+        }
+    }
+    int32_t start[LRO_EXPERTS];
+    int unique = 0, pairs = 0;
+    for (int e = 0; e < LRO_EXPERTS; ++e) {
+        start[e] = pairs;
+        if (count[e]) {
+            expert[unique] = e;
+            offset[unique] = pairs;
+            ++unique;
+        }
+        pairs += count[e];
+    }
+    offset[unique] = pairs;
+    int32_t fill[LRO_EXPERTS];
+    memcpy(fill, start, sizeof(fill));
+    for (int t = 0; t < tokens; ++t) {
+        int32_t order[LRO_TOPK];
+        for (int r = 0; r < LRO_TOPK; ++r) order[r] = r;
+        for (int i = 1; i < LRO_TOPK; ++i) {
+            for (int j = i; j > 0 && indices[t * LRO_TOPK + order[j - 1]] > indices[t * LRO_TOPK + order[j]]; --j) {
+                int32_t tmp = order[j];
+                order[j] = order[j - 1];
+                order[j - 1] = tmp;
+            }
+        }
+        for (int r = 0; r < LRO_TOPK; ++r) {
+            int slot = order[r];
+            int e = (int)indices[t * LRO_TOPK + slot];
+            int p = fill[e]++;
+            pair_token[p] = t;
+            pair_slot[p] = slot;
+            route_pair[t * LRO_TOPK + r] = p;
+        }
+    }
+    return unique;
+}
+
+/* ---- combine: fused_experts.py:27-37, block_experts.py:31-49 ------------ */
+/* out[t] = bf16 sum over token t's routes in ascending expert order of
+ * bf16(y[pair] * w[t, slot]), starting from 0, rounding after each multiply
+ * and add; then out = bf16(out + bf16(sg[t] * y_shared[t])) when y_shared is
+ * given (SparseMoeBlock.forward), then out = bf16(residual[t] + out) when a
+ * residual is given (decoder-layer residual add). */
+void lro_combine(const uint16_t *y, const int32_t *route_pair, const int32_t *pair_slot,
+                 const uint16_t *weights, const uint16_t *y_shared, const uint16_t *shared_gate,
+                 const uint16_t *residual, int tokens, uint16_t *out) {
+    for (int t = 0; t < tokens; ++t) {
+        for (int h = 0; h < LRO_HIDDEN; ++h) {
+            float acc = 0.0f;
+            for (int r = 0; r < LRO_TOPK; ++r) {
+                int p = route_pair[t * LRO_TOPK + r];
+                float scale = lro_bf16_value(weights[t * LRO_TOPK + pair_slot[p]]);
+                float value = lro_bf16_value(y[(size_t)p * LRO_HIDDEN + h]);
+                acc = rbf(acc + rbf(value * scale));
+            }
+            if (y_shared) {
+                float s = rbf(lro_bf16_value(shared_gate[t]) * lro_bf16_value(y_shared[(size_t)t * LRO_HIDDEN + h]));
+                acc = rbf(acc + s);
+            }
+            if (residual) acc = rbf(lro_bf16_value(residual[(size_t)t * LRO_HIDDEN + h]) + acc);
+            out[(size_t)t * LRO_HIDDEN + h] = lro_bf16_round(acc);
+        }
+    }
+}
+
+/* ---- a whole MoE layer for a set of tokens ------------------------------ */
+/* x: [tokens, 2048] (the layer input h when norm_weight is given, else the
+ * MoE input).  gate_up/down: 256 per-expert pointers.  The shared expert is
+ * (shared_gate_proj, shared_up_proj [512,2048], shared_down [2048,512],
+ * shared_expert_gate [2048]); pass shared_down == NULL for a routed-only
+ * layer.  With norm_weight: n = RMSNorm(h), out = bf16(h + MoE(n)). */
+void lro_moe_layer(const uint16_t *x, int tokens, const uint16_t *router,
+                   const uint16_t *const *gate_up, const uint16_t *const *down,
+                   const uint16_t *shared_gate_proj, const uint16_t *shared_up_proj,
+                   const uint16_t *shared_down, const uint16_t *shared_expert_gate,
+                   const uint16_t *norm_weight, float eps, uint16_t *out, int64_t *indices_out,
+                   uint16_t *weights_out) {
+    const size_t H = LRO_HIDDEN;
+    uint16_t *normed = NULL;
+    const uint16_t *input = x;
+    if (norm_weight) {
+        normed = (uint16_t *)malloc(sizeof(uint16_t) * tokens * H);
+        lro_rmsnorm(x, norm_weight, tokens, eps, normed);
+        input = normed;
+    }
+    uint16_t *logits = (uint16_t *)malloc(sizeof(uint16_t) * tokens * LRO_EXPERTS);
+    lro_route(input, router, tokens, logits, indices_out, weights_out);
+    int32_t expert[LRO_EXPERTS], offset[LRO_EXPERTS + 1];
+    int32_t *pair_token = (int32_t *)malloc(sizeof(int32_t) * tokens * LRO_TOPK);
+    int32_t *pair_slot = (int32_t *)malloc(sizeof(int32_t) * tokens * LRO_TOPK);
+    int32_t *route_pair = (int32_t *)malloc(sizeof(int32_t) * tokens * LRO_TOPK);
+    int unique = lro_bucket(indices_out, tokens, expert, offset, pair_token, pair_slot, route_pair);
+    uint16_t *y = (uint16_t *)malloc(sizeof(uint16_t) * tokens * LRO_TOPK * H);
+    float *hidden = (float *)malloc(sizeof(float) * tokens * H);
+    for (int t = 0; t < tokens; ++t) to_floats(input + t * H, hidden + t * H, (int)H);
+    for (int u = 0; u < unique; ++u) {
+        const uint16_t *gu = gate_up[expert[u]];
+        for (int p = offset[u]; p < offset[u + 1]; ++p) {
+            lro_expert_pair(gu, gu + (size_t)LRO_INNER * H, down[expert[u]], hidden + pair_token[p] * H, y + p * H);
+        }
+    }
+    uint16_t *y_shared = NULL, *sg = NULL;
+    if (shared_down) {
+        y_shared = (uint16_t *)malloc(sizeof(uint16_t) * tokens * H);
+        sg = (uint16_t *)malloc(sizeof(uint16_t) * tokens);
+        for (int t = 0; t < tokens; ++t) {
+            lro_expert_pair(shared_gate_proj, shared_up_proj, shared_down, hidden + t * H, y_shared + t * H);
+        }
+        lro_shared_gate(input, shared_expert_gate, tokens, sg);
+    }
+    lro_combine(y, route_pair, pair_slot, weights_out, y_shared, sg, norm_weight ? x : NULL, tokens, out);
+    free(y_shared);
+    free(sg);
+    free(hidden);
+    free(y);
+    free(route_pair);
+    free(pair_slot);
+    free(pair_token);
+    free(logits);
+    free(normed);
+}

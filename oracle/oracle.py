@@ -1,0 +1,238 @@
+"""ctypes view of the CPU oracle (lro.c) and of the reference CPU kernel.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py import this module, and only to check or time
+against it; the product package never does.
+
+Arrays are numpy: bf16 values travel as uint16 bit patterns.  ``reference()``
+loads ``_ref/libcpu_experts.so``, which oracle/Makefile compiles from the
+reference's own edge35b/cpu_experts.c; it is absent where the reference tree
+is absent, and callers must treat that as "not available", never as a pass.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "liblro.so"
+REF = HERE / "_ref" / "libcpu_experts.so"
+HIDDEN, INNER, EXPERTS, TOPK = 2048, 512, 256, 8
+EXPERT_ELEMENTS = 3 * INNER * HIDDEN
+
+_P = C.c_void_p
+
+
+def build(ref: bool | None = None) -> None:
+    """Compile liblro.so, and the reference kernel when its source exists."""
+    targets = ["oracle"]
+    if ref or (ref is None and Path("/root/reference/edge35b/cpu_experts.c").exists()):
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", str(HERE), *targets], check=True)
+
+
+def _ptr(array: np.ndarray | None) -> int | None:
+    if array is None:
+        return None
+    if not array.flags["C_CONTIGUOUS"]:
+        raise ValueError("oracle arrays must be C-contiguous")
+    return array.ctypes.data
+
+
+@lru_cache(maxsize=1)
+def lib() -> C.CDLL:
+    if not LIB.exists():
+        build(ref=False)
+    so = C.CDLL(str(LIB))
+    so.lro_bf16_value.argtypes = [C.c_uint16]
+    so.lro_bf16_value.restype = C.c_float
+    so.lro_bf16_round.argtypes = [C.c_float]
+    so.lro_bf16_round.restype = C.c_uint16
+    so.lro_exp.argtypes = [C.c_float]
+    so.lro_exp.restype = C.c_float
+    so.lro_fill_normal_bf16.argtypes = [_P, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_int64]
+    so.lro_expert_dot.argtypes = [_P, _P, C.c_int]
+    so.lro_expert_dot.restype = C.c_float
+    so.lro_canon_dot.argtypes = [_P, _P, C.c_int]
+    so.lro_canon_dot.restype = C.c_float
+    so.lro_expert_pair.argtypes = [_P, _P, _P, _P, _P]
+    so.lro_expert_rows.argtypes = [_P, _P, _P, _P, C.c_int]
+    so.lro_expert_block_rows.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int]
+    so.lro_route.argtypes = [_P, _P, C.c_int, _P, _P, _P]
+    so.lro_shared_gate.argtypes = [_P, _P, C.c_int, _P]
+    so.lro_rmsnorm.argtypes = [_P, _P, C.c_int, C.c_float, _P]
+    so.lro_bucket.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P]
+    so.lro_bucket.restype = C.c_int
+    so.lro_combine.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
+    so.lro_moe_layer.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P]
+    for name in ("lro_fill_normal_bf16", "lro_expert_pair", "lro_expert_rows", "lro_expert_block_rows",
+                 "lro_route", "lro_shared_gate", "lro_rmsnorm", "lro_combine", "lro_moe_layer"):
+        getattr(so, name).restype = None
+    return so
+
+
+@lru_cache(maxsize=1)
+def reference() -> C.CDLL | None:
+    """The reference's cpu_experts.c as compiled by oracle/Makefile, or None."""
+    if not REF.exists():
+        if Path("/root/reference/edge35b/cpu_experts.c").exists():
+            build(ref=True)
+        else:
+            return None
+    so = C.CDLL(str(REF))
+    so.expert_rows.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int]
+    so.expert_rows.restype = None
+    so.expert_block_rows.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int]
+    so.expert_block_rows.restype = None
+    return so
+
+
+# ---- scalar helpers -------------------------------------------------------
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    """cpu_experts.c:18-22 rounding (RNE, no NaN special case), vectorised."""
+    bits = np.asarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return (((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+
+
+def exp(x: float) -> float:
+    return lib().lro_exp(float(x))
+
+
+# ---- generator ------------------------------------------------------------
+
+def normal_bf16(shape, seed: int, stream: int, sigma: float, first: int = 0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint16)
+    lib().lro_fill_normal_bf16(_ptr(out), out.size, seed & (2**64 - 1), stream & (2**64 - 1), float(sigma), first)
+    return out
+
+
+# ---- expert arithmetic (cpu_experts.c restatement) -------------------------
+
+def _pointer_array(arrays):
+    return (C.c_void_p * len(arrays))(*[_ptr(a) for a in arrays])
+
+
+def expert_rows(gate_up: list[np.ndarray], down: list[np.ndarray], hidden: np.ndarray) -> np.ndarray:
+    out = np.empty((len(gate_up), HIDDEN), dtype=np.uint16)
+    lib().lro_expert_rows(_pointer_array(gate_up), _pointer_array(down), _ptr(hidden), _ptr(out), len(gate_up))
+    return out
+
+
+def expert_block_rows(gate_up, down, hidden: np.ndarray, token_ids: np.ndarray) -> np.ndarray:
+    token_ids = np.ascontiguousarray(token_ids, dtype=np.int32)
+    out = np.empty((len(gate_up), HIDDEN), dtype=np.uint16)
+    lib().lro_expert_block_rows(_pointer_array(gate_up), _pointer_array(down), _ptr(hidden), _ptr(token_ids),
+                                _ptr(out), hidden.shape[0], len(gate_up))
+    return out
+
+
+def expert_pair(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x_bf16: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(bf16_to_f32(x_bf16))
+    y = np.empty(HIDDEN, dtype=np.uint16)
+    lib().lro_expert_pair(_ptr(gate), _ptr(up), _ptr(down), _ptr(x), _ptr(y))
+    return y
+
+
+def reference_expert_rows(gate_up, down, hidden, threads: int = 1) -> np.ndarray:
+    ref = reference()
+    if ref is None:
+        raise FileNotFoundError("reference CPU kernel not built")
+    out = np.empty((len(gate_up), HIDDEN), dtype=np.uint16)
+    ref.expert_rows(_pointer_array(gate_up), _pointer_array(down), _ptr(hidden), _ptr(out), len(gate_up), threads)
+    return out
+
+
+def reference_expert_block_rows(gate_up, down, hidden, token_ids, threads: int = 1) -> np.ndarray:
+    ref = reference()
+    if ref is None:
+        raise FileNotFoundError("reference CPU kernel not built")
+    token_ids = np.ascontiguousarray(token_ids, dtype=np.int32)
+    out = np.empty((len(gate_up), HIDDEN), dtype=np.uint16)
+    ref.expert_block_rows(_pointer_array(gate_up), _pointer_array(down), _ptr(hidden), _ptr(token_ids), _ptr(out),
+                          hidden.shape[0], len(gate_up), threads)
+    return out
+
+
+# ---- router, shared gate, RMSNorm, bucketing, combine ---------------------
+
+def canon_dot(weights: np.ndarray, x_f32: np.ndarray) -> float:
+    return lib().lro_canon_dot(_ptr(weights), _ptr(np.ascontiguousarray(x_f32, dtype=np.float32)), weights.size)
+
+
+def route(x: np.ndarray, router: np.ndarray):
+    tokens = x.shape[0]
+    logits = np.empty((tokens, EXPERTS), dtype=np.uint16)
+    indices = np.empty((tokens, TOPK), dtype=np.int64)
+    weights = np.empty((tokens, TOPK), dtype=np.uint16)
+    lib().lro_route(_ptr(x), _ptr(router), tokens, _ptr(logits), _ptr(indices), _ptr(weights))
+    return logits, indices, weights
+
+
+def shared_gate(x: np.ndarray, gate_weight: np.ndarray) -> np.ndarray:
+    out = np.empty(x.shape[0], dtype=np.uint16)
+    lib().lro_shared_gate(_ptr(x), _ptr(gate_weight), x.shape[0], _ptr(out))
+    return out
+
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    out = np.empty_like(x)
+    lib().lro_rmsnorm(_ptr(x), _ptr(weight), x.shape[0], float(eps), _ptr(out))
+    return out
+
+
+def bucket(indices: np.ndarray):
+    indices = np.ascontiguousarray(indices, dtype=np.int64)
+    tokens = indices.shape[0]
+    expert = np.full(EXPERTS, -1, dtype=np.int32)
+    offset = np.zeros(EXPERTS + 1, dtype=np.int32)
+    pair_token = np.empty(tokens * TOPK, dtype=np.int32)
+    pair_slot = np.empty(tokens * TOPK, dtype=np.int32)
+    route_pair = np.empty(tokens * TOPK, dtype=np.int32)
+    unique = lib().lro_bucket(_ptr(indices), tokens, _ptr(expert), _ptr(offset), _ptr(pair_token),
+                              _ptr(pair_slot), _ptr(route_pair))
+    if unique < 0:
+        raise ValueError("invalid routes" if unique == -1 else "repeated expert in a token")
+    return dict(unique=unique, expert=expert[:unique], offset=offset[:unique + 1], pair_token=pair_token,
+                pair_slot=pair_slot, route_pair=route_pair.reshape(tokens, TOPK))
+
+
+def combine(y, route_pair, pair_slot, weights, y_shared=None, sg=None, residual=None) -> np.ndarray:
+    tokens = weights.shape[0]
+    out = np.empty((tokens, HIDDEN), dtype=np.uint16)
+    lib().lro_combine(_ptr(np.ascontiguousarray(y)), _ptr(np.ascontiguousarray(route_pair, dtype=np.int32)),
+                      _ptr(np.ascontiguousarray(pair_slot, dtype=np.int32)), _ptr(np.ascontiguousarray(weights)),
+                      _ptr(y_shared), _ptr(sg), _ptr(residual), tokens, _ptr(out))
+    return out
+
+
+def moe_layer(x, router, gate_up, down, shared=None, norm_weight=None, eps: float = 1e-6):
+    """Whole layer for ``x`` [T, 2048].  ``gate_up``/``down`` are 256-entry lists
+    of per-expert arrays (entries for unrouted experts may be any array).
+    ``shared`` = (gate_proj, up_proj, down_proj, shared_expert_gate) or None."""
+    tokens = x.shape[0]
+    out = np.empty((tokens, HIDDEN), dtype=np.uint16)
+    indices = np.empty((tokens, TOPK), dtype=np.int64)
+    weights = np.empty((tokens, TOPK), dtype=np.uint16)
+    sg_proj, su_proj, sd_proj, sgate = shared if shared is not None else (None, None, None, None)
+    lib().lro_moe_layer(_ptr(x), tokens, _ptr(router), _pointer_array(gate_up), _pointer_array(down),
+                        _ptr(sg_proj), _ptr(su_proj), _ptr(sd_proj), _ptr(sgate), _ptr(norm_weight), float(eps),
+                        _ptr(out), _ptr(indices), _ptr(weights))
+    return out, indices, weights
+
+
+def physical_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1

@@ -1,0 +1,224 @@
+"""HIP path vs the oracle on the same seeded inputs (needs an MI355X).
+
+Bar: routing indices, routing weights, logits, shared-gate values, RMSNorm
+outputs, bucketing plans, generator output and gathered bytes bit-exact;
+expert outputs within 1e-2 of the row's max magnitude (bf16 storage, fp32
+accumulation; see helpers.assert_close_bf16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (HostExperts, assert_close_bf16, from_u16, oracle_experts, to_u16, uniform_routes,
+                     zipf_routes)
+
+pytestmark = pytest.mark.gpu
+
+SEED = 4242
+
+
+@pytest.fixture(scope="module")
+def model(device):
+    from lightreason_amd.synthetic import SyntheticModel
+
+    return SyntheticModel(layers=1, device=device, seed=SEED, shared=True, norm="normal")
+
+
+@pytest.fixture(scope="module")
+def host_experts(model):
+    return HostExperts(model.bank, 0)
+
+
+def test_generator_matches_host(device, oracle):
+    from lightreason_amd.moe import fill_normal_
+
+    for count, stream, sigma, first in ((1, 3, 1.0, 0), (1000, 7, 0.02, 0), (65537, 8, 2.5, 123456789)):
+        t = fill_normal_(torch.empty(count, dtype=torch.bfloat16, device=device), 99, stream, sigma, first)
+        np.testing.assert_array_equal(to_u16(t), oracle.normal_bf16((count,), 99, stream, sigma, first))
+
+
+def test_bank_generator_matches_host(model, oracle):
+    from lightreason_amd.moe import EXPERT_ELEMENTS
+    from lightreason_amd.synthetic import STREAM_BANK
+
+    for e in (0, 77, 255):
+        got = to_u16(model.bank.bank[0, e])
+        want = oracle.normal_bf16((EXPERT_ELEMENTS,), SEED, STREAM_BANK, 0.02, first=e * EXPERT_ELEMENTS)
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 8, 16, 40, 300])
+@pytest.mark.parametrize("norm", [False, True])
+def test_route_topk_bit_exact(model, oracle, tokens, norm):
+    from lightreason_amd.moe import Workspace, route_topk
+
+    layer = model.layers[0]
+    x = model.hidden(tokens, step=tokens)
+    ws = Workspace(x.device, tokens)
+    indices, weights, logits, sg, normed = route_topk(
+        x, layer.router, norm_weight=layer.norm_weight if norm else None, eps=layer.eps,
+        shared_expert_gate=layer.shared_expert_gate, workspace=ws)
+    torch.cuda.synchronize()
+    xb = to_u16(x)
+    if norm:
+        nb = oracle.rmsnorm(xb, to_u16(layer.norm_weight), layer.eps)
+        np.testing.assert_array_equal(to_u16(normed), nb)
+        xb = nb
+    o_logits, o_idx, o_w = oracle.route(xb, to_u16(layer.router))
+    np.testing.assert_array_equal(to_u16(logits), o_logits)
+    np.testing.assert_array_equal(indices.cpu().numpy(), o_idx)
+    np.testing.assert_array_equal(to_u16(weights), o_w)
+    np.testing.assert_array_equal(to_u16(sg), oracle.shared_gate(xb, to_u16(layer.shared_expert_gate)))
+    assert ws.status() == 0
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 16, 64, 65, 500])
+def test_bucket_bit_exact(device, oracle, tokens):
+    from lightreason_amd.moe import Workspace, bucket
+
+    idx, _ = (zipf_routes if tokens % 2 == 0 else uniform_routes)(tokens, tokens)
+    plan = bucket(torch.from_numpy(idx).to(device), Workspace(device, tokens))
+    torch.cuda.synchronize()
+    ref = oracle.bucket(idx)
+    unique = int(plan["unique"].item())
+    assert int(plan["status"].item()) == 0
+    assert unique == ref["unique"]
+    np.testing.assert_array_equal(plan["expert"][:unique].cpu().numpy(), ref["expert"])
+    np.testing.assert_array_equal(plan["offset"][:unique + 1].cpu().numpy(), ref["offset"])
+    np.testing.assert_array_equal(plan["pair_token"].cpu().numpy(), ref["pair_token"])
+    np.testing.assert_array_equal(plan["pair_slot"].cpu().numpy(), ref["pair_slot"])
+    np.testing.assert_array_equal(plan["route_pair"].cpu().numpy(), ref["route_pair"])
+
+
+@pytest.mark.parametrize("tokens", [1, 100])
+def test_bucket_flags_bad_routes(device, tokens):
+    from lightreason_amd.moe import Workspace, bucket
+
+    idx, _ = uniform_routes(tokens, 5)
+    idx[-1, 3] = 300
+    plan = bucket(torch.from_numpy(idx).to(device), Workspace(device, tokens))
+    assert int(plan["status"].item()) & 1
+    idx, _ = uniform_routes(tokens, 6)
+    idx[0, 7] = idx[0, 2]
+    plan = bucket(torch.from_numpy(idx).to(device), Workspace(device, tokens))
+    assert int(plan["status"].item()) & 2
+
+
+@pytest.mark.parametrize("tokens,routes", [(1, "uniform"), (4, "uniform"), (8, "zipf"), (16, "zipf"), (33, "zipf")])
+def test_moe_experts_parity(model, oracle, host_experts, tokens, routes):
+    from lightreason_amd.moe import Workspace, moe_experts
+
+    idx, wb = (zipf_routes if routes == "zipf" else uniform_routes)(tokens, 1000 + tokens)
+    x = model.hidden(tokens, step=500 + tokens)
+    ws = Workspace(x.device, tokens)
+    out = moe_experts(x, torch.from_numpy(idx).to(x.device), from_u16(wb, x.device), model.bank.expert_ptrs(0),
+                      workspace=ws)
+    torch.cuda.synchronize()
+    want = oracle_experts(oracle, to_u16(x), idx, wb, host_experts)
+    stats = assert_close_bf16(to_u16(out), want, what=f"experts T={tokens}")
+    assert stats["exact_fraction"] > 0.5
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 16, 24])
+@pytest.mark.parametrize("norm", [False, True])
+def test_moe_layer_parity(model, oracle, host_experts, tokens, norm):
+    from lightreason_amd.moe import LayerWeights, Workspace, moe_layer
+
+    base = model.layers[0]
+    layer = LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None})
+    x = model.hidden(tokens, step=900 + tokens)
+    ws = Workspace(x.device, tokens)
+    idx_out = torch.empty((tokens, 8), dtype=torch.int64, device=x.device)
+    w_out = torch.empty((tokens, 8), dtype=torch.bfloat16, device=x.device)
+    out = moe_layer(x, layer, indices=idx_out, weights=w_out, workspace=ws)
+    torch.cuda.synchronize()
+    xb = to_u16(x)
+    xin = oracle.rmsnorm(xb, to_u16(layer.norm_weight), layer.eps) if norm else xb
+    _, o_idx, o_w = oracle.route(xin, to_u16(layer.router))
+    np.testing.assert_array_equal(idx_out.cpu().numpy(), o_idx)
+    np.testing.assert_array_equal(to_u16(w_out), o_w)
+    shared = (to_u16(layer.shared_gate_proj), to_u16(layer.shared_up_proj), to_u16(layer.shared_down_proj))
+    sg = oracle.shared_gate(xin, to_u16(layer.shared_expert_gate))
+    want = oracle_experts(oracle, xin, o_idx, o_w, host_experts, shared, sg, xb if norm else None)
+    if norm:
+        # out = bf16(h + moe): allow 1e-2 of the row's MoE magnitude plus one
+        # bf16 ulp of the output for the final residual rounding.
+        from helpers import bf16_f32
+
+        got, exp_, h = bf16_f32(to_u16(out)), bf16_f32(want), bf16_f32(xb)
+        moe_scale = np.abs(exp_ - h).max(axis=1, keepdims=True)
+        assert np.all(np.abs(got - exp_) <= 1e-2 * moe_scale + 2.0 ** -7 * np.abs(exp_))
+    else:
+        assert_close_bf16(to_u16(out), want, what=f"layer T={tokens}")
+
+
+def test_gather_raw_rows_graph_replay(device):
+    """Mirror of the reference's resident-gather fixture
+    (edge35b/test_gpu_resident_experts.py:12-57) for raw rows: sentinel -123
+    slots stay untouched, count in {2, 0, 1} under graph replay with swapped
+    descriptors."""
+    from lightreason_amd.moe import gather
+
+    gen = torch.Generator().manual_seed(7091)
+    words = torch.randint(-32768, 32767, (2, 32, 256), generator=gen, dtype=torch.int32).to(torch.int16)
+    rows = words.to(device)
+    output = torch.full((4, 32, 256), -123, device=device, dtype=torch.int16)
+    descriptors = torch.tensor([[[rows[0].data_ptr(), -1, 0], [rows[1].data_ptr(), -1, 0]]], device=device,
+                               dtype=torch.int64)
+    destinations = torch.tensor([output.data_ptr()], device=device, dtype=torch.int64)
+    sizes = torch.tensor([32 * 256 * 2], device=device, dtype=torch.int64)
+    ids = torch.tensor([0, 1], device=device, dtype=torch.int32)
+    slots = torch.tensor([1, 3], device=device, dtype=torch.int32)
+    count = torch.tensor([2], device=device, dtype=torch.int64)
+
+    def copy():
+        gather(descriptors, destinations, sizes, ids, slots, count, max_copies=2, experts=2, stripes=4)
+
+    copy()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        copy()
+    references = [words[0], words[1]]
+    for n in (2, 0, 1):
+        descriptors.copy_(descriptors.flip(1))
+        references.reverse()
+        output.fill_(-123)
+        count.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = torch.full((4, 32, 256), -123, dtype=torch.int16)
+        for slot, ref in zip((1, 3)[:n], references[:n]):
+            expected[slot] = ref
+        assert torch.equal(output.cpu(), expected)
+
+
+def test_gather_expert_rows_bit_exact(model, device):
+    """C1 shape: gather experts of the packed bank into contiguous staging."""
+    from lightreason_amd.moe import EXPERT_ELEMENTS, GATE_UP_ELEMENTS, gather
+
+    bank = model.bank
+    sel = [255, 3, 77, 128, 0, 19]
+    staging_gu = torch.full((len(sel), 1024, 2048), 0x5A5A, dtype=torch.int16, device=device)
+    staging_dn = torch.full((len(sel) + 1, 2048, 512), 0x5A5A, dtype=torch.int16, device=device)
+    ptrs = bank.expert_ptrs(0).cpu()
+    desc = torch.stack([torch.stack([ptrs[:, 0], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1),
+                        torch.stack([ptrs[:, 1], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1)])
+    desc = desc.to(device)
+    destinations = torch.tensor([staging_gu.data_ptr(), staging_dn.data_ptr()], device=device)
+    sizes = torch.tensor([GATE_UP_ELEMENTS * 2, (EXPERT_ELEMENTS - GATE_UP_ELEMENTS) * 2], device=device)
+    src = torch.tensor(sel + [-1] * 2, dtype=torch.int32, device=device)
+    dst = torch.tensor(list(range(len(sel))) + [-1] * 2, dtype=torch.int32, device=device)
+    count = torch.tensor([len(sel)], device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    gather(desc, destinations, sizes, src, dst, count, max_copies=8, experts=256, stripes=64, status=status)
+    torch.cuda.synchronize()
+    for i, e in enumerate(sel):
+        gu, dn = bank.expert(0, e)
+        assert torch.equal(staging_gu[i], gu.view(torch.int16))
+        assert torch.equal(staging_dn[i], dn.view(torch.int16))
+    assert torch.all(staging_dn[len(sel)] == 0x5A5A)
+    assert int(status.item()) == 0

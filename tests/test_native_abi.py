@@ -1,0 +1,86 @@
+"""liblrmoe.so loads on the CPU host and exports every symbol include/lrmoe.h
+declares; host-side argument checks reject misuse without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "lrmoe.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(lrmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from lightreason_amd import _native
+
+    if not _native.LIBRARY.exists():
+        pytest.fail("liblrmoe.so is not built: run `python -m lightreason_amd.build` (or __graft_entry__.build())")
+    return _native.library()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    declared = _declared()
+    assert len(declared) >= 15
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ROOT / "lightreason_amd" / "liblrmoe.so")],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s+(lrmoe_\w+)", out))
+    missing = [name for name in declared if name not in exported]
+    assert not missing, missing
+    from lightreason_amd import _native
+
+    assert sorted(_native.symbols()) == declared
+
+
+def test_host_side_queries(lib):
+    assert lib.lrmoe_version().decode().startswith("lrmoe")
+    assert lib.lrmoe_error_string(-1).decode().startswith("lrmoe: invalid argument")
+    assert lib.lrmoe_error_string(-2).decode().startswith("lrmoe: workspace")
+    small, big = lib.lrmoe_workspace_bytes(1), lib.lrmoe_workspace_bytes(2048)
+    assert 0 < small < big
+    # the workspace holds at least the expert intermediates: (8T + T) rows of 512 and 2048 bf16
+    assert big >= 9 * 2048 * (512 + 2048) * 2
+
+
+def test_argument_errors_are_reported_before_any_launch(lib):
+    null = None
+    assert lib.lrmoe_route_topk(null, 1, null, null, null, 1e-6, null, null, null, null, null, null, null, 0,
+                                null) == -1
+    assert lib.lrmoe_moe_layer(null, 1, null, null, null, null, null, null, null, null, 1e-6, null, null, null, null,
+                               0, null) == -1
+    dummy = C.c_void_p(16)
+    # both a router and logits: refused
+    assert lib.lrmoe_route_topk(dummy, 1, dummy, dummy, null, 1e-6, null, null, dummy, dummy, null, null, dummy,
+                                1 << 30, null) == -1
+    assert lib.lrmoe_moe_experts(null, -1, null, null, null, null, null, 0, null) == -1
+    dummy = C.c_void_p(16)
+    # a workspace that is too small is refused
+    assert lib.lrmoe_moe_experts(dummy, 4, dummy, dummy, dummy, dummy, dummy, 8, null) == -2
+    assert lib.lrmoe_matvec(dummy, dummy, dummy, 100, 8, 0, 1, 3, 8, null) == -1  # K not a multiple of 512
+    assert lib.lrmoe_ordered_sum(dummy, dummy, null, dummy, dummy, 5, null) == -1
+    assert lib.lrmoe_project(dummy, dummy, dummy, dummy, 2048, 1000, 0, 4, null) == -1
+    assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 0, 2, 8, 64, null, null) == -1
+    # zero tokens is a successful no-op
+    assert lib.lrmoe_moe_experts(dummy, 0, dummy, dummy, dummy, dummy, dummy, 0, null) == 0
+    from lightreason_amd import _native
+
+    with pytest.raises(ValueError):
+        _native.call("lrmoe_fill_normal_bf16", None, 4, 0, 0, 1.0, 0, None)
+
+
+def test_product_does_not_reach_the_oracle():
+    """Nothing under lightreason_amd/ imports, loads or names oracle code."""
+    for path in (ROOT / "lightreason_amd").rglob("*"):
+        if path.suffix in {".py", ".hip", ".h", ".cpp"}:
+            text = path.read_text()
+            assert "import oracle" not in text and "from oracle" not in text, path
+            assert "liblro" not in text and "lro_" not in text, path
