@@ -122,6 +122,26 @@ class Case:
         return [len(set(i.cpu().numpy().ravel().tolist())) for i in self.idx]
 
 
+class GatherCase:
+    """C1: per layer, gather its selected experts (packed 6 MiB rows) into
+    one contiguous staging buffer."""
+
+    def __init__(self, ptrs, per_layer, staging, device):
+        self.descs = [torch.stack([ptrs[l][:, 0], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1)[None]
+                      .contiguous().to(device) for l in range(len(per_layer))]
+        self.srcs = [torch.tensor(sel + [0] * (128 - len(sel)), dtype=torch.int32, device=device) for sel in per_layer]
+        self.dst = torch.arange(128, dtype=torch.int32, device=device)
+        self.counts = [torch.tensor([len(sel)], device=device) for sel in per_layer]
+        self.dests = torch.tensor([staging.data_ptr()], device=device)
+        self.sizes = torch.tensor([EXPERT_BYTES], device=device)
+        self.max_copies = max(len(sel) for sel in per_layer)
+
+    def run(self):
+        for l in range(len(self.descs)):
+            gather(self.descs[l], self.dests, self.sizes, self.srcs[l], self.dst, self.counts[l],
+                   max_copies=self.max_copies, experts=256, stripes=48)
+
+
 def bench_case(case: Case, replays: int, warmup: int) -> float:
     """Milliseconds per graph replay (one pass over the case's layers)."""
     graph = capture(case.run)
@@ -142,11 +162,13 @@ def kernel_time(case: Case, stage: int, passes: int) -> tuple[float, int]:
     return total / max(launches, 1), launches
 
 
-def cpu_baseline(model, case: Case, uniques, budget_s: float = 12.0) -> dict:
+def cpu_baseline(model, case: Case, uniques, budget_s: float = 15.0) -> dict:
     """The reference CPU expert kernel (oracle/_ref/libcpu_experts.so, built
     from edge35b/cpu_experts.c) on the headline routes: expert_block_rows over
-    the 64 (token, expert) rows of a layer, all threads of this process's
-    CPU share.  GB/s on the same unique-expert bytes as the GPU figure."""
+    the 64 (token, expert) rows of a layer, with the threads of this process's
+    CPU share.  The sample holds several layers' experts in host memory and
+    cycles through them call by call, so no call finds its weights in the host
+    caches.  GB/s on the same unique-expert bytes as the GPU figure."""
     from oracle import oracle as O
 
     ref = O.reference()
@@ -155,38 +177,39 @@ def cpu_baseline(model, case: Case, uniques, budget_s: float = 12.0) -> dict:
         return {"value": None, "unit": "GB/s", "cores": 0, "kind": kind,
                 "sample": "reference CPU kernel not built (oracle/Makefile needs the reference source)"}
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    samples, total_bytes, total_s, calls = 0, 0, 0.0, 0
-    started = time.perf_counter()
-    for j, layer in enumerate(case.layer_ids):
-        if time.perf_counter() - started > budget_s:
-            break
+    sample_layers = min(len(case.layer_ids), 8)
+    calls = []
+    for j in range(sample_layers):
+        layer = case.layer_ids[j]
         idx = case.idx[j].cpu().numpy()
         x = case.x[j].cpu().view(torch.int16).numpy().view(np.uint16)
-        experts = sorted(set(idx.ravel().tolist()))
         host = {}
-        for e in experts:
+        for e in sorted(set(idx.ravel().tolist())):
             row = model.bank.bank[layer, e].cpu().view(torch.int16).numpy().view(np.uint16)
             host[e] = (np.ascontiguousarray(row[:2 * INNER * HIDDEN]), np.ascontiguousarray(row[2 * INNER * HIDDEN:]))
         gu = [host[e][0] for e in idx.ravel().tolist()]
         dn = [host[e][1] for e in idx.ravel().tolist()]
         tok = np.repeat(np.arange(idx.shape[0], dtype=np.int32), idx.shape[1])
-        O.reference_expert_block_rows(gu, dn, x, tok, threads)  # warm the pages
-        t0 = time.perf_counter()
-        reps = 0
-        while reps < 3 or time.perf_counter() - t0 < 1.0:
-            O.reference_expert_block_rows(gu, dn, x, tok, threads)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        total_s += dt
-        total_bytes += uniques[j] * EXPERT_BYTES
-        samples += 1
-        calls += reps
-    gbs = total_bytes / total_s / 1e9 if total_s else None
-    return {"value": round(gbs, 2) if gbs else None, "unit": "GB/s", "cores": threads, "kind": kind,
-            "ms_per_layer": round(1e3 * total_s / max(samples, 1), 3),
-            "sample": f"{samples} layers of the T=8 Zipf routes (64 rows each, {calls} timed calls), "
-                      f"expert_block_rows with {threads} OpenMP threads; routed experts only "
-                      "(the reference CPU path has no router, combine or shared expert)"}
+        calls.append((gu, dn, x, tok, uniques[j] * EXPERT_BYTES, host))
+    for gu, dn, x, tok, _, _ in calls:  # first touch of every page
+        O.reference_expert_block_rows(gu, dn, x, tok, threads)
+    total_bytes, n = 0, 0
+    t0 = time.perf_counter()
+    while n < 3 * sample_layers or time.perf_counter() - t0 < budget_s:
+        gu, dn, x, tok, nbytes, _ = calls[n % sample_layers]
+        O.reference_expert_block_rows(gu, dn, x, tok, threads)
+        total_bytes += nbytes
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    gbs = total_bytes / dt / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+            "ms_per_layer": round(1e3 * dt / n, 3),
+            "sample": f"{n} calls cycling over {sample_layers} layers' T=8 Zipf routes "
+                      f"({sum(c[4] for c in calls) / 2**20:.0f} MiB of unique experts), expert_block_rows with "
+                      f"{threads} OpenMP threads, 64 rows per call; routed experts only (the reference CPU path "
+                      "has no router, combine or shared expert)"}
 
 
 def main() -> int:
@@ -198,6 +221,7 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=2026)
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4 to run (default all)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -213,6 +237,9 @@ def main() -> int:
     L = args.layers
     replays = max(1, args.steps // L)
     warm = max(1, args.warmup // L)
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c2", "c3", "c4"}
+    if args.skip_prefill:
+        only.discard("c4")
     configs = {}
 
     # ---- headline: T=8 Zipf verify ----
@@ -224,67 +251,66 @@ def main() -> int:
     bytes_step = (np.mean(uniques) * EXPERT_BYTES + SHARED_BYTES)
     gbs = bytes_step / (ms_step * 1e-3) / 1e9
     log(f"[bench] C2 T=8 zipf: {ms_step * 1e3:.1f} us/layer, U={np.mean(uniques):.1f}, {gbs:.0f} GB/s")
-    gate_ms, launches = kernel_time(c2, _native.STAGE_GATE_UP, passes=max(2, replays))
-    down_ms, _ = kernel_time(c2, _native.STAGE_DOWN, passes=max(2, replays))
+    stage_us = {}
+    for name, stage in (("route", _native.STAGE_ROUTE), ("gateup", _native.STAGE_GATE_UP),
+                        ("down", _native.STAGE_DOWN), ("combine", _native.STAGE_COMBINE)):
+        ms_k, launches = kernel_time(c2, stage, passes=max(2, replays))
+        stage_us[name] = round(ms_k * 1e3, 2)
+        if name == "gateup":
+            gate_ms, gate_launches = ms_k, launches
     gate_bytes = (np.mean(uniques) + 1) * (2 * INNER * HIDDEN * 2) + (8 * 8 + 8) * (HIDDEN * 2 + INNER * 2)
     gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
-    log(f"[bench] C2 gate/up kernel {gate_ms * 1e3:.1f} us ({gate_gbs:.0f} GB/s), down {down_ms * 1e3:.1f} us")
-    configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2), unique_experts=round(float(np.mean(uniques)), 2),
-                                        gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
-                                        gateup_us=round(gate_ms * 1e3, 2), down_us=round(down_ms * 1e3, 2))
+    log(f"[bench] C2 stages (us, event-bracketed): {stage_us}; gate/up {gate_gbs:.0f} GB/s")
+    configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2),
+                                        unique_experts=round(float(np.mean(uniques)), 2), gbs=round(gbs, 1),
+                                        frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stage_us)
 
     # ---- C0: T=1 decode layer with the router ----
-    c0 = Case(model, 1)
-    ms0 = bench_case(c0, replays, warm) / L
-    b0 = 8 * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES
-    configs["c0_decode_t1"] = dict(us_per_layer=round(ms0 * 1e3, 2), gbs=round(b0 / (ms0 * 1e-3) / 1e9, 1),
-                                   frac_hbm=round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
-    log(f"[bench] C0 T=1: {ms0 * 1e3:.1f} us/layer, {configs['c0_decode_t1']['gbs']} GB/s")
+    if "c0" in only:
+        c0 = Case(model, 1)
+        ms0 = bench_case(c0, replays, warm) / L
+        b0 = 8 * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES
+        st0 = {}
+        for name, stage in (("route", _native.STAGE_ROUTE), ("gateup", _native.STAGE_GATE_UP),
+                            ("down", _native.STAGE_DOWN), ("combine", _native.STAGE_COMBINE)):
+            st0[name] = round(kernel_time(c0, stage, passes=2)[0] * 1e3, 2)
+        configs["c0_decode_t1"] = dict(us_per_layer=round(ms0 * 1e3, 2), gbs=round(b0 / (ms0 * 1e-3) / 1e9, 1),
+                                       frac_hbm=round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), stage_us=st0)
+        log(f"[bench] C0 T=1: {ms0 * 1e3:.1f} us/layer, {configs['c0_decode_t1']['gbs']} GB/s, stages {st0}")
 
     # ---- C1: raw expert gather ----
-    gather_res = {}
-    ptrs = model.bank.tables.cpu()
-    staging = torch.empty((128, EXPERT_ELEMENTS), dtype=torch.bfloat16, device=device)
-    for T in (1, 4, 8, 16):
-        rng = np.random.default_rng(T)
-        per_layer = []
-        for l in range(L):
-            sel = sorted(set(np.concatenate([rng.choice(256, 8, replace=False) for _ in range(T)]).tolist()))
-            per_layer.append(sel)
-        descs = [torch.stack([ptrs[l][:, 0], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1)[None]
-                 .contiguous().to(device) for l in range(L)]
-        srcs = [torch.tensor(s + [0] * (128 - len(s)), dtype=torch.int32, device=device) for s in per_layer]
-        dst = torch.arange(128, dtype=torch.int32, device=device)
-        counts = [torch.tensor([len(s)], device=device) for s in per_layer]
-        dests = torch.tensor([staging.data_ptr()], device=device)
-        sizes = torch.tensor([EXPERT_BYTES], device=device)
-        max_copies = max(len(s) for s in per_layer)
-
-        def run_gather():
-            for l in range(L):
-                gather(descs[l], dests, sizes, srcs[l], dst, counts[l], max_copies=max_copies, experts=256, stripes=48)
-
-        msg = bench_case(type("G", (), {"run": staticmethod(run_gather)})(), replays, warm) / L
-        u = float(np.mean([len(s) for s in per_layer]))
-        moved = 2 * u * EXPERT_BYTES
-        gather_res[f"t{T}"] = dict(unique=round(u, 1), us=round(msg * 1e3, 2), gbs_moved=round(moved / (msg * 1e-3) / 1e9, 1))
-    configs["c1_gather"] = gather_res
-    log(f"[bench] C1 gather: {gather_res}")
-    del staging
+    if "c1" in only:
+        gather_res = {}
+        ptrs = model.bank.tables.cpu()
+        staging = torch.empty((128, EXPERT_ELEMENTS), dtype=torch.bfloat16, device=device)
+        for T in (1, 4, 8, 16):
+            rng = np.random.default_rng(T)
+            per_layer = [sorted(set(np.concatenate([rng.choice(256, 8, replace=False) for _ in range(T)]).tolist()))
+                         for _ in range(L)]
+            gcase = GatherCase(ptrs, per_layer, staging, device)
+            msg = bench_case(gcase, replays, warm) / L
+            u = float(np.mean([len(sel) for sel in per_layer]))
+            moved = 2 * u * EXPERT_BYTES
+            gather_res[f"t{T}"] = dict(unique=round(u, 1), us=round(msg * 1e3, 2),
+                                       gbs_moved=round(moved / (msg * 1e-3) / 1e9, 1))
+        configs["c1_gather"] = gather_res
+        log(f"[bench] C1 gather: {gather_res}")
+        del staging
 
     # ---- C3: 40-layer chain with RMSNorm + residual ----
-    for T in (1, 16):
-        c3 = Case(model, T, norm=True, chain=True)
-        u3 = c3.unique_counts()
-        ms3 = bench_case(c3, max(2, replays // 2), 1)
-        b3 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u3)
-        configs[f"c3_chain_t{T}"] = dict(layers=L, ms_per_step=round(ms3, 4), gbs=round(b3 / (ms3 * 1e-3) / 1e9, 1),
-                                         frac_hbm=round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                         mean_unique=round(float(np.mean(u3)), 1))
-        log(f"[bench] C3 T={T}: {ms3:.3f} ms/step over {L} layers, {configs[f'c3_chain_t{T}']['gbs']} GB/s")
+    if "c3" in only:
+        for T in (1, 16):
+            c3 = Case(model, T, norm=True, chain=True)
+            u3 = c3.unique_counts()
+            ms3 = bench_case(c3, max(2, replays // 2), 1)
+            b3 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u3)
+            configs[f"c3_chain_t{T}"] = dict(layers=L, ms_per_step=round(ms3, 4), gbs=round(b3 / (ms3 * 1e-3) / 1e9, 1),
+                                             frac_hbm=round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                             mean_unique=round(float(np.mean(u3)), 1))
+            log(f"[bench] C3 T={T}: {ms3:.3f} ms/step over {L} layers, {configs[f'c3_chain_t{T}']['gbs']} GB/s")
 
     # ---- C4: T=2048 prefill with skewed routing ----
-    if not args.skip_prefill:
+    if "c4" in only:
         T = 2048
         sigma_bias = 0.25
         rng = np.random.default_rng(args.seed + 4)
@@ -295,12 +321,9 @@ def main() -> int:
             base = (x @ model.layers[l].router.float().T).cpu().numpy()
             lg.append(bf16_from_f64(base + rng.normal(0, sigma_bias, size=(1, 256)), device))
         c4 = Case(model, T, logits=lg, layers=layer_ids)
-        idx_counts = []
         c4.run()
         torch.cuda.synchronize()
-        for i in c4.idx:
-            counts = np.bincount(i.cpu().numpy().ravel(), minlength=256)
-            idx_counts.append(counts)
+        idx_counts = [np.bincount(i.cpu().numpy().ravel(), minlength=256) for i in c4.idx]
         ms4 = bench_case(c4, 3, 1) / len(layer_ids)
         flops = (T * 8 + T) * PAIR_FLOP
         hit = float(np.mean([(c > 0).sum() for c in idx_counts]))
@@ -336,7 +359,7 @@ def main() -> int:
                    "layers_rotated": L, "mean_unique_experts": round(float(np.mean(uniques)), 2)},
         "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gateup_kernel", "avg_us": round(gate_ms * 1e3, 3), "launches": launches,
+                     "kernel": "gateup_kernel", "avg_us": round(gate_ms * 1e3, 3), "launches": gate_launches,
                      "algorithmic_bytes": int(gate_bytes)},
         "cpu_baseline": cpu,
         "configs": configs,

@@ -105,7 +105,7 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
     if (int d = check_device()) return d;
     const Workspace ws = lrmoe::carve(workspace, tokens);
     hipStream_t s = as_stream(stream);
-    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s);
+    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s, expert_ptrs);
     if (err != hipSuccess) return status_of(err);
     lrmoe::ExpertArgs a{};
     a.x = hidden;
@@ -147,6 +147,10 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
     r.indices = indices_out ? indices_out : ws.indices;
     r.weights = weights_out ? weights_out : ws.weights;
     r.sg = ws.sg;
+    r.expert_ptrs = expert_ptrs;
+    r.shared_gate_proj = shared_gate_proj;
+    r.shared_up_proj = shared_up_proj;
+    r.shared_down = shared_down_proj;
     r.plan = ws.plan;
     r.ws = ws;
     hipError_t err = lrmoe::launch_route(r, s);

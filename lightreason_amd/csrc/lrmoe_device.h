@@ -42,11 +42,11 @@ __device__ __forceinline__ float hi_bf(uint32_t word) { return __uint_as_float(w
 __device__ __forceinline__ float pow2i(int k) { return __uint_as_float(static_cast<uint32_t>(k + 127) << 23); }
 
 __device__ __forceinline__ float lr_exp(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -87.0f) return 0.0f;
-    const float k = __builtin_rintf(x * 0x1.715476p+0f);
-    float r = __builtin_fmaf(-k, 0x1.62e400p-1f, x);
+    // Branch-free: the polynomial runs on x clamped into range and the
+    // special cases are selected at the end (in-range results unchanged).
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -87.0f), 88.72283935546875f);
+    const float k = __builtin_rintf(xc * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-k, 0x1.62e400p-1f, xc);
     r = __builtin_fmaf(-k, 0x1.7f7d1cp-20f, r);
     float p = 0x1.a01a02p-13f;
     p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
@@ -58,7 +58,8 @@ __device__ __forceinline__ float lr_exp(float x) {
     p = __builtin_fmaf(p, r, 1.0f);
     const int ki = static_cast<int>(k);
     const int k1 = ki / 2;
-    return (p * pow2i(k1)) * pow2i(ki - k1);
+    const float e = (p * pow2i(k1)) * pow2i(ki - k1);
+    return x != x ? x : (x > 88.72283935546875f ? __builtin_inff() : (x < -87.0f ? 0.0f : e));
 }
 
 // The expert activation with cpu_experts.c:59-62 rounding points:
@@ -99,6 +100,17 @@ __device__ __forceinline__ float fma8(uint4 w, const float* x, float acc) {
     return acc;
 }
 
+// 16-byte load through an explicitly global (address space 1) pointer.  Weight
+// and activation addresses read from memory are generic pointers to the
+// compiler, which would otherwise emit FLAT loads; those count against the
+// LDS counter too, so every LDS access would wait for all weight loads.
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+    const u32x4 v = *reinterpret_cast<global_u32x4*>(reinterpret_cast<uintptr_t>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void unpack8(uint4 w, float* out) {
     out[0] = lo_bf(w.x); out[1] = hi_bf(w.x);
     out[2] = lo_bf(w.y); out[3] = hi_bf(w.y);
@@ -113,16 +125,6 @@ __device__ __forceinline__ void unpack8(uint4 w, float* out) {
 __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                    c, 0, 0, 0);
-}
-
-// Coherent (agent scope) loads for data written by other workgroups of the
-// same launch, read after the completion counter says they are done.
-__device__ __forceinline__ uint32_t load_agent_u32(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Orderable key for top-k: bf16 logit (with -0 folded onto +0) in the high

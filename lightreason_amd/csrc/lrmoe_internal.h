@@ -39,6 +39,22 @@ struct Plan {
     int32_t* status;      // [1] (in the control block)
 };
 
+// Per expert slot of a decode call (slot 0 = shared expert, slot s >= 1 =
+// unique routed expert s - 1): everything a wave needs in one 64-byte record,
+// so an expert tile starts streaming after a single (scalar) load.
+struct SlotDesc {
+    const uint16_t* gate_up;  // [1024][2048]: gate rows 0-511, up rows 512-1023
+    const uint16_t* up;       // up rows (gate_up + 512*2048 for routed experts)
+    const uint16_t* down;     // [2048][512]
+    int32_t pair0;            // first act/y row of the slot
+    int32_t count;            // tokens (B columns) of the slot, <= 16
+    uint8_t tokens[16];       // token of each column
+    int32_t valid;            // 0 for an unused slot (no shared expert)
+    int32_t pad[3];
+};
+static_assert(sizeof(SlotDesc) == 64, "one 64-byte record per slot");
+constexpr int kMaxSlots = 257;
+
 // Carves one caller-provided device buffer into the per-call arrays.  The
 // layout depends only on `tokens`, so any buffer of at least
 // workspace_bytes(tokens) serves a call with that many tokens.
@@ -55,6 +71,7 @@ struct Workspace {
     uint32_t* counts;     // [256] prefill histogram
     uint32_t* bitmaps;    // [256][words] prefill token bitmaps
     uint32_t* word_prefix;  // [256][words]
+    SlotDesc* slots;      // [257] decode slot records
     int words;
     size_t bytes;
 };
@@ -88,6 +105,7 @@ inline Workspace carve(void* base, int tokens) {
     ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
     ws.bitmaps = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
     ws.word_prefix = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
+    ws.slots = reinterpret_cast<SlotDesc*>(take(sizeof(SlotDesc) * kMaxSlots));
     ws.words = words;
     ws.plan.unique = &ws.control->unique;
     ws.plan.status = &ws.control->status;
@@ -111,6 +129,11 @@ struct RouteArgs {
     int64_t* indices;             // [T][8]
     uint16_t* weights;            // [T][8]
     uint16_t* sg;                 // [T]
+    // Decode slot records are built when expert_ptrs is given.
+    const int64_t* expert_ptrs;   // [256][2] or null
+    const uint16_t* shared_gate_proj;  // shared expert (all three or none)
+    const uint16_t* shared_up_proj;
+    const uint16_t* shared_down;
     Plan plan;
     Workspace ws;
 };
@@ -145,7 +168,9 @@ enum Stage : int {
 void timing_mark(int stage, hipStream_t stream, bool start);
 
 hipError_t launch_route(const RouteArgs& args, hipStream_t stream);
-hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream);
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream,
+                         const int64_t* expert_ptrs = nullptr, const uint16_t* shared_gate_proj = nullptr,
+                         const uint16_t* shared_up_proj = nullptr, const uint16_t* shared_down = nullptr);
 hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                          const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
                          int max_copies, int stripes, int32_t* status, hipStream_t stream);
@@ -161,6 +186,7 @@ hipError_t launch_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows,
 hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
                                 uint16_t* out, int tokens, int hybrid, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
+hipError_t launch_experts_decode(const ExpertArgs& args, hipStream_t stream);
 hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
                               int64_t first, hipStream_t stream);
 

@@ -83,14 +83,9 @@ __device__ __forceinline__ float lane_dot(const float* w, const uint16_t* xs, in
 // Top-8 + softmax + renormalisation for token `t` by one wave.  Lane l holds
 // the logits of experts 4l..4l+3.  Writes indices (rank order) and weights;
 // returns this lane's chosen expert when lane < 8 (else -1).
-__device__ int topk_token(const uint16_t* logits_row, int64_t* indices_row, uint16_t* weights_row, bool coherent) {
+__device__ int topk_token(const uint16_t* logits_row, int64_t* indices_row, uint16_t* weights_row) {
     const int lane = threadIdx.x & 63;
-    uint64_t packed;
-    if (coherent) {
-        packed = load_agent_u64(reinterpret_cast<const uint64_t*>(logits_row) + lane);
-    } else {
-        packed = reinterpret_cast<const uint64_t*>(logits_row)[lane];
-    }
+    const uint64_t packed = reinterpret_cast<const uint64_t*>(logits_row)[lane];
     uint32_t bits[4], keys[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -134,55 +129,117 @@ __device__ int topk_token(const uint16_t* logits_row, int64_t* indices_row, uint
     return mine_expert;
 }
 
-// Block-wide exclusive scan of one value per thread (256 threads).
-__device__ uint32_t block_exclusive_scan(uint32_t value, uint32_t* scratch, uint32_t* total) {
+// Exclusive scan of one value per thread over threads 0..255 of a workgroup
+// of >= 256 threads (every thread must call it; values of threads >= 256 are
+// ignored and get 0).  `total` receives the sum over threads 0..255.
+__device__ uint32_t scan256(uint32_t value, uint32_t* scratch, uint32_t* total) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
+    if (threadIdx.x >= kExperts) value = 0;
     uint32_t inclusive = value;
 #pragma unroll
     for (int offset = 1; offset < kWave; offset <<= 1) {
         const uint32_t up = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset, kWave));
         if (lane >= offset) inclusive += up;
     }
-    if (lane == kWave - 1) scratch[wave] = inclusive;
+    if (lane == kWave - 1 && wave < 4) scratch[wave] = inclusive;
     __syncthreads();
     uint32_t before = 0;
-    for (int w = 0; w < wave; ++w) before += scratch[w];
-    if (total != nullptr) *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    for (int w = 0; w < wave && w < 4; ++w) before += scratch[w];
+    *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
     __syncthreads();
-    return before + inclusive - value;
+    return threadIdx.x < kExperts ? before + inclusive - value : 0u;
 }
 
-// Bucket <= 64 tokens held in LDS (ids[t*8 + r]) with one 256-thread
-// workgroup: thread e owns expert e.  `valid` must already be checked.
-__device__ void bucket_small(const int32_t* ids, int tokens, const Plan& plan) {
+// Writes one decode slot record with vector stores.  `mask` has a bit per
+// token (<= 16) of the slot; its set bits in ascending order are the columns.
+__device__ void store_slot(SlotDesc* dst, const uint16_t* gate_up, const uint16_t* up, const uint16_t* down, int pair0,
+                           int count, uint32_t mask, int valid) {
+    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        if ((mask >> t) & 1u) {
+            const int pos = __popc(mask & ((1u << t) - 1u));
+            const uint32_t v = static_cast<uint32_t>(t) << (8 * (pos & 3));
+            w0 |= pos < 4 ? v : 0u;
+            w1 |= (pos >= 4 && pos < 8) ? v : 0u;
+            w2 |= (pos >= 8 && pos < 12) ? v : 0u;
+            w3 |= pos >= 12 ? v : 0u;
+        }
+    }
+    const uint64_t g = reinterpret_cast<uint64_t>(gate_up);
+    const uint64_t u = reinterpret_cast<uint64_t>(up);
+    const uint64_t d = reinterpret_cast<uint64_t>(down);
+    uint4* out = reinterpret_cast<uint4*>(dst);
+    out[0] = make_uint4(static_cast<uint32_t>(g), static_cast<uint32_t>(g >> 32), static_cast<uint32_t>(u),
+                        static_cast<uint32_t>(u >> 32));
+    out[1] = make_uint4(static_cast<uint32_t>(d), static_cast<uint32_t>(d >> 32), static_cast<uint32_t>(pair0),
+                        static_cast<uint32_t>(count));
+    out[2] = make_uint4(w0, w1, w2, w3);
+    out[3] = make_uint4(static_cast<uint32_t>(valid), 0u, 0u, 0u);
+}
+
+// Bucket <= 64 tokens held in LDS (ids[t*8 + r], already validated) with one
+// 256-thread workgroup: a token bitmap per expert (one LDS atomic per route),
+// a block scan for pair offsets and unique ranks, then every route places
+// itself in O(1).  With expert_ptrs (and tokens <= 16) also writes the decode
+// slot records, slot 0 being the shared expert.
+__device__ void build_plan_small(const int32_t* ids, int tokens, const Plan& plan, SlotDesc* slots,
+                                 const int64_t* expert_ptrs, const uint16_t* sh_gate, const uint16_t* sh_up,
+                                 const uint16_t* sh_down) {
+    __shared__ unsigned long long tokmask[kExperts];
+    __shared__ uint32_t poff[kExperts];
     __shared__ uint32_t scan_scratch[4];
     const int e = threadIdx.x;
-    uint32_t count = 0;
-    for (int i = 0; i < tokens * kTopK; ++i) count += (ids[i] == e) ? 1u : 0u;
-    uint32_t pairs_total = 0, unique_total = 0;
-    const uint32_t pair_offset = block_exclusive_scan(count, scan_scratch, &pairs_total);
-    const uint32_t rank = block_exclusive_scan(count ? 1u : 0u, scan_scratch, &unique_total);
+    if (e < kExperts) tokmask[e] = 0ull;
+    __syncthreads();
+    for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) atomicOr(&tokmask[ids[i]], 1ull << (i / kTopK));
+    __syncthreads();
+    const unsigned long long mask = e < kExperts ? tokmask[e] : 0ull;
+    const uint32_t count = static_cast<uint32_t>(__popcll(mask));
+    // One scan of (unique flag << 16 | count): counts are <= 64 and pairs <= 512.
+    uint32_t packed_total = 0;
+    const uint32_t packed = scan256((count ? (1u << 16) : 0u) | count, scan_scratch, &packed_total);
+    const uint32_t pair_offset = packed & 0xffffu;
+    const uint32_t rank = packed >> 16;
+    const uint32_t pairs_total = packed_total & 0xffffu;
+    const uint32_t unique_total = packed_total >> 16;
+    if (e < kExperts) poff[e] = pair_offset;
+    const bool describe = slots != nullptr && expert_ptrs != nullptr && tokens <= 16;
     if (count) {
         plan.expert[rank] = e;
         plan.offset[rank] = static_cast<int32_t>(pair_offset);
-        uint32_t k = 0;
-        for (int t = 0; t < tokens; ++t) {
-            for (int r = 0; r < kTopK; ++r) {
-                if (ids[t * kTopK + r] == e) {
-                    const int p = static_cast<int>(pair_offset + k++);
-                    plan.pair_token[p] = t;
-                    plan.pair_slot[p] = r;
-                    int order = 0;
-                    for (int q = 0; q < kTopK; ++q) order += (ids[t * kTopK + q] < e) ? 1 : 0;
-                    plan.route_pair[t * kTopK + order] = p;
-                }
-            }
+        unsigned long long m = mask;
+        for (int j = 0; m; ++j) {
+            const int t = __ffsll(static_cast<long long>(m)) - 1;
+            m &= m - 1ull;
+            plan.pair_token[pair_offset + j] = t;
+        }
+        if (describe) {
+            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(expert_ptrs[2 * e]);
+            store_slot(slots + rank + 1, gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
+                       reinterpret_cast<const uint16_t*>(expert_ptrs[2 * e + 1]), static_cast<int>(pair_offset),
+                       static_cast<int>(count), static_cast<uint32_t>(mask), 1);
         }
     }
     if (e == 0) {
         plan.offset[unique_total] = static_cast<int32_t>(pairs_total);
         *plan.unique = static_cast<int32_t>(unique_total);
+        if (describe) {
+            const uint32_t all = tokens >= 32 ? 0xffffffffu : ((1u << tokens) - 1u);
+            store_slot(slots, sh_gate, sh_up, sh_down, kTopK * tokens, tokens, all, sh_down != nullptr ? 1 : 0);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
+        const int t = i / kTopK;
+        const int r = i % kTopK;
+        const int ex = ids[i];
+        const int p = static_cast<int>(poff[ex]) + __popcll(tokmask[ex] & ((1ull << t) - 1ull));
+        plan.pair_slot[p] = r;
+        int order = 0;
+        for (int q = 0; q < kTopK; ++q) order += (ids[t * kTopK + q] < ex) ? 1 : 0;
+        plan.route_pair[t * kTopK + order] = p;
     }
 }
 
@@ -203,11 +260,12 @@ __device__ int32_t validate_ids(const int32_t* ids, int tokens) {
     return flags;
 }
 
-// Logits for a tile of <= 16 tokens and 4*RPW router rows per workgroup
-// (RPW rows per wave), or the shared-expert gate (the last blockIdx.y, wave
-// 0).  With FUSED_TOPK (the whole call is one token tile), the last
-// workgroup to finish also runs top-k, renormalisation and bucketing.
-template <bool FUSED_TOPK, int RPW>
+// Router logits for a tile of <= 16 tokens: 4*RPW router rows per workgroup
+// (RPW rows per wave).  With SHARED_ROW the last blockIdx.y instead computes
+// the shared-expert gate for the tile (wave 0).  PREFILL also clears the
+// bucketing histogram for the top-k kernel that follows on the stream.  No
+// workgroup waits on another: the kernel boundary publishes the logits.
+template <bool PREFILL, int RPW>
 __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[kTokTile * kXStride];
     const int wave = threadIdx.x >> 6;
@@ -216,17 +274,16 @@ __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
     const int count = min(kTokTile, a.tokens - t0);
     constexpr int kRowGroups = kExperts / (4 * RPW);
 
-    if (!FUSED_TOPK && blockIdx.x == 0 && blockIdx.y == 0) {
-        // Clear the prefill histogram and bitmaps; the top-k kernel that fills
-        // them runs after this launch on the same stream.
+    if (PREFILL && blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < kExperts; i += blockDim.x) a.ws.counts[i] = 0;
         for (int i = threadIdx.x; i < kExperts * a.ws.words; i += blockDim.x) a.ws.bitmaps[i] = 0;
         if (threadIdx.x == 0) *a.plan.status = 0;
     }
 
-    // Issue this wave's router-row loads before staging the tokens.
+    // Issue this wave's weight loads before staging the tokens.
     const bool shared_row = blockIdx.y == kRowGroups;
     const bool router_rows = !shared_row && a.router != nullptr;
+    const bool gate_row = shared_row && a.shared_gate != nullptr;
     uint4 wraw[RPW][4];
     if (router_rows) {
 #pragma unroll
@@ -236,13 +293,13 @@ __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) wraw[i][q] = src[q];
         }
-    } else if (a.shared_gate != nullptr) {
+    } else if (gate_row) {
         const uint4* src = reinterpret_cast<const uint4*>(a.shared_gate + 32 * lane);
 #pragma unroll
         for (int q = 0; q < 4; ++q) wraw[0][q] = src[q];
     }
 
-    if (router_rows || (shared_row && a.shared_gate != nullptr) || (blockIdx.y == 0 && a.norm != nullptr)) {
+    if (router_rows || gate_row || (blockIdx.y == 0 && a.norm != nullptr)) {
         stage_tokens(xs, a.x, a.norm, a.eps, t0, count, blockIdx.y == 0 ? a.normed : nullptr);
     }
     __syncthreads();
@@ -259,7 +316,7 @@ __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
                 if (lane == 0) a.logits[static_cast<size_t>(t0 + t) * kExperts + row] = static_cast<uint16_t>(f2bf(s));
             }
         }
-    } else if (wave == 0 && a.shared_gate != nullptr) {
+    } else if (gate_row && wave == 0) {
         float w[32];
 #pragma unroll
         for (int q = 0; q < 4; ++q) unpack8(wraw[0][q], w + 8 * q);
@@ -268,29 +325,127 @@ __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
             if (lane == 0) a.sg[t0 + t] = static_cast<uint16_t>(f2bf(1.0f / (1.0f + lr_exp(-z))));
         }
     }
+}
 
-    if constexpr (FUSED_TOPK) {
-        __shared__ uint32_t ticket;
-        __shared__ int32_t ids[kTokTile * kTopK];
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) ticket = atomicAdd(&a.ws.control->route_counter, 1u);
-        __syncthreads();
-        if (ticket != gridDim.x * gridDim.y - 1) return;
-        __threadfence();
-        const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
-        for (int t = wave; t < a.tokens; t += 4) {
-            const int expert = topk_token(logits + static_cast<size_t>(t) * kExperts, a.indices + t * kTopK,
-                                          a.weights + t * kTopK, true);
-            if (lane < kTopK) ids[t * kTopK + lane] = expert;
+// Top-8 of one token by ballot radix selection.  Lane l holds the logits of
+// experts 4l..4l+3 as unique 24-bit keys; the 8th largest key is found bit by
+// bit from the top with wave-wide counts.  The eight winners land in LDS with
+// their exp() terms (already computed for the softmax denominator), lane k < 8
+// ranks entry k, and probabilities and weights take one divide per lane.
+// Indices, weights and the LDS expert row are written in rank order.
+// Arithmetic and order match topk_token (and the oracle) exactly.
+__device__ void topk_token_select(uint64_t packed, int64_t* indices_row, uint16_t* weights_row, int32_t* ids_row,
+                                  uint32_t* keys8, float* vals8) {
+    const int lane = threadIdx.x & 63;
+    uint32_t bits[4], keys[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
+        keys[j] = route_key(bits[j], 4 * lane + j);
+    }
+    uint32_t best = keys[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) best = keys[j] > best ? keys[j] : best;
+    best = wave_max_u32(best);
+    uint32_t threshold = 0;
+#pragma unroll 1
+    for (int bit = 23; bit >= 0; --bit) {
+        const uint32_t candidate = threshold | (1u << bit);
+        int above = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) above += __popcll(__ballot(keys[j] >= candidate));
+        if (above >= kTopK) threshold = candidate;
+    }
+    // Softmax terms of this lane's four experts, relative to the top logit.
+    const float top = bf2f(key_bits(best));
+    float ex[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ex[j] = lr_exp(bf2f(bits[j]) - top);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part = part + ex[j];
+    const float total = wave_butterfly_sum(part);
+    // Exactly eight keys are >= threshold (keys are unique); compact them.
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool chosen = keys[j] >= threshold;
+        const uint64_t mask = __ballot(chosen);
+        if (chosen) {
+            const int at = base + __popcll(mask & ((1ull << lane) - 1ull));
+            keys8[at] = keys[j];
+            vals8[at] = ex[j];
         }
-        __syncthreads();
-        bucket_small(ids, a.tokens, a.plan);
-        if (threadIdx.x == 0) {
-            *a.plan.status = 0;
-            __hip_atomic_store(&a.ws.control->route_counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        base += __popcll(mask);
+    }
+    // LDS accesses of one wave execute in order: the reads see the writes.
+    __builtin_amdgcn_wave_barrier();
+    const int k = lane & 7;
+    const uint32_t my_key = keys8[k];
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) rank += keys8[i] > my_key ? 1 : 0;
+    const float prob = vals8[k] / total;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < kTopK) vals8[rank] = prob;
+    __builtin_amdgcn_wave_barrier();
+    float sum = vals8[0];
+#pragma unroll
+    for (int i = 1; i < kTopK; ++i) sum = sum + vals8[i];
+    const int expert = 255 - static_cast<int>(my_key & 255u);
+    if (lane < kTopK) {
+        indices_row[rank] = expert;
+        weights_row[rank] = static_cast<uint16_t>(f2bf(prob / sum));
+        ids_row[rank] = expert;
+    }
+}
+
+// Decode routing tail in one workgroup of 16 waves (T <= 16): wave t runs
+// the top-k of token t (from the router's logits or the caller's) and its
+// shared-expert gate; then the workgroup builds the bucketing plan and the
+// decode slot records.
+__global__ __launch_bounds__(1024) void topk_bucket_small(RouteArgs a) {
+    __shared__ int32_t ids[kTokTile * kTopK];
+    __shared__ uint32_t keys8[kTokTile][kTopK];
+    __shared__ float vals8[kTokTile][kTopK];
+    const int t = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
+    if (t < a.tokens) {
+        // Issue every load of this wave first: its logits row, and the
+        // shared-gate weights and token row.
+        const uint64_t packed = reinterpret_cast<const uint64_t*>(logits + static_cast<size_t>(t) * kExperts)[lane];
+        const bool gate = a.shared_gate != nullptr;
+        uint4 wsg[4], xrow[4];
+        if (gate) {
+            const uint16_t* x = a.norm != nullptr ? a.normed : a.x;
+            const uint4* src = reinterpret_cast<const uint4*>(a.shared_gate + 32 * lane);
+            const uint4* row = reinterpret_cast<const uint4*>(x + static_cast<size_t>(t) * kHidden + 32 * lane);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                wsg[q] = src[q];
+                xrow[q] = row[q];
+            }
+        }
+        topk_token_select(packed, a.indices + t * kTopK, a.weights + t * kTopK, ids + t * kTopK, keys8[t], vals8[t]);
+        if (gate) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float w[8], xf[8];
+                unpack8(wsg[q], w);
+                unpack8(xrow[q], xf);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(w[j], xf[j], acc);
+            }
+            const float z = rbf(wave_butterfly_sum(acc));
+            if (lane == 0) a.sg[t] = static_cast<uint16_t>(f2bf(1.0f / (1.0f + lr_exp(-z))));
         }
     }
+    __syncthreads();
+    build_plan_small(ids, a.tokens, a.plan, a.ws.slots, a.expert_ptrs, a.shared_gate_proj, a.shared_up_proj,
+                     a.shared_down);
+    if (threadIdx.x == 0) *a.plan.status = 0;
 }
 
 // Prefill top-k: one wave per token; also records the expert histogram and
@@ -301,7 +456,7 @@ __global__ __launch_bounds__(256) void topk_tokens(RouteArgs a) {
     if (t >= a.tokens) return;
     const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
     const int expert = topk_token(logits + static_cast<size_t>(t) * kExperts, a.indices + t * kTopK,
-                                  a.weights + t * kTopK, false);
+                                  a.weights + t * kTopK);
     if (lane < kTopK) {
         atomicAdd(&a.ws.counts[expert], 1u);
         atomicOr(&a.ws.bitmaps[expert * a.ws.words + (t >> 5)], 1u << (t & 31));
@@ -341,8 +496,8 @@ __global__ __launch_bounds__(256) void bucket_scan(Workspace ws, Plan plan) {
     const int32_t status = *plan.status;
     const uint32_t count = status ? 0u : ws.counts[e];
     uint32_t pairs_total = 0, unique_total = 0;
-    const uint32_t pair_offset = block_exclusive_scan(count, scan_scratch, &pairs_total);
-    const uint32_t rank = block_exclusive_scan(count ? 1u : 0u, scan_scratch, &unique_total);
+    const uint32_t pair_offset = scan256(count, scan_scratch, &pairs_total);
+    const uint32_t rank = scan256(count ? 1u : 0u, scan_scratch, &unique_total);
     if (count) {
         plan.expert[rank] = e;
         plan.offset[rank] = static_cast<int32_t>(pair_offset);
@@ -385,7 +540,10 @@ __global__ __launch_bounds__(256) void bucket_fill(const int64_t* indices, int t
 }
 
 // Standalone bucketing of <= 64 caller-provided tokens in one workgroup.
-__global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan) {
+__global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan,
+                                                           SlotDesc* slots, const int64_t* expert_ptrs,
+                                                           const uint16_t* sh_gate, const uint16_t* sh_up,
+                                                           const uint16_t* sh_down) {
     __shared__ int32_t ids[64 * kTopK];
     for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
         const int64_t e = indices[i];
@@ -402,7 +560,7 @@ __global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indice
         for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) plan.route_pair[i] = -1;
         return;
     }
-    bucket_small(ids, tokens, plan);
+    build_plan_small(ids, tokens, plan, slots, expert_ptrs, sh_gate, sh_up, sh_down);
     if (threadIdx.x == 0) *plan.status = 0;
 }
 
@@ -410,15 +568,20 @@ __global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indice
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
-    const int tiles = (a.tokens + kTokTile - 1) / kTokTile;
     timing_mark(kStageRoute, stream, true);
     if (a.tokens <= kTokTile) {
-        // Decode: one router row per wave, 64 workgroups + the shared gate.
-        hipLaunchKernelGGL((router_logits<true, 1>), dim3(1, kExperts / 4 + 1), dim3(256), 0, stream, a);
+        // Decode: router GEMV (one row per wave, 64 workgroups; skipped when
+        // logits are given), then top-k + shared gate + bucketing in one
+        // workgroup.
+        if (a.router != nullptr || a.norm != nullptr) {
+            hipLaunchKernelGGL((router_logits<false, 1>), dim3(1, kExperts / 4), dim3(256), 0, stream, a);
+        }
+        hipLaunchKernelGGL(topk_bucket_small, dim3(1), dim3(1024), 0, stream, a);
         timing_mark(kStageRoute, stream, false);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((router_logits<false, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, a);
+    const int tiles = (a.tokens + kTokTile - 1) / kTokTile;
+    hipLaunchKernelGGL((router_logits<true, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(topk_tokens, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, a.ws, a.plan);
     hipLaunchKernelGGL(bucket_fill, dim3((a.tokens + 255) / 256), dim3(256), 0, stream, a.indices, a.tokens, a.ws,
@@ -427,10 +590,13 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream) {
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream,
+                         const int64_t* expert_ptrs, const uint16_t* sh_gate, const uint16_t* sh_up,
+                         const uint16_t* sh_down) {
     if (tokens <= 0) return hipSuccess;
     if (tokens <= 64) {
-        hipLaunchKernelGGL(bucket_small_kernel, dim3(1), dim3(256), 0, stream, indices, tokens, plan);
+        hipLaunchKernelGGL(bucket_small_kernel, dim3(1), dim3(256), 0, stream, indices, tokens, plan, ws.slots,
+                           expert_ptrs, sh_gate, sh_up, sh_down);
         return hipGetLastError();
     }
     const int clear_blocks = min(64, (kExperts * ws.words + 255) / 256);
