@@ -45,6 +45,7 @@ BF16_PEAK_TFLOPS = 2500.0
 PAIR_FLOP = 2 * 3 * INNER * HIDDEN  # one (token, expert) SwiGLU pair
 SHARED_BYTES = EXPERT_BYTES + 2 * HIDDEN
 ROUTER_BYTES = 256 * HIDDEN * 2
+COPY_BYTES = 256 * 2**20
 
 
 def log(msg: str) -> None:
@@ -162,6 +163,23 @@ def kernel_time(case: Case, stage: int, passes: int) -> tuple[float, int]:
     return total / max(launches, 1), launches
 
 
+def measured_traffic(kernel: str) -> dict | None:
+    """HBM bytes per dispatch of ``kernel`` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE passes, scaled by a 256 MiB copy)."""
+    path = ROOT / "profiles" / "c2_t8_zipf_hbm_traffic.md"
+    if not path.exists():
+        return None
+    text = path.read_text()
+    start = text.find("```json")
+    if start < 0:
+        return None
+    block = json.loads(text[start + 7:text.index("```", start + 7)])
+    if block.get("kernel") != kernel:
+        return None
+    return {"bytes": int(block["read_bytes"]) + int(block["write_bytes"]),
+            "source": f"profiles/{path.name}"}
+
+
 def cpu_baseline(model, case: Case, uniques, budget_s: float = 15.0) -> dict:
     """The reference CPU expert kernel (oracle/_ref/libcpu_experts.so, built
     from edge35b/cpu_experts.c) on the headline routes: expert_block_rows over
@@ -222,6 +240,9 @@ def main() -> int:
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
     parser.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4 to run (default all)")
+    parser.add_argument("--calibrate-copy", action="store_true",
+                        help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
+                             "of a profiler run can be scaled by a kernel of known traffic")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -241,6 +262,13 @@ def main() -> int:
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
+    if args.calibrate_copy:
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=device).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- headline: T=8 Zipf verify ----
     logits = [bf16_from_f64(zipf_logits(8, args.seed * 1000 + l), device) for l in range(L)]
@@ -258,7 +286,9 @@ def main() -> int:
         stage_us[name] = round(ms_k * 1e3, 2)
         if name == "gateup":
             gate_ms, gate_launches = ms_k, launches
-    gate_bytes = (np.mean(uniques) + 1) * (2 * INNER * HIDDEN * 2) + (8 * 8 + 8) * (HIDDEN * 2 + INNER * 2)
+    # gate/up kernel: unique gate+up weights (routed + shared) once, the 8
+    # hidden rows once, the activation rows of 64 routes + 8 shared written.
+    gate_bytes = (np.mean(uniques) + 1) * (2 * INNER * HIDDEN * 2) + 8 * HIDDEN * 2 + (8 * 8 + 8) * INNER * 2
     gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
     log(f"[bench] C2 stages (us, event-bracketed): {stage_us}; gate/up {gate_gbs:.0f} GB/s")
     configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2),
@@ -340,6 +370,7 @@ def main() -> int:
         cpu = cpu_baseline(model, c2, uniques)
         log(f"[bench] CPU baseline: {cpu}")
 
+    traffic = measured_traffic("gateup_decode")
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -358,8 +389,10 @@ def main() -> int:
                    "tokens": 8, "hidden": HIDDEN, "experts": 256, "topk": 8, "inner": INNER,
                    "layers_rotated": L, "mean_unique_experts": round(float(np.mean(uniques)), 2)},
         "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gateup_kernel", "avg_us": round(gate_ms * 1e3, 3), "launches": gate_launches,
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else traffic["bytes"],
+                     "traffic_source": None if traffic is None else traffic["source"],
+                     "kernel": "gateup_decode", "avg_us": round(gate_ms * 1e3, 3), "launches": gate_launches,
                      "algorithmic_bytes": int(gate_bytes)},
         "cpu_baseline": cpu,
         "configs": configs,

@@ -214,10 +214,8 @@ __global__ __launch_bounds__(kDownWaves * kWave) void down_combine_decode(Expert
 
 hipError_t launch_experts_decode(const ExpertArgs& a, hipStream_t stream) {
     const int slots = min(kTopK * a.tokens, kExperts) + 1;
-    timing_mark(kStageGateUp, stream, true);
-    hipLaunchKernelGGL(gateup_decode, dim3(slots * kRowTiles), dim3(256), 0, stream, a);
-    timing_mark(kStageGateUp, stream, false);
-    timing_mark(kStageDown, stream, true);
+    const StageEvents gate_ev = timing_events(kStageGateUp);
+    LRMOE_LAUNCH(gateup_decode, dim3(slots * kRowTiles), dim3(256), 0, stream, gate_ev.start, gate_ev.stop, a);
     const size_t act_bytes = static_cast<size_t>(kTopK + 1) * a.tokens * kActStride * sizeof(uint16_t);
     static bool lds_opt_in = false;
     if (!lds_opt_in) {
@@ -226,8 +224,9 @@ hipError_t launch_experts_decode(const ExpertArgs& a, hipStream_t stream) {
         if (err != hipSuccess) return err;
         lds_opt_in = true;
     }
-    hipLaunchKernelGGL(down_combine_decode, dim3(kHidden / kDownRows), dim3(kDownWaves * kWave), act_bytes, stream, a);
-    timing_mark(kStageDown, stream, false);
+    const StageEvents down_ev = timing_events(kStageDown);
+    LRMOE_LAUNCH(down_combine_decode, dim3(kHidden / kDownRows), dim3(kDownWaves * kWave), act_bytes, stream,
+                 down_ev.start, down_ev.stop, a);
     return hipGetLastError();
 }
 

@@ -331,15 +331,12 @@ hipError_t launch_experts(const ExpertArgs& a, hipStream_t stream) {
     if (a.tokens <= 16) return launch_experts_decode(a, stream);
     const int max_unique = min(kTopK * a.tokens, kExperts);
     const int slots = max_unique + 1;
-    timing_mark(kStageGateUp, stream, true);
-    hipLaunchKernelGGL(gateup_kernel, dim3(slots * kGateTiles), dim3(256), 0, stream, a);
-    timing_mark(kStageGateUp, stream, false);
-    timing_mark(kStageDown, stream, true);
-    hipLaunchKernelGGL(down_kernel, dim3(slots * kDownTiles), dim3(256), 0, stream, a);
-    timing_mark(kStageDown, stream, false);
-    timing_mark(kStageCombine, stream, true);
-    hipLaunchKernelGGL(combine_kernel, dim3(a.tokens), dim3(256), 0, stream, a);
-    timing_mark(kStageCombine, stream, false);
+    const StageEvents gate_ev = timing_events(kStageGateUp);
+    LRMOE_LAUNCH(gateup_kernel, dim3(slots * kGateTiles), dim3(256), 0, stream, gate_ev.start, gate_ev.stop, a);
+    const StageEvents down_ev = timing_events(kStageDown);
+    LRMOE_LAUNCH(down_kernel, dim3(slots * kDownTiles), dim3(256), 0, stream, down_ev.start, down_ev.stop, a);
+    const StageEvents comb_ev = timing_events(kStageCombine);
+    LRMOE_LAUNCH(combine_kernel, dim3(a.tokens), dim3(256), 0, stream, comb_ev.start, comb_ev.stop, a);
     return hipGetLastError();
 }
 

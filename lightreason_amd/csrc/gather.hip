@@ -88,10 +88,9 @@ hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations
                          const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
                          int max_copies, int stripes, int32_t* status, hipStream_t stream) {
     if (max_copies <= 0 || banks <= 0) return hipSuccess;
-    timing_mark(kStageGather, stream, true);
-    hipLaunchKernelGGL(gather_kernel, dim3(stripes, banks, max_copies), dim3(256), 0, stream, descriptors, destinations,
-                       sizes, src_ids, dst_ids, count, experts, status);
-    timing_mark(kStageGather, stream, false);
+    const StageEvents ev = timing_events(kStageGather);
+    LRMOE_LAUNCH(gather_kernel, dim3(stripes, banks, max_copies), dim3(256), 0, stream, ev.start, ev.stop, descriptors,
+                 destinations, sizes, src_ids, dst_ids, count, experts, status);
     return hipGetLastError();
 }
 

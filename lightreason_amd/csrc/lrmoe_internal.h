@@ -2,6 +2,7 @@
 // workspace layout and the launch declarations each .hip file provides.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -156,8 +157,13 @@ struct ExpertArgs {
     Workspace ws;
 };
 
-// Optional per-stage timing: when a stage's bit is enabled, each launch of
-// that stage is bracketed by a pair of HIP events on its stream.
+// Optional per-stage timing.  When a stage's bit is enabled, timing_events()
+// hands out the next (start, stop) event pair of that stage; the stage's
+// first kernel is launched with the start event and its last kernel with the
+// stop event through hipExtLaunchKernelGGL, so the two timestamps are taken
+// by the kernels' own dispatches (no separate marker packets).  Both events
+// are null when the stage is not timed (or its event list is full), and the
+// launch is then an ordinary one.
 enum Stage : int {
     kStageRoute = 1,
     kStageGateUp = 2,
@@ -165,7 +171,23 @@ enum Stage : int {
     kStageCombine = 8,
     kStageGather = 16,
 };
-void timing_mark(int stage, hipStream_t stream, bool start);
+struct StageEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+StageEvents timing_events(int stage);
+
+// Launch with optional start/stop timing events (see timing_events).
+#define LRMOE_LAUNCH(kernel, grid, block, lds, stream, start_event, stop_event, ...)                            \
+    do {                                                                                                      \
+        const hipEvent_t lrmoe_start_ = (start_event);                                                        \
+        const hipEvent_t lrmoe_stop_ = (stop_event);                                                          \
+        if (lrmoe_start_ != nullptr || lrmoe_stop_ != nullptr) {                                              \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, lrmoe_start_, lrmoe_stop_, 0, __VA_ARGS__); \
+        } else {                                                                                              \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                \
+        }                                                                                                     \
+    } while (0)
 
 hipError_t launch_route(const RouteArgs& args, hipStream_t stream);
 hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream,

@@ -568,25 +568,25 @@ __global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indice
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
-    timing_mark(kStageRoute, stream, true);
+    const StageEvents ev = timing_events(kStageRoute);
     if (a.tokens <= kTokTile) {
         // Decode: router GEMV (one row per wave, 64 workgroups; skipped when
         // logits are given), then top-k + shared gate + bucketing in one
         // workgroup.
+        hipEvent_t start = ev.start;
         if (a.router != nullptr || a.norm != nullptr) {
-            hipLaunchKernelGGL((router_logits<false, 1>), dim3(1, kExperts / 4), dim3(256), 0, stream, a);
+            LRMOE_LAUNCH((router_logits<false, 1>), dim3(1, kExperts / 4), dim3(256), 0, stream, start, nullptr, a);
+            start = nullptr;
         }
-        hipLaunchKernelGGL(topk_bucket_small, dim3(1), dim3(1024), 0, stream, a);
-        timing_mark(kStageRoute, stream, false);
+        LRMOE_LAUNCH(topk_bucket_small, dim3(1), dim3(1024), 0, stream, start, ev.stop, a);
         return hipGetLastError();
     }
     const int tiles = (a.tokens + kTokTile - 1) / kTokTile;
-    hipLaunchKernelGGL((router_logits<true, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, a);
+    LRMOE_LAUNCH((router_logits<true, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, ev.start, nullptr, a);
     hipLaunchKernelGGL(topk_tokens, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, a.ws, a.plan);
-    hipLaunchKernelGGL(bucket_fill, dim3((a.tokens + 255) / 256), dim3(256), 0, stream, a.indices, a.tokens, a.ws,
-                       a.plan);
-    timing_mark(kStageRoute, stream, false);
+    LRMOE_LAUNCH(bucket_fill, dim3((a.tokens + 255) / 256), dim3(256), 0, stream, nullptr, ev.stop, a.indices,
+                 a.tokens, a.ws, a.plan);
     return hipGetLastError();
 }
 

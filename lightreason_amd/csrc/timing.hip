@@ -1,7 +1,8 @@
-// Optional stage timing for measurement runs: HIP events recorded around the
-// launches of selected stages.  Disabled (one branch per launch) unless
-// lrmoe_timing_enable() is called; never enable it while a stream is being
-// captured into a graph.
+// Optional stage timing for measurement runs: start/stop HIP events passed to
+// the first and last kernel launch of selected stages (hipExtLaunchKernelGGL
+// takes the timestamps from the kernels' dispatches).  Disabled (one branch
+// per launch) unless lrmoe_timing_enable() is called; never enable it while a
+// stream is being captured into a graph.
 #include <vector>
 
 #include "lrmoe_internal.h"
@@ -30,14 +31,16 @@ int stage_index(int stage) {
 
 }  // namespace
 
-void timing_mark(int stage, hipStream_t stream, bool start) {
+StageEvents timing_events(int stage) {
     Timing& t = timing();
-    if (!(t.mask & stage)) return;
+    StageEvents ev;
+    if (!(t.mask & stage)) return ev;
     const int i = stage_index(stage);
-    if (i < 0) return;
-    // A start takes a slot only when a whole start/stop pair still fits.
-    if (start ? t.used[i] + 2 > 2 * t.capacity : (t.used[i] & 1) == 0) return;
-    (void)hipEventRecord(t.events[i][t.used[i]++], stream);
+    if (i < 0 || t.used[i] + 2 > 2 * t.capacity) return ev;
+    ev.start = t.events[i][t.used[i]];
+    ev.stop = t.events[i][t.used[i] + 1];
+    t.used[i] += 2;
+    return ev;
 }
 
 }  // namespace lrmoe
