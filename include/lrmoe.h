@@ -128,13 +128,17 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
  * bytes from descriptors[(b*experts + src_ids[row])*3] to
  * destinations[b] + dst_ids[row]*sizes[b]; a descriptor whose second field is
  * >= 0 (a codec row) is skipped and LRMOE_STATUS_CODEC_ROW is or-ed into
- * *status (may be NULL).  Grid (stripes, banks, max_copies).
+ * *status (may be NULL).  Grid (stripes, banks, max_copies) of `threads`
+ * (64, 128, 192 or 256) threads; keep_in_l2 = 0 streams the rows with
+ * nontemporal accesses, 1 uses cached accesses (the reference geometries'
+ * "default" and "l2" policies).  Sizes and addresses are multiples of 16 bytes.
  * Replaces edge35b/bf16_gather_ada.cu:36-66 (gather_bf16 raw path) launched
  * by native_bf16_gather.py:71-77 (NativeBf16Gather.copy), and the staging copy
  * of scheduled_graph.py:14-26 (_stage). */
 int lrmoe_gather(const int64_t *descriptors, const int64_t *destinations, const int64_t *sizes,
                  const int32_t *src_ids, const int32_t *dst_ids, const int64_t *count, int experts,
-                 int banks, int max_copies, int stripes, int32_t *status, void *stream);
+                 int banks, int max_copies, int stripes, int threads, int keep_in_l2, int32_t *status,
+                 void *stream);
 
 /* Batched matvec with the _matvec protocol: for e < experts and r < N,
  * result[e*N + r] = bf16(sum_k W_e[r,k] x_e[k]), W_e = table[stride*e + column]

@@ -32,7 +32,7 @@ _SIGNATURES = {
     "lrmoe_bucket": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_experts": ([_P, _I, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
-    "lrmoe_gather": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
+    "lrmoe_gather": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "lrmoe_matvec": ([_P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "lrmoe_ordered_sum": ([_P, _P, _P, _P, _P, _I, _P], _I),
     "lrmoe_gate_silu": ([_P, _P, _P, _I, _I, _P], _I),

@@ -173,15 +173,15 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
 
 int lrmoe_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                  const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
-                 int max_copies, int stripes, int32_t* status, void* stream) {
+                 int max_copies, int stripes, int threads, int keep_in_l2, int32_t* status, void* stream) {
     if (!descriptors || !destinations || !sizes || !src_ids || !dst_ids || !count) return LRMOE_E_ARG;
     if (experts <= 0 || banks <= 0 || banks > 65535 || max_copies < 0 || max_copies > 65535 || stripes <= 0 ||
-        stripes > 65535)
+        stripes > 65535 || threads < 64 || threads > 256 || threads % 64 != 0)
         return LRMOE_E_ARG;
     if (max_copies == 0) return LRMOE_OK;
     if (int d = check_device()) return d;
     return status_of(lrmoe::launch_gather(descriptors, destinations, sizes, src_ids, dst_ids, count, experts, banks,
-                                          max_copies, stripes, status, as_stream(stream)));
+                                          max_copies, stripes, threads, keep_in_l2, status, as_stream(stream)));
 }
 
 int lrmoe_matvec(const int64_t* table, const uint16_t* x, uint16_t* result, int K, int N, int column, int shared_x,

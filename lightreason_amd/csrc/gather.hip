@@ -18,6 +18,10 @@ namespace {
 
 constexpr int kGatherUnroll = 8;
 
+// kStream = true: nontemporal loads and stores (the rows stream past the
+// caches, the "default" policy); false: ordinary cached accesses that leave
+// the rows in L2 ("l2").
+template <bool kStream>
 __global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors, const int64_t* destinations,
                                                      const int64_t* sizes, const int32_t* src_ids,
                                                      const int32_t* dst_ids, const int64_t* count, int experts,
@@ -44,9 +48,17 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors,
     for (; i + (kGatherUnroll - 1) * blockDim.x < end; i += step) {
         u32x4 v[kGatherUnroll];
 #pragma unroll
-        for (int u = 0; u < kGatherUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * blockDim.x);
+        for (int u = 0; u < kGatherUnroll; ++u) {
+            v[u] = kStream ? __builtin_nontemporal_load(src + i + u * blockDim.x) : src[i + u * blockDim.x];
+        }
 #pragma unroll
-        for (int u = 0; u < kGatherUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * blockDim.x);
+        for (int u = 0; u < kGatherUnroll; ++u) {
+            if (kStream) {
+                __builtin_nontemporal_store(v[u], dst + i + u * blockDim.x);
+            } else {
+                dst[i + u * blockDim.x] = v[u];
+            }
+        }
     }
     for (; i < end; i += blockDim.x) dst[i] = src[i];
 }
@@ -86,11 +98,18 @@ uint64_t host_splitmix64(uint64_t z) {
 
 hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                          const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
-                         int max_copies, int stripes, int32_t* status, hipStream_t stream) {
+                         int max_copies, int stripes, int threads, int keep_in_l2, int32_t* status,
+                         hipStream_t stream) {
     if (max_copies <= 0 || banks <= 0) return hipSuccess;
     const StageEvents ev = timing_events(kStageGather);
-    LRMOE_LAUNCH(gather_kernel, dim3(stripes, banks, max_copies), dim3(256), 0, stream, ev.start, ev.stop, descriptors,
-                 destinations, sizes, src_ids, dst_ids, count, experts, status);
+    const dim3 grid(stripes, banks, max_copies);
+    if (keep_in_l2) {
+        LRMOE_LAUNCH(gather_kernel<false>, grid, dim3(threads), 0, stream, ev.start, ev.stop, descriptors,
+                     destinations, sizes, src_ids, dst_ids, count, experts, status);
+    } else {
+        LRMOE_LAUNCH(gather_kernel<true>, grid, dim3(threads), 0, stream, ev.start, ev.stop, descriptors,
+                     destinations, sizes, src_ids, dst_ids, count, experts, status);
+    }
     return hipGetLastError();
 }
 

@@ -195,7 +195,8 @@ hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws
                          const uint16_t* shared_up_proj = nullptr, const uint16_t* shared_down = nullptr);
 hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                          const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
-                         int max_copies, int stripes, int32_t* status, hipStream_t stream);
+                         int max_copies, int stripes, int threads, int keep_in_l2, int32_t* status,
+                         hipStream_t stream);
 hipError_t launch_matvec(const int64_t* table, const uint16_t* x, uint16_t* result, int K, int N, int column,
                          int shared_x, int stride, int experts, hipStream_t stream);
 hipError_t launch_ordered_sum(const int64_t* table, const uint16_t* hot, const uint16_t* cold, const uint16_t* router,

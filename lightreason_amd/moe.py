@@ -279,9 +279,9 @@ def moe_layer(hidden: torch.Tensor, layer: LayerWeights, *, out: torch.Tensor | 
 
 
 def gather(descriptors, destinations, sizes, src, dst, count, *, max_copies: int, experts: int, stripes: int = 64,
-           status: torch.Tensor | None = None) -> None:
+           threads: int = 256, keep_in_l2: bool = False, status: torch.Tensor | None = None) -> None:
     """Raw BF16 row gather (see include/lrmoe.h lrmoe_gather)."""
     device = destinations.device
     _native.call("lrmoe_gather", descriptors.data_ptr(), destinations.data_ptr(), sizes.data_ptr(), src.data_ptr(),
                  dst.data_ptr(), count.data_ptr(), int(experts), int(destinations.numel()), int(max_copies),
-                 int(stripes), _opt(status), _stream(device))
+                 int(stripes), int(threads), int(bool(keep_in_l2)), _opt(status), _stream(device))

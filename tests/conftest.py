@@ -36,3 +36,22 @@ def device():
 
     _native.device_check()
     return torch.device("cuda:0")
+
+
+SEED = 4242
+
+
+@pytest.fixture(scope="session")
+def model(device):
+    """One synthetic layer (256 resident experts, router, shared expert,
+    RMSNorm weight) shared by the GPU test modules."""
+    from lightreason_amd.synthetic import SyntheticModel
+
+    return SyntheticModel(layers=1, device=device, seed=SEED, shared=True, norm="normal")
+
+
+@pytest.fixture(scope="session")
+def host_experts(model):
+    from helpers import HostExperts
+
+    return HostExperts(model.bank, 0)

@@ -1,0 +1,141 @@
+"""Host-side behaviour of the reference-shaped surface (no GPU needed): the
+guards, error types and protocol checks that fire before any kernel launch,
+mirroring the reference's own argument checks (fused_experts.py:41-50,
+block_experts.py:91-95, native_bf16_gather.py:17-22, packed_native.py:153-154,
+expert_stream.py:465-466)."""
+
+from __future__ import annotations
+
+import sys
+import types
+
+import pytest
+import torch
+
+from lightreason_amd.edge35b import _grid, block_experts, expert_stream, fused_experts, native_bf16_gather, \
+    packed_native
+
+
+def _layer(**kw):
+    base = dict(pool=None, module=types.SimpleNamespace(num_experts=256),
+                gate_up=torch.empty((256, 1024, 2048), dtype=torch.bfloat16, device="meta"),
+                down=torch.empty((256, 2048, 512), dtype=torch.bfloat16, device="meta"))
+    base.update(kw)
+    return types.SimpleNamespace(**base)
+
+
+def test_fused_forward_guards():
+    layer = _layer()
+    x = torch.zeros((1, 2048), dtype=torch.bfloat16)
+    idx = torch.zeros((1, 8), dtype=torch.int64)
+    w = torch.zeros((1, 8), dtype=torch.bfloat16)
+    for bad in (dict(hidden=torch.zeros((2, 2048), dtype=torch.bfloat16)),
+                dict(hidden=x.float()), dict(indices=torch.zeros((1, 7), dtype=torch.int64)),
+                dict(weights=w.float()), dict(hidden=torch.zeros((2048, 2), dtype=torch.bfloat16).t())):
+        args = dict(hidden=x, indices=idx, weights=w)
+        args.update(bad)
+        with pytest.raises(ValueError, match="single-token 35B route shape"):
+            fused_experts.fused_forward(layer, args["hidden"], args["indices"], args["weights"])
+    with pytest.raises(ValueError, match="single-token"):
+        fused_experts.fused_forward(_layer(down=torch.empty((256, 512, 2048), device="meta")), x, idx, w)
+
+
+def test_grouped_block_guards():
+    layer = _layer()
+    w = torch.zeros((4, 8), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="2–16"):
+        block_experts.grouped_block(layer, torch.zeros((17, 2048), dtype=torch.bfloat16),
+                                    torch.zeros((17, 8), dtype=torch.int64), torch.zeros((17, 8)))
+    with pytest.raises(ValueError, match="2–16"):
+        block_experts.grouped_block(layer, torch.zeros((4, 2048)), torch.zeros((4, 7), dtype=torch.int64), w)
+    with pytest.raises(ValueError, match="contiguous"):
+        block_experts.grouped_block(layer, torch.zeros((2048, 4)).t(), torch.zeros((4, 8), dtype=torch.int64), w)
+
+
+def test_grid_protocol():
+    calls = []
+    k = _grid.GridKernel("k", lambda grid, *args: calls.append((grid, args)))
+    k[(4, 8)](1, 2, num_warps=8, enable_fp_fusion=False)
+    k[16](3)
+    assert calls == [((4, 8, 1), (1, 2)), ((16, 1, 1), (3,))]
+    with pytest.raises(TypeError):
+        k[(4,)](1, bogus=1)
+    with pytest.raises(TypeError):
+        k[lambda meta: (1,)]
+    with pytest.raises(ValueError):
+        k[(0, 1)]
+    with pytest.raises(ValueError):
+        k[(1, 1, 1, 1)]
+
+
+def test_shims_check_sizes_before_launch():
+    t = torch.zeros(3 * 8, dtype=torch.int64)
+    x = torch.zeros(2048, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cover all N rows"):
+        fused_experts._matvec[(64, 8)](t, x, torch.zeros(8 * 1024, dtype=torch.bfloat16), 2048, 1024, 0, 8, True)
+    with pytest.raises(ValueError, match="table"):
+        fused_experts._matvec[(128, 9)](t, x, torch.zeros(9 * 1024, dtype=torch.bfloat16), 2048, 1024, 0, 8, True)
+    with pytest.raises(ValueError, match="device tensor"):
+        fused_experts._matvec[(128, 8)](t, x, torch.zeros(8 * 1024, dtype=torch.bfloat16), 2048, 1024, 0, 8, True)
+    with pytest.raises(ValueError, match="HIDDEN must be 2048"):
+        fused_experts._ordered_sum[(8,)](t, x, x, x, 1024, 256)
+    with pytest.raises(ValueError, match="ROWS must be 16"):
+        block_experts._project[(4, 32)](t, t, x, x, 2048, 1024, False, 8, 32, 64)
+
+
+def test_gather_geometries():
+    g = native_bf16_gather
+    assert g.select_geometry("hip-8-256-l2") == (8, 256, "l2")
+    assert g.select_geometry("cuda-8-256-l2") == (8, 256, "l2")  # reference tag
+    assert g.select_geometry("hip-4-256-cpu-tiles", shared=True) == (4, 256, "cpu-tiles")
+    assert [g.name(x) for x in g.NATIVE_GEOMETRIES][0] == "hip-4-256-default"
+    with pytest.raises(ValueError, match="Unknown"):
+        g.select_geometry("hip-4-256-cpu-tiles")
+    with pytest.raises(ValueError, match="Unknown"):
+        g.select_geometry("hip-3-256-default")
+
+
+def test_mode_validation():
+    pool = expert_stream.ExpertPool("cuda:0")
+    with pytest.raises(ValueError, match="transfer mode"):
+        with expert_stream.patch_experts(torch.nn.Module(), mode="bogus", pool=pool):
+            pass
+    with pytest.raises(ValueError, match="No experts modules"):
+        with expert_stream.patch_experts(torch.nn.Module(), mode="fused", pool=pool):
+            pass
+    with pytest.raises(ValueError, match="Unknown Packed ablation"):
+        with packed_native.configure(pool, "bogus"):
+            pass
+    with pytest.raises(ValueError, match="GPU device"):
+        expert_stream.ExpertPool("cpu")
+    with pytest.raises(ValueError, match="capacity_bytes"):
+        expert_stream.ExpertPool("cuda:0", capacity_bytes=-1)
+
+
+def test_layer_adapter_checks_shapes_and_activation():
+    pool = expert_stream.ExpertPool("cuda:0")
+
+    def module(experts=256, hidden=2048, inner=512, act=torch.nn.functional.silu):
+        m = torch.nn.Module()
+        m.num_experts, m.hidden_dim, m.intermediate_dim, m.act_fn = experts, hidden, inner, act
+        m.gate_up_proj = torch.nn.Parameter(torch.empty((experts, 2 * inner, hidden), dtype=torch.bfloat16,
+                                                        device="meta"), requires_grad=False)
+        m.down_proj = torch.nn.Parameter(torch.empty((experts, hidden, inner), dtype=torch.bfloat16, device="meta"),
+                                         requires_grad=False)
+        return m
+
+    with pytest.raises(ValueError, match="256 experts"):
+        expert_stream._Layer("l", module(experts=128), pool, "fused")
+    with pytest.raises(ValueError, match="SiLU"):
+        expert_stream._Layer("l", module(act=torch.nn.functional.gelu), pool, "fused")
+
+
+def test_install_as_edge35b():
+    import lightreason_amd.edge35b as pkg
+
+    pkg.install_as_edge35b()
+    import edge35b.fused_experts as fe  # noqa: F401 -- resolved through the alias
+
+    assert sys.modules["edge35b"] is pkg
+    assert fe is fused_experts
+    assert sys.modules["edge35b.native_bf16_gather"] is native_bf16_gather

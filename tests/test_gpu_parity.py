@@ -20,18 +20,6 @@ pytestmark = pytest.mark.gpu
 SEED = 4242
 
 
-@pytest.fixture(scope="module")
-def model(device):
-    from lightreason_amd.synthetic import SyntheticModel
-
-    return SyntheticModel(layers=1, device=device, seed=SEED, shared=True, norm="normal")
-
-
-@pytest.fixture(scope="module")
-def host_experts(model):
-    return HostExperts(model.bank, 0)
-
-
 def test_generator_matches_host(device, oracle):
     from lightreason_amd.moe import fill_normal_
 

@@ -68,7 +68,8 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_matvec(dummy, dummy, dummy, 100, 8, 0, 1, 3, 8, null) == -1  # K not a multiple of 512
     assert lib.lrmoe_ordered_sum(dummy, dummy, null, dummy, dummy, 5, null) == -1
     assert lib.lrmoe_project(dummy, dummy, dummy, dummy, 2048, 1000, 0, 4, null) == -1
-    assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 0, 2, 8, 64, null, null) == -1
+    assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 0, 2, 8, 64, 256, 0, null, null) == -1
+    assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 8, 2, 8, 64, 100, 0, null, null) == -1
     # zero tokens is a successful no-op
     assert lib.lrmoe_moe_experts(dummy, 0, dummy, dummy, dummy, dummy, dummy, 0, null) == 0
     from lightreason_amd import _native
