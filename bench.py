@@ -35,7 +35,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from lightreason_amd import _native  # noqa: E402
-from lightreason_amd.moe import (EXPERT_BYTES, EXPERT_ELEMENTS, HIDDEN, INNER, LayerWeights, Workspace,  # noqa: E402
+from lightreason_amd.moe import (EXPERT_BYTES, EXPERT_ELEMENTS, GATE_UP_ELEMENTS, HIDDEN, INNER, LayerWeights,  # noqa: E402
+                                 Workspace,
                                  gather, moe_layer)
 from lightreason_amd.synthetic import SyntheticModel  # noqa: E402
 
@@ -180,6 +181,50 @@ def measured_traffic(kernel: str) -> dict | None:
             "source": f"profiles/{path.name}"}
 
 
+def cpu_workers_t1(model, case: Case, budget_s: float = 5.0) -> dict | None:
+    """The reference's persistent CPU expert workers (oracle/_ref/
+    libpacked_workers.so, built from edge35b/packed_workers.cpp) on T=1
+    decode routes: one submit/wait of the 8 routed experts per layer, cycling
+    over 8 layers' host copies.  GB/s on the 8 x 6 MiB expert bytes."""
+    import ctypes as C
+
+    from oracle import oracle as O
+
+    ref = O.reference_workers()
+    if ref is None:
+        return None
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    calls = []
+    for j in range(min(len(case.layer_ids), 8)):
+        layer = case.layer_ids[j]
+        experts = case.idx[j][0].cpu().tolist()
+        rows = [model.bank.bank[layer, e].cpu().view(torch.int16).numpy().view(np.uint16) for e in experts]
+        gates = (C.c_void_p * 8)(*[r.ctypes.data for r in rows])
+        downs = (C.c_void_p * 8)(*[r.ctypes.data + 2 * GATE_UP_ELEMENTS for r in rows])
+        x = case.x[j].cpu().view(torch.int16).numpy().view(np.uint16)
+        calls.append((gates, downs, x, rows))
+    out = np.empty((8, HIDDEN), dtype=np.uint16)
+    workers = ref.packed_workers_create(threads)
+    try:
+        for gates, downs, x, _ in calls:
+            ref.packed_workers_submit(workers, gates, downs, x.ctypes.data, out.ctypes.data, 8)
+            ref.packed_workers_wait(workers)
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            gates, downs, x, _ = calls[n % len(calls)]
+            ref.packed_workers_submit(workers, gates, downs, x.ctypes.data, out.ctypes.data, 8)
+            ref.packed_workers_wait(workers)
+            n += 1
+        dt = time.perf_counter() - t0
+    finally:
+        ref.packed_workers_destroy(workers)
+    return {"value": round(n * 8 * EXPERT_BYTES / dt / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "reference", "us_per_layer": round(1e6 * dt / n, 1),
+            "sample": f"{n} submit/wait calls of 8 routed experts (T=1), cycling over {len(calls)} layers, "
+                      f"packed_workers with {threads} threads"}
+
+
 def cpu_baseline(model, case: Case, uniques, budget_s: float = 15.0) -> dict:
     """The reference CPU expert kernel (oracle/_ref/libcpu_experts.so, built
     from edge35b/cpu_experts.c) on the headline routes: expert_block_rows over
@@ -306,6 +351,8 @@ def main() -> int:
             st0[name] = round(kernel_time(c0, stage, passes=2)[0] * 1e3, 2)
         configs["c0_decode_t1"] = dict(us_per_layer=round(ms0 * 1e3, 2), gbs=round(b0 / (ms0 * 1e-3) / 1e9, 1),
                                        frac_hbm=round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), stage_us=st0)
+        if not args.skip_cpu:
+            configs["c0_decode_t1"]["cpu_reference_workers"] = cpu_workers_t1(model, c0)
         log(f"[bench] C0 T=1: {ms0 * 1e3:.1f} us/layer, {configs['c0_decode_t1']['gbs']} GB/s, stages {st0}")
 
     # ---- C1: raw expert gather ----

@@ -23,6 +23,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "_build" / "liblro.so"
 REF = HERE / "_ref" / "libcpu_experts.so"
+REF_WORKERS = HERE / "_ref" / "libpacked_workers.so"
 HIDDEN, INNER, EXPERTS, TOPK = 2048, 512, 256, 8
 EXPERT_ELEMENTS = 3 * INNER * HIDDEN
 
@@ -90,6 +91,29 @@ def reference() -> C.CDLL | None:
     so.expert_rows.restype = None
     so.expert_block_rows.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int]
     so.expert_block_rows.restype = None
+    return so
+
+
+@lru_cache(maxsize=1)
+def reference_workers() -> C.CDLL | None:
+    """The reference's packed_workers.cpp (persistent CPU expert workers,
+    packed_workers.cpp:14-122) as compiled by oracle/Makefile, or None."""
+    if not REF_WORKERS.exists():
+        if Path("/root/reference/edge35b/packed_workers.cpp").exists():
+            build(ref=True)
+        else:
+            return None
+    so = C.CDLL(str(REF_WORKERS))
+    so.packed_workers_create.argtypes = [C.c_int]
+    so.packed_workers_create.restype = _P
+    so.packed_workers_destroy.argtypes = [_P]
+    so.packed_workers_destroy.restype = None
+    so.packed_workers_submit.argtypes = [_P, _P, _P, _P, _P, C.c_int]
+    so.packed_workers_submit.restype = None
+    so.packed_workers_wait.argtypes = [_P]
+    so.packed_workers_wait.restype = None
+    so.packed_plan.argtypes = [_P, _P, _P, C.c_int, _P, _P]
+    so.packed_plan.restype = None
     return so
 
 

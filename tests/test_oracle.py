@@ -103,6 +103,41 @@ def test_expert_rows_match_reference_live(oracle):
         np.testing.assert_array_equal(oracle.expert_block_rows(gu, dn, tokens, ids), ref)
 
 
+def test_reference_workers_match_oracle_live(oracle):
+    """The reference's persistent CPU workers (packed_workers.cpp) produce the
+    oracle's expert rows bit for bit, and its packed_plan orders routes like
+    the oracle's bucketing (ascending expert id, slot kept)."""
+    import ctypes as C
+
+    ref = oracle.reference_workers()
+    if ref is None:
+        pytest.skip("reference workers not built (needs /root/reference)")
+    gu = [oracle.normal_bf16((1024, 2048), 5, 50 + e, 0.02) for e in range(8)]
+    dn = [oracle.normal_bf16((2048, 512), 5, 70 + e, 0.02) for e in range(8)]
+    hidden = oracle.normal_bf16((2048,), 5, 9, 1.0)
+    workers = ref.packed_workers_create(3)
+    try:
+        for count in (8, 5):
+            out = np.zeros((8, 2048), dtype=np.uint16)
+            gates = (C.c_void_p * 8)(*[g.ctypes.data for g in gu])
+            downs = (C.c_void_p * 8)(*[d.ctypes.data for d in dn])
+            ref.packed_workers_submit(workers, gates, downs, hidden.ctypes.data, out.ctypes.data, count)
+            ref.packed_workers_wait(workers)
+            np.testing.assert_array_equal(out[:count], oracle.expert_rows(gu[:count], dn[:count], hidden))
+    finally:
+        ref.packed_workers_destroy(workers)
+    ids = np.array([200, 3, 77, 150, 9, 31, 255, 0], dtype=np.int64)
+    table = np.zeros(32, dtype=np.int64)
+    last_seen = np.full(256, -4, dtype=np.int32)
+    experts = np.zeros(8, dtype=np.int32)
+    recent = np.zeros(8, dtype=np.uint8)
+    ref.packed_plan(ids.ctypes.data, table.ctypes.data, last_seen.ctypes.data, 1, experts.ctypes.data,
+                    recent.ctypes.data)
+    plan = oracle.bucket(ids[None])
+    np.testing.assert_array_equal(experts, plan["expert"][:8])
+    np.testing.assert_array_equal(table.reshape(8, 4)[:, 2], plan["pair_slot"])
+
+
 def test_expert_pair_against_float64_math(oracle):
     """The bf16-rounded SwiGLU stays within bf16 rounding of the exact math."""
     gu, dn = _experts(oracle, 1, 700)
