@@ -11,8 +11,8 @@ Also reported under "configs": T=1 decode layer with the router (latency and
 GB/s), the raw expert gather at T in {1,4,8,16}, the 40-layer decode chain
 with RMSNorm + residual at T=1 and T=16, and the T=2048 prefill (TFLOPS).
 
-`roofline` is for the gate/up kernel of the headline step, timed with HIP
-events around its launches; `cpu_baseline` is the reference CPU expert
+`roofline` is for moe_decode, the one kernel of the headline step, timed
+with HIP events stamped by its own dispatches; `cpu_baseline` is the reference CPU expert
 kernel (edge35b/cpu_experts.c built from source into oracle/_ref) on the
 host's cores over a bounded sample of the same routes.
 
@@ -324,18 +324,16 @@ def main() -> int:
     bytes_step = (np.mean(uniques) * EXPERT_BYTES + SHARED_BYTES)
     gbs = bytes_step / (ms_step * 1e-3) / 1e9
     log(f"[bench] C2 T=8 zipf: {ms_step * 1e3:.1f} us/layer, U={np.mean(uniques):.1f}, {gbs:.0f} GB/s")
-    stage_us = {}
-    for name, stage in (("route", _native.STAGE_ROUTE), ("gateup", _native.STAGE_GATE_UP),
-                        ("down", _native.STAGE_DOWN), ("combine", _native.STAGE_COMBINE)):
-        ms_k, launches = kernel_time(c2, stage, passes=max(2, replays))
-        stage_us[name] = round(ms_k * 1e3, 2)
-        if name == "gateup":
-            gate_ms, gate_launches = ms_k, launches
-    # gate/up kernel: unique gate+up weights (routed + shared) once, the 8
-    # hidden rows once, the activation rows of 64 routes + 8 shared written.
-    gate_bytes = (np.mean(uniques) + 1) * (2 * INNER * HIDDEN * 2) + 8 * HIDDEN * 2 + (8 * 8 + 8) * INNER * 2
-    gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
-    log(f"[bench] C2 stages (us, event-bracketed): {stage_us}; gate/up {gate_gbs:.0f} GB/s")
+    # The T <= 16 layer is one kernel (moe_decode): its launches are timed
+    # with start/stop events stamped by the dispatch itself.
+    layer_ms, layer_launches = kernel_time(c2, _native.STAGE_LAYER, passes=max(2, replays))
+    stage_us = {"moe_decode": round(layer_ms * 1e3, 2)}
+    # Algorithmic bytes of one launch: the unique routed experts and the
+    # shared expert (6 MiB each), the shared-expert gate row, and per token
+    # the hidden row in, the logits row in and the output row out.
+    layer_bytes = (np.mean(uniques) + 1) * EXPERT_BYTES + 2 * HIDDEN + 8 * (2 * HIDDEN + 2 * 256 + 2 * HIDDEN)
+    layer_gbs = layer_bytes / (layer_ms * 1e-3) / 1e9
+    log(f"[bench] C2 moe_decode kernel (event-bracketed): {stage_us['moe_decode']} us, {layer_gbs:.0f} GB/s")
     configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2),
                                         unique_experts=round(float(np.mean(uniques)), 2), gbs=round(gbs, 1),
                                         frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stage_us)
@@ -345,10 +343,7 @@ def main() -> int:
         c0 = Case(model, 1)
         ms0 = bench_case(c0, replays, warm) / L
         b0 = 8 * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES
-        st0 = {}
-        for name, stage in (("route", _native.STAGE_ROUTE), ("gateup", _native.STAGE_GATE_UP),
-                            ("down", _native.STAGE_DOWN), ("combine", _native.STAGE_COMBINE)):
-            st0[name] = round(kernel_time(c0, stage, passes=2)[0] * 1e3, 2)
+        st0 = {"moe_decode": round(kernel_time(c0, _native.STAGE_LAYER, passes=2)[0] * 1e3, 2)}
         configs["c0_decode_t1"] = dict(us_per_layer=round(ms0 * 1e3, 2), gbs=round(b0 / (ms0 * 1e-3) / 1e9, 1),
                                        frac_hbm=round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), stage_us=st0)
         if not args.skip_cpu:
@@ -417,7 +412,7 @@ def main() -> int:
         cpu = cpu_baseline(model, c2, uniques)
         log(f"[bench] CPU baseline: {cpu}")
 
-    traffic = measured_traffic("gateup_decode")
+    traffic = measured_traffic("moe_decode")
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -435,12 +430,12 @@ def main() -> int:
                                "shared expert, HBM GB/s on unique expert bytes; steps rotate over resident layers",
                    "tokens": 8, "hidden": HIDDEN, "experts": 256, "topk": 8, "inner": INNER,
                    "layers_rotated": L, "mean_unique_experts": round(float(np.mean(uniques)), 2)},
-        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                      "traffic": None if traffic is None else traffic["bytes"],
                      "traffic_source": None if traffic is None else traffic["source"],
-                     "kernel": "gateup_decode", "avg_us": round(gate_ms * 1e3, 3), "launches": gate_launches,
-                     "algorithmic_bytes": int(gate_bytes)},
+                     "kernel": "moe_decode", "avg_us": round(layer_ms * 1e3, 3), "launches": layer_launches,
+                     "algorithmic_bytes": int(layer_bytes)},
         "cpu_baseline": cpu,
         "configs": configs,
     }

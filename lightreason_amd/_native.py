@@ -49,6 +49,7 @@ STAGE_GATE_UP = 2
 STAGE_DOWN = 4
 STAGE_COMBINE = 8
 STAGE_GATHER = 16
+STAGE_LAYER = 32
 
 
 class NativeError(RuntimeError):

@@ -105,7 +105,22 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
     if (int d = check_device()) return d;
     const Workspace ws = lrmoe::carve(workspace, tokens);
     hipStream_t s = as_stream(stream);
-    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s, expert_ptrs);
+    if (tokens <= lrmoe::kDecodeMaxTokens) {
+        lrmoe::DecodeArgs d{};
+        d.x = hidden;
+        d.indices_in = indices;
+        d.weights_in = weights;
+        d.expert_ptrs = expert_ptrs;
+        d.out = out;
+        d.logits = ws.logits;
+        d.act = ws.act;
+        d.y = ws.y;
+        d.sync = ws.sync;
+        d.status = ws.plan.status;
+        d.tokens = tokens;
+        return status_of(lrmoe::launch_moe_decode(d, s));
+    }
+    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s);
     if (err != hipSuccess) return status_of(err);
     lrmoe::ExpertArgs a{};
     a.x = hidden;
@@ -134,6 +149,30 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
     if (int d = check_device()) return d;
     const Workspace ws = lrmoe::carve(workspace, tokens);
     hipStream_t s = as_stream(stream);
+    if (tokens <= lrmoe::kDecodeMaxTokens) {
+        lrmoe::DecodeArgs d{};
+        d.x = hidden;
+        d.norm = norm_weight;
+        d.eps = eps;
+        d.router = logits_in ? nullptr : router_weight;
+        d.logits_in = logits_in;
+        d.shared_expert_gate = shared_expert_gate;
+        d.sh_gate = shared_gate_proj;
+        d.sh_up = shared_up_proj;
+        d.sh_down = shared_down_proj;
+        d.expert_ptrs = expert_ptrs;
+        d.out = out;
+        d.indices_out = indices_out;
+        d.weights_out = weights_out;
+        d.logits = ws.logits;
+        d.act = ws.act;
+        d.y = ws.y;
+        d.sync = ws.sync;
+        d.status = ws.plan.status;
+        d.tokens = tokens;
+        d.residual = norm_weight != nullptr;
+        return status_of(lrmoe::launch_moe_decode(d, s));
+    }
     lrmoe::RouteArgs r{};
     r.x = hidden;
     r.norm = norm_weight;

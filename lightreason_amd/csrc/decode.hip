@@ -1,232 +1,732 @@
-// Decode / verify expert kernels (T <= 16 tokens, so at most 16 tokens per
-// expert: one MFMA column block).
+// Decode / verify MoE layer (T <= 16 tokens) as one persistent kernel.
 //
-// gateup_decode: one wavefront per (expert, 16-row tile) streams the tile's
-// 16 gate rows and 16 up rows over the full k = 2048 straight into MFMA A
-// operands, eight k-steps of loads in flight ahead of the MFMAs; every token
-// routed to the expert is a B column, so each weight byte is read once per
-// call however many tokens share the expert.  The epilogue applies the
-// cpu_experts.c:59-62 rounding points (bf16 gate/up, bf16 SiLU, bf16 product).
+// One 512-thread workgroup per CU.  Every workgroup
+//   1. stages the layer input rows in LDS (RMSNorm (x*r)*(1+w) applied when
+//      the layer norms, Qwen3_5MoeRMSNorm.forward) and computes the
+//      shared-expert gate bf16(sigmoid(bf16(x.w))) of every token;
+//   2. workgroups 0..31 compute 8 router rows each (fixed fp32 order, see
+//      route.hip) and publish them;
+//   3. builds the route plan itself from the logits (top-8 by ballot radix
+//      select, renormalised weights, experts ascending with their token lists,
+//      per token its routes in ascending expert order: fused_experts.py:47-54,
+//      block_experts.py:102-121), so no other kernel or host step is needed;
+//   4. walks its share of one static list of 128 KiB work items, each item's
+//      weights prefetched one item ahead:
+//        A (slot, 16-row tile): gate and up rows 16i..16i+15 of an expert over
+//          k = 2048 -> SwiGLU with the cpu_experts.c:59-62 rounding points ->
+//          act rows;
+//        B (slot, 128-row tile): down rows over k = 512 for the slot's tokens
+//          -> y rows (bf16, cpu_experts.c:64-69);
+//      slot 0 is the shared expert, slot s >= 1 the (s-1)-th unique routed
+//      expert; every token routed to an expert is an MFMA column, so each
+//      weight byte is read from HBM once per call;
+//   5. the workgroup that completes the last B item of a 128-row output tile
+//      does the ordered combine of that tile (fused_experts.py:27-37:
+//      ascending expert, acc = bf16(acc + bf16(y * w)) from 0), the
+//      shared-expert add bf16(sg * y_shared) and the residual add.
 //
-// down_combine_decode: one workgroup per 16 output rows owns those rows for
-// every routed expert and the shared expert, so the ordered combine
-// (fused_experts.py:27-37, block_experts.py:31-49: per token, ascending expert
-// order, acc = bf16(acc + bf16(y * w)) from 0), the shared-expert add
-// (bf16(sg * y_shared)) and the residual add finish inside the workgroup with
-// no cross-workgroup synchronisation.
+// Cross-workgroup data (logits, act, y) is written with agent-scope stores
+// and read with agent-scope loads (coherent across the XCDs' L2s), and
+// published by agent-scope counters: per slot the completed A items, per
+// output tile the completed B items.  A B item waits for its slot's 32 A
+// items; items are taken in list order (A before B) by co-resident
+// workgroups, so the earliest unfinished item never waits and the waits end.
+// Every wait is bounded: on timeout the status word gets kStatusTimeout and
+// the kernel still exits.  The last workgroup to finish returns every
+// counter to zero for the next call.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
 namespace lrmoe {
 namespace {
 
-constexpr int kRowTiles = kInner / 16;   // 32 gate/up row tiles per expert
-constexpr int kDepth = 8;                // k-steps of loads in flight per wave (of 16)
-constexpr int kDownRows = 16;            // output rows per down workgroup
-constexpr int kDownWaves = 8;            // 512 threads
-constexpr int kActStride = kInner + 8;   // LDS act row stride (bf16), 16-byte pad
-constexpr int kDecodeTokens = 16;
-constexpr int kDecodeSlots = kTopK * kDecodeTokens + 1;  // unique routed experts + the shared expert
-// Dynamic LDS of down_combine_decode at its largest (T = 16): 144 act rows.
-constexpr int kMaxActLds = (kTopK + 1) * kDecodeTokens * kActStride * 2;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kMaxT = kDecodeMaxTokens;
+constexpr int kATiles = kInner / 16;          // 32 A items per slot
+constexpr int kBRows = 128;                   // output rows per B item
+constexpr int kBTiles = kHidden / kBRows;     // 16 B items per slot
+constexpr int kRouterWgs = kExperts / kWaves; // 32 workgroups x 8 router rows
+constexpr int kXStride = kHidden + 8;         // LDS token row stride (bf16)
+constexpr int kActStride = kInner + 8;        // LDS act row stride (bf16)
+constexpr int kLoads = 16;                    // 16-byte weight loads per lane per item
+constexpr int kReadyTarget = kATiles;         // A items per slot
+constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
 
-__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
+// ---- agent-scope memory operations (coherent across XCDs) -------------------
 
-// Token of MFMA column n from a slot record's 16 packed token bytes.
-__device__ __forceinline__ int column_token(const uint4 packed, int n) {
-    const uint32_t word = n < 4 ? packed.x : n < 8 ? packed.y : n < 12 ? packed.z : packed.w;
-    return static_cast<int>((word >> (8 * (n & 3))) & 0xffu);
+typedef __attribute__((address_space(1))) uint64_t g_u64;
+typedef __attribute__((address_space(1))) uint32_t g_u32;
+
+__device__ __forceinline__ g_u64* as_g64(const void* p) {
+    return reinterpret_cast<g_u64*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ g_u32* as_g32(const void* p) {
+    return reinterpret_cast<g_u32*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
+    __hip_atomic_store(as_g64(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
+    return __hip_atomic_load(as_g64(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Four agent-scope (sc1) 8-byte loads at a uniform base plus a per-lane byte
+// offset.  Written as assembly so that the compiler's wait insertion does not
+// tie the next prefetch to them; the caller's "s_waitcnt vmcnt(16)" after
+// that prefetch is what makes the results valid.
+__device__ __forceinline__ void ld_agent64x4_async(uint64_t* out, const void* base, uint32_t byte_offset) {
+    asm volatile(
+        "global_load_dwordx2 %0, %4, %5 sc1\n\t"
+        "global_load_dwordx2 %1, %4, %5 offset:8 sc1\n\t"
+        "global_load_dwordx2 %2, %4, %5 offset:16 sc1\n\t"
+        "global_load_dwordx2 %3, %4, %5 offset:24 sc1"
+        : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
+        : "v"(byte_offset), "s"(base)
+        : "memory");
+}
+__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
+    return __hip_atomic_load(as_g32(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
+    __hip_atomic_store(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_agent32(void* p, uint32_t v) {
+    return __hip_atomic_fetch_add(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One workgroup per (slot, 16-row tile): wave w covers k in [512w, 512w+512)
-// with kDepth k-steps of gate, up and x loads in flight; the four partial
-// tiles meet in LDS in wave order.
-__global__ __launch_bounds__(256) void gateup_decode(ExpertArgs a) {
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int slot = blockIdx.x / kRowTiles;
-    const int row0 = (blockIdx.x % kRowTiles) * 16;
-    // The record and the unique count are independent loads, issued together.
-    const SlotDesc d = a.ws.slots[slot];
-    const int unique = *a.plan.unique;
-    if (slot > unique || !d.valid) return;
-    __shared__ f32x4 red[4][2][kWave];
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const bool live = n < d.count;
-    // Columns past the slot's token count read token 0's row: an MFMA output
-    // column depends only on its own B column, and those columns are dropped.
-    const int token = column_token(*reinterpret_cast<const uint4*>(d.tokens), n);
-    const int kb = wave * (kHidden / 4) + 8 * g;
-    const uint16_t* gp = d.gate_up + static_cast<size_t>(row0 + n) * kHidden + kb;
-    const uint16_t* up = d.up + static_cast<size_t>(row0 + n) * kHidden + kb;
-    const uint16_t* xp = a.x + static_cast<size_t>(token) * kHidden + kb;
+__device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
 
-    constexpr int kSteps = kHidden / 32 / 4;
-    uint4 ga[kDepth], ua[kDepth], xb[kDepth];
-#pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
-        ga[s] = ldg16(gp + 32 * s);
-        ua[s] = ldg16(up + 32 * s);
-        xb[s] = ldg16(xp + 32 * s);
+// Waits (bounded) until *counter >= target; returns false on timeout.
+__device__ bool wait_counter(const uint32_t* counter, uint32_t target) {
+    const uint64_t start = now_ticks();
+    while (ld_agent32(counter) < target) {
+        if (now_ticks() - start > kSpinTicks) return false;
+        __builtin_amdgcn_s_sleep(2);
     }
-    // Keep the scheduler from sinking the prefetch next to its MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 acc_g = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 acc_u = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s0 = 0; s0 < kSteps; s0 += kDepth) {
-#pragma unroll
-        for (int j = 0; j < kDepth; ++j) {
-            acc_g = mfma16x16x32(ga[j], xb[j], acc_g);
-            acc_u = mfma16x16x32(ua[j], xb[j], acc_u);
-            const int next = s0 + kDepth + j;
-            if (next < kSteps) {
-                ga[j] = ldg16(gp + 32 * next);
-                ua[j] = ldg16(up + 32 * next);
-                xb[j] = ldg16(xp + 32 * next);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    red[wave][0][lane] = acc_g;
-    red[wave][1][lane] = acc_u;
-    __syncthreads();
-    if (wave != 0 || !live) return;
-    const f32x4 sg = ((red[0][0][lane] + red[1][0][lane]) + red[2][0][lane]) + red[3][0][lane];
-    const f32x4 su = ((red[0][1][lane] + red[1][1][lane]) + red[2][1][lane]) + red[3][1][lane];
-    uint32_t act[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(sg[i]), rbf(su[i]));
-    uint16_t* dst = a.ws.act + static_cast<size_t>(d.pair0 + n) * kInner + row0 + 4 * g;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(act[0] | (act[1] << 16), act[2] | (act[3] << 16));
+    return true;
 }
 
-// One workgroup per 16 output rows; wave w takes slots w, w+8, ...  The slot
-// records and the act rows of every pair (the B operand) are staged into LDS
-// once; each wave keeps the next slot's 16 down-weight loads in flight while
-// the current slot's MFMAs run.
-__global__ __launch_bounds__(kDownWaves * kWave) void down_combine_decode(ExpertArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t act_lds[];  // [9T][kActStride]
-    __shared__ uint16_t ys[(kTopK + 1) * 16 * kDownRows];              // y bits of this tile
-    __shared__ SlotDesc descs[kDecodeSlots];
+__device__ __forceinline__ uint64_t pack4(const uint32_t* v) {
+    return static_cast<uint64_t>(v[0] | (v[1] << 16)) | (static_cast<uint64_t>(v[2] | (v[3] << 16)) << 32);
+}
+
+// ---- per-workgroup plan (LDS) -------------------------------------------------
+
+struct SlotInfo {
+    const uint16_t* gate;  // gate rows [512][2048]
+    const uint16_t* up;    // up rows [512][2048]
+    const uint16_t* down;  // [2048][512]
+    uint32_t tok[4];       // token of column n in byte n
+    int32_t count;         // tokens (columns), <= 16
+    int32_t pair0;         // first act/y row
+    int32_t pad[2];
+};
+
+struct Plan {
+    SlotInfo slot[kDecodeSlots];
+    int16_t comb_pair[kMaxT][kTopK];  // per token: pair of the k-th smallest expert
+    float comb_w[kMaxT][kTopK];       // its routing weight
+    float sg[kMaxT];                  // shared-expert gate per token
+    int32_t ids[kMaxT][kTopK];        // routed experts, rank order
+    uint16_t wts[kMaxT][kTopK];       // routing weights (bf16), rank order
+    uint32_t keys8[kMaxT][kTopK];     // top-k scratch
+    float vals8[kMaxT][kTopK];
+    uint32_t tokmask[kExperts];
+    uint32_t poff[kExperts];
+    uint32_t scan[4];
+    uint16_t lg[kMaxT][kWaves];       // router prologue: this workgroup's 8 logits per token
+    int32_t n_slots;                  // active slots (shared + unique routed)
+    int32_t first_slot;               // 0 with a shared expert, else 1
+    int32_t status;
+    int32_t last;
+};
+
+// Exclusive scan over threads 0..255 (all threads call; others contribute 0).
+__device__ uint32_t block_scan256(uint32_t value, uint32_t* scratch, uint32_t* total) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const int h0 = blockIdx.x * kDownRows;
-    const int T = a.tokens;
-    const int32_t status = *a.plan.status;
-    const int unique = status ? 0 : *a.plan.unique;
-    const int slots = unique + 1;
-
-    for (int i = threadIdx.x; i < slots * 4; i += blockDim.x) {
-        reinterpret_cast<uint4*>(descs)[i] = reinterpret_cast<const uint4*>(a.ws.slots)[i];
-    }
-    // All staging loads are issued before any LDS write, so their latencies
-    // overlap (at T = 16: 18 loads per thread).
-    const int chunks = (kTopK + 1) * T * (kInner / 8);
-    constexpr int kStageIters = (kTopK + 1) * kDecodeTokens * (kInner / 8) / (kDownWaves * kWave);
-    uint4 staged[kStageIters];
+    if (threadIdx.x >= kExperts) value = 0;
+    uint32_t inclusive = value;
 #pragma unroll
-    for (int k = 0; k < kStageIters; ++k) {
-        const int i = threadIdx.x + k * kDownWaves * kWave;
-        if (i < chunks) staged[k] = ldg16(a.ws.act + static_cast<size_t>(i) * 8);
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const uint32_t up = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset, kWave));
+        if (lane >= offset) inclusive += up;
     }
-#pragma unroll
-    for (int k = 0; k < kStageIters; ++k) {
-        const int i = threadIdx.x + k * kDownWaves * kWave;
-        if (i < chunks) {
-            const int r = i / (kInner / 8);
-            const int c = (i % (kInner / 8)) * 8;
-            *reinterpret_cast<uint4*>(act_lds + r * kActStride + c) = staged[k];
-        }
-    }
+    if (lane == kWave - 1 && wave < 4) scratch[wave] = inclusive;
     __syncthreads();
-
-    // Two register buffers alternate roles (no copies, so a prefetch is only
-    // waited for when its expert is computed).
-    auto next_valid = [&](int from) {
-        while (from < slots && !descs[from].valid) from += kDownWaves;
-        return from;
-    };
-    auto load = [&](int slot, uint4* buf) {
-        const uint16_t* wp = descs[slot].down + static_cast<size_t>(h0 + n) * kInner + 8 * g;
-#pragma unroll
-        for (int s = 0; s < 16; ++s) buf[s] = ldg16(wp + 32 * s);
-    };
-    auto compute = [&](int slot, const uint4* buf) {
-        const int pair0 = descs[slot].pair0;
-        const bool live = n < descs[slot].count;
-        // Dropped columns (n >= count) read the slot's first row instead.
-        const uint16_t* bp = act_lds + (pair0 + (live ? n : 0)) * kActStride + 8 * g;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 16; ++s) acc = mfma16x16x32(buf[s], *reinterpret_cast<const uint4*>(bp + 32 * s), acc);
-        if (live) {
-            uint16_t* dst = ys + (pair0 + n) * kDownRows + 4 * g;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[i] = static_cast<uint16_t>(f2bf(acc[i]));
-        }
-    };
-    // Prefetches are unconditional so the compiler can count outstanding
-    // loads; past the wave's last slot they re-read the slot just computed,
-    // which is still in L2.
-    uint4 buf0[16], buf1[16];
-    int s0 = next_valid(wave);
-    if (s0 < slots) {
-        load(s0, buf0);
-        int s1 = next_valid(s0 + kDownWaves);
-        while (true) {
-            load(s1 < slots ? s1 : s0, buf1);
-            compute(s0, buf0);
-            if (s1 >= slots) break;
-            s0 = next_valid(s1 + kDownWaves);
-            load(s0 < slots ? s0 : s1, buf0);
-            compute(s1, buf1);
-            if (s0 >= slots) break;
-            s1 = next_valid(s0 + kDownWaves);
-        }
-    }
+    uint32_t before = 0;
+    for (int w = 0; w < wave && w < 4; ++w) before += scratch[w];
+    *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
     __syncthreads();
+    return threadIdx.x < kExperts ? before + inclusive - value : 0u;
+}
 
-    if (static_cast<int>(threadIdx.x) >= T * kDownRows) return;
-    const int t = threadIdx.x / kDownRows;
-    const int r = threadIdx.x % kDownRows;
+// Top-8 of one token by one wave (ballot radix select over unique 24-bit
+// keys, lane l holding experts 4l..4l+3), softmax over all 256 in fp32,
+// renormalised weights.  Writes ids/wts in rank order.  Same arithmetic and
+// order as route.hip's topk_token_select and the oracle.
+__device__ void topk_wave(uint64_t packed, int32_t* ids_row, uint16_t* wts_row, uint32_t* keys8, float* vals8) {
+    const int lane = threadIdx.x & 63;
+    uint32_t bits[4], keys[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
+        keys[j] = route_key(bits[j], 4 * lane + j);
+    }
+    uint32_t best = keys[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) best = keys[j] > best ? keys[j] : best;
+    best = wave_max_u32(best);
+    uint32_t threshold = 0;
+#pragma unroll 1
+    for (int bit = 23; bit >= 0; --bit) {
+        const uint32_t candidate = threshold | (1u << bit);
+        int above = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) above += __popcll(__ballot(keys[j] >= candidate));
+        if (above >= kTopK) threshold = candidate;
+    }
+    const float top = bf2f(key_bits(best));
+    float ex[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ex[j] = lr_exp(bf2f(bits[j]) - top);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part = part + ex[j];
+    const float total = wave_butterfly_sum(part);
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool chosen = keys[j] >= threshold;
+        const uint64_t mask = __ballot(chosen);
+        if (chosen) {
+            const int at = base + __popcll(mask & ((1ull << lane) - 1ull));
+            keys8[at] = keys[j];
+            vals8[at] = ex[j];
+        }
+        base += __popcll(mask);
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int k = lane & 7;
+    const uint32_t my_key = keys8[k];
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) rank += keys8[i] > my_key ? 1 : 0;
+    const float prob = vals8[k] / total;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < kTopK) vals8[rank] = prob;
+    __builtin_amdgcn_wave_barrier();
+    float sum = vals8[0];
+#pragma unroll
+    for (int i = 1; i < kTopK; ++i) sum = sum + vals8[i];
+    if (lane < kTopK) {
+        ids_row[rank] = 255 - static_cast<int>(my_key & 255u);
+        wts_row[rank] = static_cast<uint16_t>(f2bf(prob / sum));
+    }
+}
+
+// Dot of a lane's 32 contiguous elements (4 x 16 bytes) with the same
+// elements of an LDS row, as an in-order fmaf chain from +0.
+__device__ __forceinline__ float lane_dot32(const uint4* w, const uint16_t* row, int lane) {
+    const uint4* x = reinterpret_cast<const uint4*>(row + 32 * lane);
     float acc = 0.0f;
-    if (status == 0) {
-        for (int k = 0; k < kTopK; ++k) {
-            const int p = a.plan.route_pair[t * kTopK + k];
-            const float scale = bf2f(a.weights[t * kTopK + a.plan.pair_slot[p]]);
-            acc = rbf(acc + rbf(bf2f(ys[p * kDownRows + r]) * scale));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float wf[8], xf[8];
+        unpack8(w[i], wf);
+        unpack8(x[i], xf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wf[j], xf[j], acc);
+    }
+    return acc;
+}
+
+// ---- item geometry ------------------------------------------------------------
+
+struct Item {
+    int kind;   // 0 = A (gate/up), 1 = B (down), -1 = none
+    int slot;
+    int tile;
+};
+
+__device__ __forceinline__ Item item_at(int k, int total, int n_slots, int first_slot) {
+    Item it;
+    const int n_a = kATiles * n_slots;
+    if (k >= total) {
+        it.kind = -1;
+        it.slot = first_slot;
+        it.tile = 0;
+    } else if (k < n_a) {
+        it.kind = 0;
+        it.slot = first_slot + k / kATiles;
+        it.tile = k % kATiles;
+    } else {
+        const int b = k - n_a;
+        it.kind = 1;
+        it.slot = first_slot + b / kBTiles;
+        it.tile = b % kBTiles;
+    }
+    return it;
+}
+
+// Address of this lane's first 16-byte weight load of an item; the item's 16
+// loads are at +32 elements each.  A: MFMA row m < 8 is gate row
+// 16*tile + 8*(wave/4) + m, m >= 8 the up row with the same index; k starts at
+// 512*(wave%4).  B: output row 128*tile + 16*wave + m over k = 512.  A
+// "none" item re-reads the slot's first A tile (in cache; results unused).
+__device__ __forceinline__ const uint16_t* item_base(const SlotInfo& s, const Item& it, int wave, int lane) {
+    const int m = lane & 15;
+    const int g = lane >> 4;
+    if (it.kind == 1) {
+        return s.down + static_cast<size_t>(kBRows * it.tile + 16 * wave + m) * kInner + 8 * g;
+    }
+    const uint16_t* rows = m < 8 ? s.gate : s.up;
+    const int row = 16 * it.tile + 8 * (wave >> 2) + (m & 7);
+    return rows + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * g;
+}
+
+__device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
+    return static_cast<int>((s.tok[n >> 2] >> (8 * (n & 3))) & 0xffu);
+}
+
+// Ordered combine of output rows [128*tile, +128) of every token (512
+// threads: token tid/32, rows 4*(tid%32)..+3), then the shared-expert and
+// residual adds; resets the tile's counter for the next call.
+__device__ __forceinline__ void combine_tile(const DecodeArgs& a, const Plan& P, DecodeSync* sync, int tile, int T, bool shared) {
+    const int tid = threadIdx.x;
+    const int t = tid >> 5;
+    const int h = kBRows * tile + (tid & 31) * 4;
+    if (t < T) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < kTopK; ++q) {
+            const uint64_t v = ld_agent64(a.y + static_cast<size_t>(P.comb_pair[t][q]) * kHidden + h);
+            const float w = P.comb_w[t][q];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = rbf(acc[i] + rbf(bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu) * w));
         }
-        if (a.shared_down != nullptr) {
-            const float shared = bf2f(ys[(kTopK * T + t) * kDownRows + r]);
-            acc = rbf(acc + rbf(bf2f(a.sg[t]) * shared));
+        if (shared) {
+            const uint64_t v = ld_agent64(a.y + static_cast<size_t>(kTopK * T + t) * kHidden + h);
+            const float gate = P.sg[t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = rbf(acc[i] + rbf(gate * bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu)));
+        }
+        if (a.residual) {
+            const uint64_t v = *reinterpret_cast<const uint64_t*>(a.x + static_cast<size_t>(t) * kHidden + h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = rbf(bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu) + acc[i]);
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = f2bf(acc[i]);
+        *reinterpret_cast<uint64_t*>(a.out + static_cast<size_t>(t) * kHidden + h) = pack4(o);
+    }
+    if (tid == 0) st_agent32(&sync->tile_done[tile * kSyncStride], 0u);
+}
+
+__global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
+    // A local copy: the helpers below take it by reference, which must not
+    // force the kernel-argument block into private memory.
+    const DecodeArgs a = args;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+    __shared__ Plan P;
+    const int T = a.tokens;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int tid = threadIdx.x;
+    const int G = gridDim.x;
+    uint16_t* x_lds = reinterpret_cast<uint16_t*>(dyn);                       // [T][kXStride]
+    uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
+    f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
+    DecodeSync* sync = a.sync;
+
+    // ---- 1. token rows (normalised) and shared-expert gates ----
+    for (int t = wave; t < T; t += kWaves) {
+        const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(t) * kHidden + 32 * lane);
+        uint4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = src[i];
+        if (a.norm != nullptr) {
+            float f[32];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) unpack8(v[i], f + 8 * i);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(f[j], f[j], acc);
+            const float mean = wave_butterfly_sum(acc) / static_cast<float>(kHidden);
+            const float r = 1.0f / __builtin_sqrtf(mean + a.eps);
+            const uint4* wsrc = reinterpret_cast<const uint4*>(a.norm + 32 * lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float wf[8];
+                unpack8(wsrc[i], wf);
+                uint32_t o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = f2bf((f[8 * i + j] * r) * (1.0f + wf[j]));
+                v[i] = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+            }
+        }
+        uint4* dst = reinterpret_cast<uint4*>(x_lds + t * kXStride + 32 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = v[i];
+        if (a.shared_expert_gate != nullptr) {
+            uint4 w[4];
+            const uint4* gsrc = reinterpret_cast<const uint4*>(a.shared_expert_gate + 32 * lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = gsrc[i];
+            const float z = rbf(wave_butterfly_sum(lane_dot32(w, x_lds + t * kXStride, lane)));
+            if (lane == 0) P.sg[t] = rbf(1.0f / (1.0f + lr_exp(-z)));
         }
     }
-    const size_t o = static_cast<size_t>(t) * kHidden + h0 + r;
-    if (a.residual != nullptr) acc = rbf(bf2f(a.residual[o]) + acc);
-    a.out[o] = static_cast<uint16_t>(f2bf(acc));
+    if (tid == 0) {
+        P.status = 0;
+    }
+    __syncthreads();
+
+    // ---- 2. router rows (workgroups 0..31, one row per wave) ----
+    if (a.router != nullptr && static_cast<int>(blockIdx.x) < kRouterWgs) {
+        const int row = kWaves * blockIdx.x + wave;
+        const uint4* src = reinterpret_cast<const uint4*>(a.router + static_cast<size_t>(row) * kHidden + 32 * lane);
+        uint4 w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = src[i];
+        for (int t = 0; t < T; ++t) {
+            const float s = wave_butterfly_sum(lane_dot32(w, x_lds + t * kXStride, lane));
+            if (lane == 0) P.lg[t][wave] = static_cast<uint16_t>(f2bf(s));
+        }
+        __syncthreads();
+        if (tid < 2 * T) {
+            const int t = tid >> 1;
+            const int h = tid & 1;
+            uint32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = P.lg[t][4 * h + i];
+            st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * blockIdx.x + 4 * h, pack4(v));
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) add_agent32(&sync->router_done, 1u);
+    }
+
+    // ---- 3. the route plan ----
+    if (a.router != nullptr) {
+        if (tid == 0 && !wait_counter(&sync->router_done, kRouterWgs)) P.status |= kStatusTimeout;
+        __syncthreads();
+    }
+    if (a.indices_in == nullptr) {
+        for (int t = wave; t < T; t += kWaves) {
+            const uint16_t* row = (a.router != nullptr ? a.logits : a.logits_in) + static_cast<size_t>(t) * kExperts;
+            const uint64_t packed = a.router != nullptr ? ld_agent64(row + 4 * lane)
+                                                        : *reinterpret_cast<const uint64_t*>(row + 4 * lane);
+            topk_wave(packed, P.ids[t], P.wts[t], P.keys8[t], P.vals8[t]);
+        }
+    } else if (tid < T * kTopK) {
+        const int t = tid / kTopK;
+        const int r = tid % kTopK;
+        const int64_t e = a.indices_in[tid];
+        int32_t bad = (e < 0 || e >= kExperts) ? kStatusBadExpert : 0;
+        for (int q = 0; q < r; ++q) bad |= (a.indices_in[t * kTopK + q] == e) ? kStatusRepeatedExpert : 0;
+        P.ids[t][r] = bad ? 0 : static_cast<int32_t>(e);
+        P.wts[t][r] = a.weights_in[tid];
+        if (bad) atomicOr(&P.status, bad);
+    }
+    if (tid < kExperts) P.tokmask[tid] = 0u;
+    __syncthreads();
+    if (blockIdx.x == 0 && tid < T * kTopK) {
+        if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
+        if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
+    }
+    const bool routes_ok = P.status == 0;
+    if (routes_ok && tid < T * kTopK) atomicOr(&P.tokmask[P.ids[tid / kTopK][tid % kTopK]], 1u << (tid / kTopK));
+    __syncthreads();
+    {
+        const uint32_t mask = tid < kExperts ? P.tokmask[tid] : 0u;
+        const uint32_t count = static_cast<uint32_t>(__popc(mask));
+        uint32_t packed_total = 0;
+        const uint32_t packed = block_scan256((count ? (1u << 16) : 0u) | count, P.scan, &packed_total);
+        const uint32_t pair0 = packed & 0xffffu;
+        const uint32_t rank = packed >> 16;
+        const uint32_t unique = packed_total >> 16;
+        if (tid < kExperts) P.poff[tid] = pair0;
+        if (count) {
+            SlotInfo& s = P.slot[1 + rank];
+            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * tid]);
+            s.gate = gate_up;
+            s.up = gate_up + static_cast<size_t>(kInner) * kHidden;
+            s.down = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * tid + 1]);
+            uint32_t tok[4] = {0u, 0u, 0u, 0u};
+            uint32_t m = mask;
+            for (int j = 0; m; ++j) {
+                const int t = __ffs(m) - 1;
+                m &= m - 1u;
+                tok[j >> 2] |= static_cast<uint32_t>(t) << (8 * (j & 3));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s.tok[i] = tok[i];
+            s.count = static_cast<int32_t>(count);
+            s.pair0 = static_cast<int32_t>(pair0);
+        }
+        if (tid == 0) {
+            const bool shared = a.sh_down != nullptr && routes_ok;
+            SlotInfo& s = P.slot[0];
+            s.gate = a.sh_gate;
+            s.up = a.sh_up;
+            s.down = a.sh_down;
+            uint32_t tok[4] = {0u, 0u, 0u, 0u};
+            for (int j = 0; j < T; ++j) tok[j >> 2] |= static_cast<uint32_t>(j) << (8 * (j & 3));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s.tok[i] = tok[i];
+            s.count = T;
+            s.pair0 = kTopK * T;
+            P.first_slot = shared ? 0 : 1;
+            P.n_slots = routes_ok ? static_cast<int32_t>(unique) + (shared ? 1 : 0) : 0;
+        }
+    }
+    __syncthreads();
+    if (routes_ok && tid < T * kTopK) {
+        const int t = tid / kTopK;
+        const int k = tid % kTopK;
+        const int e = P.ids[t][k];
+        const int p = static_cast<int>(P.poff[e]) + __popc(P.tokmask[e] & ((1u << t) - 1u));
+        int order = 0;
+#pragma unroll
+        for (int q = 0; q < kTopK; ++q) order += P.ids[t][q] < e ? 1 : 0;
+        P.comb_pair[t][order] = static_cast<int16_t>(p);
+        P.comb_w[t][order] = bf2f(P.wts[t][k]);
+    }
+    // This call's route status replaces the previous call's (timeouts are
+    // OR-ed in at the end).
+    if (blockIdx.x == 0 && tid == 0) st_agent32(a.status, static_cast<uint32_t>(P.status));
+    __syncthreads();
+
+    const int n_slots = P.n_slots;
+    const int first_slot = P.first_slot;
+    const int total = (kATiles + kBTiles) * n_slots;
+    const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
+
+    // Bad routes: the output is the residual (or zeros); no expert runs.
+    if (!routes_ok) {
+        if (blockIdx.x == 0) {
+            for (int i = tid; i < T * kHidden / 4; i += kThreads) {
+                uint64_t v = 0;
+                if (a.residual) v = reinterpret_cast<const uint64_t*>(a.x)[i];
+                reinterpret_cast<uint64_t*>(a.out)[i] = v;
+            }
+        }
+    }
+
+    // ---- 4. work items ----
+    int k = (static_cast<int>(blockIdx.x) - offset + G) % G;
+    uint4 b0[kLoads], b1[kLoads];
+    uint64_t stg[4];
+    const uint32_t stg_off = static_cast<uint32_t>((tid >> 5) * kInner * 2 + (tid & 31) * 32);
+    uint32_t poll = 0;        // ready count of the current item's slot (read one item ahead)
+    int sig_kind = -1;        // item whose completion is signalled next iteration
+    int sig_slot = 0, sig_tile = 0;
+    int par = 0;
+
+    auto issue = [&](const uint16_t* p, uint4* buf) {
+#pragma unroll
+        for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
+    };
+
+    // Runs one item whose weights are in buf; the next item's prefetch goes
+    // into nbuf.  Returns the next item index.
+    auto step = [&](int kk, uint4* buf, uint4* nbuf) {
+        const Item it = item_at(kk, total, n_slots, first_slot);
+        const Item nx = item_at(kk + G, total, n_slots, first_slot);
+        const SlotInfo& s = P.slot[it.slot];
+        // Next item's first weight address (a "none" item re-reads this one).
+        const uint16_t* np = nx.kind >= 0 ? item_base(P.slot[nx.slot], nx, wave, lane) : item_base(s, it, wave, lane);
+        auto signal_previous = [&]() {
+            if (tid == 0) {
+                if (sig_kind == 0) add_agent32(&sync->ready[sig_slot * kSyncStride], 1u);
+                if (sig_kind == 1) add_agent32(&sync->tile_done[sig_tile * kSyncStride], 1u);
+            }
+            sig_kind = -1;
+        };
+        // (a) The slot's act rows must be complete before a B item stages
+        //     them.  Before waiting, the workgroup publishes its own previous
+        //     item: a completed item is never held back by a wait, so two
+        //     workgroups cannot wait on each other.
+        if (it.kind == 1 && __syncthreads_or(poll < kReadyTarget)) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            signal_previous();
+            if (tid == 0 && !wait_counter(&sync->ready[it.slot * kSyncStride], kReadyTarget)) P.status |= kStatusTimeout;
+            __syncthreads();
+        }
+        // (b) staging loads (B), then the poll for the next item, then its
+        //     weights: a wait for everything but the newest 16 loads covers
+        //     this item's weights, staging and poll and the previous item's
+        //     stores and signal.
+        if (it.kind == 1) {
+            // Uniform base + loop-invariant lane offset: rows past the slot's
+            // count read the act buffer's padding (never used as columns).
+            const int pair0 = __builtin_amdgcn_readfirstlane(s.pair0);
+            const char* base = reinterpret_cast<const char*>(a.act) + static_cast<size_t>(pair0) * kInner * 2;
+            ld_agent64x4_async(stg, base, stg_off);
+        }
+        const uint32_t* poll_addr = nx.kind == 1 ? &sync->ready[nx.slot * kSyncStride] : &sync->router_done;
+        uint32_t next_poll = ld_agent32(poll_addr);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(np, nbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        // (c) Otherwise the previous item is signalled after this item's
+        //     first barrier: every wave has passed the wait above, so all of
+        //     that item's stores are complete.
+        if (it.kind == 1) {
+            // Every wave is past the previous item's reads of act_lds.
+            __syncthreads();
+            signal_previous();
+            const int r = tid >> 5;
+            const int c = (tid & 31) * 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<uint64_t*>(act_lds + r * kActStride + c + 4 * i) = stg[i];
+            __syncthreads();
+        }
+        // (d) the item itself.
+        const int m = lane & 15;
+        const int g = lane >> 4;
+        if (it.kind == 0) {
+            const int tok = column_token(s, m < s.count ? m : 0);
+            const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < kLoads; q += 2) {
+                acc0 = mfma16x16x32(buf[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                acc1 = mfma16x16x32(buf[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+            }
+            part[(par * kWaves + wave) * kWave + lane] = acc0 + acc1;
+            __syncthreads();
+            signal_previous();
+            if ((wave & 3) == 0) {
+                const f32x4* pp = part + (par * kWaves + wave) * kWave + lane;
+                const f32x4 sum = ((pp[0] + pp[kWave]) + pp[2 * kWave]) + pp[3 * kWave];
+                f32x4 up;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(sum[i], 32, kWave);
+                if (g < 2 && m < s.count) {
+                    uint32_t act[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(sum[i]), rbf(up[i]));
+                    st_agent64(a.act + static_cast<size_t>(s.pair0 + m) * kInner + 16 * it.tile + 8 * (wave >> 2) + 4 * g,
+                               pack4(act));
+                }
+            }
+            par ^= 1;
+        } else {
+            const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < kLoads; q += 2) {
+                acc0 = mfma16x16x32(buf[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                acc1 = mfma16x16x32(buf[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+            }
+            const f32x4 y = acc0 + acc1;
+            if (m < s.count) {
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = f2bf(y[i]);
+                st_agent64(a.y + static_cast<size_t>(s.pair0 + m) * kHidden + kBRows * it.tile + 16 * wave + 4 * g, pack4(o));
+            }
+        }
+        sig_kind = it.kind;
+        sig_slot = it.slot;
+        sig_tile = it.tile;
+        poll = next_poll;
+        return kk + G;
+    };
+
+    if (k < total) {
+        const Item first = item_at(k, total, n_slots, first_slot);
+        issue(item_base(P.slot[first.slot], first, wave, lane), b0);
+        poll = 0u;  // a first B item checks its slot in the bounded wait
+        while (true) {
+            k = step(k, b0, b1);
+            if (k >= total) break;
+            k = step(k, b1, b0);
+            if (k >= total) break;
+        }
+        // Flush: the last item's stores, then its signal; the workgroup whose
+        // last item is the final slot's B item of a tile (always among the
+        // last 16 items, so always a workgroup's last item) combines that
+        // tile once the other slots' B items of the tile are done.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const bool combiner = sig_kind == 1 && sig_slot == first_slot + n_slots - 1;
+        if (tid == 0) {
+            if (sig_kind == 0) add_agent32(&sync->ready[sig_slot * kSyncStride], 1u);
+            if (sig_kind == 1 && !combiner) add_agent32(&sync->tile_done[sig_tile * kSyncStride], 1u);
+            if (combiner && !wait_counter(&sync->tile_done[sig_tile * kSyncStride], static_cast<uint32_t>(n_slots - 1)))
+                P.status |= kStatusTimeout;
+        }
+        if (combiner) {
+            __syncthreads();
+            combine_tile(a, P, sync, sig_tile, T, first_slot == 0);
+        }
+    }
+
+    // ---- 5. the last workgroup to finish resets the counters ----
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        if (P.status & kStatusTimeout) atomicOr(a.status, kStatusTimeout);
+        const int bucket = blockIdx.x % 8;
+        const int in_bucket = (G - bucket + 7) / 8;
+        int last = 0;
+        if (add_agent32(&sync->xcd_done[bucket * kSyncStride], 1u) == static_cast<uint32_t>(in_bucket - 1)) {
+            last = add_agent32(&sync->all_done, 1u) == static_cast<uint32_t>(min(G, 8) - 1);
+        }
+        P.last = last;
+    }
+    __syncthreads();
+    if (P.last) {
+        for (int i = tid; i < kDecodeSlots; i += kThreads) st_agent32(&sync->ready[i * kSyncStride], 0u);
+        if (tid < 8) st_agent32(&sync->xcd_done[tid * kSyncStride], 0u);
+        if (tid == 0) {
+            st_agent32(&sync->router_done, 0u);
+            st_agent32(&sync->all_done, 0u);
+        }
+    }
 }
 
 }  // namespace
 
-hipError_t launch_experts_decode(const ExpertArgs& a, hipStream_t stream) {
-    const int slots = min(kTopK * a.tokens, kExperts) + 1;
-    const StageEvents gate_ev = timing_events(kStageGateUp);
-    LRMOE_LAUNCH(gateup_decode, dim3(slots * kRowTiles), dim3(256), 0, stream, gate_ev.start, gate_ev.stop, a);
-    const size_t act_bytes = static_cast<size_t>(kTopK + 1) * a.tokens * kActStride * sizeof(uint16_t);
+size_t decode_lds_bytes(int tokens) {
+    return static_cast<size_t>(tokens) * kXStride * 2 + static_cast<size_t>(kMaxT) * kActStride * 2 +
+           2 * kWaves * kWave * sizeof(f32x4);
+}
+
+hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
+    if (a.tokens <= 0) return hipSuccess;
+    if (a.tokens > kMaxT) return hipErrorInvalidValue;
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    static int cus[64] = {0};
     static bool lds_opt_in = false;
-    if (!lds_opt_in) {
-        const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(down_combine_decode),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxActLds);
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    if (cus[device] == 0) {
+        err = hipDeviceGetAttribute(&cus[device], hipDeviceAttributeMultiprocessorCount, device);
         if (err != hipSuccess) return err;
+    }
+    const size_t lds = decode_lds_bytes(a.tokens);
+    if (!lds_opt_in) {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_decode), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(decode_lds_bytes(kMaxT)));
+        if (err != hipSuccess) return err;
+        int blocks = 0;
+        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, moe_decode, kThreads, decode_lds_bytes(kMaxT));
+        if (err != hipSuccess) return err;
+        if (blocks < 1) return hipErrorLaunchOutOfResources;
         lds_opt_in = true;
     }
-    const StageEvents down_ev = timing_events(kStageDown);
-    LRMOE_LAUNCH(down_combine_decode, dim3(kHidden / kDownRows), dim3(kDownWaves * kWave), act_bytes, stream,
-                 down_ev.start, down_ev.stop, a);
+    // One workgroup per CU: all of them are resident at once, which the
+    // item waits rely on.
+    const StageEvents ev = timing_events(kStageLayer);
+    LRMOE_LAUNCH(moe_decode, dim3(cus[device]), dim3(kThreads), lds, stream, ev.start, ev.stop, a);
     return hipGetLastError();
 }
 

@@ -328,7 +328,6 @@ __global__ __launch_bounds__(256) void block_combine_kernel(const int32_t* inver
 
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
-    if (a.tokens <= 16) return launch_experts_decode(a, stream);
     const int max_unique = min(kTopK * a.tokens, kExperts);
     const int slots = max_unique + 1;
     const StageEvents gate_ev = timing_events(kStageGateUp);

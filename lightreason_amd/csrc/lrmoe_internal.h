@@ -15,6 +15,24 @@ namespace lrmoe {
 constexpr int32_t kStatusBadExpert = 1;     // expert id outside [0, 256)
 constexpr int32_t kStatusRepeatedExpert = 2;  // a token routes to one expert twice
 constexpr int32_t kStatusCodecRow = 4;      // gather met a codec descriptor (not a raw row)
+constexpr int32_t kStatusTimeout = 8;       // a bounded cross-workgroup wait expired (results invalid)
+
+// Decode layer (one persistent kernel) limits.
+constexpr int kDecodeMaxTokens = 16;
+constexpr int kDecodeSlots = 8 * kDecodeMaxTokens + 1;  // unique routed experts + the shared expert
+constexpr int kSyncStride = 64;  // counters 256 bytes apart (separate memory channels)
+
+// Cross-workgroup counters of the decode kernel.  Zero between calls: the
+// kernel's last workgroup (or a tile's combining workgroup) restores them.
+struct DecodeSync {
+    uint32_t router_done;               // router workgroups finished
+    uint32_t pad0[kSyncStride - 1];
+    uint32_t all_done;                  // XCD buckets finished
+    uint32_t pad1[kSyncStride - 1];
+    uint32_t xcd_done[8 * kSyncStride];   // workgroups finished per blockIdx % 8
+    uint32_t ready[kDecodeSlots * kSyncStride];  // A items finished per slot
+    uint32_t tile_done[16 * kSyncStride];  // B items finished per 128-row output tile
+};
 
 // Control block at the start of every workspace.  The route counter is reset
 // to zero by the workgroup that consumes it, so a zero-initialised workspace
@@ -67,12 +85,13 @@ struct Workspace {
     uint16_t* weights;    // [T][8]
     uint16_t* sg;         // [T]
     Plan plan;
-    uint16_t* act;        // [8T + T][512]: routed pairs, then shared rows
+    uint16_t* act;        // [8T + T + 16][512]: routed pairs, shared rows, padding
     uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
     uint32_t* counts;     // [256] prefill histogram
     uint32_t* bitmaps;    // [256][words] prefill token bitmaps
     uint32_t* word_prefix;  // [256][words]
     SlotDesc* slots;      // [257] decode slot records
+    DecodeSync* sync;     // decode kernel counters
     int words;
     size_t bytes;
 };
@@ -91,6 +110,9 @@ inline Workspace carve(void* base, int tokens) {
         return static_cast<char*>(base) + at;
     };
     ws.control = reinterpret_cast<Control*>(take(sizeof(Control)));
+    // Counters that persist between calls sit at a fixed offset, whatever
+    // the token count of the call.
+    ws.sync = reinterpret_cast<DecodeSync*>(take(sizeof(DecodeSync)));
     ws.logits = reinterpret_cast<uint16_t*>(take(T * 256 * 2));
     ws.normed = reinterpret_cast<uint16_t*>(take(T * 2048 * 2));
     ws.indices = reinterpret_cast<int64_t*>(take(T * 8 * 8));
@@ -101,7 +123,8 @@ inline Workspace carve(void* base, int tokens) {
     ws.plan.pair_token = reinterpret_cast<int32_t*>(take(P * 4));
     ws.plan.pair_slot = reinterpret_cast<int32_t*>(take(P * 4));
     ws.plan.route_pair = reinterpret_cast<int32_t*>(take(P * 4));
-    ws.act = reinterpret_cast<uint16_t*>(take((P + T) * 512 * 2));
+    // 16 rows of padding: the decode kernel stages 16 act rows per slot.
+    ws.act = reinterpret_cast<uint16_t*>(take((P + T + 16) * 512 * 2));
     ws.y = reinterpret_cast<uint16_t*>(take((P + T) * 2048 * 2));
     ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
     ws.bitmaps = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
@@ -157,6 +180,33 @@ struct ExpertArgs {
     Workspace ws;
 };
 
+// Arguments of the decode layer kernel (T <= 16).  Exactly one route source:
+// router (GEMV in the kernel), logits_in, or indices_in + weights_in.
+struct DecodeArgs {
+    const uint16_t* x;            // [T][2048] layer input
+    const uint16_t* norm;         // [2048] RMSNorm weight or null
+    float eps;
+    const uint16_t* router;       // [256][2048] or null
+    const uint16_t* logits_in;    // [T][256] or null
+    const int64_t* indices_in;    // [T][8] or null
+    const uint16_t* weights_in;   // [T][8] with indices_in
+    const uint16_t* shared_expert_gate;  // [2048] or null
+    const uint16_t* sh_gate;      // shared expert [512][2048], or null
+    const uint16_t* sh_up;        // [512][2048]
+    const uint16_t* sh_down;      // [2048][512]
+    const int64_t* expert_ptrs;   // [256][2] (gate_up, down)
+    uint16_t* out;                // [T][2048]
+    int64_t* indices_out;         // [T][8] or null
+    uint16_t* weights_out;        // [T][8] or null
+    uint16_t* logits;             // [T][256] workspace (router output)
+    uint16_t* act;                // [9T][512] workspace
+    uint16_t* y;                  // [9T][2048] workspace
+    DecodeSync* sync;             // workspace counters
+    int32_t* status;              // workspace status word
+    int tokens;
+    int residual;                 // out = x + MoE(...) (decoder layer with norm)
+};
+
 // Optional per-stage timing.  When a stage's bit is enabled, timing_events()
 // hands out the next (start, stop) event pair of that stage; the stage's
 // first kernel is launched with the start event and its last kernel with the
@@ -170,6 +220,7 @@ enum Stage : int {
     kStageDown = 4,
     kStageCombine = 8,
     kStageGather = 16,
+    kStageLayer = 32,
 };
 struct StageEvents {
     hipEvent_t start = nullptr;
@@ -209,7 +260,8 @@ hipError_t launch_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows,
 hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
                                 uint16_t* out, int tokens, int hybrid, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
-hipError_t launch_experts_decode(const ExpertArgs& args, hipStream_t stream);
+hipError_t launch_moe_decode(const DecodeArgs& args, hipStream_t stream);
+size_t decode_lds_bytes(int tokens);
 hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
                               int64_t first, hipStream_t stream);
 

@@ -13,8 +13,8 @@ namespace {
 struct Timing {
     int mask = 0;
     int capacity = 0;
-    std::vector<hipEvent_t> events[5];  // per stage: start, stop, start, stop, ...
-    int used[5] = {0, 0, 0, 0, 0};
+    std::vector<hipEvent_t> events[6];  // per stage: start, stop, start, stop, ...
+    int used[6] = {0, 0, 0, 0, 0, 0};
 };
 
 Timing& timing() {
@@ -23,7 +23,7 @@ Timing& timing() {
 }
 
 int stage_index(int stage) {
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < 6; ++i) {
         if (stage == (1 << i)) return i;
     }
     return -1;
@@ -60,8 +60,8 @@ int lrmoe_timing_enable(int mask, int launches) {
     t.mask = 0;
     t.capacity = 0;
     if (mask == 0) return LRMOE_OK;
-    if (launches <= 0 || launches > (1 << 20) || (mask & ~31)) return LRMOE_E_ARG;
-    for (int i = 0; i < 5; ++i) {
+    if (launches <= 0 || launches > (1 << 20) || (mask & ~63)) return LRMOE_E_ARG;
+    for (int i = 0; i < 6; ++i) {
         if (!(mask & (1 << i))) continue;
         t.events[i].resize(2 * static_cast<size_t>(launches));
         for (auto& e : t.events[i]) {

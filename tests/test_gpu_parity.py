@@ -210,3 +210,57 @@ def test_gather_expert_rows_bit_exact(model, device):
         assert torch.equal(staging_dn[i], dn.view(torch.int16))
     assert torch.all(staging_dn[len(sel)] == 0x5A5A)
     assert int(status.item()) == 0
+
+
+def _check_layer(oracle, host_experts, layer, x, idx_out, w_out, out, what):
+    xb = to_u16(x)
+    _, o_idx, o_w = oracle.route(xb, to_u16(layer.router))
+    np.testing.assert_array_equal(idx_out.cpu().numpy(), o_idx)
+    np.testing.assert_array_equal(to_u16(w_out), o_w)
+    shared = (to_u16(layer.shared_gate_proj), to_u16(layer.shared_up_proj), to_u16(layer.shared_down_proj))
+    sg = oracle.shared_gate(xb, to_u16(layer.shared_expert_gate))
+    want = oracle_experts(oracle, xb, o_idx, o_w, host_experts, shared, sg)
+    assert_close_bf16(to_u16(out), want, what=what)
+
+
+def test_decode_layer_reuses_workspace_and_replays(model, oracle, host_experts):
+    """The T <= 16 layer runs as one kernel whose cross-workgroup counters
+    live in the workspace and return to zero after every call: consecutive
+    calls of different sizes on one workspace, then replays of a captured
+    graph with new inputs between replays, all match the oracle and leave the
+    status word clear."""
+    from lightreason_amd.moe import LayerWeights, Workspace, moe_layer
+
+    layer = LayerWeights(**{**model.layers[0].__dict__, "norm_weight": None})
+    device = model.device
+    ws = Workspace(device, 16)
+    for i, tokens in enumerate((8, 1, 16, 3, 8)):
+        x = model.hidden(tokens, step=1300 + i)
+        idx_out = torch.empty((tokens, 8), dtype=torch.int64, device=device)
+        w_out = torch.empty((tokens, 8), dtype=torch.bfloat16, device=device)
+        out = moe_layer(x, layer, indices=idx_out, weights=w_out, workspace=ws)
+        torch.cuda.synchronize()
+        _check_layer(oracle, host_experts, layer, x, idx_out, w_out, out, f"call {i} T={tokens}")
+        assert ws.status() == 0
+
+    tokens = 8
+    x = model.hidden(tokens, step=1400)
+    idx_out = torch.empty((tokens, 8), dtype=torch.int64, device=device)
+    w_out = torch.empty((tokens, 8), dtype=torch.bfloat16, device=device)
+    out = torch.empty_like(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe_layer(x, layer, out=out, indices=idx_out, weights=w_out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        moe_layer(x, layer, out=out, indices=idx_out, weights=w_out, workspace=ws)
+    for r in range(3):
+        x.copy_(model.hidden(tokens, step=1500 + r))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _check_layer(oracle, host_experts, layer, x, idx_out, w_out, out, f"replay {r}")
+        assert ws.status() == 0
