@@ -129,8 +129,7 @@ struct Plan {
     float sg[kMaxT];                  // shared-expert gate per token
     int32_t ids[kMaxT][kTopK];        // routed experts, rank order
     uint16_t wts[kMaxT][kTopK];       // routing weights (bf16), rank order
-    uint32_t keys8[kMaxT][kTopK];     // top-k scratch
-    float vals8[kMaxT][kTopK];
+    uint4 eptr[kExperts];             // (gate_up, down) address of every expert
     uint32_t tokmask[kExperts];
     uint32_t poff[kExperts];
     uint32_t scan[4];
@@ -161,67 +160,44 @@ __device__ uint32_t block_scan256(uint32_t value, uint32_t* scratch, uint32_t* t
     return threadIdx.x < kExperts ? before + inclusive - value : 0u;
 }
 
-// Top-8 of one token by one wave (ballot radix select over unique 24-bit
-// keys, lane l holding experts 4l..4l+3), softmax over all 256 in fp32,
-// renormalised weights.  Writes ids/wts in rank order.  Same arithmetic and
-// order as route.hip's topk_token_select and the oracle.
-__device__ void topk_wave(uint64_t packed, int32_t* ids_row, uint16_t* wts_row, uint32_t* keys8, float* vals8) {
+// Top-8 of one token by one wave: lane l holds experts 4l..4l+3 as unique
+// keys (bf16 logit order, then lower expert id); eight wave-wide maximum
+// extractions give the winners in rank order.  Softmax over all 256 in fp32
+// relative to the top logit (the per-lane sums meet in the fixed butterfly),
+// then the eight probabilities are renormalised by their sum in rank order
+// and rounded to bf16.  Same arithmetic and order as the oracle.
+__device__ void topk_wave(uint64_t packed, int32_t* ids_row, uint16_t* wts_row) {
     const int lane = threadIdx.x & 63;
     uint32_t bits[4], keys[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
-        keys[j] = route_key(bits[j], 4 * lane + j);
+        keys[j] = route_key(bits[j], 4 * lane + j) + 1u;  // 0 marks a taken key
     }
-    uint32_t best = keys[0];
+    uint32_t chosen[kTopK];
 #pragma unroll
-    for (int j = 1; j < 4; ++j) best = keys[j] > best ? keys[j] : best;
-    best = wave_max_u32(best);
-    uint32_t threshold = 0;
-#pragma unroll 1
-    for (int bit = 23; bit >= 0; --bit) {
-        const uint32_t candidate = threshold | (1u << bit);
-        int above = 0;
+    for (int k = 0; k < kTopK; ++k) {
+        const uint32_t mine = max(max(keys[0], keys[1]), max(keys[2], keys[3]));
+        chosen[k] = wave_max_u32(mine);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) above += __popcll(__ballot(keys[j] >= candidate));
-        if (above >= kTopK) threshold = candidate;
+        for (int j = 0; j < 4; ++j) keys[j] = keys[j] == chosen[k] ? 0u : keys[j];
     }
-    const float top = bf2f(key_bits(best));
-    float ex[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ex[j] = lr_exp(bf2f(bits[j]) - top);
+    const float top = bf2f(key_bits(chosen[0] - 1u));
     float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) part = part + ex[j];
+    for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
     const float total = wave_butterfly_sum(part);
-    int base = 0;
+    // Lane k < 8 owns rank k.
+    uint32_t my = chosen[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const bool chosen = keys[j] >= threshold;
-        const uint64_t mask = __ballot(chosen);
-        if (chosen) {
-            const int at = base + __popcll(mask & ((1ull << lane) - 1ull));
-            keys8[at] = keys[j];
-            vals8[at] = ex[j];
-        }
-        base += __popcll(mask);
-    }
-    __builtin_amdgcn_wave_barrier();
-    const int k = lane & 7;
-    const uint32_t my_key = keys8[k];
-    int rank = 0;
+    for (int k = 1; k < kTopK; ++k) my = lane == k ? chosen[k] : my;
+    const float prob = lr_exp(bf2f(key_bits(my - 1u)) - top) / total;
+    float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), 0));
 #pragma unroll
-    for (int i = 0; i < kTopK; ++i) rank += keys8[i] > my_key ? 1 : 0;
-    const float prob = vals8[k] / total;
-    __builtin_amdgcn_wave_barrier();
-    if (lane < kTopK) vals8[rank] = prob;
-    __builtin_amdgcn_wave_barrier();
-    float sum = vals8[0];
-#pragma unroll
-    for (int i = 1; i < kTopK; ++i) sum = sum + vals8[i];
+    for (int k = 1; k < kTopK; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), k));
     if (lane < kTopK) {
-        ids_row[rank] = 255 - static_cast<int>(my_key & 255u);
-        wts_row[rank] = static_cast<uint16_t>(f2bf(prob / sum));
+        ids_row[lane] = 255 - static_cast<int>((my - 1u) & 255u);
+        wts_row[lane] = static_cast<uint16_t>(f2bf(prob / sum));
     }
 }
 
@@ -340,12 +316,46 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
     DecodeSync* sync = a.sync;
 
-    // ---- 1. token rows (normalised) and shared-expert gates ----
-    for (int t = wave; t < T; t += kWaves) {
-        const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(t) * kHidden + 32 * lane);
-        uint4 v[4];
+    // ---- 1. every load that depends on nothing, issued first ----
+    // In order of need: the caller's logits rows of this wave's tokens
+    // (tokens wave and wave + 8), the 256-entry expert address table, the
+    // token rows, the RMSNorm and shared-gate rows and a router workgroup's
+    // router row.  Absent rows load a valid dummy row instead, so that every
+    // path issues the same loads (exact wait counts).
+    const int t_lo = wave;
+    const int t_hi = wave + kWaves;
+    const bool has_lo = t_lo < T;
+    const bool has_hi = t_hi < T;
+    const bool router_wg = a.router != nullptr && static_cast<int>(blockIdx.x) < kRouterWgs;
+    const bool logits_given = a.logits_in != nullptr;
+    const uint16_t* lg_src = logits_given ? a.logits_in : a.x;
+    uint64_t lg_lo = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_lo ? t_lo : 0) * kExperts * logits_given + 4 * lane);
+    uint64_t lg_hi = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_hi ? t_hi : 0) * kExperts * logits_given + 4 * lane);
+    const uint4 eptr = ldg16(a.expert_ptrs + 2 * (tid & (kExperts - 1)));
+    const uint16_t* xr_lo = a.x + static_cast<size_t>(has_lo ? t_lo : 0) * kHidden + 32 * lane;
+    const uint16_t* xr_hi = a.x + static_cast<size_t>(has_hi ? t_hi : 0) * kHidden + 32 * lane;
+    const uint16_t* nr = (a.norm != nullptr ? a.norm : a.x) + 32 * lane;
+    const uint16_t* gr = (a.shared_expert_gate != nullptr ? a.shared_expert_gate : a.x) + 32 * lane;
+    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * blockIdx.x + wave) * kHidden + 32 * lane
+                                   : a.x + 32 * lane;
+    uint4 x_lo[4], x_hi[4], w_norm[4], w_sg[4], w_router[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = src[i];
+    for (int i = 0; i < 4; ++i) x_lo[i] = ldg16(xr_lo + 8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x_hi[i] = ldg16(xr_hi + 8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w_norm[i] = ldg16(nr + 8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w_sg[i] = ldg16(gr + 8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
+    if (tid < kExperts) P.tokmask[tid] = 0u;
+    if (tid == 0) P.status = 0;
+    __syncthreads();
+
+    // Token rows (normalised when the layer norms) into LDS, and the
+    // shared-expert gate of each token.
+    auto stage_row = [&](int t, uint4* v) {
         if (a.norm != nullptr) {
             float f[32];
 #pragma unroll
@@ -355,11 +365,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(f[j], f[j], acc);
             const float mean = wave_butterfly_sum(acc) / static_cast<float>(kHidden);
             const float r = 1.0f / __builtin_sqrtf(mean + a.eps);
-            const uint4* wsrc = reinterpret_cast<const uint4*>(a.norm + 32 * lane);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float wf[8];
-                unpack8(wsrc[i], wf);
+                unpack8(w_norm[i], wf);
                 uint32_t o[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = f2bf((f[8 * i + j] * r) * (1.0f + wf[j]));
@@ -370,56 +379,51 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = v[i];
         if (a.shared_expert_gate != nullptr) {
-            uint4 w[4];
-            const uint4* gsrc = reinterpret_cast<const uint4*>(a.shared_expert_gate + 32 * lane);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = gsrc[i];
-            const float z = rbf(wave_butterfly_sum(lane_dot32(w, x_lds + t * kXStride, lane)));
+            const float z = rbf(wave_butterfly_sum(lane_dot32(w_sg, x_lds + t * kXStride, lane)));
             if (lane == 0) P.sg[t] = rbf(1.0f / (1.0f + lr_exp(-z)));
         }
-    }
-    if (tid == 0) {
-        P.status = 0;
-    }
-    __syncthreads();
+    };
+    auto stage_rows = [&]() {
+        if (has_lo) stage_row(t_lo, x_lo);
+        if (has_hi) stage_row(t_hi, x_hi);
+    };
 
     // ---- 2. router rows (workgroups 0..31, one row per wave) ----
-    if (a.router != nullptr && static_cast<int>(blockIdx.x) < kRouterWgs) {
-        const int row = kWaves * blockIdx.x + wave;
-        const uint4* src = reinterpret_cast<const uint4*>(a.router + static_cast<size_t>(row) * kHidden + 32 * lane);
-        uint4 w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = src[i];
-        for (int t = 0; t < T; ++t) {
-            const float s = wave_butterfly_sum(lane_dot32(w, x_lds + t * kXStride, lane));
-            if (lane == 0) P.lg[t][wave] = static_cast<uint16_t>(f2bf(s));
-        }
+    // The router needs the token rows first; with caller logits the rows are
+    // staged later, while the first weights are already streaming.
+    if (a.router != nullptr) {
+        stage_rows();
         __syncthreads();
-        if (tid < 2 * T) {
-            const int t = tid >> 1;
-            const int h = tid & 1;
-            uint32_t v[4];
+        if (router_wg) {
+            for (int t = 0; t < T; ++t) {
+                const float s = wave_butterfly_sum(lane_dot32(w_router, x_lds + t * kXStride, lane));
+                if (lane == 0) P.lg[t][wave] = static_cast<uint16_t>(f2bf(s));
+            }
+            __syncthreads();
+            if (tid < 2 * T) {
+                const int t = tid >> 1;
+                const int h = tid & 1;
+                uint32_t v[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = P.lg[t][4 * h + i];
-            st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * blockIdx.x + 4 * h, pack4(v));
+                for (int i = 0; i < 4; ++i) v[i] = P.lg[t][4 * h + i];
+                st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * blockIdx.x + 4 * h, pack4(v));
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0) add_agent32(&sync->router_done, 1u);
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) add_agent32(&sync->router_done, 1u);
     }
 
-    // ---- 3. the route plan ----
+    // ---- 4. the route plan ----
     if (a.router != nullptr) {
         if (tid == 0 && !wait_counter(&sync->router_done, kRouterWgs)) P.status |= kStatusTimeout;
         __syncthreads();
+        if (has_lo) lg_lo = ld_agent64(a.logits + static_cast<size_t>(t_lo) * kExperts + 4 * lane);
+        if (has_hi) lg_hi = ld_agent64(a.logits + static_cast<size_t>(t_hi) * kExperts + 4 * lane);
     }
     if (a.indices_in == nullptr) {
-        for (int t = wave; t < T; t += kWaves) {
-            const uint16_t* row = (a.router != nullptr ? a.logits : a.logits_in) + static_cast<size_t>(t) * kExperts;
-            const uint64_t packed = a.router != nullptr ? ld_agent64(row + 4 * lane)
-                                                        : *reinterpret_cast<const uint64_t*>(row + 4 * lane);
-            topk_wave(packed, P.ids[t], P.wts[t], P.keys8[t], P.vals8[t]);
-        }
+        if (has_lo) topk_wave(lg_lo, P.ids[t_lo], P.wts[t_lo]);
+        if (has_hi) topk_wave(lg_hi, P.ids[t_hi], P.wts[t_hi]);
     } else if (tid < T * kTopK) {
         const int t = tid / kTopK;
         const int r = tid % kTopK;
@@ -430,13 +434,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         P.wts[t][r] = a.weights_in[tid];
         if (bad) atomicOr(&P.status, bad);
     }
-    if (tid < kExperts) P.tokmask[tid] = 0u;
+    if (tid < kExperts) P.eptr[tid] = eptr;
     __syncthreads();
     if (blockIdx.x == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
     }
-    const bool routes_ok = P.status == 0;
+    const bool routes_ok = (P.status & ~kStatusTimeout) == 0;
     if (routes_ok && tid < T * kTopK) atomicOr(&P.tokmask[P.ids[tid / kTopK][tid % kTopK]], 1u << (tid / kTopK));
     __syncthreads();
     {
@@ -450,16 +454,23 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         if (tid < kExperts) P.poff[tid] = pair0;
         if (count) {
             SlotInfo& s = P.slot[1 + rank];
-            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * tid]);
+            const uint4 ptrs = P.eptr[tid];
+            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
+                                                                        (static_cast<uintptr_t>(ptrs.y) << 32));
             s.gate = gate_up;
             s.up = gate_up + static_cast<size_t>(kInner) * kHidden;
-            s.down = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * tid + 1]);
+            s.down = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) | (static_cast<uintptr_t>(ptrs.w) << 32));
             uint32_t tok[4] = {0u, 0u, 0u, 0u};
             uint32_t m = mask;
-            for (int j = 0; m; ++j) {
-                const int t = __ffs(m) - 1;
+#pragma unroll
+            for (int j = 0; j < kMaxT; ++j) {
+                const int t = m ? __ffs(m) - 1 : 0;
+                const uint32_t v = m ? static_cast<uint32_t>(t) << (8 * (j & 3)) : 0u;
+                tok[0] |= (j >> 2) == 0 ? v : 0u;
+                tok[1] |= (j >> 2) == 1 ? v : 0u;
+                tok[2] |= (j >> 2) == 2 ? v : 0u;
+                tok[3] |= (j >> 2) == 3 ? v : 0u;
                 m &= m - 1u;
-                tok[j >> 2] |= static_cast<uint32_t>(t) << (8 * (j & 3));
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) s.tok[i] = tok[i];
@@ -473,7 +484,14 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             s.up = a.sh_up;
             s.down = a.sh_down;
             uint32_t tok[4] = {0u, 0u, 0u, 0u};
-            for (int j = 0; j < T; ++j) tok[j >> 2] |= static_cast<uint32_t>(j) << (8 * (j & 3));
+#pragma unroll
+            for (int j = 0; j < kMaxT; ++j) {
+                const uint32_t v = j < T ? static_cast<uint32_t>(j) << (8 * (j & 3)) : 0u;
+                tok[0] |= (j >> 2) == 0 ? v : 0u;
+                tok[1] |= (j >> 2) == 1 ? v : 0u;
+                tok[2] |= (j >> 2) == 2 ? v : 0u;
+                tok[3] |= (j >> 2) == 3 ? v : 0u;
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) s.tok[i] = tok[i];
             s.count = T;
@@ -496,7 +514,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
     // This call's route status replaces the previous call's (timeouts are
     // OR-ed in at the end).
-    if (blockIdx.x == 0 && tid == 0) st_agent32(a.status, static_cast<uint32_t>(P.status));
+    if (blockIdx.x == 0 && tid == 0) st_agent32(a.status, static_cast<uint32_t>(P.status & ~kStatusTimeout));
     __syncthreads();
 
     const int n_slots = P.n_slots;
@@ -643,6 +661,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         const Item first = item_at(k, total, n_slots, first_slot);
         issue(item_base(P.slot[first.slot], first, wave, lane), b0);
         poll = 0u;  // a first B item checks its slot in the bounded wait
+        if (a.router == nullptr) {
+            // Token rows staged while the first weights stream in.
+            stage_rows();
+            __syncthreads();
+        }
         while (true) {
             k = step(k, b0, b1);
             if (k >= total) break;

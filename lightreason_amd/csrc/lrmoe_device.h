@@ -69,21 +69,46 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float gate, float up) {
     return f2bf(silu * up);
 }
 
+// Value of lane (l ^ OFF) for a full wavefront: DPP quad permutes for 1 and
+// 2, swizzles inside 32-lane halves for 4, 8 and 16, a permute for 32 (no
+// bounds arithmetic, which __shfl_xor adds).
+template <int OFF>
+__device__ __forceinline__ int lane_xor(int x) {
+    if constexpr (OFF == 1) {
+        return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (OFF == 2) {
+        return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (OFF == 32) {
+        return __builtin_amdgcn_ds_bpermute(static_cast<int>((__lane_id() ^ 32u) << 2), x);
+    } else {
+        return __builtin_amdgcn_ds_swizzle(x, 0x1F | (OFF << 10));  // bitmask mode: lane ^ OFF
+    }
+}
+
 // xor butterfly over the 64 lanes with offsets 1,2,4,...,32: the fixed
-// reduction order shared with the oracle for router and norm sums.
+// reduction order shared with the oracle for router and norm sums (every lane
+// ends with the same total).
 __device__ __forceinline__ float wave_butterfly_sum(float value) {
-#pragma unroll
-    for (int offset = 1; offset < kWave; offset <<= 1) value = value + __shfl_xor(value, offset, kWave);
+    value = value + __int_as_float(lane_xor<1>(__float_as_int(value)));
+    value = value + __int_as_float(lane_xor<2>(__float_as_int(value)));
+    value = value + __int_as_float(lane_xor<4>(__float_as_int(value)));
+    value = value + __int_as_float(lane_xor<8>(__float_as_int(value)));
+    value = value + __int_as_float(lane_xor<16>(__float_as_int(value)));
+    value = value + __int_as_float(lane_xor<32>(__float_as_int(value)));
     return value;
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t value) {
-#pragma unroll
-    for (int offset = 1; offset < kWave; offset <<= 1) {
-        const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(value), offset, kWave));
-        value = other > value ? other : value;
-    }
-    return value;
+// Maximum over the wavefront, returned to every lane (a wave-uniform value):
+// running maxima inside 16-lane rows (row_shr 1,2,4,8), row broadcasts of
+// lanes 15 and 31, then lane 63.  The order is irrelevant for a maximum.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false)));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
 // Dot product of 8 bf16 weights (one 16-byte load) with 8 floats, as an
