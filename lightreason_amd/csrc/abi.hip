@@ -120,7 +120,7 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
         d.tokens = tokens;
         return status_of(lrmoe::launch_moe_decode(d, s));
     }
-    hipError_t err = lrmoe::launch_bucket(indices, tokens, ws, ws.plan, s);
+    hipError_t err = lrmoe::launch_prefill_plan(nullptr, indices, weights, nullptr, nullptr, tokens, 0, ws, ws.plan, s);
     if (err != hipSuccess) return status_of(err);
     lrmoe::ExpertArgs a{};
     a.x = hidden;

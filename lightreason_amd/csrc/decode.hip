@@ -140,67 +140,6 @@ struct Plan {
     int32_t last;
 };
 
-// Exclusive scan over threads 0..255 (all threads call; others contribute 0).
-__device__ uint32_t block_scan256(uint32_t value, uint32_t* scratch, uint32_t* total) {
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    if (threadIdx.x >= kExperts) value = 0;
-    uint32_t inclusive = value;
-#pragma unroll
-    for (int offset = 1; offset < kWave; offset <<= 1) {
-        const uint32_t up = static_cast<uint32_t>(__shfl_up(static_cast<int>(inclusive), offset, kWave));
-        if (lane >= offset) inclusive += up;
-    }
-    if (lane == kWave - 1 && wave < 4) scratch[wave] = inclusive;
-    __syncthreads();
-    uint32_t before = 0;
-    for (int w = 0; w < wave && w < 4; ++w) before += scratch[w];
-    *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
-    __syncthreads();
-    return threadIdx.x < kExperts ? before + inclusive - value : 0u;
-}
-
-// Top-8 of one token by one wave: lane l holds experts 4l..4l+3 as unique
-// keys (bf16 logit order, then lower expert id); eight wave-wide maximum
-// extractions give the winners in rank order.  Softmax over all 256 in fp32
-// relative to the top logit (the per-lane sums meet in the fixed butterfly),
-// then the eight probabilities are renormalised by their sum in rank order
-// and rounded to bf16.  Same arithmetic and order as the oracle.
-__device__ void topk_wave(uint64_t packed, int32_t* ids_row, uint16_t* wts_row) {
-    const int lane = threadIdx.x & 63;
-    uint32_t bits[4], keys[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
-        keys[j] = route_key(bits[j], 4 * lane + j) + 1u;  // 0 marks a taken key
-    }
-    uint32_t chosen[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        const uint32_t mine = max(max(keys[0], keys[1]), max(keys[2], keys[3]));
-        chosen[k] = wave_max_u32(mine);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) keys[j] = keys[j] == chosen[k] ? 0u : keys[j];
-    }
-    const float top = bf2f(key_bits(chosen[0] - 1u));
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
-    const float total = wave_butterfly_sum(part);
-    // Lane k < 8 owns rank k.
-    uint32_t my = chosen[0];
-#pragma unroll
-    for (int k = 1; k < kTopK; ++k) my = lane == k ? chosen[k] : my;
-    const float prob = lr_exp(bf2f(key_bits(my - 1u)) - top) / total;
-    float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), 0));
-#pragma unroll
-    for (int k = 1; k < kTopK; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), k));
-    if (lane < kTopK) {
-        ids_row[lane] = 255 - static_cast<int>((my - 1u) & 255u);
-        wts_row[lane] = static_cast<uint16_t>(f2bf(prob / sum));
-    }
-}
-
 // Dot of a lane's 32 contiguous elements (4 x 16 bytes) with the same
 // elements of an LDS row, as an in-order fmaf chain from +0.
 __device__ __forceinline__ float lane_dot32(const uint4* w, const uint16_t* row, int lane) {
@@ -422,8 +361,22 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         if (has_hi) lg_hi = ld_agent64(a.logits + static_cast<size_t>(t_hi) * kExperts + 4 * lane);
     }
     if (a.indices_in == nullptr) {
-        if (has_lo) topk_wave(lg_lo, P.ids[t_lo], P.wts[t_lo]);
-        if (has_hi) topk_wave(lg_hi, P.ids[t_hi], P.wts[t_hi]);
+        int e_lo, e_hi;
+        uint32_t w_lo, w_hi;
+        if (has_lo) {
+            topk8_wave(lg_lo, e_lo, w_lo);
+            if (lane < kTopK) {
+                P.ids[t_lo][lane] = e_lo;
+                P.wts[t_lo][lane] = static_cast<uint16_t>(w_lo);
+            }
+        }
+        if (has_hi) {
+            topk8_wave(lg_hi, e_hi, w_hi);
+            if (lane < kTopK) {
+                P.ids[t_hi][lane] = e_hi;
+                P.wts[t_hi][lane] = static_cast<uint16_t>(w_hi);
+            }
+        }
     } else if (tid < T * kTopK) {
         const int t = tid / kTopK;
         const int r = tid % kTopK;

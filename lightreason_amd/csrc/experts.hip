@@ -8,147 +8,15 @@
 // (out = bf16(routed + bf16(sigmoid_gate * shared))) and, for a decoder layer,
 // the residual add.
 //
-// Layout of the work: a workgroup owns one (expert, 16-row tile) and streams
-// that tile's weights exactly once from HBM straight into MFMA A operands;
-// every token routed to the expert is a column of the B operand (up to 16
-// per MFMA), so a weight byte read from HBM serves all of its tokens.  The
-// 16x16x32 bf16 MFMA accumulates in fp32.
+// The grouped expert GEMMs of a prefill live in prefill.hip; this file holds
+// the ordered combine that follows them and the reference-shaped kernels.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
 namespace lrmoe {
 namespace {
 
-constexpr int kGateTiles = kInner / 16;      // 32 tiles of 16 gate (and 16 up) rows
-constexpr int kDownRowsPerWg = 64;           // 4 waves x 16 output rows
-constexpr int kDownTiles = kHidden / kDownRowsPerWg;
-
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
-
-struct Group {
-    const uint16_t* gate;   // [512][2048]
-    const uint16_t* up;     // [512][2048]
-    const uint16_t* down;   // [2048][512]
-    const int32_t* tokens;  // token of each column, or null for 0..n-1
-    int pair0;              // first act/y row of this group
-    int count;              // tokens in the group
-};
-
-// slot 0 is the shared expert, slot s >= 1 the (s-1)-th unique routed expert.
-__device__ __forceinline__ bool load_group(const ExpertArgs& a, int slot, Group& g) {
-    if (slot == 0) {
-        if (a.shared_down == nullptr) return false;
-        g.gate = a.shared_gate_proj;
-        g.up = a.shared_up_proj;
-        g.down = a.shared_down;
-        g.tokens = nullptr;
-        g.pair0 = kTopK * a.tokens;
-        g.count = a.tokens;
-        return true;
-    }
-    const int u = slot - 1;
-    if (u >= *a.plan.unique) return false;
-    const int e = a.plan.expert[u];
-    const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e]);
-    g.gate = gate_up;
-    g.up = gate_up + static_cast<size_t>(kInner) * kHidden;
-    g.down = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e + 1]);
-    g.pair0 = a.plan.offset[u];
-    g.count = a.plan.offset[u + 1] - g.pair0;
-    g.tokens = a.plan.pair_token + g.pair0;
-    return true;
-}
-
-// Gate/up + SwiGLU.  Wave w covers k in [512w, 512w+512) of a 16-row tile;
-// the four partial tiles meet in LDS in wave order.  Columns beyond 16 tokens
-// are handled in successive 16-token blocks that re-read the (now cached)
-// weight tile.
-__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
-    Group grp;
-    if (!load_group(a, blockIdx.x / kGateTiles, grp)) return;
-    const int tile = blockIdx.x % kGateTiles;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const int row0 = tile * 16;
-    const int k0 = wave * 512 + 8 * g;
-    const uint16_t* gate_row = grp.gate + static_cast<size_t>(row0 + n) * kHidden + k0;
-    const uint16_t* up_row = grp.up + static_cast<size_t>(row0 + n) * kHidden + k0;
-    __shared__ f32x4 red[4][2][kWave];
-
-    for (int nb = 0; nb < grp.count; nb += 16) {
-        const int col = nb + n;
-        const bool live = col < grp.count;
-        const int token = live ? (grp.tokens ? grp.tokens[col] : col) : 0;
-        const uint16_t* x_row = a.x + static_cast<size_t>(token) * kHidden + k0;
-        f32x4 acc_g = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4 acc_u = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            uint4 ag[8], au[8], bx[8];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const int k = 32 * (8 * half + s);
-                ag[s] = *reinterpret_cast<const uint4*>(gate_row + k);
-                au[s] = *reinterpret_cast<const uint4*>(up_row + k);
-                bx[s] = live ? *reinterpret_cast<const uint4*>(x_row + k) : zero4();
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                acc_g = mfma16x16x32(ag[s], bx[s], acc_g);
-                acc_u = mfma16x16x32(au[s], bx[s], acc_u);
-            }
-        }
-        red[wave][0][lane] = acc_g;
-        red[wave][1][lane] = acc_u;
-        __syncthreads();
-        if (wave == 0) {
-            const f32x4 sg = ((red[0][0][lane] + red[1][0][lane]) + red[2][0][lane]) + red[3][0][lane];
-            const f32x4 su = ((red[0][1][lane] + red[1][1][lane]) + red[2][1][lane]) + red[3][1][lane];
-            if (live) {
-                uint32_t act[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(sg[i]), rbf(su[i]));
-                uint16_t* dst = a.ws.act + static_cast<size_t>(grp.pair0 + col) * kInner + row0 + 4 * g;
-                *reinterpret_cast<uint2*>(dst) = make_uint2(act[0] | (act[1] << 16), act[2] | (act[3] << 16));
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// Down projection: wave w owns 16 output rows of a 64-row tile, full k = 512.
-__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
-    Group grp;
-    if (!load_group(a, blockIdx.x / kDownTiles, grp)) return;
-    const int tile = blockIdx.x % kDownTiles;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const int h0 = tile * kDownRowsPerWg + 16 * wave;
-    const uint16_t* w_row = grp.down + static_cast<size_t>(h0 + n) * kInner + 8 * g;
-    uint4 aw[16];
-#pragma unroll
-    for (int s = 0; s < 16; ++s) aw[s] = *reinterpret_cast<const uint4*>(w_row + 32 * s);
-    for (int nb = 0; nb < grp.count; nb += 16) {
-        const int col = nb + n;
-        const bool live = col < grp.count;
-        const uint16_t* act_row = a.ws.act + static_cast<size_t>(grp.pair0 + (live ? col : 0)) * kInner + 8 * g;
-        uint4 bx[16];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) bx[s] = live ? *reinterpret_cast<const uint4*>(act_row + 32 * s) : zero4();
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 16; ++s) acc = mfma16x16x32(aw[s], bx[s], acc);
-        if (live) {
-            uint16_t* dst = a.ws.y + static_cast<size_t>(grp.pair0 + col) * kHidden + h0 + 4 * g;
-            *reinterpret_cast<uint2*>(dst) = make_uint2(f2bf(acc[0]) | (f2bf(acc[1]) << 16),
-                                                        f2bf(acc[2]) | (f2bf(acc[3]) << 16));
-        }
-    }
-}
 
 // Ordered combine: one workgroup per token, 8 columns per thread.
 __global__ __launch_bounds__(256) void combine_kernel(ExpertArgs a) {
@@ -328,12 +196,8 @@ __global__ __launch_bounds__(256) void block_combine_kernel(const int32_t* inver
 
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
-    const int max_unique = min(kTopK * a.tokens, kExperts);
-    const int slots = max_unique + 1;
-    const StageEvents gate_ev = timing_events(kStageGateUp);
-    LRMOE_LAUNCH(gateup_kernel, dim3(slots * kGateTiles), dim3(256), 0, stream, gate_ev.start, gate_ev.stop, a);
-    const StageEvents down_ev = timing_events(kStageDown);
-    LRMOE_LAUNCH(down_kernel, dim3(slots * kDownTiles), dim3(256), 0, stream, down_ev.start, down_ev.stop, a);
+    const hipError_t err = launch_prefill_experts(a, stream);
+    if (err != hipSuccess) return err;
     const StageEvents comb_ev = timing_events(kStageCombine);
     LRMOE_LAUNCH(combine_kernel, dim3(a.tokens), dim3(256), 0, stream, comb_ev.start, comb_ev.stop, a);
     return hipGetLastError();

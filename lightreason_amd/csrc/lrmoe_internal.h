@@ -20,7 +20,8 @@ constexpr int32_t kStatusTimeout = 8;       // a bounded cross-workgroup wait ex
 // Decode layer (one persistent kernel) limits.
 constexpr int kDecodeMaxTokens = 16;
 constexpr int kDecodeSlots = 8 * kDecodeMaxTokens + 1;  // unique routed experts + the shared expert
-constexpr int kSyncStride = 64;  // counters 256 bytes apart (separate memory channels)
+constexpr int kSyncStride = 64;
+constexpr int kPassTok = 128;    // prefill: tokens of one expert per work unit  // counters 256 bytes apart (separate memory channels)
 
 // Cross-workgroup counters of the decode kernel.  Zero between calls: the
 // kernel's last workgroup (or a tile's combining workgroup) restores them.
@@ -41,7 +42,7 @@ struct Control {
     uint32_t route_counter;
     int32_t status;
     int32_t unique;
-    int32_t pad0;
+    int32_t n_units;    // prefill work units of the current plan
     uint32_t reserved[60];
 };
 
@@ -92,6 +93,11 @@ struct Workspace {
     uint32_t* word_prefix;  // [256][words]
     SlotDesc* slots;      // [257] decode slot records
     DecodeSync* sync;     // decode kernel counters
+    uint8_t* bmask;       // prefill: [256][nblk_pad] token masks per 8-token block
+    uint32_t* blk_base;   // prefill: [256][nblk_pad] pairs of the expert before the block
+    int32_t* bstatus;     // prefill: [nblk] route status per block
+    int2* units;          // prefill: (slot, first pair) work units
+    int nblk_pad;
     int words;
     size_t bytes;
 };
@@ -130,6 +136,14 @@ inline Workspace carve(void* base, int tokens) {
     ws.bitmaps = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
     ws.word_prefix = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
     ws.slots = reinterpret_cast<SlotDesc*>(take(sizeof(SlotDesc) * kMaxSlots));
+    const size_t nblk = (T + 7) / 8;
+    const size_t nblk_pad = (nblk + 15) / 16 * 16;
+    ws.nblk_pad = static_cast<int>(nblk_pad);
+    ws.bmask = reinterpret_cast<uint8_t*>(take(256 * nblk_pad));
+    ws.blk_base = reinterpret_cast<uint32_t*>(take(256 * nblk_pad * 4));
+    ws.bstatus = reinterpret_cast<int32_t*>(take(nblk * 4));
+    const size_t units = (T + kPassTok - 1) / kPassTok + 256 + (8 * T + kPassTok - 1) / kPassTok + 8;
+    ws.units = reinterpret_cast<int2*>(take(units * sizeof(int2)));
     ws.words = words;
     ws.plan.unique = &ws.control->unique;
     ws.plan.status = &ws.control->status;
@@ -261,6 +275,12 @@ hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const
                                 uint16_t* out, int tokens, int hybrid, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
 hipError_t launch_moe_decode(const DecodeArgs& args, hipStream_t stream);
+// Prefill plan (T > 16): top-8 from `logits` (or the validated caller indices)
+// and the bucketing plan with its work units.
+hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in, const uint16_t* weights_in,
+                               int64_t* indices, uint16_t* weights, int tokens, int shared_present,
+                               const Workspace& ws, const Plan& plan, hipStream_t stream);
+hipError_t launch_prefill_experts(const ExpertArgs& args, hipStream_t stream);
 size_t decode_lds_bytes(int tokens);
 hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
                               int64_t first, hipStream_t stream);

@@ -80,55 +80,6 @@ __device__ __forceinline__ float lane_dot(const float* w, const uint16_t* xs, in
     return acc;
 }
 
-// Top-8 + softmax + renormalisation for token `t` by one wave.  Lane l holds
-// the logits of experts 4l..4l+3.  Writes indices (rank order) and weights;
-// returns this lane's chosen expert when lane < 8 (else -1).
-__device__ int topk_token(const uint16_t* logits_row, int64_t* indices_row, uint16_t* weights_row) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t packed = reinterpret_cast<const uint64_t*>(logits_row)[lane];
-    uint32_t bits[4], keys[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
-        keys[j] = route_key(bits[j], 4 * lane + j) + 1u;  // +1 keeps 0 free as "taken"
-    }
-    uint32_t chosen[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        uint32_t mine = keys[0];
-#pragma unroll
-        for (int j = 1; j < 4; ++j) mine = keys[j] > mine ? keys[j] : mine;
-        const uint32_t best = wave_max_u32(mine);
-        chosen[k] = best - 1u;
-        const int expert = 255 - static_cast<int>((best - 1u) & 255u);
-        if ((expert >> 2) == lane) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) keys[j] = (j == (expert & 3)) ? 0u : keys[j];
-        }
-    }
-    const float top = bf2f(key_bits(chosen[0]));
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
-    const float total = wave_butterfly_sum(part);
-    float prob[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) prob[k] = lr_exp(bf2f(key_bits(chosen[k])) - top) / total;
-    float sum = prob[0];
-#pragma unroll
-    for (int k = 1; k < kTopK; ++k) sum = sum + prob[k];
-    int mine_expert = -1;
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        if (lane == k) {
-            mine_expert = 255 - static_cast<int>(chosen[k] & 255u);
-            indices_row[k] = mine_expert;
-            weights_row[k] = static_cast<uint16_t>(f2bf(prob[k] / sum));
-        }
-    }
-    return mine_expert;
-}
-
 // Exclusive scan of one value per thread over threads 0..255 of a workgroup
 // of >= 256 threads (every thread must call it; values of threads >= 256 are
 // ignored and get 0).  `total` receives the sum over threads 0..255.
@@ -448,97 +399,6 @@ __global__ __launch_bounds__(1024) void topk_bucket_small(RouteArgs a) {
     if (threadIdx.x == 0) *a.plan.status = 0;
 }
 
-// Prefill top-k: one wave per token; also records the expert histogram and
-// per-expert token bitmaps used by the bucketing kernels.
-__global__ __launch_bounds__(256) void topk_tokens(RouteArgs a) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (t >= a.tokens) return;
-    const uint16_t* logits = a.logits_in != nullptr ? a.logits_in : a.logits;
-    const int expert = topk_token(logits + static_cast<size_t>(t) * kExperts, a.indices + t * kTopK,
-                                  a.weights + t * kTopK);
-    if (lane < kTopK) {
-        atomicAdd(&a.ws.counts[expert], 1u);
-        atomicOr(&a.ws.bitmaps[expert * a.ws.words + (t >> 5)], 1u << (t & 31));
-    }
-}
-
-// Histogram + bitmaps from caller-provided indices (standalone bucketing of
-// more than 64 tokens), with validation.
-__global__ __launch_bounds__(256) void bucket_histogram(const int64_t* indices, int tokens, Workspace ws, Plan plan) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= tokens * kTopK) return;
-    const int t = i / kTopK;
-    const int64_t e = indices[i];
-    int32_t bad = 0;
-    if (e < 0 || e >= kExperts) bad |= kStatusBadExpert;
-    for (int q = t * kTopK; q < i; ++q) bad |= (indices[q] == e) ? kStatusRepeatedExpert : 0;
-    if (bad) {
-        atomicOr(plan.status, bad);
-        return;
-    }
-    atomicAdd(&ws.counts[e], 1u);
-    atomicOr(&ws.bitmaps[e * ws.words + (t >> 5)], 1u << (t & 31));
-}
-
-__global__ __launch_bounds__(256) void clear_histogram(Workspace ws, Plan plan) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i == 0) *plan.status = 0;
-    if (i < kExperts) ws.counts[i] = 0;
-    for (int j = i; j < kExperts * ws.words; j += gridDim.x * blockDim.x) ws.bitmaps[j] = 0;
-}
-
-// Single workgroup: pair offsets and unique list from the histogram, and the
-// per-expert exclusive prefix of bitmap popcounts by 32-token word.
-__global__ __launch_bounds__(256) void bucket_scan(Workspace ws, Plan plan) {
-    __shared__ uint32_t scan_scratch[4];
-    const int e = threadIdx.x;
-    const int32_t status = *plan.status;
-    const uint32_t count = status ? 0u : ws.counts[e];
-    uint32_t pairs_total = 0, unique_total = 0;
-    const uint32_t pair_offset = scan256(count, scan_scratch, &pairs_total);
-    const uint32_t rank = scan256(count ? 1u : 0u, scan_scratch, &unique_total);
-    if (count) {
-        plan.expert[rank] = e;
-        plan.offset[rank] = static_cast<int32_t>(pair_offset);
-    }
-    uint32_t running = pair_offset;
-    for (int w = 0; w < ws.words; ++w) {
-        ws.word_prefix[e * ws.words + w] = running;
-        running += __popc(ws.bitmaps[e * ws.words + w]);
-    }
-    if (e == 0) {
-        plan.offset[unique_total] = static_cast<int32_t>(pairs_total);
-        *plan.unique = static_cast<int32_t>(unique_total);
-    }
-}
-
-// One thread per token: place its 8 routes.
-__global__ __launch_bounds__(256) void bucket_fill(const int64_t* indices, int tokens, Workspace ws, Plan plan) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= tokens) return;
-    if (*plan.status) {
-        for (int r = 0; r < kTopK; ++r) plan.route_pair[t * kTopK + r] = -1;
-        return;
-    }
-    int ids[kTopK];
-#pragma unroll
-    for (int r = 0; r < kTopK; ++r) ids[r] = static_cast<int>(indices[t * kTopK + r]);
-    const uint32_t below = (1u << (t & 31)) - 1u;
-#pragma unroll
-    for (int r = 0; r < kTopK; ++r) {
-        const int e = ids[r];
-        const int word = e * ws.words + (t >> 5);
-        const int p = static_cast<int>(ws.word_prefix[word] + __popc(ws.bitmaps[word] & below));
-        plan.pair_token[p] = t;
-        plan.pair_slot[p] = r;
-        int order = 0;
-#pragma unroll
-        for (int q = 0; q < kTopK; ++q) order += (ids[q] < e) ? 1 : 0;
-        plan.route_pair[t * kTopK + order] = p;
-    }
-}
-
 // Standalone bucketing of <= 64 caller-provided tokens in one workgroup.
 __global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan,
                                                            SlotDesc* slots, const int64_t* expert_ptrs,
@@ -583,10 +443,11 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
     }
     const int tiles = (a.tokens + kTokTile - 1) / kTokTile;
     LRMOE_LAUNCH((router_logits<true, 4>), dim3(tiles, kExperts / 16 + 1), dim3(256), 0, stream, ev.start, nullptr, a);
-    hipLaunchKernelGGL(topk_tokens, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, a.ws, a.plan);
-    LRMOE_LAUNCH(bucket_fill, dim3((a.tokens + 255) / 256), dim3(256), 0, stream, nullptr, ev.stop, a.indices,
-                 a.tokens, a.ws, a.plan);
+    const hipError_t err = launch_prefill_plan(a.logits_in != nullptr ? a.logits_in : a.logits, nullptr, nullptr,
+                                               a.indices, a.weights, a.tokens, a.shared_down != nullptr, a.ws, a.plan,
+                                               stream);
+    if (err != hipSuccess) return err;
+    if (ev.stop != nullptr) return hipEventRecord(ev.stop, stream);
     return hipGetLastError();
 }
 
@@ -599,13 +460,8 @@ hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws
                            expert_ptrs, sh_gate, sh_up, sh_down);
         return hipGetLastError();
     }
-    const int clear_blocks = min(64, (kExperts * ws.words + 255) / 256);
-    hipLaunchKernelGGL(clear_histogram, dim3(clear_blocks > 0 ? clear_blocks : 1), dim3(256), 0, stream, ws, plan);
-    hipLaunchKernelGGL(bucket_histogram, dim3((tokens * kTopK + 255) / 256), dim3(256), 0, stream, indices, tokens, ws,
-                       plan);
-    hipLaunchKernelGGL(bucket_scan, dim3(1), dim3(256), 0, stream, ws, plan);
-    hipLaunchKernelGGL(bucket_fill, dim3((tokens + 255) / 256), dim3(256), 0, stream, indices, tokens, ws, plan);
-    return hipGetLastError();
+    return launch_prefill_plan(nullptr, indices, nullptr, nullptr, nullptr, tokens, sh_down != nullptr, ws, plan,
+                               stream);
 }
 
 }  // namespace lrmoe
