@@ -35,14 +35,13 @@ namespace {
 constexpr int kBlkTok = 8;                 // tokens per routing block
 constexpr int kPfThreads = 512;            // expert kernels: 8 waves
 constexpr int kGuTiles = kInner / 64;      // 8 gate/up tiles of 64 rows per expert
-constexpr int kGuChunk = 256;              // k per LDS chunk
+constexpr int kGuChunk = 128;              // k per LDS chunk
 constexpr int kGuChunks = kHidden / kGuChunk;
 constexpr int kGuSteps = kGuChunk / 32;    // MFMA k-steps (and A loads per lane) per chunk
 constexpr int kXsStride = kGuChunk + 8;    // LDS token row stride (bf16)
 constexpr int kDnTiles = kHidden / 128;    // 16 down tiles of 128 rows per expert
 constexpr int kDnTok = 64;                 // act rows per LDS pass
 constexpr int kActStride = kInner + 8;     // LDS act row stride (bf16)
-constexpr int kBlocks = kPassTok / 16;     // MFMA column blocks per unit
 
 // ---- plan ----------------------------------------------------------------------
 
@@ -221,7 +220,84 @@ __device__ __forceinline__ void unit_tile(int b, int tiles, int& unit, int& tile
     tile = within / 8;
 }
 
-__global__ __launch_bounds__(kPfThreads, 1) void pf_gateup(ExpertArgs a) {
+// gate/up workgroup: 4 MFMA waves, each owning two 16-row MFMA tiles (tile r
+// = 8 gate rows and the 8 up rows with the same indices), and 4 loader waves
+// that move the unit's token rows into LDS one chunk ahead.  Each role waits
+// only on its own loads (the memory counter is in order); one barrier per
+// chunk joins them.  A B operand read from LDS feeds both row tiles.
+constexpr int kGuMfmaWaves = 4;
+constexpr int kGuLoadWaves = 4;
+constexpr int kGuThreads = (kGuMfmaWaves + kGuLoadWaves) * kWave;
+constexpr int kGuLoaderThreads = kGuLoadWaves * kWave;
+constexpr int kGuPieces = kPassTok * kGuChunk / 8 / kGuLoaderThreads;  // 16-byte pieces per loader thread per chunk
+constexpr int kGuRing = 8;                                            // k-steps of weights in registers per MFMA wave
+
+// The MFMA waves' K loop for NB 16-token column blocks (blocks past the
+// unit's tokens read rows whose results are dropped), then SwiGLU.
+template <int NB>
+__device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_t* arow1, const uint16_t* xb,
+                                            uint16_t* act0, uint16_t* act1, int count) {
+    f32x4 acc[2][NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[0][b] = acc[1][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Weights stream through a ring of kGuRing k-steps (both tiles), kGuRing-1
+    // k-steps ahead of the MFMAs.
+    uint4 ring[kGuRing][2];
+    auto load_step = [&](int step, uint4* slot) {
+        slot[0] = ldg16(arow0 + 32 * step);
+        slot[1] = ldg16(arow1 + 32 * step);
+    };
+#pragma unroll
+    for (int s = 0; s < kGuRing - 1; ++s) load_step(s, ring[s]);
+    __syncthreads();  // loaders: chunk 0 in LDS
+    constexpr int kSteps = kHidden / 32;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        if (s + kGuRing - 1 < kSteps) load_step(s + kGuRing - 1, ring[(s + kGuRing - 1) % kGuRing]);
+        const int c = s / kGuSteps;
+        const uint16_t* xc = xb + (c & 1) * kPassTok * kXsStride + 32 * (s % kGuSteps);
+        const uint4* ab = ring[s % kGuRing];
+        // All B operands of the k-step are read before its MFMAs, so the LDS
+        // latency is paid once per k-step.
+        uint4 bv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) bv[b] = *reinterpret_cast<const uint4*>(xc + 16 * b * kXsStride);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            acc[0][b] = mfma16x16x32(ab[0], bv[b], acc[0][b]);
+            acc[1][b] = mfma16x16x32(ab[1], bv[b], acc[1][b]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // After a chunk's last k-step its LDS buffer is free; the loaders fill
+        // it with chunk c+2 before the barrier that ends chunk c+1.
+        if (s % kGuSteps == kGuSteps - 1) __syncthreads();
+    }
+    // SwiGLU: lanes g < 2 hold gate rows 4g..4g+3 of a tile's 8, lane + 32 the
+    // up rows with the same index.  act0/act1 point at this lane's first act
+    // element of column 0 for tile 0 and 1 (4 consecutive intermediate rows).
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            f32x4 up;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[r][b][i], 32, kWave);
+            const int col = 16 * b + m;
+            if (g < 2 && col < count) {
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = swiglu_bf16(rbf(acc[r][b][i]), rbf(up[i]));
+                *reinterpret_cast<uint2*>((r ? act1 : act0) + static_cast<size_t>(16 * b) * kInner) =
+                    make_uint2(v[0] | (v[1] << 16), v[2] | (v[3] << 16));
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [2][kPassTok][kXsStride]
     int ui, tile;
     unit_tile(blockIdx.x, kGuTiles, ui, tile);
@@ -230,91 +306,54 @@ __global__ __launch_bounds__(kPfThreads, 1) void pf_gateup(ExpertArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
+
+    if (wave >= kGuMfmaWaves) {
+        // ---- loader waves: token chunk c into LDS buffer c & 1 ----
+        const int lt = tid - kGuMfmaWaves * kWave;       // 0..255
+        const int piece = lt & 15;                       // 16-byte piece of a 256-byte chunk row
+        const uint16_t* xrow[kGuPieces];
+#pragma unroll
+        for (int j = 0; j < kGuPieces; ++j) {
+            const int c = lt / 16 + 16 * j;              // token row of the unit, 0..127
+            const int cc = c < w.count ? c : 0;
+            const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
+            xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
+        }
+        uint4 xr[kGuPieces];
+#pragma unroll
+        for (int c = 0; c < kGuChunks; ++c) {
+#pragma unroll
+            for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j] + c * kGuChunk);
+#pragma unroll
+            for (int j = 0; j < kGuPieces; ++j)
+                *reinterpret_cast<uint4*>(xs + ((c & 1) * kPassTok + lt / 16 + 16 * j) * kXsStride + 8 * piece) = xr[j];
+            // Chunk c is in LDS; buffer c & 1 last held chunk c-2, which the
+            // MFMA waves finished before the previous barrier.
+            __syncthreads();
+        }
+        __syncthreads();  // matches the MFMA waves' last barrier
+        return;
+    }
+
+    // ---- MFMA waves ----
     const int m = lane & 15;
     const int g = lane >> 4;
     const int nblk = (w.count + 15) / 16;
-
-    // This lane's weight row: MFMA row m < 8 is gate row 64*tile + 8*wave + m,
-    // m >= 8 the up row with the same index.
-    const uint16_t* arow = (m < 8 ? w.gate : w.up) + static_cast<size_t>(64 * tile + 8 * wave + (m & 7)) * kHidden + 8 * g;
-    // Token rows staged by this thread: tokens tid/32 + 16j, 16-byte piece tid%32.
-    const int piece = tid & 31;
-    const uint16_t* xrow[kPassTok / 16];
-#pragma unroll
-    for (int j = 0; j < kPassTok / 16; ++j) {
-        const int c = tid / 32 + 16 * j;
-        const int cc = c < w.count ? c : 0;
-        const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
-        xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
-    }
-
-    uint4 abuf[3][kGuSteps];
-    uint4 xr[kPassTok / 16];
-    f32x4 acc[kBlocks];
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    auto load_a = [&](int chunk, uint4* buf) {
-#pragma unroll
-        for (int s = 0; s < kGuSteps; ++s) buf[s] = ldg16(arow + chunk * kGuChunk + 32 * s);
-    };
-    auto load_x = [&](int chunk) {
-#pragma unroll
-        for (int j = 0; j < kPassTok / 16; ++j) xr[j] = ldg16(xrow[j] + chunk * kGuChunk);
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < kPassTok / 16; ++j)
-            *reinterpret_cast<uint4*>(xs + (buf * kPassTok + tid / 32 + 16 * j) * kXsStride + 8 * piece) = xr[j];
-    };
-    auto mfma_chunk = [&](int buf, const uint4* ab) {
-        const uint16_t* xb = xs + (buf * kPassTok + m) * kXsStride + 8 * g;
-#pragma unroll
-        for (int s = 0; s < kGuSteps; ++s) {
-#pragma unroll
-            for (int b = 0; b < kBlocks; ++b) {
-                if (b < nblk) acc[b] = mfma16x16x32(ab[s], *reinterpret_cast<const uint4*>(xb + 16 * b * kXsStride + 32 * s), acc[b]);
-            }
-        }
-    };
-
-    // Prologue: token chunk 0 into LDS; weight chunks 0 and 1 in flight.
-    load_x(0);
-    load_a(0, abuf[0]);
-    load_a(1, abuf[1]);
-    store_x(0);
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < kGuChunks; ++c) {
-        // Next token chunk and the weight chunk after next go out before
-        // this chunk's MFMAs.
-        if (c + 1 < kGuChunks) load_x(c + 1);
-        if (c + 2 < kGuChunks) load_a(c + 2, abuf[(c + 2) % 3]);
-        mfma_chunk(c & 1, abuf[c % 3]);
-        if (c + 1 < kGuChunks) {
-            // Buffer (c+1)&1 held chunk c-1, which every wave finished before
-            // the previous barrier.
-            store_x((c + 1) & 1);
-            __syncthreads();
-        }
-    }
-
-    // SwiGLU: lanes g < 2 hold gate rows 4g..4g+3 of the wave's 8, lane + 32
-    // the up rows with the same index.
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) {
-        if (b >= nblk) break;
-        f32x4 up;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[b][i], 32, kWave);
-        const int col = 16 * b + m;
-        if (g < 2 && col < w.count) {
-            uint32_t act[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(acc[b][i]), rbf(up[i]));
-            uint16_t* dst = a.ws.act + static_cast<size_t>(w.pair0 + col) * kInner + 64 * tile + 8 * wave + 4 * g;
-            *reinterpret_cast<uint2*>(dst) = make_uint2(act[0] | (act[1] << 16), act[2] | (act[3] << 16));
-        }
+    // MFMA row m < 8 of tile r is gate row 64*tile + 16*wave + 8r + m, m >= 8
+    // the up row with the same index.
+    const uint16_t* rows = m < 8 ? w.gate : w.up;
+    const int row0 = 64 * tile + 16 * wave + (m & 7);
+    const uint16_t* arow0 = rows + static_cast<size_t>(row0) * kHidden + 8 * g;
+    const uint16_t* arow1 = rows + static_cast<size_t>(row0 + 8) * kHidden + 8 * g;
+    const uint16_t* xb = xs + m * kXsStride + 8 * g;
+    uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + 64 * tile + 16 * wave + 4 * g;
+    uint16_t* act1 = act0 + 8;
+    if (nblk <= 2) {
+        gateup_mfma<2>(arow0, arow1, xb, act0, act1, w.count);
+    } else if (nblk <= 4) {
+        gateup_mfma<4>(arow0, arow1, xb, act0, act1, w.count);
+    } else {
+        gateup_mfma<8>(arow0, arow1, xb, act0, act1, w.count);
     }
 }
 
@@ -408,7 +447,7 @@ hipError_t launch_prefill_experts(const ExpertArgs& a, hipStream_t stream) {
     }
     const int units = (max_units(a.tokens) + 7) / 8 * 8;
     const StageEvents gate_ev = timing_events(kStageGateUp);
-    LRMOE_LAUNCH(pf_gateup, dim3(units * kGuTiles), dim3(kPfThreads), prefill_gateup_lds(), stream, gate_ev.start,
+    LRMOE_LAUNCH(pf_gateup, dim3(units * kGuTiles), dim3(kGuThreads), prefill_gateup_lds(), stream, gate_ev.start,
                  gate_ev.stop, a);
     const StageEvents down_ev = timing_events(kStageDown);
     LRMOE_LAUNCH(pf_down, dim3(units * kDnTiles), dim3(kPfThreads), prefill_down_lds(), stream, down_ev.start,
