@@ -10,8 +10,10 @@
 //      select, renormalised weights, experts ascending with their token lists,
 //      per token its routes in ascending expert order: fused_experts.py:47-54,
 //      block_experts.py:102-121), so no other kernel or host step is needed;
-//   4. walks its share of one static list of 128 KiB work items, each item's
-//      weights prefetched one item ahead:
+//   4. walks its share of one list of 128 KiB work items, each item's
+//      weights prefetched one item ahead (the first two items of a workgroup
+//      are fixed by its index, later ones are claimed from a counter two
+//      items ahead, so faster workgroups take more of them):
 //        A (slot, 16-row tile): gate and up rows 16i..16i+15 of an expert over
 //          k = 2048 -> SwiGLU with the cpu_experts.c:59-62 rounding points ->
 //          act rows;
@@ -20,20 +22,22 @@
 //      slot 0 is the shared expert, slot s >= 1 the (s-1)-th unique routed
 //      expert; every token routed to an expert is an MFMA column, so each
 //      weight byte is read from HBM once per call;
-//   5. the workgroup that completes the last B item of a 128-row output tile
-//      does the ordered combine of that tile (fused_experts.py:27-37:
-//      ascending expert, acc = bf16(acc + bf16(y * w)) from 0), the
-//      shared-expert add bf16(sg * y_shared) and the residual add.
+//        C (128-row tile), the last 16 items: once every slot's B item of the
+//          tile is done, the ordered combine of that tile (fused_experts.py:
+//          27-37: ascending expert, acc = bf16(acc + bf16(y * w)) from 0),
+//          the shared-expert add bf16(sg * y_shared) and the residual add.
 //
 // Cross-workgroup data (logits, act, y) is written with agent-scope stores
 // and read with agent-scope loads (coherent across the XCDs' L2s), and
 // published by agent-scope counters: per slot the completed A items, per
 // output tile the completed B items.  A B item waits for its slot's 32 A
-// items; items are taken in list order (A before B) by co-resident
-// workgroups, so the earliest unfinished item never waits and the waits end.
-// Every wait is bounded: on timeout the status word gets kStatusTimeout and
-// the kernel still exits.  The last workgroup to finish returns every
-// counter to zero for the next call.
+// items and a C item for its tile's B items, which come earlier in the list.
+// Every workgroup takes its items in increasing list order, all workgroups
+// are co-resident, and a workgroup publishes its finished items before it
+// waits, so the earliest waiting item always has its inputs in progress and
+// the waits end.  Every wait is bounded: on timeout the status word gets
+// kStatusTimeout and the kernel still exits.  Each call uses one of two
+// counter sets (by call parity) and zeroes the other for the next call.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
@@ -51,6 +55,7 @@ constexpr int kXStride = kHidden + 8;         // LDS token row stride (bf16)
 constexpr int kActStride = kInner + 8;        // LDS act row stride (bf16)
 constexpr int kLoads = 16;                    // 16-byte weight loads per lane per item
 constexpr int kReadyTarget = kATiles;         // A items per slot
+constexpr int kCombineItems = kBTiles;        // C items, one per 128-row output tile
 constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
 
 // ---- agent-scope memory operations (coherent across XCDs) -------------------
@@ -92,6 +97,29 @@ __device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
 }
 __device__ __forceinline__ uint32_t add_agent32(void* p, uint32_t v) {
     return __hip_atomic_fetch_add(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Claims a work item: one agent-scope fetch-add by the lanes in `lanes`
+// (wave-uniform: 1 = lane 0 in the claiming wave, 0 in the others), written
+// as assembly so that no wait is tied to it.  The result is
+// valid in lane 0 once the caller's "s_waitcnt vmcnt(16)" after the next
+// prefetch has passed (returning atomics count in vmcnt, in order).
+__device__ __forceinline__ uint32_t claim_async(uint32_t* counter, uint32_t lanes) {
+    uint32_t old;
+    uint64_t saved_exec;
+    uint32_t mask;
+    asm volatile(
+        "v_readfirstlane_b32 %2, %6\n\t"
+        "s_nop 4\n\t"
+        "s_mov_b64 %1, exec\n\t"
+        "s_mov_b32 exec_lo, %2\n\t"
+        "s_mov_b32 exec_hi, 0\n\t"
+        "global_atomic_add %0, %3, %4, %5 sc0\n\t"
+        "s_mov_b64 exec, %1"
+        : "=&v"(old), "=&s"(saved_exec), "=&s"(mask)
+        : "v"(0u), "v"(1u), "s"(counter), "v"(lanes)
+        : "memory");
+    return old;
 }
 
 __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
@@ -137,7 +165,7 @@ struct Plan {
     int32_t n_slots;                  // active slots (shared + unique routed)
     int32_t first_slot;               // 0 with a shared expert, else 1
     int32_t status;
-    int32_t last;
+    int32_t claim[2];                 // claimed item index, by step parity
 };
 
 // Dot of a lane's 32 contiguous elements (4 x 16 bytes) with the same
@@ -159,7 +187,7 @@ __device__ __forceinline__ float lane_dot32(const uint4* w, const uint16_t* row,
 // ---- item geometry ------------------------------------------------------------
 
 struct Item {
-    int kind;   // 0 = A (gate/up), 1 = B (down), -1 = none
+    int kind;   // 0 = A (gate/up), 1 = B (down), 2 = C (combine), -1 = none
     int slot;
     int tile;
 };
@@ -167,10 +195,14 @@ struct Item {
 __device__ __forceinline__ Item item_at(int k, int total, int n_slots, int first_slot) {
     Item it;
     const int n_a = kATiles * n_slots;
-    if (k >= total) {
+    if (k >= total + kCombineItems || n_slots == 0) {
         it.kind = -1;
         it.slot = first_slot;
         it.tile = 0;
+    } else if (k >= total) {
+        it.kind = 2;
+        it.slot = first_slot;
+        it.tile = k - total;
     } else if (k < n_a) {
         it.kind = 0;
         it.slot = first_slot + k / kATiles;
@@ -187,8 +219,7 @@ __device__ __forceinline__ Item item_at(int k, int total, int n_slots, int first
 // Address of this lane's first 16-byte weight load of an item; the item's 16
 // loads are at +32 elements each.  A: MFMA row m < 8 is gate row
 // 16*tile + 8*(wave/4) + m, m >= 8 the up row with the same index; k starts at
-// 512*(wave%4).  B: output row 128*tile + 16*wave + m over k = 512.  A
-// "none" item re-reads the slot's first A tile (in cache; results unused).
+// 512*(wave%4).  B: output row 128*tile + 16*wave + m over k = 512.
 __device__ __forceinline__ const uint16_t* item_base(const SlotInfo& s, const Item& it, int wave, int lane) {
     const int m = lane & 15;
     const int g = lane >> 4;
@@ -206,8 +237,8 @@ __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
 
 // Ordered combine of output rows [128*tile, +128) of every token (512
 // threads: token tid/32, rows 4*(tid%32)..+3), then the shared-expert and
-// residual adds; resets the tile's counter for the next call.
-__device__ __forceinline__ void combine_tile(const DecodeArgs& a, const Plan& P, DecodeSync* sync, int tile, int T, bool shared) {
+// residual adds.
+__device__ __forceinline__ void combine_tile(const DecodeArgs& a, const Plan& P, int tile, int T, bool shared) {
     const int tid = threadIdx.x;
     const int t = tid >> 5;
     const int h = kBRows * tile + (tid & 31) * 4;
@@ -236,7 +267,6 @@ __device__ __forceinline__ void combine_tile(const DecodeArgs& a, const Plan& P,
         for (int i = 0; i < 4; ++i) o[i] = f2bf(acc[i]);
         *reinterpret_cast<uint64_t*>(a.out + static_cast<size_t>(t) * kHidden + h) = pack4(o);
     }
-    if (tid == 0) st_agent32(&sync->tile_done[tile * kSyncStride], 0u);
 }
 
 __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
@@ -254,6 +284,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
     DecodeSync* sync = a.sync;
+    // The call's parity, from the count of finished workgroups (DecodeSync).
+    const uint32_t arrivals = ld_agent32(&sync->arrivals);
 
     // ---- 1. every load that depends on nothing, issued first ----
     // In order of need: the caller's logits rows of this wave's tokens
@@ -290,6 +322,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
     if (tid < kExperts) P.tokmask[tid] = 0u;
     if (tid == 0) P.status = 0;
+    const int parity = arrivals >= static_cast<uint32_t>(G) ? 1 : 0;
+    DecodeCounters* const cnt = &sync->set[parity];
+    if (blockIdx.x == 0) {
+        // The next call's counters (this call never touches them).
+        DecodeCounters* const nxt = &sync->set[parity ^ 1];
+        if (tid < kDecodeSlots) st_agent32(&nxt->ready[tid * kSyncStride], 0u);
+        if (tid >= kExperts && tid < kExperts + kCombineItems) st_agent32(&nxt->tile_done[(tid - kExperts) * kSyncStride], 0u);
+        if (tid == kThreads - 1) st_agent32(&nxt->router_done, 0u);
+        if (tid == kThreads - 2) st_agent32(&nxt->claim, 0u);
+    }
     __syncthreads();
 
     // Token rows (normalised when the layer norms) into LDS, and the
@@ -349,13 +391,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (tid == 0) add_agent32(&sync->router_done, 1u);
+            if (tid == 0) add_agent32(&cnt->router_done, 1u);
         }
     }
 
     // ---- 4. the route plan ----
     if (a.router != nullptr) {
-        if (tid == 0 && !wait_counter(&sync->router_done, kRouterWgs)) P.status |= kStatusTimeout;
+        if (tid == 0 && !wait_counter(&cnt->router_done, kRouterWgs)) P.status |= kStatusTimeout;
         __syncthreads();
         if (has_lo) lg_lo = ld_agent64(a.logits + static_cast<size_t>(t_lo) * kExperts + 4 * lane);
         if (has_hi) lg_hi = ld_agent64(a.logits + static_cast<size_t>(t_hi) * kExperts + 4 * lane);
@@ -472,7 +514,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
 
     const int n_slots = P.n_slots;
     const int first_slot = P.first_slot;
-    const int total = (kATiles + kBTiles) * n_slots;
+    const int total = (kATiles + kBTiles) * n_slots;          // A and B items
+    const int end = n_slots > 0 ? total + kCombineItems : 0;  // and the C items
     const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
 
     // Bad routes: the output is the residual (or zeros); no expert runs.
@@ -487,50 +530,59 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
 
     // ---- 4. work items ----
-    int k = (static_cast<int>(blockIdx.x) - offset + G) % G;
     uint4 b0[kLoads], b1[kLoads];
     uint64_t stg[4];
     const uint32_t stg_off = static_cast<uint32_t>((tid >> 5) * kInner * 2 + (tid & 31) * 32);
-    uint32_t poll = 0;        // ready count of the current item's slot (read one item ahead)
-    int sig_kind = -1;        // item whose completion is signalled next iteration
+    // Prefetch target of an item without weights (C items): 1 KiB of token
+    // row 0, in cache after the first read.
+    const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
+    // Lanes of the claiming atomic: lane 0 of wave 0.
+    const uint32_t claim_lanes = wave == 0 ? 1u : 0u;
+    uint32_t poll = 0;        // counter of the current item's dependency (read one item ahead)
+    int sig_kind = -1;        // item whose completion is signalled next step
     int sig_slot = 0, sig_tile = 0;
-    int par = 0;
+    int par = 0;              // A partial-sum buffer
+    int cpar = 0;             // claim buffer
 
     auto issue = [&](const uint16_t* p, uint4* buf) {
 #pragma unroll
         for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
     };
+    auto weights_of = [&](const Item& it) -> const uint16_t* {
+        return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
+    };
 
-    // Runs one item whose weights are in buf; the next item's prefetch goes
-    // into nbuf.  Returns the next item index.
-    auto step = [&](int kk, uint4* buf, uint4* nbuf) {
+    // Runs item kk, whose weights are in buf, and prefetches item kn into
+    // nbuf.  Returns the item claimed for the step after next.
+    auto step = [&](int kk, int kn, uint4* buf, uint4* nbuf) -> int {
         const Item it = item_at(kk, total, n_slots, first_slot);
-        const Item nx = item_at(kk + G, total, n_slots, first_slot);
+        const Item nx = item_at(kn, total, n_slots, first_slot);
         const SlotInfo& s = P.slot[it.slot];
-        // Next item's first weight address (a "none" item re-reads this one).
-        const uint16_t* np = nx.kind >= 0 ? item_base(P.slot[nx.slot], nx, wave, lane) : item_base(s, it, wave, lane);
+        const uint16_t* np = weights_of(nx);
         auto signal_previous = [&]() {
             if (tid == 0) {
-                if (sig_kind == 0) add_agent32(&sync->ready[sig_slot * kSyncStride], 1u);
-                if (sig_kind == 1) add_agent32(&sync->tile_done[sig_tile * kSyncStride], 1u);
+                if (sig_kind == 0) add_agent32(&cnt->ready[sig_slot * kSyncStride], 1u);
+                if (sig_kind == 1) add_agent32(&cnt->tile_done[sig_tile * kSyncStride], 1u);
             }
             sig_kind = -1;
         };
-        // (a) The slot's act rows must be complete before a B item stages
-        //     them.  Before waiting, the workgroup publishes its own previous
-        //     item: a completed item is never held back by a wait, so two
-        //     workgroups cannot wait on each other.
-        if (it.kind == 1 && __syncthreads_or(poll < kReadyTarget)) {
+        // (a) A B item needs its slot's act rows, a C item every slot's y
+        //     rows of its tile.  Before waiting, the workgroup publishes its
+        //     own previous item: a completed item is never held back by a
+        //     wait, so two workgroups cannot wait on each other.
+        const uint32_t need = it.kind == 1 ? static_cast<uint32_t>(kReadyTarget) : static_cast<uint32_t>(n_slots);
+        if (it.kind >= 1 && __syncthreads_or(poll < need)) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             signal_previous();
-            if (tid == 0 && !wait_counter(&sync->ready[it.slot * kSyncStride], kReadyTarget)) P.status |= kStatusTimeout;
+            const uint32_t* c = it.kind == 1 ? &cnt->ready[it.slot * kSyncStride] : &cnt->tile_done[it.tile * kSyncStride];
+            if (tid == 0 && !wait_counter(c, need)) P.status |= kStatusTimeout;
             __syncthreads();
         }
-        // (b) staging loads (B), then the poll for the next item, then its
-        //     weights: a wait for everything but the newest 16 loads covers
-        //     this item's weights, staging and poll and the previous item's
-        //     stores and signal.
+        // (b) staging loads (B), the poll for the next item, the claim of the
+        //     item after it, then the next item's weights: a wait for
+        //     everything but the newest 16 loads covers this item's weights,
+        //     staging, poll and claim and the previous item's stores.
         if (it.kind == 1) {
             // Uniform base + loop-invariant lane offset: rows past the slot's
             // count read the act buffer's padding (never used as columns).
@@ -538,14 +590,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             const char* base = reinterpret_cast<const char*>(a.act) + static_cast<size_t>(pair0) * kInner * 2;
             ld_agent64x4_async(stg, base, stg_off);
         }
-        const uint32_t* poll_addr = nx.kind == 1 ? &sync->ready[nx.slot * kSyncStride] : &sync->router_done;
+        const uint32_t* poll_addr = nx.kind == 1 ? &cnt->ready[nx.slot * kSyncStride]
+                                  : nx.kind == 2 ? &cnt->tile_done[nx.tile * kSyncStride]
+                                                 : &cnt->router_done;
         uint32_t next_poll = ld_agent32(poll_addr);
+        const uint32_t claimed = claim_async(&cnt->claim, claim_lanes);
         __builtin_amdgcn_sched_barrier(0);
         issue(np, nbuf);
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + 2 * G;
         // (c) Otherwise the previous item is signalled after this item's
-        //     first barrier: every wave has passed the wait above, so all of
+        //     first barrier: every wave is past the wait above, so all of
         //     that item's stores are complete.
         if (it.kind == 1) {
             // Every wave is past the previous item's reads of act_lds.
@@ -587,7 +644,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                 }
             }
             par ^= 1;
-        } else {
+        } else if (it.kind == 1) {
             const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -602,69 +659,56 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                 for (int i = 0; i < 4; ++i) o[i] = f2bf(y[i]);
                 st_agent64(a.y + static_cast<size_t>(s.pair0 + m) * kHidden + kBRows * it.tile + 16 * wave + 4 * g, pack4(o));
             }
+        } else {
+            signal_previous();
+            combine_tile(a, P, it.tile, T, first_slot == 0);
+            // Wave 0's claim above is visible to every wave after this.
+            __syncthreads();
         }
-        sig_kind = it.kind;
+        const int after = P.claim[cpar];
+        cpar ^= 1;
+        sig_kind = it.kind <= 1 ? it.kind : -1;
         sig_slot = it.slot;
         sig_tile = it.tile;
         poll = next_poll;
-        return kk + G;
+        return after;
     };
 
-    if (k < total) {
-        const Item first = item_at(k, total, n_slots, first_slot);
-        issue(item_base(P.slot[first.slot], first, wave, lane), b0);
-        poll = 0u;  // a first B item checks its slot in the bounded wait
+    // The first two items of a workgroup are fixed; the rest are claimed.
+    int cur = (static_cast<int>(blockIdx.x) - offset + G) % G;
+    if (cur < end) {
+        int nxt = cur + G;
+        issue(weights_of(item_at(cur, total, n_slots, first_slot)), b0);
+        poll = 0u;  // a first B or C item checks its counter in the bounded wait
         if (a.router == nullptr) {
             // Token rows staged while the first weights stream in.
             stage_rows();
             __syncthreads();
         }
         while (true) {
-            k = step(k, b0, b1);
-            if (k >= total) break;
-            k = step(k, b1, b0);
-            if (k >= total) break;
+            int after = step(cur, nxt, b0, b1);
+            cur = nxt;
+            nxt = after;
+            if (cur >= end) break;
+            after = step(cur, nxt, b1, b0);
+            cur = nxt;
+            nxt = after;
+            if (cur >= end) break;
         }
-        // Flush: the last item's stores, then its signal; the workgroup whose
-        // last item is the final slot's B item of a tile (always among the
-        // last 16 items, so always a workgroup's last item) combines that
-        // tile once the other slots' B items of the tile are done.
+        // Flush: the last item's stores, then its signal.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        const bool combiner = sig_kind == 1 && sig_slot == first_slot + n_slots - 1;
         if (tid == 0) {
-            if (sig_kind == 0) add_agent32(&sync->ready[sig_slot * kSyncStride], 1u);
-            if (sig_kind == 1 && !combiner) add_agent32(&sync->tile_done[sig_tile * kSyncStride], 1u);
-            if (combiner && !wait_counter(&sync->tile_done[sig_tile * kSyncStride], static_cast<uint32_t>(n_slots - 1)))
-                P.status |= kStatusTimeout;
-        }
-        if (combiner) {
-            __syncthreads();
-            combine_tile(a, P, sync, sig_tile, T, first_slot == 0);
+            if (sig_kind == 0) add_agent32(&cnt->ready[sig_slot * kSyncStride], 1u);
+            if (sig_kind == 1) add_agent32(&cnt->tile_done[sig_tile * kSyncStride], 1u);
         }
     }
 
-    // ---- 5. the last workgroup to finish resets the counters ----
-    __builtin_amdgcn_s_waitcnt(0);
+    // ---- 5. this workgroup is finished ----
     __syncthreads();
     if (tid == 0) {
         if (P.status & kStatusTimeout) atomicOr(a.status, kStatusTimeout);
-        const int bucket = blockIdx.x % 8;
-        const int in_bucket = (G - bucket + 7) / 8;
-        int last = 0;
-        if (add_agent32(&sync->xcd_done[bucket * kSyncStride], 1u) == static_cast<uint32_t>(in_bucket - 1)) {
-            last = add_agent32(&sync->all_done, 1u) == static_cast<uint32_t>(min(G, 8) - 1);
-        }
-        P.last = last;
-    }
-    __syncthreads();
-    if (P.last) {
-        for (int i = tid; i < kDecodeSlots; i += kThreads) st_agent32(&sync->ready[i * kSyncStride], 0u);
-        if (tid < 8) st_agent32(&sync->xcd_done[tid * kSyncStride], 0u);
-        if (tid == 0) {
-            st_agent32(&sync->router_done, 0u);
-            st_agent32(&sync->all_done, 0u);
-        }
+        __builtin_amdgcn_atomic_inc32(&sync->arrivals, static_cast<uint32_t>(2 * G - 1), __ATOMIC_RELAXED, "agent");
     }
 }
 

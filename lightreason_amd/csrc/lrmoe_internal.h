@@ -20,19 +20,29 @@ constexpr int32_t kStatusTimeout = 8;       // a bounded cross-workgroup wait ex
 // Decode layer (one persistent kernel) limits.
 constexpr int kDecodeMaxTokens = 16;
 constexpr int kDecodeSlots = 8 * kDecodeMaxTokens + 1;  // unique routed experts + the shared expert
-constexpr int kSyncStride = 64;
-constexpr int kPassTok = 128;    // prefill: tokens of one expert per work unit  // counters 256 bytes apart (separate memory channels)
+constexpr int kSyncStride = 64;  // counters 256 bytes apart (separate memory channels)
+constexpr int kPassTok = 128;    // prefill: tokens of one expert per work unit
 
-// Cross-workgroup counters of the decode kernel.  Zero between calls: the
-// kernel's last workgroup (or a tile's combining workgroup) restores them.
-struct DecodeSync {
-    uint32_t router_done;               // router workgroups finished
+// Cross-workgroup counters of one decode call.
+struct DecodeCounters {
+    uint32_t router_done;                        // router workgroups finished
     uint32_t pad0[kSyncStride - 1];
-    uint32_t all_done;                  // XCD buckets finished
+    uint32_t claim;                              // work items handed out past the first two rounds
     uint32_t pad1[kSyncStride - 1];
-    uint32_t xcd_done[8 * kSyncStride];   // workgroups finished per blockIdx % 8
     uint32_t ready[kDecodeSlots * kSyncStride];  // A items finished per slot
-    uint32_t tile_done[16 * kSyncStride];  // B items finished per 128-row output tile
+    uint32_t tile_done[16 * kSyncStride];        // B items finished per 128-row output tile
+};
+
+// Decode kernel synchronisation.  `arrivals` counts finished workgroups
+// modulo 2G (G = grid size, fixed per device), so a call reads the parity of
+// its call number as arrivals >= G: at most G - 1 of its own workgroups can
+// have finished before any of them reads it.  Call parity p uses set[p] and
+// zeroes set[p ^ 1] for the next call, so nothing is reset at the end of a
+// call and a zero-initialised workspace is valid.
+struct DecodeSync {
+    uint32_t arrivals;
+    uint32_t pad0[kSyncStride - 1];
+    DecodeCounters set[2];
 };
 
 // Control block at the start of every workspace.  The route counter is reset
