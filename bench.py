@@ -167,7 +167,7 @@ def kernel_time(case: Case, stage: int, passes: int) -> tuple[float, int]:
 def measured_traffic(kernel: str) -> dict | None:
     """HBM bytes per dispatch of ``kernel`` from the committed rocprofv3 --pmc
     summary (FETCH_SIZE and WRITE_SIZE passes, scaled by a 256 MiB copy)."""
-    path = ROOT / "profiles" / "c2_t8_zipf_hbm_traffic.md"
+    path = ROOT / "profiles" / "moe_decode_t8_zipf_hbm_traffic.md"
     if not path.exists():
         return None
     text = path.read_text()

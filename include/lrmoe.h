@@ -13,7 +13,8 @@
  *   - the library never allocates: scratch comes from a caller-provided
  *     `workspace` of at least lrmoe_workspace_bytes(tokens) bytes, zeroed once
  *     by the caller after allocation (its counters reset themselves), and used
- *     by one stream at a time;
+ *     on one device by one stream at a time (calls that overlap on one
+ *     workspace race);
  *   - route problems found on the device (an expert id outside [0, 256) or a
  *     token routed twice to one expert) set bits in the int32 status word at
  *     byte offset LRMOE_WS_STATUS_OFFSET of the workspace; the affected call

@@ -186,9 +186,6 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
     r.indices = indices_out ? indices_out : ws.indices;
     r.weights = weights_out ? weights_out : ws.weights;
     r.sg = ws.sg;
-    r.expert_ptrs = expert_ptrs;
-    r.shared_gate_proj = shared_gate_proj;
-    r.shared_up_proj = shared_up_proj;
     r.shared_down = shared_down_proj;
     r.plan = ws.plan;
     r.ws = ws;

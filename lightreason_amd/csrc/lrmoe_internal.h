@@ -69,22 +69,6 @@ struct Plan {
     int32_t* status;      // [1] (in the control block)
 };
 
-// Per expert slot of a decode call (slot 0 = shared expert, slot s >= 1 =
-// unique routed expert s - 1): everything a wave needs in one 64-byte record,
-// so an expert tile starts streaming after a single (scalar) load.
-struct SlotDesc {
-    const uint16_t* gate_up;  // [1024][2048]: gate rows 0-511, up rows 512-1023
-    const uint16_t* up;       // up rows (gate_up + 512*2048 for routed experts)
-    const uint16_t* down;     // [2048][512]
-    int32_t pair0;            // first act/y row of the slot
-    int32_t count;            // tokens (B columns) of the slot, <= 16
-    uint8_t tokens[16];       // token of each column
-    int32_t valid;            // 0 for an unused slot (no shared expert)
-    int32_t pad[3];
-};
-static_assert(sizeof(SlotDesc) == 64, "one 64-byte record per slot");
-constexpr int kMaxSlots = 257;
-
 // Carves one caller-provided device buffer into the per-call arrays.  The
 // layout depends only on `tokens`, so any buffer of at least
 // workspace_bytes(tokens) serves a call with that many tokens.
@@ -98,17 +82,13 @@ struct Workspace {
     Plan plan;
     uint16_t* act;        // [8T + T + 16][512]: routed pairs, shared rows, padding
     uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
-    uint32_t* counts;     // [256] prefill histogram
-    uint32_t* bitmaps;    // [256][words] prefill token bitmaps
-    uint32_t* word_prefix;  // [256][words]
-    SlotDesc* slots;      // [257] decode slot records
+    uint32_t* counts;     // [256] prefill: pairs per expert
     DecodeSync* sync;     // decode kernel counters
     uint8_t* bmask;       // prefill: [256][nblk_pad] token masks per 8-token block
     uint32_t* blk_base;   // prefill: [256][nblk_pad] pairs of the expert before the block
     int32_t* bstatus;     // prefill: [nblk] route status per block
     int2* units;          // prefill: (slot, first pair) work units
     int nblk_pad;
-    int words;
     size_t bytes;
 };
 
@@ -118,7 +98,6 @@ inline Workspace carve(void* base, int tokens) {
     Workspace ws{};
     const size_t T = static_cast<size_t>(tokens > 0 ? tokens : 1);
     const size_t P = 8 * T;
-    const int words = static_cast<int>((T + 31) / 32);
     size_t offset = 0;
     auto take = [&](size_t bytes) {
         const size_t at = offset;
@@ -143,9 +122,6 @@ inline Workspace carve(void* base, int tokens) {
     ws.act = reinterpret_cast<uint16_t*>(take((P + T + 16) * 512 * 2));
     ws.y = reinterpret_cast<uint16_t*>(take((P + T) * 2048 * 2));
     ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
-    ws.bitmaps = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
-    ws.word_prefix = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(256) * words * 4));
-    ws.slots = reinterpret_cast<SlotDesc*>(take(sizeof(SlotDesc) * kMaxSlots));
     const size_t nblk = (T + 7) / 8;
     const size_t nblk_pad = (nblk + 15) / 16 * 16;
     ws.nblk_pad = static_cast<int>(nblk_pad);
@@ -154,7 +130,6 @@ inline Workspace carve(void* base, int tokens) {
     ws.bstatus = reinterpret_cast<int32_t*>(take(nblk * 4));
     const size_t units = (T + kPassTok - 1) / kPassTok + 256 + (8 * T + kPassTok - 1) / kPassTok + 8;
     ws.units = reinterpret_cast<int2*>(take(units * sizeof(int2)));
-    ws.words = words;
     ws.plan.unique = &ws.control->unique;
     ws.plan.status = &ws.control->status;
     ws.bytes = offset;
@@ -177,11 +152,7 @@ struct RouteArgs {
     int64_t* indices;             // [T][8]
     uint16_t* weights;            // [T][8]
     uint16_t* sg;                 // [T]
-    // Decode slot records are built when expert_ptrs is given.
-    const int64_t* expert_ptrs;   // [256][2] or null
-    const uint16_t* shared_gate_proj;  // shared expert (all three or none)
-    const uint16_t* shared_up_proj;
-    const uint16_t* shared_down;
+    const uint16_t* shared_down;  // shared expert present (prefill work units) when non-null
     Plan plan;
     Workspace ws;
 };
@@ -265,9 +236,7 @@ StageEvents timing_events(int stage);
     } while (0)
 
 hipError_t launch_route(const RouteArgs& args, hipStream_t stream);
-hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream,
-                         const int64_t* expert_ptrs = nullptr, const uint16_t* shared_gate_proj = nullptr,
-                         const uint16_t* shared_up_proj = nullptr, const uint16_t* shared_down = nullptr);
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream);
 hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                          const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
                          int max_copies, int stripes, int threads, int keep_in_l2, int32_t* status,

@@ -102,42 +102,11 @@ __device__ uint32_t scan256(uint32_t value, uint32_t* scratch, uint32_t* total) 
     return threadIdx.x < kExperts ? before + inclusive - value : 0u;
 }
 
-// Writes one decode slot record with vector stores.  `mask` has a bit per
-// token (<= 16) of the slot; its set bits in ascending order are the columns.
-__device__ void store_slot(SlotDesc* dst, const uint16_t* gate_up, const uint16_t* up, const uint16_t* down, int pair0,
-                           int count, uint32_t mask, int valid) {
-    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        if ((mask >> t) & 1u) {
-            const int pos = __popc(mask & ((1u << t) - 1u));
-            const uint32_t v = static_cast<uint32_t>(t) << (8 * (pos & 3));
-            w0 |= pos < 4 ? v : 0u;
-            w1 |= (pos >= 4 && pos < 8) ? v : 0u;
-            w2 |= (pos >= 8 && pos < 12) ? v : 0u;
-            w3 |= pos >= 12 ? v : 0u;
-        }
-    }
-    const uint64_t g = reinterpret_cast<uint64_t>(gate_up);
-    const uint64_t u = reinterpret_cast<uint64_t>(up);
-    const uint64_t d = reinterpret_cast<uint64_t>(down);
-    uint4* out = reinterpret_cast<uint4*>(dst);
-    out[0] = make_uint4(static_cast<uint32_t>(g), static_cast<uint32_t>(g >> 32), static_cast<uint32_t>(u),
-                        static_cast<uint32_t>(u >> 32));
-    out[1] = make_uint4(static_cast<uint32_t>(d), static_cast<uint32_t>(d >> 32), static_cast<uint32_t>(pair0),
-                        static_cast<uint32_t>(count));
-    out[2] = make_uint4(w0, w1, w2, w3);
-    out[3] = make_uint4(static_cast<uint32_t>(valid), 0u, 0u, 0u);
-}
-
 // Bucket <= 64 tokens held in LDS (ids[t*8 + r], already validated) with one
 // 256-thread workgroup: a token bitmap per expert (one LDS atomic per route),
 // a block scan for pair offsets and unique ranks, then every route places
-// itself in O(1).  With expert_ptrs (and tokens <= 16) also writes the decode
-// slot records, slot 0 being the shared expert.
-__device__ void build_plan_small(const int32_t* ids, int tokens, const Plan& plan, SlotDesc* slots,
-                                 const int64_t* expert_ptrs, const uint16_t* sh_gate, const uint16_t* sh_up,
-                                 const uint16_t* sh_down) {
+// itself in O(1).
+__device__ void build_plan_small(const int32_t* ids, int tokens, const Plan& plan) {
     __shared__ unsigned long long tokmask[kExperts];
     __shared__ uint32_t poff[kExperts];
     __shared__ uint32_t scan_scratch[4];
@@ -156,7 +125,6 @@ __device__ void build_plan_small(const int32_t* ids, int tokens, const Plan& pla
     const uint32_t pairs_total = packed_total & 0xffffu;
     const uint32_t unique_total = packed_total >> 16;
     if (e < kExperts) poff[e] = pair_offset;
-    const bool describe = slots != nullptr && expert_ptrs != nullptr && tokens <= 16;
     if (count) {
         plan.expert[rank] = e;
         plan.offset[rank] = static_cast<int32_t>(pair_offset);
@@ -166,20 +134,10 @@ __device__ void build_plan_small(const int32_t* ids, int tokens, const Plan& pla
             m &= m - 1ull;
             plan.pair_token[pair_offset + j] = t;
         }
-        if (describe) {
-            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(expert_ptrs[2 * e]);
-            store_slot(slots + rank + 1, gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
-                       reinterpret_cast<const uint16_t*>(expert_ptrs[2 * e + 1]), static_cast<int>(pair_offset),
-                       static_cast<int>(count), static_cast<uint32_t>(mask), 1);
-        }
     }
     if (e == 0) {
         plan.offset[unique_total] = static_cast<int32_t>(pairs_total);
         *plan.unique = static_cast<int32_t>(unique_total);
-        if (describe) {
-            const uint32_t all = tokens >= 32 ? 0xffffffffu : ((1u << tokens) - 1u);
-            store_slot(slots, sh_gate, sh_up, sh_down, kTopK * tokens, tokens, all, sh_down != nullptr ? 1 : 0);
-        }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
@@ -226,8 +184,6 @@ __global__ __launch_bounds__(256) void router_logits(RouteArgs a) {
     constexpr int kRowGroups = kExperts / (4 * RPW);
 
     if (PREFILL && blockIdx.x == 0 && blockIdx.y == 0) {
-        for (int i = threadIdx.x; i < kExperts; i += blockDim.x) a.ws.counts[i] = 0;
-        for (int i = threadIdx.x; i < kExperts * a.ws.words; i += blockDim.x) a.ws.bitmaps[i] = 0;
         if (threadIdx.x == 0) *a.plan.status = 0;
     }
 
@@ -394,16 +350,12 @@ __global__ __launch_bounds__(1024) void topk_bucket_small(RouteArgs a) {
         }
     }
     __syncthreads();
-    build_plan_small(ids, a.tokens, a.plan, a.ws.slots, a.expert_ptrs, a.shared_gate_proj, a.shared_up_proj,
-                     a.shared_down);
+    build_plan_small(ids, a.tokens, a.plan);
     if (threadIdx.x == 0) *a.plan.status = 0;
 }
 
 // Standalone bucketing of <= 64 caller-provided tokens in one workgroup.
-__global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan,
-                                                           SlotDesc* slots, const int64_t* expert_ptrs,
-                                                           const uint16_t* sh_gate, const uint16_t* sh_up,
-                                                           const uint16_t* sh_down) {
+__global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indices, int tokens, Plan plan) {
     __shared__ int32_t ids[64 * kTopK];
     for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) {
         const int64_t e = indices[i];
@@ -420,7 +372,7 @@ __global__ __launch_bounds__(256) void bucket_small_kernel(const int64_t* indice
         for (int i = threadIdx.x; i < tokens * kTopK; i += blockDim.x) plan.route_pair[i] = -1;
         return;
     }
-    build_plan_small(ids, tokens, plan, slots, expert_ptrs, sh_gate, sh_up, sh_down);
+    build_plan_small(ids, tokens, plan);
     if (threadIdx.x == 0) *plan.status = 0;
 }
 
@@ -451,17 +403,13 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream,
-                         const int64_t* expert_ptrs, const uint16_t* sh_gate, const uint16_t* sh_up,
-                         const uint16_t* sh_down) {
+hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream) {
     if (tokens <= 0) return hipSuccess;
     if (tokens <= 64) {
-        hipLaunchKernelGGL(bucket_small_kernel, dim3(1), dim3(256), 0, stream, indices, tokens, plan, ws.slots,
-                           expert_ptrs, sh_gate, sh_up, sh_down);
+        hipLaunchKernelGGL(bucket_small_kernel, dim3(1), dim3(256), 0, stream, indices, tokens, plan);
         return hipGetLastError();
     }
-    return launch_prefill_plan(nullptr, indices, nullptr, nullptr, nullptr, tokens, sh_down != nullptr, ws, plan,
-                               stream);
+    return launch_prefill_plan(nullptr, indices, nullptr, nullptr, nullptr, tokens, false, ws, plan, stream);
 }
 
 }  // namespace lrmoe
