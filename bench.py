@@ -79,6 +79,40 @@ def timed_replays(graph, replays: int) -> float:
     return start.elapsed_time(stop)
 
 
+def replay_percentiles(graph, replays: int, layers: int) -> dict:
+    """p10/p50/p90 of the per-layer time over single replays, each bracketed
+    by its own events (a separate pass from the timed one)."""
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    torch.cuda.synchronize()
+    for start, stop in events:
+        start.record()
+        graph.replay()
+        stop.record()
+    torch.cuda.synchronize()
+    us = np.array([start.elapsed_time(stop) * 1e3 / layers for start, stop in events])
+    return {f"p{q}": round(float(np.percentile(us, q)), 2) for q in (10, 50, 90)}
+
+
+def copy_peak_gbs(device, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Achievable HBM bandwidth of a plain device copy (read + write bytes
+    per second, best of `reps`), to report fractions against a measured peak
+    beside the spec one."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        dst.copy_(src)
+        stop.record()
+        torch.cuda.synchronize()
+        best = min(best, start.elapsed_time(stop))
+    del src, dst
+    return 2 * nbytes / (best * 1e-3) / 1e9
+
+
 def capture(fn):
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -144,12 +178,16 @@ class GatherCase:
                    max_copies=self.max_copies, experts=256, stripes=48)
 
 
-def bench_case(case: Case, replays: int, warmup: int) -> float:
-    """Milliseconds per graph replay (one pass over the case's layers)."""
+def bench_case(case: Case, replays: int, warmup: int, spread: dict | None = None) -> float:
+    """Milliseconds per graph replay (one pass over the case's layers).  With
+    `spread`, also fills it with per-layer percentiles from a separate pass."""
     graph = capture(case.run)
     for _ in range(warmup):
         graph.replay()
-    return timed_replays(graph, replays) / replays
+    ms = timed_replays(graph, replays) / replays
+    if spread is not None:
+        spread.update(replay_percentiles(graph, max(replays, 10), len(case.layers)))
+    return ms
 
 
 def kernel_time(case: Case, stage: int, passes: int) -> tuple[float, int]:
@@ -319,11 +357,13 @@ def main() -> int:
     logits = [bf16_from_f64(zipf_logits(8, args.seed * 1000 + l), device) for l in range(L)]
     c2 = Case(model, 8, logits=logits)
     uniques = c2.unique_counts()
-    ms = bench_case(c2, replays, warm)
+    spread = {}
+    ms = bench_case(c2, replays, warm, spread)
     ms_step = ms / L
     bytes_step = (np.mean(uniques) * EXPERT_BYTES + SHARED_BYTES)
     gbs = bytes_step / (ms_step * 1e-3) / 1e9
-    log(f"[bench] C2 T=8 zipf: {ms_step * 1e3:.1f} us/layer, U={np.mean(uniques):.1f}, {gbs:.0f} GB/s")
+    log(f"[bench] C2 T=8 zipf: {ms_step * 1e3:.1f} us/layer, U={np.mean(uniques):.1f}, {gbs:.0f} GB/s, "
+        f"per-replay us/layer {spread}")
     # The T <= 16 layer is one kernel (moe_decode): its launches are timed
     # with start/stop events stamped by the dispatch itself.
     layer_ms, layer_launches = kernel_time(c2, _native.STAGE_LAYER, passes=max(2, replays))
@@ -336,7 +376,8 @@ def main() -> int:
     log(f"[bench] C2 moe_decode kernel (event-bracketed): {stage_us['moe_decode']} us, {layer_gbs:.0f} GB/s")
     configs["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms_step * 1e3, 2),
                                         unique_experts=round(float(np.mean(uniques)), 2), gbs=round(gbs, 1),
-                                        frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stage_us)
+                                        frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stage_us,
+                                        us_per_layer_spread=spread)
 
     # ---- C0: T=1 decode layer with the router ----
     if "c0" in only:
@@ -413,6 +454,8 @@ def main() -> int:
         log(f"[bench] CPU baseline: {cpu}")
 
     traffic = measured_traffic("moe_decode")
+    copy_gbs = copy_peak_gbs(device)
+    log(f"[bench] measured copy peak {copy_gbs:.0f} GB/s (read + write)")
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -434,6 +477,7 @@ def main() -> int:
                      "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                      "traffic": None if traffic is None else traffic["bytes"],
                      "traffic_source": None if traffic is None else traffic["source"],
+                     "measured_peak": round(copy_gbs, 1), "frac_of_measured": round(layer_gbs / copy_gbs, 4),
                      "kernel": "moe_decode", "avg_us": round(layer_ms * 1e3, 3), "launches": layer_launches,
                      "algorithmic_bytes": int(layer_bytes)},
         "cpu_baseline": cpu,

@@ -6,10 +6,12 @@
 //      shared-expert gate bf16(sigmoid(bf16(x.w))) of every token;
 //   2. workgroups 0..31 compute 8 router rows each (fixed fp32 order, see
 //      route.hip) and publish them;
-//   3. builds the route plan itself from the logits (top-8 by ballot radix
-//      select, renormalised weights, experts ascending with their token lists,
+//   3. builds the route plan itself from the logits (top-8 by eight wave-max
+//      extractions, renormalised weights, the unique experts as slots in
+//      discovery order -- token 0's routes first -- with their token lists,
 //      per token its routes in ascending expert order: fused_experts.py:47-54,
 //      block_experts.py:102-121), so no other kernel or host step is needed;
+//      the first item's weights are already streaming by then;
 //   4. walks its share of one list of 128 KiB work items, each item's
 //      weights prefetched one item ahead (the first two items of a workgroup
 //      are fixed by its index, later ones are claimed from a counter two
@@ -20,7 +22,8 @@
 //        B (slot, 128-row tile): down rows over k = 512 for the slot's tokens
 //          -> y rows (bf16, cpu_experts.c:64-69);
 //      slot 0 is the shared expert, slot s >= 1 the (s-1)-th unique routed
-//      expert; every token routed to an expert is an MFMA column, so each
+//      expert in discovery order; every token routed to an expert is an MFMA
+//      column (tokens ascending), so each
 //      weight byte is read from HBM once per call;
 //        C (128-row tile), the last 16 items: once every slot's B item of the
 //          tile is done, the ordered combine of that tile (fused_experts.py:
@@ -431,6 +434,33 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
     if (tid < kExperts) P.eptr[tid] = eptr;
     __syncthreads();
+
+    // ---- the first item's weights, before the rest of the plan ----
+    // Slots are numbered in discovery order (token 0's routes first, in rank
+    // order), so a workgroup's first item -- A tile k % 32 of slot
+    // first_slot + k / 32 with k < G <= 256 -- names slot 0 (the shared
+    // expert) or one of token 0's experts, and streams in while the rest of
+    // the plan is built.
+    uint4 b0[kLoads], b1[kLoads];
+    auto issue = [&](const uint16_t* p, uint4* buf) {
+#pragma unroll
+        for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
+    };
+    const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
+    int cur = (static_cast<int>(blockIdx.x) - offset + G) % G;
+    {
+        const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
+        const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
+        const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
+                                                                    (static_cast<uintptr_t>(ptrs.y) << 32));
+        const uint16_t* gate = s0 == 0 ? a.sh_gate : gate_up;
+        const uint16_t* up = s0 == 0 ? a.sh_up : gate_up + static_cast<size_t>(kInner) * kHidden;
+        // item_base's A geometry for tile cur % 32.
+        const int m = lane & 15;
+        const int row = 16 * (cur % kATiles) + 8 * (wave >> 2) + (m & 7);
+        issue((m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4), b0);
+    }
+
     if (blockIdx.x == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
@@ -439,17 +469,27 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     if (routes_ok && tid < T * kTopK) atomicOr(&P.tokmask[P.ids[tid / kTopK][tid % kTopK]], 1u << (tid / kTopK));
     __syncthreads();
     {
-        const uint32_t mask = tid < kExperts ? P.tokmask[tid] : 0u;
-        const uint32_t count = static_cast<uint32_t>(__popc(mask));
+        // Route i = tid (token i / 8, rank i % 8) opens a slot when its token
+        // is the first routed to the expert; one scan over the routes gives
+        // each new expert its slot and its first pair.
+        int e = 0;
+        uint32_t mask = 0u;
+        uint32_t opens = 0u;
+        if (routes_ok && tid < T * kTopK) {
+            const int t = tid / kTopK;
+            e = P.ids[t][tid % kTopK];
+            mask = P.tokmask[e];
+            if ((mask & ((1u << t) - 1u)) == 0u) opens = (1u << 16) | static_cast<uint32_t>(__popc(mask));
+        }
         uint32_t packed_total = 0;
-        const uint32_t packed = block_scan256((count ? (1u << 16) : 0u) | count, P.scan, &packed_total);
+        const uint32_t packed = block_scan256(opens, P.scan, &packed_total);
         const uint32_t pair0 = packed & 0xffffu;
         const uint32_t rank = packed >> 16;
         const uint32_t unique = packed_total >> 16;
-        if (tid < kExperts) P.poff[tid] = pair0;
-        if (count) {
+        if (opens) {
+            P.poff[e] = pair0;
             SlotInfo& s = P.slot[1 + rank];
-            const uint4 ptrs = P.eptr[tid];
+            const uint4 ptrs = P.eptr[e];
             const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
                                                                         (static_cast<uintptr_t>(ptrs.y) << 32));
             s.gate = gate_up;
@@ -469,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) s.tok[i] = tok[i];
-            s.count = static_cast<int32_t>(count);
+            s.count = static_cast<int32_t>(opens & 0xffffu);
             s.pair0 = static_cast<int32_t>(pair0);
         }
         if (tid == 0) {
@@ -516,7 +556,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     const int first_slot = P.first_slot;
     const int total = (kATiles + kBTiles) * n_slots;          // A and B items
     const int end = n_slots > 0 ? total + kCombineItems : 0;  // and the C items
-    const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
 
     // Bad routes: the output is the residual (or zeros); no expert runs.
     if (!routes_ok) {
@@ -530,7 +569,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
 
     // ---- 4. work items ----
-    uint4 b0[kLoads], b1[kLoads];
     uint64_t stg[4];
     const uint32_t stg_off = static_cast<uint32_t>((tid >> 5) * kInner * 2 + (tid & 31) * 32);
     // Prefetch target of an item without weights (C items): 1 KiB of token
@@ -544,10 +582,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
 
-    auto issue = [&](const uint16_t* p, uint4* buf) {
-#pragma unroll
-        for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
-    };
     auto weights_of = [&](const Item& it) -> const uint16_t* {
         return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
     };
@@ -674,11 +708,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         return after;
     };
 
-    // The first two items of a workgroup are fixed; the rest are claimed.
-    int cur = (static_cast<int>(blockIdx.x) - offset + G) % G;
+    // The first two items of a workgroup are fixed (the first one's weights
+    // are already in flight); the rest are claimed.
     if (cur < end) {
         int nxt = cur + G;
-        issue(weights_of(item_at(cur, total, n_slots, first_slot)), b0);
         poll = 0u;  // a first B or C item checks its counter in the bounded wait
         if (a.router == nullptr) {
             // Token rows staged while the first weights stream in.
@@ -705,6 +738,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
 
     // ---- 5. this workgroup is finished ----
+    __builtin_amdgcn_s_waitcnt(0);  // also the first-item loads of a call without items
     __syncthreads();
     if (tid == 0) {
         if (P.status & kStatusTimeout) atomicOr(a.status, kStatusTimeout);
@@ -744,7 +778,8 @@ hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
         lds_opt_in = true;
     }
     // One workgroup per CU: all of them are resident at once, which the
-    // item waits rely on.
+    // item waits rely on.  The first items name at most 8 slots (G <= 256).
+    if (cus[device] > kExperts) return hipErrorNotSupported;
     const StageEvents ev = timing_events(kStageLayer);
     LRMOE_LAUNCH(moe_decode, dim3(cus[device]), dim3(kThreads), lds, stream, ev.start, ev.stop, a);
     return hipGetLastError();
