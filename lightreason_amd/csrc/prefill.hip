@@ -230,7 +230,7 @@ constexpr int kGuLoadWaves = 4;
 constexpr int kGuThreads = (kGuMfmaWaves + kGuLoadWaves) * kWave;
 constexpr int kGuLoaderThreads = kGuLoadWaves * kWave;
 constexpr int kGuPieces = kPassTok * kGuChunk / 8 / kGuLoaderThreads;  // 16-byte pieces per loader thread per chunk
-constexpr int kGuRing = 8;                                            // k-steps of weights in registers per MFMA wave
+constexpr int kGuRing = 6;                                            // k-steps of weights in registers per MFMA wave
 
 // The MFMA waves' K loop for NB 16-token column blocks (blocks past the
 // unit's tokens read rows whose results are dropped), then SwiGLU.
@@ -319,17 +319,23 @@ __global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
             const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
             xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
         }
+        // Chunk c+1 is loaded into registers before the barrier that opens
+        // chunk c, so its gathered rows have two chunks' time to arrive.
         uint4 xr[kGuPieces];
 #pragma unroll
-        for (int c = 0; c < kGuChunks; ++c) {
+        for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j]);
 #pragma unroll
-            for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j] + c * kGuChunk);
+        for (int c = 0; c < kGuChunks; ++c) {
+            // Buffer c & 1 last held chunk c-2, which the MFMA waves finished
+            // before the previous barrier.
 #pragma unroll
             for (int j = 0; j < kGuPieces; ++j)
                 *reinterpret_cast<uint4*>(xs + ((c & 1) * kPassTok + lt / 16 + 16 * j) * kXsStride + 8 * piece) = xr[j];
-            // Chunk c is in LDS; buffer c & 1 last held chunk c-2, which the
-            // MFMA waves finished before the previous barrier.
-            __syncthreads();
+            if (c + 1 < kGuChunks) {
+#pragma unroll
+                for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j] + (c + 1) * kGuChunk);
+            }
+            __syncthreads();  // chunk c is in LDS
         }
         __syncthreads();  // matches the MFMA waves' last barrier
         return;
