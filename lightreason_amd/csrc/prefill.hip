@@ -34,7 +34,8 @@ namespace {
 
 constexpr int kBlkTok = 8;                 // tokens per routing block
 constexpr int kPfThreads = 512;            // expert kernels: 8 waves
-constexpr int kGuTiles = kInner / 64;      // 8 gate/up tiles of 64 rows per expert
+constexpr int kGuRows = 128;                // intermediate rows (gate and up) per gate/up workgroup
+constexpr int kGuTiles = kInner / kGuRows;  // 4 gate/up tiles per expert
 constexpr int kGuChunk = 128;              // k per LDS chunk
 constexpr int kGuChunks = kHidden / kGuChunk;
 constexpr int kGuSteps = kGuChunk / 32;    // MFMA k-steps (and A loads per lane) per chunk
@@ -220,17 +221,18 @@ __device__ __forceinline__ void unit_tile(int b, int tiles, int& unit, int& tile
     tile = within / 8;
 }
 
-// gate/up workgroup: 4 MFMA waves, each owning two 16-row MFMA tiles (tile r
-// = 8 gate rows and the 8 up rows with the same indices), and 4 loader waves
-// that move the unit's token rows into LDS one chunk ahead.  Each role waits
-// only on its own loads (the memory counter is in order); one barrier per
-// chunk joins them.  A B operand read from LDS feeds both row tiles.
-constexpr int kGuMfmaWaves = 4;
+// gate/up workgroup (128 intermediate rows of one work unit): 8 MFMA waves,
+// each owning two 16-row MFMA tiles (tile r = 8 gate rows and the 8 up rows
+// with the same indices), and 4 loader waves that move the unit's token rows
+// into LDS two chunks ahead.  Each role waits only on its own loads (the
+// memory counter is in order); one barrier per chunk joins them.  A B operand
+// read from LDS feeds both row tiles, and the 4 workgroups of a unit each read
+// its token rows once.
+constexpr int kGuMfmaWaves = kGuRows / 16;
 constexpr int kGuLoadWaves = 4;
 constexpr int kGuThreads = (kGuMfmaWaves + kGuLoadWaves) * kWave;
 constexpr int kGuLoaderThreads = kGuLoadWaves * kWave;
 constexpr int kGuPieces = kPassTok * kGuChunk / 8 / kGuLoaderThreads;  // 16-byte pieces per loader thread per chunk
-constexpr int kGuRing = 6;                                            // k-steps of weights in registers per MFMA wave
 
 // The MFMA waves' K loop for NB 16-token column blocks (blocks past the
 // unit's tokens read rows whose results are dropped), then SwiGLU.
@@ -240,37 +242,36 @@ __device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_
     f32x4 acc[2][NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[0][b] = acc[1][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // Weights stream through a ring of kGuRing k-steps (both tiles), kGuRing-1
-    // k-steps ahead of the MFMAs.
-    uint4 ring[kGuRing][2];
-    auto load_step = [&](int step, uint4* slot) {
-        slot[0] = ldg16(arow0 + 32 * step);
-        slot[1] = ldg16(arow1 + 32 * step);
-    };
+    // Weights arrive a whole chunk (kGuSteps k-steps of both tiles, 256
+    // contiguous bytes per row) at a time, one chunk ahead of the MFMAs: each
+    // DRAM row is read in one burst rather than 64 bytes per k-step.
+    uint4 wb[2][kGuSteps][2];
+    auto load_chunk = [&](int c, uint4 (*dst)[2]) {
 #pragma unroll
-    for (int s = 0; s < kGuRing - 1; ++s) load_step(s, ring[s]);
-    __syncthreads();  // loaders: chunk 0 in LDS
-    constexpr int kSteps = kHidden / 32;
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-        if (s + kGuRing - 1 < kSteps) load_step(s + kGuRing - 1, ring[(s + kGuRing - 1) % kGuRing]);
-        const int c = s / kGuSteps;
-        const uint16_t* xc = xb + (c & 1) * kPassTok * kXsStride + 32 * (s % kGuSteps);
-        const uint4* ab = ring[s % kGuRing];
-        // All B operands of the k-step are read before its MFMAs, so the LDS
-        // latency is paid once per k-step.
-        uint4 bv[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) bv[b] = *reinterpret_cast<const uint4*>(xc + 16 * b * kXsStride);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            acc[0][b] = mfma16x16x32(ab[0], bv[b], acc[0][b]);
-            acc[1][b] = mfma16x16x32(ab[1], bv[b], acc[1][b]);
+        for (int j = 0; j < kGuSteps; ++j) {
+            dst[j][0] = ldg16(arow0 + 32 * (kGuSteps * c + j));
+            dst[j][1] = ldg16(arow1 + 32 * (kGuSteps * c + j));
         }
-        __builtin_amdgcn_sched_barrier(0);
-        // After a chunk's last k-step its LDS buffer is free; the loaders fill
-        // it with chunk c+2 before the barrier that ends chunk c+1.
-        if (s % kGuSteps == kGuSteps - 1) __syncthreads();
+    };
+    load_chunk(0, wb[0]);
+    __syncthreads();  // loaders: chunk 0 in LDS
+#pragma unroll
+    for (int c = 0; c < kGuChunks; ++c) {
+        if (c + 1 < kGuChunks) load_chunk(c + 1, wb[(c + 1) & 1]);
+        const uint16_t* xcb = xb + (c & 1) * kPassTok * kXsStride;
+#pragma unroll
+        for (int j = 0; j < kGuSteps; ++j) {
+            const uint4* ab = wb[c & 1][j];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint4 bv = *reinterpret_cast<const uint4*>(xcb + 16 * b * kXsStride + 32 * j);
+                acc[0][b] = mfma16x16x32(ab[0], bv, acc[0][b]);
+                acc[1][b] = mfma16x16x32(ab[1], bv, acc[1][b]);
+            }
+        }
+        // Chunk c's LDS buffer is free after this barrier; the loaders fill it
+        // with chunk c+2 before the barrier that ends chunk c+1.
+        __syncthreads();
     }
     // SwiGLU: lanes g < 2 hold gate rows 4g..4g+3 of a tile's 8, lane + 32 the
     // up rows with the same index.  act0/act1 point at this lane's first act
@@ -345,14 +346,14 @@ __global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
     const int m = lane & 15;
     const int g = lane >> 4;
     const int nblk = (w.count + 15) / 16;
-    // MFMA row m < 8 of tile r is gate row 64*tile + 16*wave + 8r + m, m >= 8
+    // MFMA row m < 8 of tile r is gate row 128*tile + 16*wave + 8r + m, m >= 8
     // the up row with the same index.
     const uint16_t* rows = m < 8 ? w.gate : w.up;
-    const int row0 = 64 * tile + 16 * wave + (m & 7);
+    const int row0 = kGuRows * tile + 16 * wave + (m & 7);
     const uint16_t* arow0 = rows + static_cast<size_t>(row0) * kHidden + 8 * g;
     const uint16_t* arow1 = rows + static_cast<size_t>(row0 + 8) * kHidden + 8 * g;
     const uint16_t* xb = xs + m * kXsStride + 8 * g;
-    uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + 64 * tile + 16 * wave + 4 * g;
+    uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + kGuRows * tile + 16 * wave + 4 * g;
     uint16_t* act1 = act0 + 8;
     if (nblk <= 2) {
         gateup_mfma<2>(arow0, arow1, xb, act0, act1, w.count);
