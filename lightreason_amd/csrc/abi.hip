@@ -113,8 +113,8 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
         d.expert_ptrs = expert_ptrs;
         d.out = out;
         d.logits = ws.logits;
-        d.act = ws.act;
-        d.y = ws.y;
+        d.act = ws.dact;
+        d.y = ws.dy;
         d.sync = ws.sync;
         d.status = ws.plan.status;
         d.tokens = tokens;
@@ -165,8 +165,8 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
         d.indices_out = indices_out;
         d.weights_out = weights_out;
         d.logits = ws.logits;
-        d.act = ws.act;
-        d.y = ws.y;
+        d.act = ws.dact;
+        d.y = ws.dy;
         d.sync = ws.sync;
         d.status = ws.plan.status;
         d.tokens = tokens;

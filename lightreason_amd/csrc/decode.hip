@@ -30,17 +30,19 @@
 //          27-37: ascending expert, acc = bf16(acc + bf16(y * w)) from 0),
 //          the shared-expert add bf16(sg * y_shared) and the residual add.
 //
-// Cross-workgroup data (logits, act, y) is written with agent-scope stores
-// and read with agent-scope loads (coherent across the XCDs' L2s), and
-// published by agent-scope counters: per slot the completed A items, per
-// output tile the completed B items.  A B item waits for its slot's 32 A
-// items and a C item for its tile's B items, which come earlier in the list.
-// Every workgroup takes its items in increasing list order, all workgroups
-// are co-resident, and a workgroup publishes its finished items before it
-// waits, so the earliest waiting item always has its inputs in progress and
-// the waits end.  Every wait is bounded: on timeout the status word gets
-// kStatusTimeout and the kernel still exits.  Each call uses one of two
-// counter sets (by call parity) and zeroes the other for the next call.
+// Cross-workgroup data is written with agent-scope stores and read with
+// agent-scope loads (coherent across the XCDs' L2s).  The router logits are
+// published by a counter.  The act and y rows are 8-byte words that carry the
+// call's tag beside two bf16 values, so a B item knows its slot's act rows
+// are complete, and a C item its tile's y rows, by checking the tags of what
+// it loaded: no producer waits for its own stores or signals anything.  A B
+// item needs its slot's A items and a C item its tile's B items, all earlier
+// in the list; every workgroup takes its items in increasing list order and
+// all workgroups are co-resident, so the earliest waiting item always has
+// its inputs written or in progress and the waits end.  Every wait is
+// bounded: on timeout the status word gets kStatusTimeout and the kernel
+// still exits.  Each call uses one of two counter sets (by call parity) and
+// zeroes the other for the next call.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
@@ -57,7 +59,6 @@ constexpr int kRouterWgs = kExperts / kWaves; // 32 workgroups x 8 router rows
 constexpr int kXStride = kHidden + 8;         // LDS token row stride (bf16)
 constexpr int kActStride = kInner + 8;        // LDS act row stride (bf16)
 constexpr int kLoads = 16;                    // 16-byte weight loads per lane per item
-constexpr int kReadyTarget = kATiles;         // A items per slot
 constexpr int kCombineItems = kBTiles;        // C items, one per 128-row output tile
 constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
 
@@ -240,30 +241,59 @@ __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
 
 // Ordered combine of output rows [128*tile, +128) of every token (512
 // threads: token tid/32, rows 4*(tid%32)..+3), then the shared-expert and
-// residual adds.
-__device__ __forceinline__ void combine_tile(const DecodeArgs& a, const Plan& P, int tile, int T, bool shared) {
+// residual adds.  The tile's y words are reloaded (bounded) until each
+// carries this call's tag.
+__device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int tile, int T, bool shared,
+                                             uint32_t tag) {
     const int tid = threadIdx.x;
     const int t = tid >> 5;
+    const bool active = t < T;
     const int h = kBRows * tile + (tid & 31) * 4;
-    if (t < T) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // One pass over the pairs in combine order; it reports whether any word
+    // was stale (the sums of such a pass are discarded and the pass re-run).
+    float acc[4];
+    auto pass = [&]() {
+        bool stale = false;
 #pragma unroll
-        for (int q = 0; q < kTopK; ++q) {
-            const uint64_t v = ld_agent64(a.y + static_cast<size_t>(P.comb_pair[t][q]) * kHidden + h);
-            const float w = P.comb_w[t][q];
+        for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
+        if (!active) return false;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = rbf(acc[i] + rbf(bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu) * w));
+        for (int q = 0; q <= kTopK; ++q) {
+            if (q == kTopK && !shared) break;
+            const int pair = q < kTopK ? P.comb_pair[t][q] : kTopK * T + t;
+            const uint64_t* row = a.y + static_cast<size_t>(pair) * (kHidden / 2) + h / 2;
+            const uint64_t w0 = ld_agent64(row);
+            const uint64_t w1 = ld_agent64(row + 1);
+            stale |= static_cast<uint32_t>(w0 >> kDecodeTagShift) != tag ||
+                     static_cast<uint32_t>(w1 >> kDecodeTagShift) != tag;
+            const uint32_t bits[4] = {static_cast<uint32_t>(w0) & 0xffffu, static_cast<uint32_t>(w0 >> 16) & 0xffffu,
+                                      static_cast<uint32_t>(w1) & 0xffffu, static_cast<uint32_t>(w1 >> 16) & 0xffffu};
+            const float w = q < kTopK ? P.comb_w[t][q] : P.sg[t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // acc + bf16(y * w) for a routed pair, acc + bf16(gate * y) for the shared row.
+                const float prod = q < kTopK ? bf2f(bits[i]) * w : w * bf2f(bits[i]);
+                acc[i] = rbf(acc[i] + rbf(prod));
+            }
         }
-        if (shared) {
-            const uint64_t v = ld_agent64(a.y + static_cast<size_t>(kTopK * T + t) * kHidden + h);
-            const float gate = P.sg[t];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = rbf(acc[i] + rbf(gate * bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu)));
+        return stale;
+    };
+    if (__syncthreads_or(pass())) {
+        const uint64_t start = now_ticks();
+        while (true) {
+            if (__syncthreads_or(now_ticks() - start > kSpinTicks)) {
+                if (tid == 0) P.status |= kStatusTimeout;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            if (!__syncthreads_or(pass())) break;
         }
+    }
+    if (active) {
         if (a.residual) {
-            const uint64_t v = *reinterpret_cast<const uint64_t*>(a.x + static_cast<size_t>(t) * kHidden + h);
+            const uint64_t x = *reinterpret_cast<const uint64_t*>(a.x + static_cast<size_t>(t) * kHidden + h);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = rbf(bf2f(static_cast<uint32_t>(v >> (16 * i)) & 0xffffu) + acc[i]);
+            for (int i = 0; i < 4; ++i) acc[i] = rbf(bf2f(static_cast<uint32_t>(x >> (16 * i)) & 0xffffu) + acc[i]);
         }
         uint32_t o[4];
 #pragma unroll
@@ -287,8 +317,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
     DecodeSync* sync = a.sync;
-    // The call's parity, from the count of finished workgroups (DecodeSync).
-    const uint32_t arrivals = ld_agent32(&sync->arrivals);
+    // This call's number, from the count of finished workgroups (DecodeSync).
+    const unsigned long long finished = ld_agent64(&sync->finished);
 
     // ---- 1. every load that depends on nothing, issued first ----
     // In order of need: the caller's logits rows of this wave's tokens
@@ -325,13 +355,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
     if (tid < kExperts) P.tokmask[tid] = 0u;
     if (tid == 0) P.status = 0;
-    const int parity = arrivals >= static_cast<uint32_t>(G) ? 1 : 0;
+    const unsigned long long call = finished / static_cast<unsigned long long>(G);
+    const int parity = static_cast<int>(call & 1ull);
+    const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
     DecodeCounters* const cnt = &sync->set[parity];
     if (blockIdx.x == 0) {
         // The next call's counters (this call never touches them).
         DecodeCounters* const nxt = &sync->set[parity ^ 1];
-        if (tid < kDecodeSlots) st_agent32(&nxt->ready[tid * kSyncStride], 0u);
-        if (tid >= kExperts && tid < kExperts + kCombineItems) st_agent32(&nxt->tile_done[(tid - kExperts) * kSyncStride], 0u);
         if (tid == kThreads - 1) st_agent32(&nxt->router_done, 0u);
         if (tid == kThreads - 2) st_agent32(&nxt->claim, 0u);
     }
@@ -569,22 +599,23 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     }
 
     // ---- 4. work items ----
-    uint64_t stg[4];
-    const uint32_t stg_off = static_cast<uint32_t>((tid >> 5) * kInner * 2 + (tid & 31) * 32);
+    // B staging: thread tid loads words 8*(tid%32)..+7 of act row tid/32.
+    uint64_t stg[8];
+    const int stg_row = tid >> 5;
+    const uint32_t stg_off = static_cast<uint32_t>(stg_row * (kInner / 2) * 8 + (tid & 31) * 64);
     // Prefetch target of an item without weights (C items): 1 KiB of token
     // row 0, in cache after the first read.
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
     // Lanes of the claiming atomic: lane 0 of wave 0.
     const uint32_t claim_lanes = wave == 0 ? 1u : 0u;
-    uint32_t poll = 0;        // counter of the current item's dependency (read one item ahead)
-    int sig_kind = -1;        // item whose completion is signalled next step
-    int sig_slot = 0, sig_tile = 0;
+    const uint64_t tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
 
     auto weights_of = [&](const Item& it) -> const uint16_t* {
         return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
     };
+    auto stale_word = [&](uint64_t w) { return static_cast<uint32_t>(w >> kDecodeTagShift) != tag; };
 
     // Runs item kk, whose weights are in buf, and prefetches item kn into
     // nbuf.  Returns the item claimed for the step after next.
@@ -593,41 +624,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         const Item nx = item_at(kn, total, n_slots, first_slot);
         const SlotInfo& s = P.slot[it.slot];
         const uint16_t* np = weights_of(nx);
-        auto signal_previous = [&]() {
-            if (tid == 0) {
-                if (sig_kind == 0) add_agent32(&cnt->ready[sig_slot * kSyncStride], 1u);
-                if (sig_kind == 1) add_agent32(&cnt->tile_done[sig_tile * kSyncStride], 1u);
-            }
-            sig_kind = -1;
-        };
-        // (a) A B item needs its slot's act rows, a C item every slot's y
-        //     rows of its tile.  Before waiting, the workgroup publishes its
-        //     own previous item: a completed item is never held back by a
-        //     wait, so two workgroups cannot wait on each other.
-        const uint32_t need = it.kind == 1 ? static_cast<uint32_t>(kReadyTarget) : static_cast<uint32_t>(n_slots);
-        if (it.kind >= 1 && __syncthreads_or(poll < need)) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            signal_previous();
-            const uint32_t* c = it.kind == 1 ? &cnt->ready[it.slot * kSyncStride] : &cnt->tile_done[it.tile * kSyncStride];
-            if (tid == 0 && !wait_counter(c, need)) P.status |= kStatusTimeout;
-            __syncthreads();
+        // Uniform base of the slot's 16 act rows (rows past its count are
+        // padding, loaded but never used).
+        const char* stg_base = reinterpret_cast<const char*>(a.act) +
+                               static_cast<size_t>(__builtin_amdgcn_readfirstlane(s.pair0)) * (kInner / 2) * 8;
+        // (a) staging loads (B), the claim of the item after next, then the
+        //     next item's weights: a wait for everything but the newest 16
+        //     loads covers this item's weights, staging and claim.
+        // Only the slot's count rows are loaded: the other threads issue
+        // fewer loads, which the wait below (an upper bound) allows.
+        if (it.kind == 1 && stg_row < s.count) {
+            ld_agent64x4_async(stg, stg_base, stg_off);
+            ld_agent64x4_async(stg + 4, stg_base, stg_off + 32);
         }
-        // (b) staging loads (B), the poll for the next item, the claim of the
-        //     item after it, then the next item's weights: a wait for
-        //     everything but the newest 16 loads covers this item's weights,
-        //     staging, poll and claim and the previous item's stores.
-        if (it.kind == 1) {
-            // Uniform base + loop-invariant lane offset: rows past the slot's
-            // count read the act buffer's padding (never used as columns).
-            const int pair0 = __builtin_amdgcn_readfirstlane(s.pair0);
-            const char* base = reinterpret_cast<const char*>(a.act) + static_cast<size_t>(pair0) * kInner * 2;
-            ld_agent64x4_async(stg, base, stg_off);
-        }
-        const uint32_t* poll_addr = nx.kind == 1 ? &cnt->ready[nx.slot * kSyncStride]
-                                  : nx.kind == 2 ? &cnt->tile_done[nx.tile * kSyncStride]
-                                                 : &cnt->router_done;
-        uint32_t next_poll = ld_agent32(poll_addr);
         const uint32_t claimed = claim_async(&cnt->claim, claim_lanes);
         __builtin_amdgcn_sched_barrier(0);
         issue(np, nbuf);
@@ -635,22 +644,42 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + 2 * G;
-        // (c) Otherwise the previous item is signalled after this item's
-        //     first barrier: every wave is past the wait above, so all of
-        //     that item's stores are complete.
-        if (it.kind == 1) {
-            // Every wave is past the previous item's reads of act_lds.
-            __syncthreads();
-            signal_previous();
-            const int r = tid >> 5;
-            const int c = (tid & 31) * 16;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) *reinterpret_cast<uint64_t*>(act_lds + r * kActStride + c + 4 * i) = stg[i];
-            __syncthreads();
-        }
-        // (d) the item itself.
         const int m = lane & 15;
         const int g = lane >> 4;
+        if (it.kind == 1) {
+            // (b) the slot's act rows, once every word used carries this
+            //     call's tag; a slot whose A items are still being written is
+            //     reloaded (bounded).  The first barrier also means every wave
+            //     is past the previous item's reads of act_lds.
+            const bool used = stg_row < s.count;
+            bool stale = false;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) stale |= used && stale_word(stg[i]);
+            if (__syncthreads_or(stale)) {
+                const uint64_t start = now_ticks();
+                while (true) {
+                    if (__syncthreads_or(now_ticks() - start > kSpinTicks)) {
+                        if (tid == 0) P.status |= kStatusTimeout;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                    stale = false;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        stg[i] = ld_agent64(stg_base + stg_off + 8 * i);
+                        stale |= used && stale_word(stg[i]);
+                    }
+                    if (!__syncthreads_or(stale)) break;
+                }
+            }
+            uint4* dst = reinterpret_cast<uint4*>(act_lds + stg_row * kActStride + 16 * (tid & 31));
+            dst[0] = make_uint4(static_cast<uint32_t>(stg[0]), static_cast<uint32_t>(stg[1]),
+                                static_cast<uint32_t>(stg[2]), static_cast<uint32_t>(stg[3]));
+            dst[1] = make_uint4(static_cast<uint32_t>(stg[4]), static_cast<uint32_t>(stg[5]),
+                                static_cast<uint32_t>(stg[6]), static_cast<uint32_t>(stg[7]));
+            __syncthreads();
+        }
+        // (c) the item itself.
         if (it.kind == 0) {
             const int tok = column_token(s, m < s.count ? m : 0);
             const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
@@ -662,7 +691,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             }
             part[(par * kWaves + wave) * kWave + lane] = acc0 + acc1;
             __syncthreads();
-            signal_previous();
             if ((wave & 3) == 0) {
                 const f32x4* pp = part + (par * kWaves + wave) * kWave + lane;
                 const f32x4 sum = ((pp[0] + pp[kWave]) + pp[2 * kWave]) + pp[3 * kWave];
@@ -673,8 +701,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                     uint32_t act[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(sum[i]), rbf(up[i]));
-                    st_agent64(a.act + static_cast<size_t>(s.pair0 + m) * kInner + 16 * it.tile + 8 * (wave >> 2) + 4 * g,
-                               pack4(act));
+                    uint64_t* dst = a.act + static_cast<size_t>(s.pair0 + m) * (kInner / 2) +
+                                    (16 * it.tile + 8 * (wave >> 2) + 4 * g) / 2;
+                    st_agent64(dst, tag_bits | (act[0] | (act[1] << 16)));
+                    st_agent64(dst + 1, tag_bits | (act[2] | (act[3] << 16)));
                 }
             }
             par ^= 1;
@@ -691,20 +721,18 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                 uint32_t o[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[i] = f2bf(y[i]);
-                st_agent64(a.y + static_cast<size_t>(s.pair0 + m) * kHidden + kBRows * it.tile + 16 * wave + 4 * g, pack4(o));
+                uint64_t* dst = a.y + static_cast<size_t>(s.pair0 + m) * (kHidden / 2) +
+                                (kBRows * it.tile + 16 * wave + 4 * g) / 2;
+                st_agent64(dst, tag_bits | (o[0] | (o[1] << 16)));
+                st_agent64(dst + 1, tag_bits | (o[2] | (o[3] << 16)));
             }
         } else {
-            signal_previous();
-            combine_tile(a, P, it.tile, T, first_slot == 0);
+            combine_tile(a, P, it.tile, T, first_slot == 0, tag);
             // Wave 0's claim above is visible to every wave after this.
             __syncthreads();
         }
         const int after = P.claim[cpar];
         cpar ^= 1;
-        sig_kind = it.kind <= 1 ? it.kind : -1;
-        sig_slot = it.slot;
-        sig_tile = it.tile;
-        poll = next_poll;
         return after;
     };
 
@@ -712,7 +740,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     // are already in flight); the rest are claimed.
     if (cur < end) {
         int nxt = cur + G;
-        poll = 0u;  // a first B or C item checks its counter in the bounded wait
         if (a.router == nullptr) {
             // Token rows staged while the first weights stream in.
             stage_rows();
@@ -728,13 +755,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
             nxt = after;
             if (cur >= end) break;
         }
-        // Flush: the last item's stores, then its signal.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) {
-            if (sig_kind == 0) add_agent32(&cnt->ready[sig_slot * kSyncStride], 1u);
-            if (sig_kind == 1) add_agent32(&cnt->tile_done[sig_tile * kSyncStride], 1u);
-        }
     }
 
     // ---- 5. this workgroup is finished ----
@@ -742,7 +762,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     __syncthreads();
     if (tid == 0) {
         if (P.status & kStatusTimeout) atomicOr(a.status, kStatusTimeout);
-        __builtin_amdgcn_atomic_inc32(&sync->arrivals, static_cast<uint32_t>(2 * G - 1), __ATOMIC_RELAXED, "agent");
+        __hip_atomic_fetch_add(&sync->finished, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

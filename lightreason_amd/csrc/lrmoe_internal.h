@@ -29,21 +29,27 @@ struct DecodeCounters {
     uint32_t pad0[kSyncStride - 1];
     uint32_t claim;                              // work items handed out past the first two rounds
     uint32_t pad1[kSyncStride - 1];
-    uint32_t ready[kDecodeSlots * kSyncStride];  // A items finished per slot
-    uint32_t tile_done[16 * kSyncStride];        // B items finished per 128-row output tile
 };
 
-// Decode kernel synchronisation.  `arrivals` counts finished workgroups
-// modulo 2G (G = grid size, fixed per device), so a call reads the parity of
-// its call number as arrivals >= G: at most G - 1 of its own workgroups can
-// have finished before any of them reads it.  Call parity p uses set[p] and
-// zeroes set[p ^ 1] for the next call, so nothing is reset at the end of a
-// call and a zero-initialised workspace is valid.
+// Decode kernel synchronisation.  `finished` counts finished workgroups over
+// all calls, so a call's number is finished / G (G = grid size, fixed per
+// device) whenever one of its workgroups reads it: at most G - 1 of its own
+// workgroups can have finished by then.  Call c uses set[c % 2] and zeroes
+// set[(c + 1) % 2] for the next call, so nothing is reset at the end of a
+// call and a zero-initialised workspace is valid.  The call number also tags
+// the rows one workgroup writes for another (see kDecodeTagShift).
 struct DecodeSync {
-    uint32_t arrivals;
-    uint32_t pad0[kSyncStride - 1];
+    unsigned long long finished;
+    uint32_t pad0[kSyncStride - 2];
     DecodeCounters set[2];
 };
+
+// Rows exchanged between decode workgroups are 8-byte words: two bf16 values
+// in the low half and the writing call's tag (call number mod 2^32 - 1, plus
+// 1, so never 0) in the high half.  A reader that sees its own call's tag in
+// a word has that word's data; an 8-byte store is seen whole or not at all.
+// (A tag repeats only after 2^32 - 1 decode calls on one workspace.)
+constexpr int kDecodeTagShift = 32;
 
 // Control block at the start of every workspace.  The route counter is reset
 // to zero by the workgroup that consumes it, so a zero-initialised workspace
@@ -82,6 +88,8 @@ struct Workspace {
     Plan plan;
     uint16_t* act;        // [8T + T + 16][512]: routed pairs, shared rows, padding
     uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
+    uint64_t* dact;       // decode: act as tagged words, [9*16 + 16][256]
+    uint64_t* dy;         // decode: y as tagged words, [9*16][1024]
     uint32_t* counts;     // [256] prefill: pairs per expert
     DecodeSync* sync;     // decode kernel counters
     uint8_t* bmask;       // prefill: [256][nblk_pad] token masks per 8-token block
@@ -108,6 +116,11 @@ inline Workspace carve(void* base, int tokens) {
     // Counters that persist between calls sit at a fixed offset, whatever
     // the token count of the call.
     ws.sync = reinterpret_cast<DecodeSync*>(take(sizeof(DecodeSync)));
+    // So are the decode kernel's tagged rows (sized for 16 tokens): only
+    // decode calls ever write them, so a word carrying a call's tag was
+    // written by that call.
+    ws.dact = reinterpret_cast<uint64_t*>(take((9 * kDecodeMaxTokens + 16) * 256 * 8));
+    ws.dy = reinterpret_cast<uint64_t*>(take(9 * kDecodeMaxTokens * 1024 * 8));
     ws.logits = reinterpret_cast<uint16_t*>(take(T * 256 * 2));
     ws.normed = reinterpret_cast<uint16_t*>(take(T * 2048 * 2));
     ws.indices = reinterpret_cast<int64_t*>(take(T * 8 * 8));
@@ -121,6 +134,7 @@ inline Workspace carve(void* base, int tokens) {
     // 16 rows of padding: the decode kernel stages 16 act rows per slot.
     ws.act = reinterpret_cast<uint16_t*>(take((P + T + 16) * 512 * 2));
     ws.y = reinterpret_cast<uint16_t*>(take((P + T) * 2048 * 2));
+
     ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
     const size_t nblk = (T + 7) / 8;
     const size_t nblk_pad = (nblk + 15) / 16 * 16;
@@ -194,8 +208,8 @@ struct DecodeArgs {
     int64_t* indices_out;         // [T][8] or null
     uint16_t* weights_out;        // [T][8] or null
     uint16_t* logits;             // [T][256] workspace (router output)
-    uint16_t* act;                // [9T][512] workspace
-    uint16_t* y;                  // [9T][2048] workspace
+    uint64_t* act;                // [9T + 16][256] tagged words (workspace)
+    uint64_t* y;                  // [9T][1024] tagged words (workspace)
     DecodeSync* sync;             // workspace counters
     int32_t* status;              // workspace status word
     int tokens;
