@@ -175,32 +175,51 @@ __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
 // rank k.  Same arithmetic and order as the oracle.
 __device__ __forceinline__ void topk8_wave(uint64_t packed, int& expert, uint32_t& weight_bits) {
     const int lane = threadIdx.x & 63;
-    uint32_t bits[4], keys[4];
+    uint32_t bits[4], k[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
-        keys[j] = route_key(bits[j], 4 * lane + j) + 1u;  // 0 marks a taken key
+        k[j] = route_key(bits[j], 4 * lane + j) + 1u;  // 0 marks an empty place
     }
+    // The lane's keys in descending order (keys are unique): each extraction
+    // then looks at one head key and shifts the lane's list when it wins.
+    auto order2 = [](uint32_t& hi, uint32_t& lo) {
+        const uint32_t a = max(hi, lo), b = min(hi, lo);
+        hi = a;
+        lo = b;
+    };
+    order2(k[0], k[1]);
+    order2(k[2], k[3]);
+    order2(k[0], k[2]);
+    order2(k[1], k[3]);
+    order2(k[1], k[2]);
     uint32_t chosen[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        const uint32_t mine = max(max(keys[0], keys[1]), max(keys[2], keys[3]));
-        chosen[k] = wave_max_u32(mine);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) keys[j] = keys[j] == chosen[k] ? 0u : keys[j];
-    }
-    const float top = bf2f(key_bits(chosen[0] - 1u));
     float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
+    for (int r = 0; r < kTopK; ++r) {
+        chosen[r] = wave_max_u32(k[0]);
+        if (r == 0) {
+            // Softmax terms relative to the top logit, computed here so that
+            // they fill the wave-maximum chains below.
+            const float top = bf2f(key_bits(chosen[0] - 1u));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
+        }
+        const bool won = k[0] == chosen[r];
+        k[0] = won ? k[1] : k[0];
+        k[1] = won ? k[2] : k[1];
+        k[2] = won ? k[3] : k[2];
+        k[3] = won ? 0u : k[3];
+    }
+    const float top = bf2f(key_bits(chosen[0] - 1u));
     const float total = wave_butterfly_sum(part);
     uint32_t my = chosen[0];
 #pragma unroll
-    for (int k = 1; k < kTopK; ++k) my = lane == k ? chosen[k] : my;
+    for (int r = 1; r < kTopK; ++r) my = lane == r ? chosen[r] : my;
     const float prob = lr_exp(bf2f(key_bits(my - 1u)) - top) / total;
     float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), 0));
 #pragma unroll
-    for (int k = 1; k < kTopK; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), k));
+    for (int r = 1; r < kTopK; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), r));
     expert = 255 - static_cast<int>((my - 1u) & 255u);
     weight_bits = f2bf(prob / sum);
 }
