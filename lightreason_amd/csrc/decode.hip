@@ -438,18 +438,31 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     if (a.indices_in == nullptr) {
         int e_lo, e_hi;
         uint32_t w_lo, w_hi;
-        if (has_lo) {
+        if (T > kWaves) {
+            // Two tokens per wave: both selections in one block, so that
+            // each fills the other's wave-maximum chains (an absent second
+            // token selects over a dummy row and is dropped).
+            const uint64_t both[2] = {lg_lo, lg_hi};
+            int e2[2];
+            uint32_t w2[2];
+            topk8_waves<2>(both, e2, w2);
+            e_lo = e2[0];
+            e_hi = e2[1];
+            w_lo = w2[0];
+            w_hi = w2[1];
+            if (lane < kTopK) {
+                P.ids[t_lo][lane] = e_lo;
+                P.wts[t_lo][lane] = static_cast<uint16_t>(w_lo);
+                if (has_hi) {
+                    P.ids[t_hi][lane] = e_hi;
+                    P.wts[t_hi][lane] = static_cast<uint16_t>(w_hi);
+                }
+            }
+        } else if (has_lo) {
             topk8_wave(lg_lo, e_lo, w_lo);
             if (lane < kTopK) {
                 P.ids[t_lo][lane] = e_lo;
                 P.wts[t_lo][lane] = static_cast<uint16_t>(w_lo);
-            }
-        }
-        if (has_hi) {
-            topk8_wave(lg_hi, e_hi, w_hi);
-            if (lane < kTopK) {
-                P.ids[t_hi][lane] = e_hi;
-                P.wts[t_hi][lane] = static_cast<uint16_t>(w_hi);
             }
         }
     } else if (tid < T * kTopK) {

@@ -59,7 +59,11 @@ __device__ __forceinline__ float lr_exp(float x) {
     const int ki = static_cast<int>(k);
     const int k1 = ki / 2;
     const float e = (p * pow2i(k1)) * pow2i(ki - k1);
-    return x != x ? x : (x > 88.72283935546875f ? __builtin_inff() : (x < -87.0f ? 0.0f : e));
+    const float r2 = x > 88.72283935546875f ? __builtin_inff() : (x < -87.0f ? 0.0f : e);
+    // NaN passes through; selected with bit operations so that no branch
+    // splits the caller's code.
+    const uint32_t nan_mask = 0u - static_cast<uint32_t>(x != x);
+    return __uint_as_float((__float_as_uint(x) & nan_mask) | (__float_as_uint(r2) & ~nan_mask));
 }
 
 // The expert activation with cpu_experts.c:59-62 rounding points:
@@ -109,6 +113,24 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false)));
     v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false)));
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// N independent wave maxima with their DPP steps interleaved, so that each
+// chain's wait states are filled by the others.
+template <int N>
+__device__ __forceinline__ void wave_max_u32_n(uint32_t* v) {
+#define LR_DPP_MAX_STEP(ctrl, row_mask)                                                                            \
+    _Pragma("unroll") for (int n = 0; n < N; ++n) v[n] =                                                           \
+        max(v[n], static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v[n]), ctrl, row_mask, 0xf, false)));
+    LR_DPP_MAX_STEP(0x111, 0xf)
+    LR_DPP_MAX_STEP(0x112, 0xf)
+    LR_DPP_MAX_STEP(0x114, 0xf)
+    LR_DPP_MAX_STEP(0x118, 0xf)
+    LR_DPP_MAX_STEP(0x142, 0xa)
+    LR_DPP_MAX_STEP(0x143, 0xc)
+#undef LR_DPP_MAX_STEP
+#pragma unroll
+    for (int n = 0; n < N; ++n) v[n] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v[n]), 63));
 }
 
 // Dot product of 8 bf16 weights (one 16-byte load) with 8 floats, as an
@@ -172,56 +194,79 @@ __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
 // relative to the top logit (the per-lane sums meet in the fixed butterfly),
 // then the eight probabilities are renormalised by their sum in rank order
 // and rounded to bf16.  Lane k < 8 receives the expert and weight bits of
-// rank k.  Same arithmetic and order as the oracle.
-__device__ __forceinline__ void topk8_wave(uint64_t packed, int& expert, uint32_t& weight_bits) {
+// rank k.  Same arithmetic and order as the oracle.  topk8_waves does this
+// for N tokens at once, their steps interleaved.
+template <int N>
+__device__ __forceinline__ void topk8_waves(const uint64_t* packed, int* expert, uint32_t* weight_bits) {
     const int lane = threadIdx.x & 63;
-    uint32_t bits[4], k[4];
+    uint32_t bits[N][4], k[N][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bits[j] = static_cast<uint32_t>(packed >> (16 * j)) & 0xffffu;
-        k[j] = route_key(bits[j], 4 * lane + j) + 1u;  // 0 marks an empty place
+    for (int n = 0; n < N; ++n) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bits[n][j] = static_cast<uint32_t>(packed[n] >> (16 * j)) & 0xffffu;
+            k[n][j] = route_key(bits[n][j], 4 * lane + j) + 1u;  // 0 marks an empty place
+        }
     }
-    // The lane's keys in descending order (keys are unique): each extraction
+    // Each lane's keys in descending order (keys are unique): an extraction
     // then looks at one head key and shifts the lane's list when it wins.
     auto order2 = [](uint32_t& hi, uint32_t& lo) {
         const uint32_t a = max(hi, lo), b = min(hi, lo);
         hi = a;
         lo = b;
     };
-    order2(k[0], k[1]);
-    order2(k[2], k[3]);
-    order2(k[0], k[2]);
-    order2(k[1], k[3]);
-    order2(k[1], k[2]);
-    uint32_t chosen[kTopK];
-    float part = 0.0f;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        order2(k[n][0], k[n][1]);
+        order2(k[n][2], k[n][3]);
+        order2(k[n][0], k[n][2]);
+        order2(k[n][1], k[n][3]);
+        order2(k[n][1], k[n][2]);
+    }
+    uint32_t chosen[N][kTopK];
+    float part[N];
 #pragma unroll
     for (int r = 0; r < kTopK; ++r) {
-        chosen[r] = wave_max_u32(k[0]);
-        if (r == 0) {
-            // Softmax terms relative to the top logit, computed here so that
-            // they fill the wave-maximum chains below.
-            const float top = bf2f(key_bits(chosen[0] - 1u));
+        uint32_t head[N];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) part = part + lr_exp(bf2f(bits[j]) - top);
+        for (int n = 0; n < N; ++n) head[n] = k[n][0];
+        wave_max_u32_n<N>(head);
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            chosen[n][r] = head[n];
+            if (r == 0) {
+                // Softmax terms relative to the top logit, computed here so
+                // that they fill the extraction chains that follow.
+                const float top = bf2f(key_bits(head[n] - 1u));
+                part[n] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[n] = part[n] + lr_exp(bf2f(bits[n][j]) - top);
+            }
+            const bool won = k[n][0] == head[n];
+            k[n][0] = won ? k[n][1] : k[n][0];
+            k[n][1] = won ? k[n][2] : k[n][1];
+            k[n][2] = won ? k[n][3] : k[n][2];
+            k[n][3] = won ? 0u : k[n][3];
         }
-        const bool won = k[0] == chosen[r];
-        k[0] = won ? k[1] : k[0];
-        k[1] = won ? k[2] : k[1];
-        k[2] = won ? k[3] : k[2];
-        k[3] = won ? 0u : k[3];
     }
-    const float top = bf2f(key_bits(chosen[0] - 1u));
-    const float total = wave_butterfly_sum(part);
-    uint32_t my = chosen[0];
 #pragma unroll
-    for (int r = 1; r < kTopK; ++r) my = lane == r ? chosen[r] : my;
-    const float prob = lr_exp(bf2f(key_bits(my - 1u)) - top) / total;
-    float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), 0));
+    for (int n = 0; n < N; ++n) {
+        const float top = bf2f(key_bits(chosen[n][0] - 1u));
+        const float total = wave_butterfly_sum(part[n]);
+        uint32_t my = chosen[n][0];
 #pragma unroll
-    for (int r = 1; r < kTopK; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), r));
-    expert = 255 - static_cast<int>((my - 1u) & 255u);
-    weight_bits = f2bf(prob / sum);
+        for (int r = 1; r < kTopK; ++r) my = lane == r ? chosen[n][r] : my;
+        const float prob = lr_exp(bf2f(key_bits(my - 1u)) - top) / total;
+        float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), 0));
+#pragma unroll
+        for (int r = 1; r < kTopK; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), r));
+        expert[n] = 255 - static_cast<int>((my - 1u) & 255u);
+        weight_bits[n] = f2bf(prob / sum);
+    }
+}
+
+__device__ __forceinline__ void topk8_wave(uint64_t packed, int& expert, uint32_t& weight_bits) {
+    topk8_waves<1>(&packed, &expert, &weight_bits);
 }
 
 // Exclusive scan over threads 0..255 (all threads call; others contribute 0).
