@@ -95,7 +95,7 @@ struct Workspace {
     uint8_t* bmask;       // prefill: [256][nblk_pad] token masks per 8-token block
     uint32_t* blk_base;   // prefill: [256][nblk_pad] pairs of the expert before the block
     int32_t* bstatus;     // prefill: [nblk] route status per block
-    int2* units;          // prefill: (slot, first pair) work units
+    int4* units;          // prefill: work units (expert + 1 or 0 = shared, first pair, pairs, 0)
     int nblk_pad;
     size_t bytes;
 };
@@ -143,7 +143,7 @@ inline Workspace carve(void* base, int tokens) {
     ws.blk_base = reinterpret_cast<uint32_t*>(take(256 * nblk_pad * 4));
     ws.bstatus = reinterpret_cast<int32_t*>(take(nblk * 4));
     const size_t units = (T + kPassTok - 1) / kPassTok + 256 + (8 * T + kPassTok - 1) / kPassTok + 8;
-    ws.units = reinterpret_cast<int2*>(take(units * sizeof(int2)));
+    ws.units = reinterpret_cast<int4*>(take(units * sizeof(int4)));
     ws.plan.unique = &ws.control->unique;
     ws.plan.status = &ws.control->status;
     ws.bytes = offset;

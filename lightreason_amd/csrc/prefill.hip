@@ -149,8 +149,17 @@ __global__ __launch_bounds__(256) void pf_fill(const int64_t* indices, int token
         uint32_t unit_total = 0;
         const uint32_t shared_units = shared_present ? (tokens + kPassTok - 1) / kPassTok : 0u;
         const uint32_t first_unit = shared_units + block_scan256(passes, scratch, &unit_total);
-        for (uint32_t j = threadIdx.x; j < shared_units; j += 256) ws.units[j] = make_int2(0, static_cast<int>(j) * kPassTok);
-        for (uint32_t j = 0; j < passes; ++j) ws.units[first_unit + j] = make_int2(1 + static_cast<int>(rank), static_cast<int>(j) * kPassTok);
+        // A unit names its expert and pair range directly, so an expert
+        // workgroup reaches its weight addresses in two dependent loads.
+        for (uint32_t j = threadIdx.x; j < shared_units; j += 256) {
+            const int first = static_cast<int>(j) * kPassTok;
+            ws.units[j] = make_int4(0, kTopK * tokens + first, min(kPassTok, tokens - first), 0);
+        }
+        for (uint32_t j = 0; j < passes; ++j) {
+            const int first = static_cast<int>(j) * kPassTok;
+            ws.units[first_unit + j] = make_int4(1 + e, static_cast<int>(pair0) + first,
+                                                 min(kPassTok, static_cast<int>(count) - first), 0);
+        }
         if (threadIdx.x == 0) {
             plan.offset[unique] = static_cast<int32_t>(pairs);
             *plan.unique = static_cast<int32_t>(unique);
@@ -189,27 +198,22 @@ struct Unit {
 
 __device__ __forceinline__ bool load_unit(const ExpertArgs& a, int u, Unit& w) {
     if (u >= a.ws.control->n_units) return false;
-    const int2 unit = a.ws.units[u];
+    const int4 unit = a.ws.units[u];
+    w.pair0 = unit.y;
+    w.count = unit.z;
     if (unit.x == 0) {
         w.gate = a.shared_gate_proj;
         w.up = a.shared_up_proj;
         w.down = a.shared_down;
         w.tokens = nullptr;
-        w.pair0 = kTopK * a.tokens + unit.y;
-        w.count = min(kPassTok, a.tokens - unit.y);
         return true;
     }
-    const int s = unit.x - 1;
-    const int e = a.plan.expert[s];
-    const int first = a.plan.offset[s];
-    const int end = a.plan.offset[s + 1];
+    const int e = unit.x - 1;
     const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e]);
     w.gate = gate_up;
     w.up = gate_up + static_cast<size_t>(kInner) * kHidden;
     w.down = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e + 1]);
-    w.tokens = a.plan.pair_token + first + unit.y;
-    w.pair0 = first + unit.y;
-    w.count = min(kPassTok, end - first - unit.y);
+    w.tokens = a.plan.pair_token + unit.y;
     return true;
 }
 
