@@ -33,15 +33,17 @@ namespace lrmoe {
 namespace {
 
 constexpr int kBlkTok = 8;                 // tokens per routing block
-constexpr int kPfThreads = 512;            // expert kernels: 8 waves
 constexpr int kGuRows = 128;                // intermediate rows (gate and up) per gate/up workgroup
 constexpr int kGuTiles = kInner / kGuRows;  // 4 gate/up tiles per expert
 constexpr int kGuChunk = 128;              // k per LDS chunk
 constexpr int kGuChunks = kHidden / kGuChunk;
 constexpr int kGuSteps = kGuChunk / 32;    // MFMA k-steps (and A loads per lane) per chunk
 constexpr int kXsStride = kGuChunk + 8;    // LDS token row stride (bf16)
-constexpr int kDnTiles = kHidden / 128;    // 16 down tiles of 128 rows per expert
+constexpr int kDnThreads = 512;            // down workgroup: 8 waves of 16 output rows
+constexpr int kDnRows = kDnThreads / kWave * 16;  // 128 output rows per down workgroup
+constexpr int kDnTiles = kHidden / kDnRows;       // 16 down tiles per expert
 constexpr int kDnTok = 64;                 // act rows per LDS pass
+constexpr int kDnPieces = kDnTok * (kInner / 8) / kDnThreads;  // 16-byte act pieces per thread per pass
 constexpr int kActStride = kInner + 8;     // LDS act row stride (bf16)
 
 // ---- plan ----------------------------------------------------------------------
@@ -368,7 +370,7 @@ __global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
     }
 }
 
-__global__ __launch_bounds__(kPfThreads, 1) void pf_down(ExpertArgs a) {
+__global__ __launch_bounds__(kDnThreads, 1) void pf_down(ExpertArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t as[];  // [kDnTok][kActStride]
     int ui, tile;
     unit_tile(blockIdx.x, kDnTiles, ui, tile);
@@ -379,7 +381,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void pf_down(ExpertArgs a) {
     const int lane = tid & 63;
     const int m = lane & 15;
     const int g = lane >> 4;
-    const int h0 = 128 * tile + 16 * wave;
+    const int h0 = kDnRows * tile + 16 * wave;
     // The tile's 16 rows x 512 of this wave, kept in registers for every pass.
     const uint16_t* arow = w.down + static_cast<size_t>(h0 + m) * kInner + 8 * g;
     uint4 ab[kInner / 32];
@@ -387,19 +389,19 @@ __global__ __launch_bounds__(kPfThreads, 1) void pf_down(ExpertArgs a) {
     for (int s = 0; s < kInner / 32; ++s) ab[s] = ldg16(arow + 32 * s);
     for (int q0 = 0; q0 < w.count; q0 += kDnTok) {
         const int nt = min(kDnTok, w.count - q0);
-        // Stage act rows q0..q0+63 (64 x 1 KiB): thread tid moves row tid/8 + 64*?.. 8 pieces.
-        uint4 st[8];
+        // Stage act rows q0..q0+kDnTok-1 (1 KiB each, 64 pieces of 16 bytes).
+        uint4 st[kDnPieces];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int idx = tid + kPfThreads * j;   // 0..4095 16-byte pieces
+        for (int j = 0; j < kDnPieces; ++j) {
+            const int idx = tid + kDnThreads * j;
             const int r = idx / 64;
             const int rr = r < nt ? r : 0;
             st[j] = ldg16(a.ws.act + static_cast<size_t>(w.pair0 + q0 + rr) * kInner + 8 * (idx % 64));
         }
         if (q0 > 0) __syncthreads();  // previous pass done with the LDS rows
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int idx = tid + kPfThreads * j;
+        for (int j = 0; j < kDnPieces; ++j) {
+            const int idx = tid + kDnThreads * j;
             *reinterpret_cast<uint4*>(as + (idx / 64) * kActStride + 8 * (idx % 64)) = st[j];
         }
         __syncthreads();
@@ -461,7 +463,7 @@ hipError_t launch_prefill_experts(const ExpertArgs& a, hipStream_t stream) {
     LRMOE_LAUNCH(pf_gateup, dim3(units * kGuTiles), dim3(kGuThreads), prefill_gateup_lds(), stream, gate_ev.start,
                  gate_ev.stop, a);
     const StageEvents down_ev = timing_events(kStageDown);
-    LRMOE_LAUNCH(pf_down, dim3(units * kDnTiles), dim3(kPfThreads), prefill_down_lds(), stream, down_ev.start,
+    LRMOE_LAUNCH(pf_down, dim3(units * kDnTiles), dim3(kDnThreads), prefill_down_lds(), stream, down_ev.start,
                  down_ev.stop, a);
     return hipGetLastError();
 }
