@@ -792,15 +792,16 @@ hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
     int device = 0;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return err;
+    // Per device: CU count, and whether the LDS limit and occupancy were set up.
     static int cus[64] = {0};
-    static bool lds_opt_in = false;
+    static bool lds_opt_in[64] = {false};
     if (device < 0 || device >= 64) return hipErrorInvalidDevice;
     if (cus[device] == 0) {
         err = hipDeviceGetAttribute(&cus[device], hipDeviceAttributeMultiprocessorCount, device);
         if (err != hipSuccess) return err;
     }
     const size_t lds = decode_lds_bytes(a.tokens);
-    if (!lds_opt_in) {
+    if (!lds_opt_in[device]) {
         err = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_decode), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(decode_lds_bytes(kMaxT)));
         if (err != hipSuccess) return err;
@@ -808,7 +809,7 @@ hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
         err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, moe_decode, kThreads, decode_lds_bytes(kMaxT));
         if (err != hipSuccess) return err;
         if (blocks < 1) return hipErrorLaunchOutOfResources;
-        lds_opt_in = true;
+        lds_opt_in[device] = true;
     }
     // One workgroup per CU: all of them are resident at once, which the
     // item waits rely on.  The first items name at most 8 slots (G <= 256).

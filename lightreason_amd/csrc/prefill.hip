@@ -447,8 +447,12 @@ hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in
 }
 
 hipError_t launch_prefill_experts(const ExpertArgs& a, hipStream_t stream) {
-    static bool attrs = false;
-    if (!attrs) {
+    int device = 0;
+    hipError_t dev_err = hipGetDevice(&device);
+    if (dev_err != hipSuccess) return dev_err;
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    static bool attrs[64] = {false};  // per device: dynamic LDS limits raised
+    if (!attrs[device]) {
         hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gateup),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(prefill_gateup_lds()));
@@ -456,7 +460,7 @@ hipError_t launch_prefill_experts(const ExpertArgs& a, hipStream_t stream) {
         err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_down), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(prefill_down_lds()));
         if (err != hipSuccess) return err;
-        attrs = true;
+        attrs[device] = true;
     }
     const int units = (max_units(a.tokens) + 7) / 8 * 8;
     const StageEvents gate_ev = timing_events(kStageGateUp);
