@@ -9,7 +9,9 @@ not Infinity-Cache resident; the steps run as HIP-graph replays.
 
 Also reported under "configs": T=1 decode layer with the router (latency and
 GB/s), the raw expert gather at T in {1,4,8,16}, the 40-layer decode chain
-with RMSNorm + residual at T=1 and T=16, and the T=2048 prefill (TFLOPS).
+with RMSNorm + residual at T=1 and T=16 (one persistent launch, and for
+comparison one launch per layer in a graph), and the T=2048 prefill
+(TFLOPS).
 
 `roofline` is for moe_decode, the one kernel of the headline step, timed
 with HIP events stamped by its own dispatches; `cpu_baseline` is the reference CPU expert
@@ -37,7 +39,7 @@ sys.path.insert(0, str(ROOT))
 from lightreason_amd import _native  # noqa: E402
 from lightreason_amd.moe import (EXPERT_BYTES, EXPERT_ELEMENTS, GATE_UP_ELEMENTS, HIDDEN, INNER, LayerWeights,  # noqa: E402
                                  Workspace,
-                                 gather, moe_layer)
+                                 gather, moe_chain, moe_layer)
 from lightreason_amd.synthetic import SyntheticModel  # noqa: E402
 
 METRIC = "MoE layer µs + HBM GB/s vs peak at T=1,8; prefill BF16 TFLOPS at T=2048"
@@ -130,7 +132,7 @@ class Case:
     """One workload: per-layer static inputs and outputs, run as one graph
     that steps through the layers in order."""
 
-    def __init__(self, model, tokens, *, logits=None, norm=False, chain=False, layers=None):
+    def __init__(self, model, tokens, *, logits=None, norm=False, chain=False, layers=None, one_launch=False):
         self.model = model
         self.tokens = tokens
         self.layer_ids = list(range(len(model.layers))) if layers is None else layers
@@ -138,15 +140,21 @@ class Case:
         self.ws = Workspace(device, tokens)
         self.x = [model.hidden(tokens, step=100 + i) for i in self.layer_ids]
         self.out = [torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=device) for _ in self.layer_ids]
-        self.idx = [torch.empty((tokens, 8), dtype=torch.int64, device=device) for _ in self.layer_ids]
+        self.idx_all = torch.empty((len(self.layer_ids), tokens, 8), dtype=torch.int64, device=device)
+        self.idx = list(self.idx_all)
         self.logits = logits
         self.chain = chain
+        self.one_launch = one_launch
         self.layers = []
         for i in self.layer_ids:
             base = model.layers[i]
             self.layers.append(LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None}))
 
     def run(self):
+        if self.one_launch:
+            # The whole stack as persistent chain launches (48 layers each).
+            moe_chain(self.x[0], self.layers, out=self.out[-1], indices=self.idx_all, workspace=self.ws)
+            return
         for j, layer in enumerate(self.layers):
             x = self.out[j - 1] if (self.chain and j > 0) else self.x[j]
             moe_layer(x, layer, out=self.out[j], indices=self.idx[j],
@@ -413,14 +421,18 @@ def main() -> int:
     # ---- C3: 40-layer chain with RMSNorm + residual ----
     if "c3" in only:
         for T in (1, 16):
-            c3 = Case(model, T, norm=True, chain=True)
-            u3 = c3.unique_counts()
-            ms3 = bench_case(c3, max(2, replays // 2), 1)
-            b3 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u3)
-            configs[f"c3_chain_t{T}"] = dict(layers=L, ms_per_step=round(ms3, 4), gbs=round(b3 / (ms3 * 1e-3) / 1e9, 1),
-                                             frac_hbm=round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                             mean_unique=round(float(np.mean(u3)), 1))
-            log(f"[bench] C3 T={T}: {ms3:.3f} ms/step over {L} layers, {configs[f'c3_chain_t{T}']['gbs']} GB/s")
+            for one_launch in (True, False):
+                c3 = Case(model, T, norm=True, chain=True, one_launch=one_launch)
+                u3 = c3.unique_counts()
+                ms3 = bench_case(c3, max(2, replays // 2), 1)
+                b3 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u3)
+                key = f"c3_chain_t{T}" if one_launch else f"c3_layer_graph_t{T}"
+                configs[key] = dict(layers=L, ms_per_step=round(ms3, 4), gbs=round(b3 / (ms3 * 1e-3) / 1e9, 1),
+                                    frac_hbm=round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                    mean_unique=round(float(np.mean(u3)), 1),
+                                    launches="one persistent launch" if one_launch else "one per layer, in a graph")
+                log(f"[bench] C3 T={T} {'chain' if one_launch else 'per-layer'}: {ms3:.3f} ms/step over {L} layers, "
+                    f"{configs[key]['gbs']} GB/s")
 
     # ---- C4: T=2048 prefill with skewed routing ----
     if "c4" in only:

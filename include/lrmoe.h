@@ -125,6 +125,36 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
                     uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* Several MoE decode layers (tokens <= 16) chained in one persistent launch:
+ * h_0 = hidden, h_{l+1} = MoE layer l applied to h_l exactly as
+ * lrmoe_moe_layer with that layer's router and weights, out = h_layers
+ * (out must not overlap hidden).  layer_table is a HOST array
+ * [layers][LRMOE_CHAIN_PTRS] of device addresses per layer, in the order of
+ * the LRMOE_CHAIN_* indices below: the router (required), the expert
+ * address table (required), the shared expert's gate_proj, up_proj,
+ * down_proj and shared_expert_gate (all four or none), the RMSNorm weight
+ * (0 = no norm and no residual add); the last entry is unused.  The table is
+ * copied into the launch, so it may be freed or changed once the call has
+ * returned (also while a stream is captured).  layers <=
+ * LRMOE_CHAIN_MAX_LAYERS; longer stacks take several calls.  indices_out /
+ * weights_out may be NULL, else [layers][T][8].  Replaces the MoE halves of
+ * the 40 Qwen3_5MoeDecoderLayer.forward calls of one decode step ([HF]
+ * 834-875: the post-attention RMSNorm 801-818, Qwen3_5MoeSparseMoeBlock.forward
+ * 787-798, the residual add 875), which the reference replays as one
+ * captured graph per step (edge35b/packed_native.py:58-63). */
+#define LRMOE_CHAIN_PTRS 8
+#define LRMOE_CHAIN_MAX_LAYERS 48
+#define LRMOE_CHAIN_ROUTER 0
+#define LRMOE_CHAIN_EXPERTS 1
+#define LRMOE_CHAIN_SHARED_GATE_PROJ 2
+#define LRMOE_CHAIN_SHARED_UP_PROJ 3
+#define LRMOE_CHAIN_SHARED_DOWN_PROJ 4
+#define LRMOE_CHAIN_SHARED_EXPERT_GATE 5
+#define LRMOE_CHAIN_NORM 6
+int lrmoe_moe_chain(const uint16_t *hidden, int tokens, int layers, const int64_t *layer_table, float eps,
+                    uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
 /* Raw BF16 row gather: for row < *count and bank b < banks, copy sizes[b]
  * bytes from descriptors[(b*experts + src_ids[row])*3] to
  * destinations[b] + dst_ids[row]*sizes[b]; a descriptor whose second field is

@@ -21,6 +21,9 @@ STATUS_BAD_EXPERT = 1
 STATUS_REPEATED_EXPERT = 2
 STATUS_CODEC_ROW = 4
 
+CHAIN_PTRS = 8           # int64 addresses per layer in a chain's layer table
+CHAIN_MAX_LAYERS = 48    # layers per lrmoe_moe_chain call
+
 _P = C.c_void_p
 _I = C.c_int
 _SIGNATURES = {
@@ -32,6 +35,7 @@ _SIGNATURES = {
     "lrmoe_bucket": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_experts": ([_P, _I, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
+    "lrmoe_moe_chain": ([_P, _I, _I, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_gather": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "lrmoe_matvec": ([_P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "lrmoe_ordered_sum": ([_P, _P, _P, _P, _P, _I, _P], _I),

@@ -207,6 +207,50 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
     return status_of(lrmoe::launch_experts(a, s));
 }
 
+int lrmoe_moe_chain(const uint16_t* hidden, int tokens, int layers, const int64_t* layer_table, float eps,
+                    uint16_t* out, int64_t* indices_out, uint16_t* weights_out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    static_assert(lrmoe::kChainMaxLayers == LRMOE_CHAIN_MAX_LAYERS, "chain layer limit");
+    if (tokens < 0 || tokens > lrmoe::kDecodeMaxTokens || layers < 0 || layers > LRMOE_CHAIN_MAX_LAYERS)
+        return LRMOE_E_ARG;
+    if (tokens == 0 || layers == 0) return LRMOE_OK;
+    if (!hidden || !layer_table || !out || !workspace) return LRMOE_E_ARG;
+    if (workspace_bytes < lrmoe::workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    lrmoe::ChainArgs c{};
+    for (int l = 0; l < layers; ++l) {
+        const int64_t* row = layer_table + static_cast<size_t>(l) * LRMOE_CHAIN_PTRS;
+        auto at = [&](int i) { return reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(row[i])); };
+        lrmoe::ChainLayer& w = c.layer[l];
+        w.router = at(LRMOE_CHAIN_ROUTER);
+        w.expert_ptrs = reinterpret_cast<const int64_t*>(at(LRMOE_CHAIN_EXPERTS));
+        w.sh_gate = at(LRMOE_CHAIN_SHARED_GATE_PROJ);
+        w.sh_up = at(LRMOE_CHAIN_SHARED_UP_PROJ);
+        w.sh_down = at(LRMOE_CHAIN_SHARED_DOWN_PROJ);
+        w.shared_expert_gate = at(LRMOE_CHAIN_SHARED_EXPERT_GATE);
+        w.norm = at(LRMOE_CHAIN_NORM);
+        if (!w.router || !w.expert_ptrs) return LRMOE_E_ARG;
+        const bool any_shared = w.sh_gate || w.sh_up || w.sh_down || w.shared_expert_gate;
+        const bool all_shared = w.sh_gate && w.sh_up && w.sh_down && w.shared_expert_gate;
+        if (any_shared && !all_shared) return LRMOE_E_ARG;
+    }
+    if (int d = check_device()) return d;
+    const Workspace ws = lrmoe::carve(workspace, tokens);
+    c.base.eps = eps;
+    c.base.indices_out = indices_out;
+    c.base.weights_out = weights_out;
+    c.base.logits = ws.logits;
+    c.base.act = ws.dact;
+    c.base.y = ws.dy;
+    c.base.sync = ws.sync;
+    c.base.status = ws.plan.status;
+    c.base.tokens = tokens;
+    c.hidden = hidden;
+    c.out = out;
+    c.inner = ws.chain;
+    c.layers = layers;
+    return status_of(lrmoe::launch_moe_chain(c, as_stream(stream)));
+}
+
 int lrmoe_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
                  const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
                  int max_copies, int stripes, int threads, int keep_in_l2, int32_t* status, void* stream) {

@@ -103,12 +103,23 @@ __device__ __forceinline__ uint32_t add_agent32(void* p, uint32_t v) {
     return __hip_atomic_fetch_add(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A wave-uniform copy of a 64-bit value (each half through readfirstlane,
+// whose int result is taken as unsigned before widening).
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
 // Claims a work item: one agent-scope fetch-add by the lanes in `lanes`
 // (wave-uniform: 1 = lane 0 in the claiming wave, 0 in the others), written
 // as assembly so that no wait is tied to it.  The result is
 // valid in lane 0 once the caller's "s_waitcnt vmcnt(16)" after the next
 // prefetch has passed (returning atomics count in vmcnt, in order).
 __device__ __forceinline__ uint32_t claim_async(uint32_t* counter, uint32_t lanes) {
+    // The address operand must be scalar: pass it through readfirstlane (a
+    // uniform value computed in vector registers is not moved by itself).
+    counter = reinterpret_cast<uint32_t*>(uniform64(reinterpret_cast<uint64_t>(counter)));
     uint32_t old;
     uint64_t saved_exec;
     uint32_t mask;
@@ -127,6 +138,42 @@ __device__ __forceinline__ uint32_t claim_async(uint32_t* counter, uint32_t lane
 }
 
 __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
+
+
+// 16 bytes of token rows at base + byte_offset (base wave-uniform).  In a
+// chain, the rows were written by other workgroups of the same launch
+// (possibly through another XCD's L2), so they are read with agent-scope
+// (sc1) buffer loads.
+template <bool kChained>
+__device__ __forceinline__ uint4 ld_row16(const uint16_t* base, uint32_t byte_offset) {
+    if constexpr (kChained) {
+        // Raw buffer over 2 GiB from base; dword 3 = gfx9 untyped 32-bit data format.
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff, 0x00020000);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        constexpr int kSc1 = 16;  // cache policy: sc1 (agent scope)
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(byte_offset), 0, kSc1);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return ldg16(reinterpret_cast<const uint8_t*>(base) + byte_offset);
+    }
+}
+template <bool kChained>
+__device__ __forceinline__ uint64_t ld_row8(const uint16_t* p) {
+    if constexpr (kChained) {
+        return ld_agent64(p);
+    } else {
+        return *reinterpret_cast<const uint64_t*>(p);
+    }
+}
+template <bool kChained>
+__device__ __forceinline__ void st_row8(uint16_t* p, uint64_t v) {
+    if constexpr (kChained) {
+        st_agent64(p, v);
+    } else {
+        *reinterpret_cast<uint64_t*>(p) = v;
+    }
+}
 
 // Waits (bounded) until *counter >= target; returns false on timeout.
 __device__ bool wait_counter(const uint32_t* counter, uint32_t target) {
@@ -243,27 +290,37 @@ __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
 // threads: token tid/32, rows 4*(tid%32)..+3), then the shared-expert and
 // residual adds.  The tile's y words are reloaded (bounded) until each
 // carries this call's tag.
-__device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int tile, int T, bool shared,
+template <bool kChained>
+__device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int tid, int tile, int T, bool shared,
                                              uint32_t tag) {
-    const int tid = threadIdx.x;
     const int t = tid >> 5;
     const bool active = t < T;
     const int h = kBRows * tile + (tid & 31) * 4;
     // One pass over the pairs in combine order; it reports whether any word
     // was stale (the sums of such a pass are discarded and the pass re-run).
+    // The pass's loads are all issued before any is used, so that their
+    // latencies overlap.
     float acc[4];
     auto pass = [&]() {
         bool stale = false;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
         if (!active) return false;
+        uint64_t words[kTopK + 1][2];
+#pragma unroll
+        for (int q = 0; q <= kTopK; ++q) {
+            const int pair = q < kTopK ? P.comb_pair[t][q] : kTopK * T + t;
+            const uint64_t* row = a.y + static_cast<size_t>(pair) * (kHidden / 2) + h / 2;
+            if (q < kTopK || shared) {
+                words[q][0] = ld_agent64(row);
+                words[q][1] = ld_agent64(row + 1);
+            }
+        }
 #pragma unroll
         for (int q = 0; q <= kTopK; ++q) {
             if (q == kTopK && !shared) break;
-            const int pair = q < kTopK ? P.comb_pair[t][q] : kTopK * T + t;
-            const uint64_t* row = a.y + static_cast<size_t>(pair) * (kHidden / 2) + h / 2;
-            const uint64_t w0 = ld_agent64(row);
-            const uint64_t w1 = ld_agent64(row + 1);
+            const uint64_t w0 = words[q][0];
+            const uint64_t w1 = words[q][1];
             stale |= static_cast<uint32_t>(w0 >> kDecodeTagShift) != tag ||
                      static_cast<uint32_t>(w1 >> kDecodeTagShift) != tag;
             const uint32_t bits[4] = {static_cast<uint32_t>(w0) & 0xffffu, static_cast<uint32_t>(w0 >> 16) & 0xffffu,
@@ -291,34 +348,42 @@ __device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int t
     }
     if (active) {
         if (a.residual) {
-            const uint64_t x = *reinterpret_cast<const uint64_t*>(a.x + static_cast<size_t>(t) * kHidden + h);
+            const uint64_t x = ld_row8<kChained>(a.x + static_cast<size_t>(t) * kHidden + h);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = rbf(bf2f(static_cast<uint32_t>(x >> (16 * i)) & 0xffffu) + acc[i]);
         }
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = f2bf(acc[i]);
-        *reinterpret_cast<uint64_t*>(a.out + static_cast<size_t>(t) * kHidden + h) = pack4(o);
+        st_row8<kChained>(a.out + static_cast<size_t>(t) * kHidden + h, pack4(o));
     }
 }
 
-__global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
-    // A local copy: the helpers below take it by reference, which must not
-    // force the kernel-argument block into private memory.
-    const DecodeArgs a = args;
-    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
-    __shared__ Plan P;
+// One decode layer, run by every workgroup of the grid.  `finished` is the
+// value of DecodeSync::finished read at the start of the launch, `layer` the
+// index of this layer in the launch (0 for a single layer).  wait_input() is
+// called by every thread once the loads that do not depend on the layer
+// input are issued; it returns when the input rows are complete.  Ends with
+// all of the workgroup's memory operations complete; returns kStatusTimeout
+// when one of its bounded waits expired.
+template <bool kChained, typename WaitInput>
+__device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, uint8_t* dyn,
+                                                unsigned long long finished, int layer, WaitInput wait_input) {
     const int T = a.tokens;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int tid = threadIdx.x;
+    // Thread and workgroup indices as opaque values: what is derived from
+    // them is computed again for each layer of a chain rather than held in
+    // registers across layers.
+    int lane = static_cast<int>(threadIdx.x & 63);
+    int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    int block = static_cast<int>(blockIdx.x);
+    asm volatile("" : "+v"(lane));
+    asm volatile("" : "+s"(wave), "+s"(block));
+    const int tid = wave * kWave + lane;
     const int G = gridDim.x;
     uint16_t* x_lds = reinterpret_cast<uint16_t*>(dyn);                       // [T][kXStride]
     uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
     DecodeSync* sync = a.sync;
-    // This call's number, from the count of finished workgroups (DecodeSync).
-    const unsigned long long finished = ld_agent64(&sync->finished);
 
     // ---- 1. every load that depends on nothing, issued first ----
     // In order of need: the caller's logits rows of this wave's tokens
@@ -330,23 +395,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     const int t_hi = wave + kWaves;
     const bool has_lo = t_lo < T;
     const bool has_hi = t_hi < T;
-    const bool router_wg = a.router != nullptr && static_cast<int>(blockIdx.x) < kRouterWgs;
+    const bool router_wg = a.router != nullptr && block < kRouterWgs;
     const bool logits_given = a.logits_in != nullptr;
     const uint16_t* lg_src = logits_given ? a.logits_in : a.x;
     uint64_t lg_lo = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_lo ? t_lo : 0) * kExperts * logits_given + 4 * lane);
     uint64_t lg_hi = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_hi ? t_hi : 0) * kExperts * logits_given + 4 * lane);
     const uint4 eptr = ldg16(a.expert_ptrs + 2 * (tid & (kExperts - 1)));
-    const uint16_t* xr_lo = a.x + static_cast<size_t>(has_lo ? t_lo : 0) * kHidden + 32 * lane;
-    const uint16_t* xr_hi = a.x + static_cast<size_t>(has_hi ? t_hi : 0) * kHidden + 32 * lane;
+    const uint32_t xr_lo = static_cast<uint32_t>(((has_lo ? t_lo : 0) * kHidden + 32 * lane) * 2);
+    const uint32_t xr_hi = static_cast<uint32_t>(((has_hi ? t_hi : 0) * kHidden + 32 * lane) * 2);
     const uint16_t* nr = (a.norm != nullptr ? a.norm : a.x) + 32 * lane;
     const uint16_t* gr = (a.shared_expert_gate != nullptr ? a.shared_expert_gate : a.x) + 32 * lane;
-    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * blockIdx.x + wave) * kHidden + 32 * lane
+    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * block + wave) * kHidden + 32 * lane
                                    : a.x + 32 * lane;
     uint4 x_lo[4], x_hi[4], w_norm[4], w_sg[4], w_router[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x_lo[i] = ldg16(xr_lo + 8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x_hi[i] = ldg16(xr_hi + 8 * i);
 #pragma unroll
     for (int i = 0; i < 4; ++i) w_norm[i] = ldg16(nr + 8 * i);
 #pragma unroll
@@ -355,11 +416,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
     if (tid < kExperts) P.tokmask[tid] = 0u;
     if (tid == 0) P.status = 0;
-    const unsigned long long call = finished / static_cast<unsigned long long>(G);
+    // The layer input and the counters are touched only once the input is
+    // complete (a chain waits for the previous layer here; the loads above
+    // are already in flight).
+    wait_input();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x_lo[i] = ld_row16<kChained>(a.x, xr_lo + 16 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x_hi[i] = ld_row16<kChained>(a.x, xr_hi + 16 * i);
+    const unsigned long long call = finished / static_cast<unsigned long long>(G) + static_cast<unsigned>(layer);
     const int parity = static_cast<int>(call & 1ull);
     const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
     DecodeCounters* const cnt = &sync->set[parity];
-    if (blockIdx.x == 0) {
+    if (block == 0) {
         // The next call's counters (this call never touches them).
         DecodeCounters* const nxt = &sync->set[parity ^ 1];
         if (tid == kThreads - 1) st_agent32(&nxt->router_done, 0u);
@@ -420,7 +489,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                 uint32_t v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = P.lg[t][4 * h + i];
-                st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * blockIdx.x + 4 * h, pack4(v));
+                st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * block + 4 * h, pack4(v));
             }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
@@ -490,7 +559,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
     };
     const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
-    int cur = (static_cast<int>(blockIdx.x) - offset + G) % G;
+    int cur = (block - offset + G) % G;
     {
         const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
         const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
@@ -504,7 +573,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         issue((m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4), b0);
     }
 
-    if (blockIdx.x == 0 && tid < T * kTopK) {
+    if (block == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
     }
@@ -590,9 +659,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         P.comb_pair[t][order] = static_cast<int16_t>(p);
         P.comb_w[t][order] = bf2f(P.wts[t][k]);
     }
-    // This call's route status replaces the previous call's (timeouts are
-    // OR-ed in at the end).
-    if (blockIdx.x == 0 && tid == 0) st_agent32(a.status, static_cast<uint32_t>(P.status & ~kStatusTimeout));
+    // The route status of a launch's first layer replaces the previous
+    // launch's; later layers add theirs (timeouts are OR-ed in at the end).
+    if (block == 0 && tid == 0) {
+        const int32_t route_status = P.status & ~kStatusTimeout;
+        if (layer == 0) {
+            st_agent32(a.status, static_cast<uint32_t>(route_status));
+        } else if (route_status != 0) {
+            atomicOr(a.status, route_status);
+        }
+    }
     __syncthreads();
 
     const int n_slots = P.n_slots;
@@ -602,11 +678,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
 
     // Bad routes: the output is the residual (or zeros); no expert runs.
     if (!routes_ok) {
-        if (blockIdx.x == 0) {
+        if (block == 0) {
             for (int i = tid; i < T * kHidden / 4; i += kThreads) {
                 uint64_t v = 0;
-                if (a.residual) v = reinterpret_cast<const uint64_t*>(a.x)[i];
-                reinterpret_cast<uint64_t*>(a.out)[i] = v;
+                if (a.residual) v = ld_row8<kChained>(a.x + 4 * static_cast<size_t>(i));
+                st_row8<kChained>(a.out + 4 * static_cast<size_t>(i), v);
             }
         }
     }
@@ -740,7 +816,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
                 st_agent64(dst + 1, tag_bits | (o[2] | (o[3] << 16)));
             }
         } else {
-            combine_tile(a, P, it.tile, T, first_slot == 0, tag);
+            combine_tile<kChained>(a, P, tid, it.tile, T, first_slot == 0, tag);
             // Wave 0's claim above is visible to every wave after this.
             __syncthreads();
         }
@@ -770,12 +846,125 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
         }
     }
 
-    // ---- 5. this workgroup is finished ----
+    // ---- 5. this workgroup's share of the layer is done ----
     __builtin_amdgcn_s_waitcnt(0);  // also the first-item loads of a call without items
     __syncthreads();
-    if (tid == 0) {
-        if (P.status & kStatusTimeout) atomicOr(a.status, kStatusTimeout);
-        __hip_atomic_fetch_add(&sync->finished, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return P.status & kStatusTimeout;
+}
+
+__global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
+    // A local copy: the helpers take it by reference, which must not force
+    // the kernel-argument block into private memory.
+    const DecodeArgs a = args;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+    __shared__ Plan P;
+    // This call's number, from the count of finished workgroups (DecodeSync).
+    const unsigned long long finished = ld_agent64(&a.sync->finished);
+    const int32_t timeout = decode_layer<false>(a, P, dyn, finished, 0, [] {});
+    if (threadIdx.x == 0) {
+        if (timeout) atomicOr(a.status, kStatusTimeout);
+        __hip_atomic_fetch_add(&a.sync->finished, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Launch-wide values of a chain, kept in LDS: only the layer index stays
+// in registers across layers.
+struct ChainState {
+    unsigned long long finished;  // DecodeSync::finished at the start
+    unsigned long long arrived;   // chain_arrive at the start, rounded down to a multiple of G
+    int32_t timeout;
+};
+
+// Several decode layers in one launch, with a grid barrier between layers
+// (every workgroup is resident).  Layer l is decode call c + l, with c the
+// call number read at the start (DecodeSync).
+__global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+    __shared__ Plan P;
+    __shared__ ChainState S;
+    const unsigned long long G = gridDim.x;
+    if (threadIdx.x == 0) {
+        S.finished = ld_agent64(&args.base.sync->finished);
+        S.arrived = ld_agent64(&args.base.sync->chain_arrive) / G * G;
+        S.timeout = 0;
+    }
+    __syncthreads();
+    for (int layer = 0;; ++layer) {
+        const int l = __builtin_amdgcn_readfirstlane(layer);
+        // The arguments are read again for every layer (an opaque copy of
+        // their address), so that they are not held in registers across
+        // the layer.
+        typedef const __attribute__((address_space(4))) ChainArgs KernelArgs;
+        KernelArgs* cp = (KernelArgs*)(__builtin_amdgcn_kernarg_segment_ptr());
+        asm volatile("" : "+s"(cp));
+        KernelArgs& c = *cp;
+        if (l >= c.layers) break;
+        const int T = c.base.tokens;
+        DecodeArgs a{};
+        a.eps = c.base.eps;
+        a.logits = c.base.logits;
+        a.act = c.base.act;
+        a.y = c.base.y;
+        a.sync = c.base.sync;
+        a.status = c.base.status;
+        a.tokens = T;
+        const auto& w = c.layer[l];
+        a.router = w.router;
+        a.expert_ptrs = w.expert_ptrs;
+        a.sh_gate = w.sh_gate;
+        a.sh_up = w.sh_up;
+        a.sh_down = w.sh_down;
+        a.shared_expert_gate = w.shared_expert_gate;
+        a.norm = w.norm;
+        // The chain always routes with the layer's router.
+        a.logits_in = nullptr;
+        a.indices_in = nullptr;
+        a.weights_in = nullptr;
+        a.residual = w.norm != nullptr;
+        a.x = l == 0 ? c.hidden : c.inner + static_cast<size_t>((l - 1) & 1) * T * kHidden;
+        a.out = l == c.layers - 1 ? c.out : c.inner + static_cast<size_t>(l & 1) * T * kHidden;
+        a.indices_out = c.base.indices_out != nullptr ? c.base.indices_out + static_cast<size_t>(l) * T * kTopK : nullptr;
+        a.weights_out = c.base.weights_out != nullptr ? c.base.weights_out + static_cast<size_t>(l) * T * kTopK : nullptr;
+        const unsigned long long finished = uniform64(S.finished);
+        DecodeSync* const sync = c.base.sync;
+        // Arrivals completed by the barrier before layer l.
+        const unsigned long long target = S.arrived + G * static_cast<unsigned long long>(l);
+        auto wait_input = [&] {
+            // Grid barrier before every layer but the first: the previous
+            // layer's output rows are all written.
+            if (l > 0) {
+                if (threadIdx.x == 0) {
+                    const uint64_t start = now_ticks();
+                    while (ld_agent64(&sync->chain_release) < target) {
+                        if (now_ticks() - start > kSpinTicks) {
+                            S.timeout = kStatusTimeout;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                }
+                __syncthreads();
+            }
+        };
+        const int32_t timeout = decode_layer<true>(a, P, dyn, finished, l, wait_input);
+        if (threadIdx.x == 0) {
+            S.timeout |= timeout;
+            if (l + 1 < c.layers) {
+                // Arrival: this workgroup's output rows are written (agent
+                // scope, waited for at the end of the layer).  The arrival
+                // that completes the barrier releases the others.
+                const unsigned long long next = target + G;
+                const unsigned long long before =
+                    __hip_atomic_fetch_add(&sync->chain_arrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (before + 1 == next) st_agent64(&sync->chain_release, next);
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        if (S.timeout) atomicOr(args.base.status, kStatusTimeout);
+        __hip_atomic_fetch_add(&args.base.sync->finished, static_cast<unsigned long long>(args.layers),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -786,36 +975,68 @@ size_t decode_lds_bytes(int tokens) {
            2 * kWaves * kWave * sizeof(f32x4);
 }
 
-hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
-    if (a.tokens <= 0) return hipSuccess;
-    if (a.tokens > kMaxT) return hipErrorInvalidValue;
+namespace {
+
+// Per device and kernel: the CU count, and whether the LDS limit was raised
+// and the occupancy checked.
+struct LaunchSetup {
+    int cus = 0;
+    bool ready = false;
+};
+
+// Grid size of a persistent decode launch on the current device (one
+// workgroup per CU, all resident at once, which the cross-workgroup waits
+// rely on).
+template <typename Kernel>
+hipError_t persistent_grid(Kernel kernel, LaunchSetup (&setup)[64], int* grid) {
     int device = 0;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return err;
-    // Per device: CU count, and whether the LDS limit and occupancy were set up.
-    static int cus[64] = {0};
-    static bool lds_opt_in[64] = {false};
     if (device < 0 || device >= 64) return hipErrorInvalidDevice;
-    if (cus[device] == 0) {
-        err = hipDeviceGetAttribute(&cus[device], hipDeviceAttributeMultiprocessorCount, device);
+    LaunchSetup& d = setup[device];
+    if (d.cus == 0) {
+        err = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, device);
         if (err != hipSuccess) return err;
     }
-    const size_t lds = decode_lds_bytes(a.tokens);
-    if (!lds_opt_in[device]) {
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_decode), hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (!d.ready) {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   static_cast<int>(decode_lds_bytes(kMaxT)));
         if (err != hipSuccess) return err;
         int blocks = 0;
-        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, moe_decode, kThreads, decode_lds_bytes(kMaxT));
+        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, decode_lds_bytes(kMaxT));
         if (err != hipSuccess) return err;
         if (blocks < 1) return hipErrorLaunchOutOfResources;
-        lds_opt_in[device] = true;
+        d.ready = true;
     }
-    // One workgroup per CU: all of them are resident at once, which the
-    // item waits rely on.  The first items name at most 8 slots (G <= 256).
-    if (cus[device] > kExperts) return hipErrorNotSupported;
+    // The first items name at most 8 slots (G <= 256).
+    if (d.cus > kExperts) return hipErrorNotSupported;
+    *grid = d.cus;
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
+    if (a.tokens <= 0) return hipSuccess;
+    if (a.tokens > kMaxT) return hipErrorInvalidValue;
+    static LaunchSetup setup[64];
+    int grid = 0;
+    const hipError_t err = persistent_grid(moe_decode, setup, &grid);
+    if (err != hipSuccess) return err;
     const StageEvents ev = timing_events(kStageLayer);
-    LRMOE_LAUNCH(moe_decode, dim3(cus[device]), dim3(kThreads), lds, stream, ev.start, ev.stop, a);
+    LRMOE_LAUNCH(moe_decode, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start, ev.stop, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_chain(const ChainArgs& a, hipStream_t stream) {
+    if (a.base.tokens <= 0 || a.layers <= 0) return hipSuccess;
+    if (a.base.tokens > kMaxT) return hipErrorInvalidValue;
+    static LaunchSetup setup[64];
+    int grid = 0;
+    const hipError_t err = persistent_grid(moe_chain, setup, &grid);
+    if (err != hipSuccess) return err;
+    const StageEvents ev = timing_events(kStageLayer);
+    LRMOE_LAUNCH(moe_chain, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start, ev.stop, a);
     return hipGetLastError();
 }
 

@@ -38,9 +38,22 @@ struct DecodeCounters {
 // set[(c + 1) % 2] for the next call, so nothing is reset at the end of a
 // call and a zero-initialised workspace is valid.  The call number also tags
 // the rows one workgroup writes for another (see kDecodeTagShift).
+// A chain launch (several layers in one grid) numbers its layers c, c + 1,
+// ... and adds its layer count per workgroup to `finished` at its end.
+// `chain_arrive` counts workgroup arrivals at the grid barriers between a
+// chain's layers and is never reset: a chain launch reads it at its start and
+// rounds down to a multiple of G, since at most G - 1 of its own workgroups
+// can have arrived at its first barrier by then.  The workgroup whose arrival
+// completes a barrier stores the arrival count it completed in
+// `chain_release`, which the others poll (a word that takes no atomics:
+// polling the arrival counter itself slows the other workgroups' traffic).
 struct DecodeSync {
     unsigned long long finished;
     uint32_t pad0[kSyncStride - 2];
+    unsigned long long chain_arrive;
+    uint32_t pad1[kSyncStride - 2];
+    unsigned long long chain_release;
+    uint32_t pad2[kSyncStride - 2];
     DecodeCounters set[2];
 };
 
@@ -90,6 +103,7 @@ struct Workspace {
     uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
     uint64_t* dact;       // decode: act as tagged words, [9*16 + 16][256]
     uint64_t* dy;         // decode: y as tagged words, [9*16][1024]
+    uint16_t* chain;      // decode chain: [2][T][2048] outputs of the inner layers
     uint32_t* counts;     // [256] prefill: pairs per expert
     DecodeSync* sync;     // decode kernel counters
     uint8_t* bmask;       // prefill: [256][nblk_pad] token masks per 8-token block
@@ -135,6 +149,7 @@ inline Workspace carve(void* base, int tokens) {
     ws.act = reinterpret_cast<uint16_t*>(take((P + T + 16) * 512 * 2));
     ws.y = reinterpret_cast<uint16_t*>(take((P + T) * 2048 * 2));
 
+    ws.chain = reinterpret_cast<uint16_t*>(take(2 * T * 2048 * 2));
     ws.counts = reinterpret_cast<uint32_t*>(take(256 * 4));
     const size_t nblk = (T + 7) / 8;
     const size_t nblk_pad = (nblk + 15) / 16 * 16;
@@ -216,6 +231,30 @@ struct DecodeArgs {
     int residual;                 // out = x + MoE(...) (decoder layer with norm)
 };
 
+// A chain of decode layers in one launch.  Layer l reads the previous
+// layer's output (layer 0 the caller's rows) and, when it is not the last,
+// writes the next one's input to a workspace buffer.  The per-layer weight
+// addresses travel in the kernel arguments.
+struct ChainLayer {
+    const uint16_t* router;              // [256][2048]
+    const int64_t* expert_ptrs;          // [256][2] (gate_up, down)
+    const uint16_t* sh_gate;             // shared expert [512][2048], or null (no shared expert)
+    const uint16_t* sh_up;               // [512][2048]
+    const uint16_t* sh_down;             // [2048][512]
+    const uint16_t* shared_expert_gate;  // [2048]
+    const uint16_t* norm;                // [2048] RMSNorm weight, or null (no norm, no residual)
+};
+constexpr int kChainMaxLayers = 48;  // the arguments stay under 4 KiB
+struct ChainArgs {
+    DecodeArgs base;              // tokens, eps, workspace buffers, status; per-layer fields unset
+    const uint16_t* hidden;       // [T][2048] input of layer 0
+    uint16_t* out;                // [T][2048] output of the last layer
+    uint16_t* inner;              // [2][T][2048] outputs of the inner layers (ping-pong)
+    int layers;
+    ChainLayer layer[kChainMaxLayers];
+};
+static_assert(sizeof(ChainArgs) <= 4096, "chain kernel arguments must stay under 4 KiB");
+
 // Optional per-stage timing.  When a stage's bit is enabled, timing_events()
 // hands out the next (start, stop) event pair of that stage; the stage's
 // first kernel is launched with the start event and its last kernel with the
@@ -268,6 +307,7 @@ hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const
                                 uint16_t* out, int tokens, int hybrid, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
 hipError_t launch_moe_decode(const DecodeArgs& args, hipStream_t stream);
+hipError_t launch_moe_chain(const ChainArgs& args, hipStream_t stream);
 // Prefill plan (T > 16): top-8 from `logits` (or the validated caller indices)
 // and the bucketing plan with its work units.
 hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in, const uint16_t* weights_in,

@@ -12,6 +12,7 @@ Expert weights live in an :class:`ExpertBank`: one HBM allocation holding
 
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import torch
@@ -22,6 +23,7 @@ HIDDEN = 2048
 INNER = 512
 EXPERTS = 256
 TOPK = 8
+DECODE_MAX_TOKENS = 16  # token counts of the one-launch decode layer and chain
 EXPERT_ELEMENTS = 3 * INNER * HIDDEN
 GATE_UP_ELEMENTS = 2 * INNER * HIDDEN
 EXPERT_BYTES = 2 * EXPERT_ELEMENTS
@@ -275,6 +277,65 @@ def moe_layer(hidden: torch.Tensor, layer: LayerWeights, *, out: torch.Tensor | 
                  _opt(layer.shared_gate_proj), _opt(layer.shared_up_proj), _opt(layer.shared_down_proj),
                  _opt(layer.shared_expert_gate), _opt(layer.norm_weight), float(layer.eps), out.data_ptr(),
                  _opt(indices), _opt(weights), ws.ptr, ws.nbytes, _stream(device))
+    return out
+
+
+def chain_table(layers) -> "C.Array":
+    """Host layer table of lrmoe_moe_chain: per layer the router, the expert
+    address table, the shared expert's gate/up/down projections and gate row
+    (0 when absent) and the RMSNorm weight (0 for none)."""
+    table = (C.c_int64 * (_native.CHAIN_PTRS * len(layers)))()
+    for l, w in enumerate(layers):
+        row = [w.router.data_ptr(), w.expert_ptrs.data_ptr(), _opt(w.shared_gate_proj), _opt(w.shared_up_proj),
+               _opt(w.shared_down_proj), _opt(w.shared_expert_gate), _opt(w.norm_weight), 0]
+        for i, v in enumerate(row):
+            table[_native.CHAIN_PTRS * l + i] = v or 0
+    return table
+
+
+def moe_chain(hidden: torch.Tensor, layers, *, out: torch.Tensor | None = None, indices: torch.Tensor | None = None,
+              weights: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """Decode (T <= 16) through a stack of MoE layers in persistent launches
+    of up to 48 layers each: h = moe_layer(h, layer) for every layer in
+    order, with results identical to those successive calls.  ``indices`` /
+    ``weights``, when given, receive every layer's routes ([L, T, 8])."""
+    tokens = hidden.shape[0]
+    device = hidden.device
+    layers = list(layers)
+    _check(hidden, "hidden", torch.bfloat16, (tokens, HIDDEN))
+    if not 0 < tokens <= DECODE_MAX_TOKENS:
+        raise ValueError(f"moe_chain takes 1..{DECODE_MAX_TOKENS} tokens, got {tokens}")
+    if not layers:
+        raise ValueError("moe_chain needs at least one layer")
+    for w in layers:
+        w.check(device)
+    eps = {float(w.eps) for w in layers}
+    if len(eps) != 1:
+        raise ValueError("all layers of a chain use one RMSNorm eps")
+    if indices is not None:
+        _check(indices, "indices", torch.int64, (len(layers), tokens, TOPK), device)
+    if weights is not None:
+        _check(weights, "weights", torch.bfloat16, (len(layers), tokens, TOPK), device)
+    ws = workspace.ensure(tokens) if workspace is not None else default_workspace(device, tokens)
+    if out is None:
+        out = torch.empty_like(hidden)
+    else:
+        _check(out, "out", torch.bfloat16, (tokens, HIDDEN), device)
+    step = _native.CHAIN_MAX_LAYERS
+    groups = [layers[i:i + step] for i in range(0, len(layers), step)]
+    # Stacks longer than one call pass their rows between calls through two
+    # scratch buffers; the last call writes `out`.
+    inner = [torch.empty_like(hidden) for _ in range(min(len(groups) - 1, 2))]
+    src = hidden
+    for g, group in enumerate(groups):
+        dst = out if g == len(groups) - 1 else inner[g % 2]
+        first = g * step
+        table = chain_table(group)  # held until the call returns (the launch copies it)
+        _native.call("lrmoe_moe_chain", src.data_ptr(), tokens, len(group), C.addressof(table),
+                     float(layers[0].eps), dst.data_ptr(),
+                     None if indices is None else indices[first].data_ptr(),
+                     None if weights is None else weights[first].data_ptr(), ws.ptr, ws.nbytes, _stream(device))
+        src = dst
     return out
 
 

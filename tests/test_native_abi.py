@@ -70,6 +70,21 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_project(dummy, dummy, dummy, dummy, 2048, 1000, 0, 4, null) == -1
     assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 0, 2, 8, 64, 256, 0, null, null) == -1
     assert lib.lrmoe_gather(dummy, dummy, dummy, dummy, dummy, dummy, 8, 2, 8, 64, 100, 0, null, null) == -1
+    # chain: more than 16 tokens, more than 48 layers per call, a layer
+    # without a router, or only some of the shared-expert tensors: refused
+    big = 1 << 30
+    table = (C.c_int64 * 8)(16, 16, 16, 16, 16, 16, 0, 0)
+    for tokens, layers, entry in ((17, 1, None), (1, 49, None), (1, 1, (0, 0)), (1, 1, (4, 0))):
+        t = (C.c_int64 * (8 * max(layers, 1)))()
+        for l in range(layers):
+            for i in range(8):
+                t[8 * l + i] = table[i]
+        if entry is not None:
+            t[entry[0]] = entry[1]
+        assert lib.lrmoe_moe_chain(dummy, tokens, layers, t, C.c_float(1e-6), dummy, null, null, dummy, big,
+                                   null) == -1, (tokens, layers, entry)
+    assert lib.lrmoe_moe_chain(dummy, 1, 1, table, C.c_float(1e-6), dummy, null, null, dummy, 8, null) == -2
+    assert lib.lrmoe_moe_chain(dummy, 1, 0, table, C.c_float(1e-6), dummy, null, null, dummy, 8, null) == 0
     # zero tokens is a successful no-op
     assert lib.lrmoe_moe_experts(dummy, 0, dummy, dummy, dummy, dummy, dummy, 0, null) == 0
     from lightreason_amd import _native
