@@ -61,6 +61,8 @@ constexpr int kActStride = kInner + 8;        // LDS act row stride (bf16)
 constexpr int kLoads = 16;                    // 16-byte weight loads per lane per item
 constexpr int kCombineItems = kBTiles;        // C items, one per 128-row output tile
 constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
+// gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14.
+constexpr int kWaitVm16 = (16 & 15) | (7 << 4) | (15 << 8) | ((16 >> 4) << 14);
 
 // ---- agent-scope memory operations (coherent across XCDs) -------------------
 
@@ -217,7 +219,26 @@ struct Plan {
     int32_t first_slot;               // 0 with a shared expert, else 1
     int32_t status;
     int32_t claim[2];                 // claimed item index, by step parity
+    uint32_t vote[2][kWaves];         // block_or: per-wave votes, two alternating rows
 };
+
+// Block-wide OR of a predicate.  Every thread of the workgroup calls it, in
+// the same order, with the same `row` (flipped by each call).  A wave ballot
+// and one LDS word per wave, then one barrier: a row is written again only
+// two votes later, after a barrier that every thread reaches once it has read
+// the row.  (__syncthreads_or reads the workgroup size from the dispatch
+// packet with vector loads; the wait for those also waits for every older
+// load in flight, such as the next item's prefetch.)
+__device__ __forceinline__ bool block_or(bool pred, Plan& P, int& row, int wave, int lane) {
+    const uint64_t ballot = __ballot(pred);
+    if (lane == 0) P.vote[row][wave] = ballot != 0ull ? 1u : 0u;
+    __syncthreads();
+    uint32_t any = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) any |= P.vote[row][w];
+    row ^= 1;
+    return any != 0u;
+}
 
 // Dot of a lane's 32 contiguous elements (4 x 16 bytes) with the same
 // elements of an LDS row, as an in-order fmaf chain from +0.
@@ -292,7 +313,9 @@ __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
 // carries this call's tag.
 template <bool kChained>
 __device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int tid, int tile, int T, bool shared,
-                                             uint32_t tag) {
+                                             uint32_t tag, int& vote_row) {
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
     const int t = tid >> 5;
     const bool active = t < T;
     const int h = kBRows * tile + (tid & 31) * 4;
@@ -335,15 +358,15 @@ __device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int t
         }
         return stale;
     };
-    if (__syncthreads_or(pass())) {
+    if (block_or(pass(), P, vote_row, wave, lane)) {
         const uint64_t start = now_ticks();
         while (true) {
-            if (__syncthreads_or(now_ticks() - start > kSpinTicks)) {
+            if (block_or(now_ticks() - start > kSpinTicks, P, vote_row, wave, lane)) {
                 if (tid == 0) P.status |= kStatusTimeout;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
-            if (!__syncthreads_or(pass())) break;
+            if (!block_or(pass(), P, vote_row, wave, lane)) break;
         }
     }
     if (active) {
@@ -700,6 +723,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     const uint64_t tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
+    int vote_row = 0;         // block_or row
 
     auto weights_of = [&](const Item& it) -> const uint16_t* {
         return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
@@ -730,7 +754,10 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         __builtin_amdgcn_sched_barrier(0);
         issue(np, nbuf);
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        // s_waitcnt vmcnt(16) (expcnt and lgkmcnt left at their maximum)
+        // as a builtin, so that the compiler's own wait insertion knows
+        // what it completed.
+        __builtin_amdgcn_s_waitcnt(kWaitVm16);
         __builtin_amdgcn_sched_barrier(0);
         if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + 2 * G;
         const int m = lane & 15;
@@ -744,10 +771,10 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             bool stale = false;
 #pragma unroll
             for (int i = 0; i < 8; ++i) stale |= used && stale_word(stg[i]);
-            if (__syncthreads_or(stale)) {
+            if (block_or(stale, P, vote_row, wave, lane)) {
                 const uint64_t start = now_ticks();
                 while (true) {
-                    if (__syncthreads_or(now_ticks() - start > kSpinTicks)) {
+                    if (block_or(now_ticks() - start > kSpinTicks, P, vote_row, wave, lane)) {
                         if (tid == 0) P.status |= kStatusTimeout;
                         break;
                     }
@@ -758,7 +785,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                         stg[i] = ld_agent64(stg_base + stg_off + 8 * i);
                         stale |= used && stale_word(stg[i]);
                     }
-                    if (!__syncthreads_or(stale)) break;
+                    if (!block_or(stale, P, vote_row, wave, lane)) break;
                 }
             }
             uint4* dst = reinterpret_cast<uint4*>(act_lds + stg_row * kActStride + 16 * (tid & 31));
@@ -815,9 +842,12 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                 st_agent64(dst, tag_bits | (o[0] | (o[1] << 16)));
                 st_agent64(dst + 1, tag_bits | (o[2] | (o[3] << 16)));
             }
-        } else {
-            combine_tile<kChained>(a, P, tid, it.tile, T, first_slot == 0, tag);
+        } else if (it.kind == 2) {
+            combine_tile<kChained>(a, P, tid, it.tile, T, first_slot == 0, tag, vote_row);
             // Wave 0's claim above is visible to every wave after this.
+            __syncthreads();
+        } else {
+            // No item; the barrier publishes the claim.
             __syncthreads();
         }
         const int after = P.claim[cpar];
@@ -834,16 +864,28 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             stage_rows();
             __syncthreads();
         }
-        while (true) {
+        // Everything but the first item's 16 loads is complete by now; the
+        // wait tells the compiler so, which keeps it from draining the
+        // first item's loads where the loop reuses the prologue's
+        // registers.
+        __builtin_amdgcn_s_waitcnt(kWaitVm16);
+        // Two steps per iteration (the register sets swap roles) and one
+        // exit, at the bottom.  A workgroup with an odd number of items ends
+        // with a step of no item: a prefetch of cached rows and one more
+        // claim, of a number past the end like all of its later claims.
+        // (With an exit after each step, the compiler's control-flow
+        // structuring adds a path from the first step straight back to the
+        // top, on which that step's prefetch is still in flight; every
+        // iteration then waits for all loads before issuing the next
+        // prefetch.)
+        do {
             int after = step(cur, nxt, b0, b1);
             cur = nxt;
             nxt = after;
-            if (cur >= end) break;
             after = step(cur, nxt, b1, b0);
             cur = nxt;
             nxt = after;
-            if (cur >= end) break;
-        }
+        } while (cur < end);
     }
 
     // ---- 5. this workgroup's share of the layer is done ----
