@@ -12,13 +12,14 @@
 //             work units (slot, first pair) of at most kPassTok tokens.
 //
 // Experts (cpu_experts.c:54-69 rounding points; the shared expert is slot 0):
-//   pf_gateup one workgroup per (unit, 64-row tile): 64 gate + 64 up rows of
-//             one expert against up to 128 tokens.  Each wave streams its 16
-//             weight rows (8 gate, 8 up) from HBM straight into MFMA A
-//             operands, two K-chunks ahead; the token rows of the unit are
-//             staged in LDS chunk by chunk and shared by the 8 waves, so a
-//             weight byte is read once per 128 tokens and feeds up to 8
-//             16x16x32 MFMAs.  SwiGLU in the epilogue, act rows out.
+//   pf_gateup one workgroup per (unit, 128-row tile): 128 gate + 128 up rows
+//             of one expert against up to 128 tokens.  Each of the 8 waves
+//             streams its 32 weight rows (16 gate, 16 up) from HBM straight
+//             into MFMA A operands, two K-chunks ahead; the same waves stage
+//             the unit's token rows in LDS chunk by chunk (three chunks ahead
+//             in registers), shared by all 8 waves, so a weight byte is read
+//             once per 128 tokens and feeds up to 8 16x16x32 MFMAs.  SwiGLU
+//             in the epilogue, act rows out.
 //   pf_down   one workgroup per (unit, 128-row tile): the tile's down rows over
 //             k = 512 stay in registers while the unit's act rows pass through
 //             LDS 64 at a time; y rows out (bf16).
@@ -227,47 +228,75 @@ __device__ __forceinline__ void unit_tile(int b, int tiles, int& unit, int& tile
     tile = within / 8;
 }
 
-// gate/up workgroup (128 intermediate rows of one work unit): 8 MFMA waves,
-// each owning two 16-row MFMA tiles (tile r = 8 gate rows and the 8 up rows
-// with the same indices), and 4 loader waves that move the unit's token rows
-// into LDS two chunks ahead.  Each role waits only on its own loads (the
-// memory counter is in order); one barrier per chunk joins them.  A B operand
-// read from LDS feeds both row tiles, and the 4 workgroups of a unit each read
-// its token rows once.
-constexpr int kGuMfmaWaves = kGuRows / 16;
-constexpr int kGuLoadWaves = 4;
-constexpr int kGuThreads = (kGuMfmaWaves + kGuLoadWaves) * kWave;
-constexpr int kGuLoaderThreads = kGuLoadWaves * kWave;
-constexpr int kGuPieces = kPassTok * kGuChunk / 8 / kGuLoaderThreads;  // 16-byte pieces per loader thread per chunk
+// gate/up workgroup (128 intermediate rows of one work unit): 8 waves, each
+// owning two 16-row MFMA tiles (tile r = 8 gate rows and the 8 up rows with
+// the same indices).  The waves also move the unit's token rows into LDS,
+// one 128-column chunk at a time.  A wave issues, per chunk, its token pieces
+// three chunks ahead and its weights two chunks ahead, in that order; every
+// wait is then for exactly the data used next (the memory counter retires in
+// order), and two chunks of weights (16 KiB per wave) stay in flight.  With
+// 8 waves per CU each wave has 256 VGPRs for the 3 weight buffers, the 3
+// token-piece buffers and the accumulators.  A B operand read from LDS feeds
+// both row tiles, and the 4 workgroups of a unit each read its token rows
+// once.
+constexpr int kGuWaves = kGuRows / 16;
+constexpr int kGuThreads = kGuWaves * kWave;
+constexpr int kGuPieces = kPassTok * kGuChunk / 8 / kGuThreads;  // 16-byte token pieces per thread per chunk
+constexpr int kGuWAhead = 2;  // weight chunks in flight ahead of the MFMAs
+constexpr int kGuTAhead = 3;  // token chunks in flight ahead of the MFMAs
 
-// The MFMA waves' K loop for NB 16-token column blocks (blocks past the
-// unit's tokens read rows whose results are dropped), then SwiGLU.
+// The K loop for NB 16-token column blocks (blocks past the unit's tokens
+// read rows whose results are dropped), then SwiGLU.  xrow[j] is this
+// thread's token piece j (row xrow_row[j] of the unit, 16 bytes at column
+// 8 * piece of each chunk).
 template <int NB>
-__device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_t* arow1, const uint16_t* xb,
-                                            uint16_t* act0, uint16_t* act1, int count) {
+__device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_t* arow1, const uint16_t* const* xrow,
+                                            const int* xrow_row, int piece, uint16_t* xs, uint16_t* act0,
+                                            uint16_t* act1, int count) {
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15;
+    const int g = lane >> 4;
     f32x4 acc[2][NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[0][b] = acc[1][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // Weights arrive a whole chunk (kGuSteps k-steps of both tiles, 256
-    // contiguous bytes per row) at a time, one chunk ahead of the MFMAs: each
-    // DRAM row is read in one burst rather than 64 bytes per k-step.
-    uint4 wb[2][kGuSteps][2];
-    auto load_chunk = [&](int c, uint4 (*dst)[2]) {
+    // Weights of a chunk: kGuSteps k-steps of both tiles, 256 contiguous
+    // bytes per row, so each DRAM row is read in one burst.
+    uint4 wb[kGuWAhead + 1][kGuSteps][2];
+    uint4 xr[kGuTAhead][kGuPieces];
+    auto load_w = [&](int c, uint4 (*dst)[2]) {
 #pragma unroll
         for (int j = 0; j < kGuSteps; ++j) {
             dst[j][0] = ldg16(arow0 + 32 * (kGuSteps * c + j));
             dst[j][1] = ldg16(arow1 + 32 * (kGuSteps * c + j));
         }
     };
-    load_chunk(0, wb[0]);
-    __syncthreads();  // loaders: chunk 0 in LDS
+    auto load_t = [&](int c, uint4* dst) {
+#pragma unroll
+        for (int j = 0; j < kGuPieces; ++j) dst[j] = ldg16(xrow[j] + c * kGuChunk);
+    };
+    auto store_t = [&](int c, const uint4* src) {
+#pragma unroll
+        for (int j = 0; j < kGuPieces; ++j)
+            *reinterpret_cast<uint4*>(xs + ((c & 1) * kPassTok + xrow_row[j]) * kXsStride + 8 * piece) = src[j];
+    };
+#pragma unroll
+    for (int c = 0; c < kGuTAhead; ++c) load_t(c, xr[c]);
+#pragma unroll
+    for (int c = 0; c < kGuWAhead; ++c) load_w(c, wb[c]);
+    store_t(0, xr[0]);
+    const uint16_t* xb = xs + m * kXsStride + 8 * g;
 #pragma unroll
     for (int c = 0; c < kGuChunks; ++c) {
-        if (c + 1 < kGuChunks) load_chunk(c + 1, wb[(c + 1) & 1]);
+        // Chunk c is in LDS buffer c & 1; chunk c-1's buffer and registers
+        // are free.
+        __syncthreads();
+        if (c + 1 < kGuChunks) store_t(c + 1, xr[(c + 1) % kGuTAhead]);
+        if (c + kGuTAhead < kGuChunks) load_t(c + kGuTAhead, xr[(c + kGuTAhead) % kGuTAhead]);
+        if (c + kGuWAhead < kGuChunks) load_w(c + kGuWAhead, wb[(c + kGuWAhead) % (kGuWAhead + 1)]);
         const uint16_t* xcb = xb + (c & 1) * kPassTok * kXsStride;
 #pragma unroll
         for (int j = 0; j < kGuSteps; ++j) {
-            const uint4* ab = wb[c & 1][j];
+            const uint4* ab = wb[c % (kGuWAhead + 1)][j];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const uint4 bv = *reinterpret_cast<const uint4*>(xcb + 16 * b * kXsStride + 32 * j);
@@ -275,16 +304,10 @@ __device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_
                 acc[1][b] = mfma16x16x32(ab[1], bv, acc[1][b]);
             }
         }
-        // Chunk c's LDS buffer is free after this barrier; the loaders fill it
-        // with chunk c+2 before the barrier that ends chunk c+1.
-        __syncthreads();
     }
     // SwiGLU: lanes g < 2 hold gate rows 4g..4g+3 of a tile's 8, lane + 32 the
     // up rows with the same index.  act0/act1 point at this lane's first act
     // element of column 0 for tile 0 and 1 (4 consecutive intermediate rows).
-    const int lane = threadIdx.x & 63;
-    const int m = lane & 15;
-    const int g = lane >> 4;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -313,42 +336,19 @@ __global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-
-    if (wave >= kGuMfmaWaves) {
-        // ---- loader waves: token chunk c into LDS buffer c & 1 ----
-        const int lt = tid - kGuMfmaWaves * kWave;       // 0..255
-        const int piece = lt & 15;                       // 16-byte piece of a 256-byte chunk row
-        const uint16_t* xrow[kGuPieces];
+    // Token pieces of this thread: piece tid % 16 of unit rows tid / 16 + 32 j
+    // (rows past the unit's count repeat its first token).
+    const int piece = tid & 15;
+    const uint16_t* xrow[kGuPieces];
+    int xrow_row[kGuPieces];
 #pragma unroll
-        for (int j = 0; j < kGuPieces; ++j) {
-            const int c = lt / 16 + 16 * j;              // token row of the unit, 0..127
-            const int cc = c < w.count ? c : 0;
-            const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
-            xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
-        }
-        // Chunk c+1 is loaded into registers before the barrier that opens
-        // chunk c, so its gathered rows have two chunks' time to arrive.
-        uint4 xr[kGuPieces];
-#pragma unroll
-        for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j]);
-#pragma unroll
-        for (int c = 0; c < kGuChunks; ++c) {
-            // Buffer c & 1 last held chunk c-2, which the MFMA waves finished
-            // before the previous barrier.
-#pragma unroll
-            for (int j = 0; j < kGuPieces; ++j)
-                *reinterpret_cast<uint4*>(xs + ((c & 1) * kPassTok + lt / 16 + 16 * j) * kXsStride + 8 * piece) = xr[j];
-            if (c + 1 < kGuChunks) {
-#pragma unroll
-                for (int j = 0; j < kGuPieces; ++j) xr[j] = ldg16(xrow[j] + (c + 1) * kGuChunk);
-            }
-            __syncthreads();  // chunk c is in LDS
-        }
-        __syncthreads();  // matches the MFMA waves' last barrier
-        return;
+    for (int j = 0; j < kGuPieces; ++j) {
+        const int c = tid / 16 + (kGuThreads / 16) * j;  // token row of the unit, 0..127
+        const int cc = c < w.count ? c : 0;
+        const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
+        xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
+        xrow_row[j] = c;
     }
-
-    // ---- MFMA waves ----
     const int m = lane & 15;
     const int g = lane >> 4;
     const int nblk = (w.count + 15) / 16;
@@ -358,15 +358,14 @@ __global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
     const int row0 = kGuRows * tile + 16 * wave + (m & 7);
     const uint16_t* arow0 = rows + static_cast<size_t>(row0) * kHidden + 8 * g;
     const uint16_t* arow1 = rows + static_cast<size_t>(row0 + 8) * kHidden + 8 * g;
-    const uint16_t* xb = xs + m * kXsStride + 8 * g;
     uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + kGuRows * tile + 16 * wave + 4 * g;
     uint16_t* act1 = act0 + 8;
     if (nblk <= 2) {
-        gateup_mfma<2>(arow0, arow1, xb, act0, act1, w.count);
+        gateup_mfma<2>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
     } else if (nblk <= 4) {
-        gateup_mfma<4>(arow0, arow1, xb, act0, act1, w.count);
+        gateup_mfma<4>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
     } else {
-        gateup_mfma<8>(arow0, arow1, xb, act0, act1, w.count);
+        gateup_mfma<8>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
     }
 }
 
