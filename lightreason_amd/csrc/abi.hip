@@ -112,7 +112,7 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
         d.weights_in = weights;
         d.expert_ptrs = expert_ptrs;
         d.out = out;
-        d.logits = ws.logits;
+        d.logits = ws.dlogits;
         d.act = ws.dact;
         d.y = ws.dy;
         d.sync = ws.sync;
@@ -164,7 +164,7 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
         d.out = out;
         d.indices_out = indices_out;
         d.weights_out = weights_out;
-        d.logits = ws.logits;
+        d.logits = ws.dlogits;
         d.act = ws.dact;
         d.y = ws.dy;
         d.sync = ws.sync;
@@ -238,7 +238,7 @@ int lrmoe_moe_chain(const uint16_t* hidden, int tokens, int layers, const int64_
     c.base.eps = eps;
     c.base.indices_out = indices_out;
     c.base.weights_out = weights_out;
-    c.base.logits = ws.logits;
+    c.base.logits = ws.dlogits;
     c.base.act = ws.dact;
     c.base.y = ws.dy;
     c.base.sync = ws.sync;

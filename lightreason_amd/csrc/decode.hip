@@ -31,11 +31,11 @@
 //          the shared-expert add bf16(sg * y_shared) and the residual add.
 //
 // Cross-workgroup data is written with agent-scope stores and read with
-// agent-scope loads (coherent across the XCDs' L2s).  The router logits are
-// published by a counter.  The act and y rows are 8-byte words that carry the
-// call's tag beside two bf16 values, so a B item knows its slot's act rows
-// are complete, and a C item its tile's y rows, by checking the tags of what
-// it loaded: no producer waits for its own stores or signals anything.  A B
+// agent-scope loads (coherent across the XCDs' L2s).  The router logits and
+// the act and y rows are 8-byte words that carry the call's tag beside two
+// bf16 values, so the plan knows its logits are complete, a B item its
+// slot's act rows and a C item its tile's y rows, by checking the tags of
+// what it loaded: no producer waits for its own stores or signals anything.  A B
 // item needs its slot's A items and a C item its tile's B items, all earlier
 // in the list; every workgroup takes its items in increasing list order and
 // all workgroups are co-resident, so the earliest waiting item always has
@@ -95,14 +95,8 @@ __device__ __forceinline__ void ld_agent64x4_async(uint64_t* out, const void* ba
         : "v"(byte_offset), "s"(base)
         : "memory");
 }
-__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
-    return __hip_atomic_load(as_g32(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
     __hip_atomic_store(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t add_agent32(void* p, uint32_t v) {
-    return __hip_atomic_fetch_add(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // A wave-uniform copy of a 64-bit value (each half through readfirstlane,
@@ -177,15 +171,8 @@ __device__ __forceinline__ void st_row8(uint16_t* p, uint64_t v) {
     }
 }
 
-// Waits (bounded) until *counter >= target; returns false on timeout.
-__device__ bool wait_counter(const uint32_t* counter, uint32_t target) {
-    const uint64_t start = now_ticks();
-    while (ld_agent32(counter) < target) {
-        if (now_ticks() - start > kSpinTicks) return false;
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return true;
-}
+// The call tag of a tagged 8-byte word.
+__device__ __forceinline__ uint32_t tag_of(uint64_t word) { return static_cast<uint32_t>(word >> kDecodeTagShift); }
 
 __device__ __forceinline__ uint64_t pack4(const uint32_t* v) {
     return static_cast<uint64_t>(v[0] | (v[1] << 16)) | (static_cast<uint64_t>(v[2] | (v[3] << 16)) << 32);
@@ -451,11 +438,11 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     const int parity = static_cast<int>(call & 1ull);
     const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
     DecodeCounters* const cnt = &sync->set[parity];
-    if (block == 0) {
-        // The next call's counters (this call never touches them).
-        DecodeCounters* const nxt = &sync->set[parity ^ 1];
-        if (tid == kThreads - 1) st_agent32(&nxt->router_done, 0u);
-        if (tid == kThreads - 2) st_agent32(&nxt->claim, 0u);
+    const uint64_t tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
+    int vote_row = 0;  // block_or row
+    if (block == 0 && tid == kThreads - 1) {
+        // The next call's counter (this call never touches it).
+        st_agent32(&sync->set[parity ^ 1].claim, 0u);
     }
     __syncthreads();
 
@@ -506,26 +493,45 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                 if (lane == 0) P.lg[t][wave] = static_cast<uint16_t>(f2bf(s));
             }
             __syncthreads();
-            if (tid < 2 * T) {
-                const int t = tid >> 1;
-                const int h = tid & 1;
-                uint32_t v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = P.lg[t][4 * h + i];
-                st_agent64(a.logits + static_cast<size_t>(t) * kExperts + kWaves * block + 4 * h, pack4(v));
+            // This workgroup's 8 logits of token t as 4 tagged words (logits
+            // 2k and 2k+1 in word k of the token's row).
+            if (tid < 4 * T) {
+                const int t = tid >> 2;
+                const int q = tid & 3;
+                const uint32_t pair = static_cast<uint32_t>(P.lg[t][2 * q]) | (static_cast<uint32_t>(P.lg[t][2 * q + 1]) << 16);
+                st_agent64(a.logits + static_cast<size_t>(t) * (kExperts / 2) + (kWaves / 2) * block + q, tag_bits | pair);
             }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid == 0) add_agent32(&cnt->router_done, 1u);
         }
     }
 
     // ---- 4. the route plan ----
     if (a.router != nullptr) {
-        if (tid == 0 && !wait_counter(&cnt->router_done, kRouterWgs)) P.status |= kStatusTimeout;
-        __syncthreads();
-        if (has_lo) lg_lo = ld_agent64(a.logits + static_cast<size_t>(t_lo) * kExperts + 4 * lane);
-        if (has_hi) lg_hi = ld_agent64(a.logits + static_cast<size_t>(t_hi) * kExperts + 4 * lane);
+        // Each wave reloads its tokens' logit rows (bounded) until every word
+        // carries this call's tag; lane l ends with logits 4l..4l+3.
+        const uint64_t* row_lo = a.logits + static_cast<size_t>(has_lo ? t_lo : 0) * (kExperts / 2) + 2 * lane;
+        const uint64_t* row_hi = a.logits + static_cast<size_t>(has_hi ? t_hi : 0) * (kExperts / 2) + 2 * lane;
+        uint64_t lw[4];
+        auto fetch = [&]() {
+            lw[0] = ld_agent64(row_lo);
+            lw[1] = ld_agent64(row_lo + 1);
+            lw[2] = ld_agent64(row_hi);
+            lw[3] = ld_agent64(row_hi + 1);
+            return (has_lo && (tag_of(lw[0]) != tag || tag_of(lw[1]) != tag)) ||
+                   (has_hi && (tag_of(lw[2]) != tag || tag_of(lw[3]) != tag));
+        };
+        if (block_or(fetch(), P, vote_row, wave, lane)) {
+            const uint64_t start = now_ticks();
+            while (true) {
+                if (block_or(now_ticks() - start > kSpinTicks, P, vote_row, wave, lane)) {
+                    if (tid == 0) P.status |= kStatusTimeout;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                if (!block_or(fetch(), P, vote_row, wave, lane)) break;
+            }
+        }
+        lg_lo = (lw[0] & 0xffffffffull) | (lw[1] << 32);
+        lg_hi = (lw[2] & 0xffffffffull) | (lw[3] << 32);
     }
     if (a.indices_in == nullptr) {
         int e_lo, e_hi;
@@ -720,15 +726,13 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
     // Lanes of the claiming atomic: lane 0 of wave 0.
     const uint32_t claim_lanes = wave == 0 ? 1u : 0u;
-    const uint64_t tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
-    int vote_row = 0;         // block_or row
 
     auto weights_of = [&](const Item& it) -> const uint16_t* {
         return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
     };
-    auto stale_word = [&](uint64_t w) { return static_cast<uint32_t>(w >> kDecodeTagShift) != tag; };
+    auto stale_word = [&](uint64_t w) { return tag_of(w) != tag; };
 
     // Runs item kk, whose weights are in buf, and prefetches item kn into
     // nbuf.  Returns the item claimed for the step after next.

@@ -23,12 +23,10 @@ constexpr int kDecodeSlots = 8 * kDecodeMaxTokens + 1;  // unique routed experts
 constexpr int kSyncStride = 64;  // counters 256 bytes apart (separate memory channels)
 constexpr int kPassTok = 128;    // prefill: tokens of one expert per work unit
 
-// Cross-workgroup counters of one decode call.
+// Cross-workgroup counter of one decode call.
 struct DecodeCounters {
-    uint32_t router_done;                        // router workgroups finished
-    uint32_t pad0[kSyncStride - 1];
     uint32_t claim;                              // work items handed out past the first two rounds
-    uint32_t pad1[kSyncStride - 1];
+    uint32_t pad[kSyncStride - 1];
 };
 
 // Decode kernel synchronisation.  `finished` counts finished workgroups over
@@ -103,6 +101,7 @@ struct Workspace {
     uint16_t* y;          // [8T + T][2048]: routed pairs, then shared rows
     uint64_t* dact;       // decode: act as tagged words, [9*16 + 16][256]
     uint64_t* dy;         // decode: y as tagged words, [9*16][1024]
+    uint64_t* dlogits;    // decode: router logits as tagged words, [16][128]
     uint16_t* chain;      // decode chain: [2][T][2048] outputs of the inner layers
     uint32_t* counts;     // [256] prefill: pairs per expert
     DecodeSync* sync;     // decode kernel counters
@@ -135,6 +134,7 @@ inline Workspace carve(void* base, int tokens) {
     // written by that call.
     ws.dact = reinterpret_cast<uint64_t*>(take((9 * kDecodeMaxTokens + 16) * 256 * 8));
     ws.dy = reinterpret_cast<uint64_t*>(take(9 * kDecodeMaxTokens * 1024 * 8));
+    ws.dlogits = reinterpret_cast<uint64_t*>(take(kDecodeMaxTokens * 128 * 8));
     ws.logits = reinterpret_cast<uint16_t*>(take(T * 256 * 2));
     ws.normed = reinterpret_cast<uint16_t*>(take(T * 2048 * 2));
     ws.indices = reinterpret_cast<int64_t*>(take(T * 8 * 8));
@@ -222,7 +222,7 @@ struct DecodeArgs {
     uint16_t* out;                // [T][2048]
     int64_t* indices_out;         // [T][8] or null
     uint16_t* weights_out;        // [T][8] or null
-    uint16_t* logits;             // [T][256] workspace (router output)
+    uint64_t* logits;             // [16][128] tagged words (workspace): router output, logits 2k, 2k+1 in word k
     uint64_t* act;                // [9T + 16][256] tagged words (workspace)
     uint64_t* y;                  // [9T][1024] tagged words (workspace)
     DecodeSync* sync;             // workspace counters
