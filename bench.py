@@ -37,9 +37,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from lightreason_amd import _native  # noqa: E402
-from lightreason_amd.moe import (EXPERT_BYTES, EXPERT_ELEMENTS, GATE_UP_ELEMENTS, HIDDEN, INNER, LayerWeights,  # noqa: E402
-                                 Workspace,
-                                 gather, moe_chain, moe_layer)
+from lightreason_amd.moe import (CODEC_DN_BASES, CODEC_GU_BASES, EXPERT_BYTES, EXPERT_ELEMENTS,  # noqa: E402
+                                 GATE_UP_ELEMENTS, HIDDEN, INNER, CodecBank, LayerWeights, Workspace, gather,
+                                 moe_chain, moe_layer)
 from lightreason_amd.synthetic import SyntheticModel  # noqa: E402
 
 METRIC = "MoE layer µs + HBM GB/s vs peak at T=1,8; prefill BF16 TFLOPS at T=2048"
@@ -132,7 +132,8 @@ class Case:
     """One workload: per-layer static inputs and outputs, run as one graph
     that steps through the layers in order."""
 
-    def __init__(self, model, tokens, *, logits=None, norm=False, chain=False, layers=None, one_launch=False):
+    def __init__(self, model, tokens, *, logits=None, norm=False, chain=False, layers=None, one_launch=False,
+                 codec=None):
         self.model = model
         self.tokens = tokens
         self.layer_ids = list(range(len(model.layers))) if layers is None else layers
@@ -148,7 +149,8 @@ class Case:
         self.layers = []
         for i in self.layer_ids:
             base = model.layers[i]
-            self.layers.append(LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None}))
+            self.layers.append(LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None,
+                                               "codec": None if codec is None else codec.table(i)}))
 
     def run(self):
         if self.one_launch:
@@ -330,7 +332,7 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=2026)
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
-    parser.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4 to run (default all)")
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4,c5 to run (default all)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
                              "of a profiler run can be scaled by a kernel of known traffic")
@@ -349,7 +351,7 @@ def main() -> int:
     L = args.layers
     replays = max(1, args.steps // L)
     warm = max(1, args.warmup // L)
-    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c2", "c3", "c4"}
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c2", "c3", "c4", "c5"}
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
@@ -433,6 +435,42 @@ def main() -> int:
                                     launches="one persistent launch" if one_launch else "one per layer, in a graph")
                 log(f"[bench] C3 T={T} {'chain' if one_launch else 'per-layer'}: {ms3:.3f} ms/step over {L} layers, "
                     f"{configs[key]['gbs']} GB/s")
+
+    # ---- C5: the decode layers reading tile-codec experts ----
+    if "c5" in only:
+        t0 = time.perf_counter()
+        bank = CodecBank(model.bank, [(ly.shared_gate_proj, ly.shared_up_proj, ly.shared_down_proj)
+                                      for ly in model.layers])
+        torch.cuda.synchronize()
+        packed_frac = bank.packed_fraction
+        misfit_tiles = float(bank.misfit.sum()) / (bank.misfit.numel() * (CODEC_GU_BASES + CODEC_DN_BASES))
+        # Bytes a unit reads: 3/4 of its raw bytes when packed (plus 16 bytes
+        # of bases per lane, 1/64 of the packed bytes), all of them when raw.
+        read_frac = packed_frac * 0.75 * (1 + 1 / 64) + (1 - packed_frac)
+        log(f"[bench] C5 codec bank in {time.perf_counter() - t0:.1f}s: {bank.nbytes / 2**30:.1f} GiB, "
+            f"units packed {packed_frac:.3f}, tiles misfit {misfit_tiles:.4f}")
+        res = dict(units_packed=round(packed_frac, 4), tiles_misfit=round(misfit_tiles, 5),
+                   weight_bytes_read_frac=round(read_frac, 4))
+        c5 = Case(model, 8, logits=logits, codec=bank)
+        assert c5.unique_counts() == uniques
+        ms5 = bench_case(c5, replays, warm) / L
+        res["c2_verify_t8_zipf"] = dict(us_per_layer=round(ms5 * 1e3, 2),
+                                        raw_equivalent_gbs=round(bytes_step / (ms5 * 1e-3) / 1e9, 1),
+                                        speedup_vs_raw=round(ms_step / ms5, 3))
+        log(f"[bench] C5 T=8 zipf codec: {ms5 * 1e3:.1f} us/layer (raw {ms_step * 1e3:.1f})")
+        for T in (1, 16):
+            c5 = Case(model, T, norm=True, chain=True, one_launch=True, codec=bank)
+            u5 = c5.unique_counts()
+            ms5 = bench_case(c5, max(2, replays // 2), 1)
+            b5 = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in u5)
+            res[f"c3_chain_t{T}"] = dict(ms_per_step=round(ms5, 4),
+                                         raw_equivalent_gbs=round(b5 / (ms5 * 1e-3) / 1e9, 1))
+            raw = configs.get(f"c3_chain_t{T}")
+            if raw is not None:
+                res[f"c3_chain_t{T}"]["speedup_vs_raw"] = round(raw["ms_per_step"] / ms5, 3)
+            log(f"[bench] C5 T={T} chain codec: {ms5:.3f} ms/step")
+        configs["c5_codec"] = res
+        del bank
 
     # ---- C4: T=2048 prefill with skewed routing ----
     if "c4" in only:

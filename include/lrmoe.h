@@ -114,12 +114,25 @@ int lrmoe_moe_experts(const uint16_t *hidden, int tokens, const int64_t *indices
  * out = bf16(hidden + MoE(RMSNorm(hidden))) (the decoder layer's MLP half);
  * without: out = MoE(hidden).  Shared expert pointers may all be NULL.
  * Exactly one of router_weight and logits_in is given (see lrmoe_route_topk).
- * indices_out / weights_out may be NULL.  Replaces Transformers
+ * indices_out / weights_out may be NULL.  expert_codec (may be NULL; 16-byte
+ * aligned) is a device table [257][LRMOE_CODEC_TABLE_COLUMNS] int64, row 256
+ * the shared expert (whose packed gate_up is gate_proj then up_proj): four
+ * tile-codec addresses (packed gate_up, packed down, gate_up bases, down
+ * bases, as written by lrmoe_codec_pack), then 48 bytes of raw flags: byte
+ * i < 32 for gate_up item i, byte 32 + i for down item i, bit w set when a
+ * tile that wave w of the item reads has base 255 (gate_up item i, wave w:
+ * tiles 2(w%4), 2(w%4)+1 of gate_proj and up_proj rows 16i + 8(w/4) .. +7;
+ * down item i, wave w: both tiles of rows 128i + 16w .. +15).  For tokens
+ * <= 16 an expert whose four addresses are non-zero is read from its codec
+ * form, except the flagged (item, wave) units, which read the raw rows;
+ * results are identical to the raw rows'.  The raw pointers stay required.
+ * Replaces Transformers
  * Qwen3_5MoeSparseMoeBlock.forward + the residual add of
  * Qwen3_5MoeDecoderLayer.forward, as driven by edge35b/expert_stream.py:457-526
  * (patch_experts). */
 int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_weight,
-                    const uint16_t *logits_in, const int64_t *expert_ptrs, const uint16_t *shared_gate_proj,
+                    const uint16_t *logits_in, const int64_t *expert_ptrs, const int64_t *expert_codec,
+                    const uint16_t *shared_gate_proj,
                     const uint16_t *shared_up_proj, const uint16_t *shared_down_proj,
                     const uint16_t *shared_expert_gate, const uint16_t *norm_weight, float eps,
                     uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
@@ -133,7 +146,8 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
  * the LRMOE_CHAIN_* indices below: the router (required), the expert
  * address table (required), the shared expert's gate_proj, up_proj,
  * down_proj and shared_expert_gate (all four or none), the RMSNorm weight
- * (0 = no norm and no residual add); the last entry is unused.  The table is
+ * (0 = no norm and no residual add), and the tile-codec table (0 = none;
+ * see lrmoe_moe_layer's expert_codec).  The table is
  * copied into the launch, so it may be freed or changed once the call has
  * returned (also while a stream is captured).  layers <=
  * LRMOE_CHAIN_MAX_LAYERS; longer stacks take several calls.  indices_out /
@@ -142,6 +156,7 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
  * 834-875: the post-attention RMSNorm 801-818, Qwen3_5MoeSparseMoeBlock.forward
  * 787-798, the residual add 875), which the reference replays as one
  * captured graph per step (edge35b/packed_native.py:58-63). */
+#define LRMOE_CODEC_TABLE_COLUMNS 10
 #define LRMOE_CHAIN_PTRS 8
 #define LRMOE_CHAIN_MAX_LAYERS 48
 #define LRMOE_CHAIN_ROUTER 0
@@ -151,9 +166,26 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
 #define LRMOE_CHAIN_SHARED_DOWN_PROJ 4
 #define LRMOE_CHAIN_SHARED_EXPERT_GATE 5
 #define LRMOE_CHAIN_NORM 6
+#define LRMOE_CHAIN_CODEC 7
 int lrmoe_moe_chain(const uint16_t *hidden, int tokens, int layers, const int64_t *layer_table, float eps,
                     uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
                     size_t workspace_bytes, void *stream);
+
+/* Lossless BF16 tile codec (the format of the reference's tile packer,
+ * edge35b/cpu_bf16_reads.h:16-52 pack_cpu_read_tiles, decoded by
+ * bf16_gather_ada.cu:117-123; bytes reordered for the decode kernel's MFMA
+ * lanes, see lightreason_amd/csrc/codec.hip).  w is [rows][cols] bf16 with
+ * cols a multiple of 256; packed receives rows * cols / 256 tiles of 384
+ * bytes and bases one byte per tile (255: the tile's exponent fields span
+ * more than 8 values and it is not encoded).  *misfit (device, may be NULL)
+ * is increased by the number of such tiles.  Replaces the packing that
+ * edge35b/gpu_resident_experts.py:29 and cpu_read_packing.py:138 run on the
+ * host. */
+int lrmoe_codec_pack(const uint16_t *w, int64_t rows, int cols, uint8_t *packed, uint8_t *bases,
+                     unsigned long long *misfit, void *stream);
+/* Inverse of lrmoe_codec_pack (tiles with base 255 decode to 0xffff). */
+int lrmoe_codec_unpack(const uint8_t *packed, const uint8_t *bases, int64_t rows, int cols, uint16_t *w,
+                       void *stream);
 
 /* Raw BF16 row gather: for row < *count and bank b < banks, copy sizes[b]
  * bytes from descriptors[(b*experts + src_ids[row])*3] to

@@ -23,6 +23,7 @@ STATUS_CODEC_ROW = 4
 
 CHAIN_PTRS = 8           # int64 addresses per layer in a chain's layer table
 CHAIN_MAX_LAYERS = 48    # layers per lrmoe_moe_chain call
+CODEC_TABLE_COLUMNS = 10  # int64 per expert in a decode codec table (4 addresses, 48 flag bytes)
 
 _P = C.c_void_p
 _I = C.c_int
@@ -34,8 +35,10 @@ _SIGNATURES = {
     "lrmoe_route_topk": ([_P, _I, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_bucket": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_experts": ([_P, _I, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
-    "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
+    "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_chain": ([_P, _I, _I, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
+    "lrmoe_codec_pack": ([_P, C.c_int64, _I, _P, _P, _P, _P], _I),
+    "lrmoe_codec_unpack": ([_P, _P, C.c_int64, _I, _P, _P], _I),
     "lrmoe_gather": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "lrmoe_matvec": ([_P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "lrmoe_ordered_sum": ([_P, _P, _P, _P, _P, _I, _P], _I),

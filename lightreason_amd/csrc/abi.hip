@@ -134,7 +134,7 @@ int lrmoe_moe_experts(const uint16_t* hidden, int tokens, const int64_t* indices
 }
 
 int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_weight, const uint16_t* logits_in,
-                    const int64_t* expert_ptrs,
+                    const int64_t* expert_ptrs, const int64_t* expert_codec,
                     const uint16_t* shared_gate_proj, const uint16_t* shared_up_proj,
                     const uint16_t* shared_down_proj, const uint16_t* shared_expert_gate,
                     const uint16_t* norm_weight, float eps, uint16_t* out, int64_t* indices_out,
@@ -161,6 +161,7 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
         d.sh_up = shared_up_proj;
         d.sh_down = shared_down_proj;
         d.expert_ptrs = expert_ptrs;
+        d.codec = expert_codec;
         d.out = out;
         d.indices_out = indices_out;
         d.weights_out = weights_out;
@@ -228,6 +229,7 @@ int lrmoe_moe_chain(const uint16_t* hidden, int tokens, int layers, const int64_
         w.sh_down = at(LRMOE_CHAIN_SHARED_DOWN_PROJ);
         w.shared_expert_gate = at(LRMOE_CHAIN_SHARED_EXPERT_GATE);
         w.norm = at(LRMOE_CHAIN_NORM);
+        w.codec = reinterpret_cast<const int64_t*>(at(LRMOE_CHAIN_CODEC));
         if (!w.router || !w.expert_ptrs) return LRMOE_E_ARG;
         const bool any_shared = w.sh_gate || w.sh_up || w.sh_down || w.shared_expert_gate;
         const bool all_shared = w.sh_gate && w.sh_up && w.sh_down && w.shared_expert_gate;
@@ -249,6 +251,24 @@ int lrmoe_moe_chain(const uint16_t* hidden, int tokens, int layers, const int64_
     c.inner = ws.chain;
     c.layers = layers;
     return status_of(lrmoe::launch_moe_chain(c, as_stream(stream)));
+}
+
+int lrmoe_codec_pack(const uint16_t* w, int64_t rows, int cols, uint8_t* packed, uint8_t* bases,
+                     unsigned long long* misfit, void* stream) {
+    if (rows < 0 || cols < 0 || cols % lrmoe::kCodecTile != 0) return LRMOE_E_ARG;
+    if (rows == 0 || cols == 0) return LRMOE_OK;
+    if (!w || !packed || !bases) return LRMOE_E_ARG;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_codec_pack(w, rows, cols, packed, bases, misfit, as_stream(stream)));
+}
+
+int lrmoe_codec_unpack(const uint8_t* packed, const uint8_t* bases, int64_t rows, int cols, uint16_t* w,
+                       void* stream) {
+    if (rows < 0 || cols < 0 || cols % lrmoe::kCodecTile != 0) return LRMOE_E_ARG;
+    if (rows == 0 || cols == 0) return LRMOE_OK;
+    if (!w || !packed || !bases) return LRMOE_E_ARG;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_codec_unpack(packed, bases, rows, cols, w, as_stream(stream)));
 }
 
 int lrmoe_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,

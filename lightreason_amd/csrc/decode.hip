@@ -184,10 +184,15 @@ struct SlotInfo {
     const uint16_t* gate;  // gate rows [512][2048]
     const uint16_t* up;    // up rows [512][2048]
     const uint16_t* down;  // [2048][512]
+    const uint8_t* pk_gu;  // tile-codec gate_up [1024 rows][8 tiles][384 B], or null (raw expert)
+    const uint8_t* pk_dn;  // tile-codec down [2048][2][384]
+    const uint8_t* b_gu;   // tile bases of gate_up [1024][8]
+    const uint8_t* b_dn;   // tile bases of down [2048][2]
     uint32_t tok[4];       // token of column n in byte n
     int32_t count;         // tokens (columns), <= 16
     int32_t pair0;         // first act/y row
-    int32_t pad[2];
+    int32_t crow;          // row of Plan::ecodec holding the expert's raw flags (codec slots)
+    int32_t pad;
 };
 
 struct Plan {
@@ -198,6 +203,8 @@ struct Plan {
     int32_t ids[kMaxT][kTopK];        // routed experts, rank order
     uint16_t wts[kMaxT][kTopK];       // routing weights (bf16), rank order
     uint4 eptr[kExperts];             // (gate_up, down) address of every expert
+    uint4 ecodec[kExperts + 1][5];    // codec table rows of every expert and the shared one (codec calls):
+                                      // 4 addresses, then 48 bytes of per-(item, wave) raw flags
     uint32_t tokmask[kExperts];
     uint32_t poff[kExperts];
     uint32_t scan[4];
@@ -241,6 +248,24 @@ __device__ __forceinline__ float lane_dot32(const uint4* w, const uint16_t* row,
         for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(wf[j], xf[j], acc);
     }
     return acc;
+}
+
+// Weight addresses of a slot: the raw rows, and the tile-codec rows when the
+// expert has them (codec = {packed gate_up, packed down, gate_up bases, down
+// bases} as two uint4, or null; crow = its row of Plan::ecodec).
+__device__ __forceinline__ void set_slot_weights(SlotInfo& s, const uint16_t* gate, const uint16_t* up,
+                                                 const uint16_t* down, const uint4* codec, int crow) {
+    auto ptr = [](uint32_t lo, uint32_t hi) {
+        return reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(lo) | (static_cast<uintptr_t>(hi) << 32));
+    };
+    s.gate = gate;
+    s.up = up;
+    s.down = down;
+    s.pk_gu = codec != nullptr ? ptr(codec[0].x, codec[0].y) : nullptr;
+    s.pk_dn = codec != nullptr ? ptr(codec[0].z, codec[0].w) : nullptr;
+    s.b_gu = codec != nullptr ? ptr(codec[1].x, codec[1].y) : nullptr;
+    s.b_dn = codec != nullptr ? ptr(codec[1].z, codec[1].w) : nullptr;
+    s.crow = crow;
 }
 
 // ---- item geometry ------------------------------------------------------------
@@ -288,6 +313,88 @@ __device__ __forceinline__ const uint16_t* item_base(const SlotInfo& s, const It
     const uint16_t* rows = m < 8 ? s.gate : s.up;
     const int row = 16 * it.tile + 8 * (wave >> 2) + (m & 7);
     return rows + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * g;
+}
+
+// Tile-codec rows of a lane in an item of a codec slot (format in
+// codec.hip): the lane's MFMA row has two tiles in the item's k range (A:
+// tiles 2q, 2q+1 of the gate/up row, q = wave % 4; B: tiles 0, 1 of the down
+// row), with their bases side by side (an even byte).  Per tile the lane
+// issues 8 loads, like the 8 of a raw row's tile: when the tile fits the
+// codec, its six 16-byte blocks at tile + 16g + 64u (u = 0..5, the offsets of
+// the raw loads) and the 16-byte aligned block holding both bases, twice.
+struct PackedLane {
+    const uint8_t* tile0;    // first of the lane's two tiles
+    const uint8_t* bases16;  // 16-byte block holding its two tile bases
+    const uint8_t* bases2;   // the two bases
+    int base_byte;           // byte of the first base in that block
+};
+
+__device__ __forceinline__ PackedLane packed_lane(const SlotInfo& s, const Item& it, int wave, int lane) {
+    const int m = lane & 15;
+    PackedLane p;
+    uintptr_t b;
+    if (it.kind == 1) {
+        const int row = kBRows * it.tile + 16 * wave + m;
+        p.tile0 = s.pk_dn + static_cast<size_t>(row) * 2 * kCodecTileBytes;
+        b = reinterpret_cast<uintptr_t>(s.b_dn) + static_cast<uintptr_t>(row) * 2;
+    } else {
+        // Gate row (m < 8) or up row (m >= 8) 16*tile + 8*(wave/4) + m%8 of the packed gate_up.
+        const int row = (m < 8 ? 0 : kInner) + 16 * it.tile + 8 * (wave >> 2) + (m & 7);
+        const int q = wave & 3;
+        p.tile0 = s.pk_gu + (static_cast<size_t>(row) * 8 + 2 * q) * kCodecTileBytes;
+        b = reinterpret_cast<uintptr_t>(s.b_gu) + static_cast<uintptr_t>(row) * 8 + 2 * q;
+    }
+    p.bases2 = reinterpret_cast<const uint8_t*>(b);
+    p.bases16 = reinterpret_cast<const uint8_t*>(b & ~static_cast<uintptr_t>(15));
+    p.base_byte = static_cast<int>(b & 15);
+    return p;
+}
+
+// Byte i (0..15) of a 16-byte block, by shifts (an indexed pick of a
+// component would put the whole register array in scratch memory).
+__device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
+    const uint64_t lo = static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32);
+    const uint64_t hi = static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32);
+    return static_cast<uint32_t>(((i < 8 ? lo : hi) >> (8 * (i & 7))) & 0xffu);
+}
+
+// Register order of a raw tile's 8 loads (every item, so that one load
+// sequence serves all): register 8t + j holds k-step 8t + kRawStep[j].  Packed, register j
+// holds block j, whose last reader is k-step 1, 3, 5, 7, 3, 7 for j = 0..5
+// (registers 6, 7: the bases, read first); this order ends each register's
+// raw use near its packed one, which keeps the registers of a wave that
+// mixes packed and raw lanes free as early as those of a packed one.
+__device__ constexpr int kRawStep[8] = {2, 3, 5, 6, 4, 7, 0, 1};
+__device__ constexpr int raw_reg(int s) {
+    const int u = s & 7;
+    int j = 0;
+    for (int i = 0; i < 8; ++i) j = kRawStep[i] == u ? i : j;
+    return (s & 8) + j;
+}
+
+// a where mask is all ones, b where it is zero, as bit operations (a
+// conditional would let the compiler branch around the computation of a).
+__device__ __forceinline__ uint4 pick(uint32_t mask, const uint4& a, const uint4& b) {
+    return make_uint4((a.x & mask) | (b.x & ~mask), (a.y & mask) | (b.y & ~mask), (a.z & mask) | (b.z & ~mask),
+                      (a.w & mask) | (b.w & ~mask));
+}
+
+// A bases pair of two tiles that do not fit the codec: the dummy source of
+// items without codec rows.
+__device__ const uint16_t kBothMisfit = 0xffffu;
+
+// The MFMA A operand of k-step s (0..15) of a lane's packed tile s / 8: the
+// 8 bf16 values a raw item's load s holds (k = 8g + 32s .. +7 of the lane's
+// row); base4 = the tile's base * 0x01010101.
+__device__ __forceinline__ uint4 packed_operand(const uint4* buf, int s, uint32_t base4) {
+    const int t = s >> 3;
+    const int u = s & 7;
+    const uint4 l = buf[8 * t + (u >> 1)];
+    const uint32_t lo = (u & 1) ? l.z : l.x;
+    const uint32_t hi = (u & 1) ? l.w : l.y;
+    const uint4 cq = buf[8 * t + 4 + (u >> 2)];
+    const uint32_t c = (u & 3) == 0 ? cq.x : (u & 3) == 1 ? cq.y : (u & 3) == 2 ? cq.z : cq.w;
+    return codec_decode8(lo, hi, c, base4);
 }
 
 __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
@@ -376,7 +483,7 @@ __device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int t
 // input are issued; it returns when the input rows are complete.  Ends with
 // all of the workgroup's memory operations complete; returns kStatusTimeout
 // when one of its bounded waits expired.
-template <bool kChained, typename WaitInput>
+template <bool kChained, bool kCodec, typename WaitInput>
 __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, uint8_t* dyn,
                                                 unsigned long long finished, int layer, WaitInput wait_input) {
     const int T = a.tokens;
@@ -411,6 +518,14 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     uint64_t lg_lo = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_lo ? t_lo : 0) * kExperts * logits_given + 4 * lane);
     uint64_t lg_hi = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_hi ? t_hi : 0) * kExperts * logits_given + 4 * lane);
     const uint4 eptr = ldg16(a.expert_ptrs + 2 * (tid & (kExperts - 1)));
+    // Codec table row of expert tid (tid 256: the shared expert).
+    uint4 ec[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) ec[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (a.codec != nullptr && tid <= kExperts) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) ec[i] = ldg16(a.codec + kCodecTableColumns * tid + 2 * i);
+    }
     const uint32_t xr_lo = static_cast<uint32_t>(((has_lo ? t_lo : 0) * kHidden + 32 * lane) * 2);
     const uint32_t xr_hi = static_cast<uint32_t>(((has_hi ? t_hi : 0) * kHidden + 32 * lane) * 2);
     const uint16_t* nr = (a.norm != nullptr ? a.norm : a.x) + 32 * lane;
@@ -543,7 +658,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const uint64_t both[2] = {lg_lo, lg_hi};
             int e2[2];
             uint32_t w2[2];
-            topk8_waves<2>(both, e2, w2);
+            topk8_waves<2>(both, e2, w2, lane);
             e_lo = e2[0];
             e_hi = e2[1];
             w_lo = w2[0];
@@ -557,7 +672,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                 }
             }
         } else if (has_lo) {
-            topk8_wave(lg_lo, e_lo, w_lo);
+            topk8_wave(lg_lo, e_lo, w_lo, lane);
             if (lane < kTopK) {
                 P.ids[t_lo][lane] = e_lo;
                 P.wts[t_lo][lane] = static_cast<uint16_t>(w_lo);
@@ -574,6 +689,10 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         if (bad) atomicOr(&P.status, bad);
     }
     if (tid < kExperts) P.eptr[tid] = eptr;
+    if (a.codec != nullptr && tid <= kExperts) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) P.ecodec[tid][i] = ec[i];
+    }
     __syncthreads();
 
     // ---- the first item's weights, before the rest of the plan ----
@@ -583,23 +702,111 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // expert) or one of token 0's experts, and streams in while the rest of
     // the plan is built.
     uint4 b0[kLoads], b1[kLoads];
-    auto issue = [&](const uint16_t* p, uint4* buf) {
-#pragma unroll
-        for (int s = 0; s < kLoads; ++s) buf[s] = ldg16(p + 32 * s);
+    // Prefetch target of an item without weights (C items): 1 KiB of token
+    // row 0, in cache after the first read.
+    const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
+    // Which of the lane's two tiles of an item it reads packed: bit t of
+    // `dec`.  A workgroup's first two items take it from the codec table's
+    // per-(item, wave) flags (both tiles packed when every tile of the
+    // wave's share fits; wave-uniform), later items from their tile bases,
+    // loaded one step before the item's own loads (tile_choice).
+    auto unit_choice = [&](const Item& it) __attribute__((always_inline)) -> uint32_t {
+        if (it.kind > 1) return 0u;
+        const SlotInfo& s = P.slot[it.slot];
+        if (s.pk_gu == nullptr) return 0u;
+        const uint8_t* flags = reinterpret_cast<const uint8_t*>(&P.ecodec[s.crow][2]);
+        return ((flags[(it.kind == 1 ? 32 : 0) + it.tile] >> wave) & 1u) == 0u ? 3u : 0u;
     };
+    // The bases of an item's two tiles of this lane (tile 0 in bits 0..7,
+    // tile 1 in bits 8..15), loaded (2 bytes) for the A/B items of codec
+    // slots; other items load kBothMisfit (both tiles raw).  The load is
+    // issued for every item, so that its register is never merged at a join
+    // before the wait.
+    auto load_bases = [&](const Item& it) __attribute__((always_inline)) -> uint32_t {
+        const void* at = &kBothMisfit;
+        if (it.kind == 0 || it.kind == 1) {
+            const SlotInfo& s = P.slot[it.slot];
+            if (s.pk_gu != nullptr) at = packed_lane(s, it, wave, lane).bases2;
+        }
+        return ldg_u16(at);
+    };
+    auto tile_choice = [](uint32_t bases) -> uint32_t {
+        return ((bases & 0xffu) != kCodecMisfit ? 1u : 0u) | ((bases >> 8) != kCodecMisfit ? 2u : 0u);
+    };
+    // One load sequence for every kind of item (only the addresses differ),
+    // so that no loaded register is copied at a join, which would wait for
+    // the loads.  Without codec tables: load i at the item's base + 64i (C
+    // items: cached token rows).  With them, tile t, register 8t + j:
+    // packed, block j of the tile (j < 6) or its bases block (j = 6, 7); raw,
+    // k-step kRawStep[j] of the tile.
+    auto issue_item = [&](const Item& it, uint4* buf, uint32_t dec) __attribute__((always_inline)) {
+        if constexpr (!kCodec) {
+            const uint16_t* p = (it.kind == 0 || it.kind == 1) ? item_base(P.slot[it.slot], it, wave, lane)
+                                                                : idle_rows;
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) buf[i] = ldg16(p + 32 * i);
+            return;
+        }
+        const uint8_t* raw = reinterpret_cast<const uint8_t*>(idle_rows);
+        const uint8_t* pk = raw;
+        const uint8_t* bases = raw;
+        if (it.kind == 0 || it.kind == 1) {
+            const SlotInfo& s = P.slot[it.slot];
+            raw = reinterpret_cast<const uint8_t*>(item_base(s, it, wave, lane));
+            if (s.pk_gu != nullptr) {
+                const PackedLane p = packed_lane(s, it, wave, lane);
+                pk = p.tile0 + 16 * (lane >> 4);
+                bases = p.bases16;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const bool packed = ((dec >> t) & 1u) != 0u;
+            const uint8_t* pt = pk + t * kCodecTileBytes;
+            const uint8_t* rt = raw + 512 * t;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                buf[8 * t + j] = ldg16(packed ? (j < 6 ? pt + 64 * j : bases) : rt + 64 * kRawStep[j]);
+            }
+        }
+    };
+    // The tile-codec addresses of an expert (kExperts: the shared one), or
+    // null when the call has no codec table or the expert's row does not
+    // give all four addresses (then it is read raw).
+    auto codec_of = [&](int row) -> const uint4* {
+        if (a.codec == nullptr) return nullptr;
+        const uint4* c = P.ecodec[row];
+        const bool all = (c[0].x | c[0].y) != 0u && (c[0].z | c[0].w) != 0u && (c[1].x | c[1].y) != 0u &&
+                         (c[1].z | c[1].w) != 0u;
+        return all ? c : nullptr;
+    };
+    // Slots 0..8 -- the shared expert and token 0's experts in rank order,
+    // the first slots in discovery order -- get their weight addresses now.
+    if (tid <= kTopK) {
+        if (tid == 0) {
+            set_slot_weights(P.slot[0], a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
+        } else {
+            const int e = P.ids[0][tid - 1];
+            const uint4 ptrs = P.eptr[e];
+            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
+                                                                        (static_cast<uintptr_t>(ptrs.y) << 32));
+            set_slot_weights(P.slot[tid], gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
+                             reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) |
+                                                               (static_cast<uintptr_t>(ptrs.w) << 32)),
+                             codec_of(e), e);
+        }
+    }
+    __syncthreads();
     const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
     int cur = (block - offset + G) % G;
+    uint32_t dec;  // tile choice of the item being run
     {
-        const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
-        const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
-        const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
-                                                                    (static_cast<uintptr_t>(ptrs.y) << 32));
-        const uint16_t* gate = s0 == 0 ? a.sh_gate : gate_up;
-        const uint16_t* up = s0 == 0 ? a.sh_up : gate_up + static_cast<size_t>(kInner) * kHidden;
-        // item_base's A geometry for tile cur % 32.
-        const int m = lane & 15;
-        const int row = 16 * (cur % kATiles) + 8 * (wave >> 2) + (m & 7);
-        issue((m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4), b0);
+        Item first;
+        first.kind = 0;
+        first.slot = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
+        first.tile = cur % kATiles;
+        dec = kCodec ? unit_choice(first) : 0u;
+        issue_item(first, b0, dec);
     }
 
     if (block == 0 && tid < T * kTopK) {
@@ -623,7 +830,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             if ((mask & ((1u << t) - 1u)) == 0u) opens = (1u << 16) | static_cast<uint32_t>(__popc(mask));
         }
         uint32_t packed_total = 0;
-        const uint32_t packed = block_scan256(opens, P.scan, &packed_total);
+        const uint32_t packed = block_scan256(opens, P.scan, &packed_total, tid);
         const uint32_t pair0 = packed & 0xffffu;
         const uint32_t rank = packed >> 16;
         const uint32_t unique = packed_total >> 16;
@@ -633,9 +840,10 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const uint4 ptrs = P.eptr[e];
             const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
                                                                         (static_cast<uintptr_t>(ptrs.y) << 32));
-            s.gate = gate_up;
-            s.up = gate_up + static_cast<size_t>(kInner) * kHidden;
-            s.down = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) | (static_cast<uintptr_t>(ptrs.w) << 32));
+            set_slot_weights(s, gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
+                             reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) |
+                                                               (static_cast<uintptr_t>(ptrs.w) << 32)),
+                             codec_of(e), e);
             uint32_t tok[4] = {0u, 0u, 0u, 0u};
             uint32_t m = mask;
 #pragma unroll
@@ -656,9 +864,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         if (tid == 0) {
             const bool shared = a.sh_down != nullptr && routes_ok;
             SlotInfo& s = P.slot[0];
-            s.gate = a.sh_gate;
-            s.up = a.sh_up;
-            s.down = a.sh_down;
+            set_slot_weights(s, a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
             uint32_t tok[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int j = 0; j < kMaxT; ++j) {
@@ -721,26 +927,23 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     uint64_t stg[8];
     const int stg_row = tid >> 5;
     const uint32_t stg_off = static_cast<uint32_t>(stg_row * (kInner / 2) * 8 + (tid & 31) * 64);
-    // Prefetch target of an item without weights (C items): 1 KiB of token
-    // row 0, in cache after the first read.
-    const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
     // Lanes of the claiming atomic: lane 0 of wave 0.
     const uint32_t claim_lanes = wave == 0 ? 1u : 0u;
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
 
-    auto weights_of = [&](const Item& it) -> const uint16_t* {
-        return it.kind == 0 || it.kind == 1 ? item_base(P.slot[it.slot], it, wave, lane) : idle_rows;
-    };
     auto stale_word = [&](uint64_t w) { return tag_of(w) != tag; };
 
-    // Runs item kk, whose weights are in buf, and prefetches item kn into
-    // nbuf.  Returns the item claimed for the step after next.
-    auto step = [&](int kk, int kn, uint4* buf, uint4* nbuf) -> int {
+    // Runs item kk, whose weights are in buf (tile choice `dec`), prefetches
+    // item kn into nbuf (tile choice from `bases`, its tile bases, which
+    // become those of kn2) and loads the tile bases of kn2.  Returns the item
+    // claimed for the step after kn2; ndec receives kn's tile choice.
+    auto step = [&](int kk, int kn, int kn2, uint4* buf, uint4* nbuf, uint32_t dec, uint32_t& ndec,
+                    uint32_t& bases) __attribute__((always_inline)) -> int {
         const Item it = item_at(kk, total, n_slots, first_slot);
         const Item nx = item_at(kn, total, n_slots, first_slot);
+        const Item nx2 = item_at(kn2, total, n_slots, first_slot);
         const SlotInfo& s = P.slot[it.slot];
-        const uint16_t* np = weights_of(nx);
         // Uniform base of the slot's 16 act rows (rows past its count are
         // padding, loaded but never used).
         const char* stg_base = reinterpret_cast<const char*>(a.act) +
@@ -755,15 +958,22 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             ld_agent64x4_async(stg + 4, stg_base, stg_off + 32);
         }
         const uint32_t claimed = claim_async(&cnt->claim, claim_lanes);
+        uint32_t next_bases = 0u;
+        ndec = 0u;
+        if constexpr (kCodec) {
+            next_bases = load_bases(nx2);
+            ndec = tile_choice(bases);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        issue(np, nbuf);
+        issue_item(nx, nbuf, ndec);
         __builtin_amdgcn_sched_barrier(0);
         // s_waitcnt vmcnt(16) (expcnt and lgkmcnt left at their maximum)
         // as a builtin, so that the compiler's own wait insertion knows
         // what it completed.
         __builtin_amdgcn_s_waitcnt(kWaitVm16);
         __builtin_amdgcn_sched_barrier(0);
-        if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + 2 * G;
+        bases = next_bases;
+        if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + (kCodec ? 3 : 2) * G;
         const int m = lane & 15;
         const int g = lane >> 4;
         if (it.kind == 1) {
@@ -804,10 +1014,28 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const int tok = column_token(s, m < s.count ? m : 0);
             const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (kCodec && s.pk_gu != nullptr) {
+                // Per tile: the decoded packed values or the raw row's.
+                const int bb = packed_lane(s, it, wave, lane).base_byte;
+                const uint32_t base0 = byte_of(buf[6], bb) * 0x01010101u;
+                const uint32_t base1 = byte_of(buf[14], bb + 1) * 0x01010101u;
 #pragma unroll
-            for (int q = 0; q < kLoads; q += 2) {
-                acc0 = mfma16x16x32(buf[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
-                acc1 = mfma16x16x32(buf[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                for (int q = 0; q < kLoads; q += 2) {
+                    const uint32_t base = q < kLoads / 2 ? base0 : base1;
+                    const uint32_t pk = 0u - ((dec >> (q >> 3)) & 1u);
+                    acc0 = mfma16x16x32(pick(pk, packed_operand(buf, q, base), buf[raw_reg(q)]),
+                                        *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                    acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
+                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kLoads; q += 2) {
+                    acc0 = mfma16x16x32(buf[kCodec ? raw_reg(q) : q], *reinterpret_cast<const uint4*>(bp + 32 * q),
+                                        acc0);
+                    acc1 = mfma16x16x32(buf[kCodec ? raw_reg(q + 1) : q + 1],
+                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                }
             }
             part[(par * kWaves + wave) * kWave + lane] = acc0 + acc1;
             __syncthreads();
@@ -831,10 +1059,28 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         } else if (it.kind == 1) {
             const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (kCodec && s.pk_gu != nullptr) {
+                // Per tile: the decoded packed values or the raw row's.
+                const int bb = packed_lane(s, it, wave, lane).base_byte;
+                const uint32_t base0 = byte_of(buf[6], bb) * 0x01010101u;
+                const uint32_t base1 = byte_of(buf[14], bb + 1) * 0x01010101u;
 #pragma unroll
-            for (int q = 0; q < kLoads; q += 2) {
-                acc0 = mfma16x16x32(buf[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
-                acc1 = mfma16x16x32(buf[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                for (int q = 0; q < kLoads; q += 2) {
+                    const uint32_t base = q < kLoads / 2 ? base0 : base1;
+                    const uint32_t pk = 0u - ((dec >> (q >> 3)) & 1u);
+                    acc0 = mfma16x16x32(pick(pk, packed_operand(buf, q, base), buf[raw_reg(q)]),
+                                        *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                    acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
+                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kLoads; q += 2) {
+                    acc0 = mfma16x16x32(buf[kCodec ? raw_reg(q) : q], *reinterpret_cast<const uint4*>(bp + 32 * q),
+                                        acc0);
+                    acc1 = mfma16x16x32(buf[kCodec ? raw_reg(q + 1) : q + 1],
+                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+                }
             }
             const f32x4 y = acc0 + acc1;
             if (m < s.count) {
@@ -859,10 +1105,11 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         return after;
     };
 
-    // The first two items of a workgroup are fixed (the first one's weights
-    // are already in flight); the rest are claimed.
+    // The first three items of a workgroup are fixed (the first one's
+    // weights are already in flight); the rest are claimed.
     if (cur < end) {
         int nxt = cur + G;
+        int nxt2 = cur + 2 * G;
         if (a.router == nullptr) {
             // Token rows staged while the first weights stream in.
             stage_rows();
@@ -882,14 +1129,38 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         // top, on which that step's prefetch is still in flight; every
         // iteration then waits for all loads before issuing the next
         // prefetch.)
-        do {
-            int after = step(cur, nxt, b0, b1);
-            cur = nxt;
-            nxt = after;
-            after = step(cur, nxt, b1, b0);
-            cur = nxt;
-            nxt = after;
-        } while (cur < end);
+        if constexpr (kCodec) {
+            // Items are claimed three ahead, so that each item's tile bases
+            // are loaded a step before its weights.  The second item's tile
+            // choice comes from the per-(item, wave) flags (as a bases value:
+            // 0 packs both tiles, 0xffff reads both raw).
+            uint32_t bases = unit_choice(item_at(nxt, total, n_slots, first_slot)) == 3u ? 0u : 0xffffu;
+            do {
+                uint32_t ndec;
+                int after = step(cur, nxt, nxt2, b0, b1, dec, ndec, bases);
+                cur = nxt;
+                nxt = nxt2;
+                nxt2 = after;
+                dec = ndec;
+                after = step(cur, nxt, nxt2, b1, b0, dec, ndec, bases);
+                cur = nxt;
+                nxt = nxt2;
+                nxt2 = after;
+                dec = ndec;
+            } while (cur < end);
+        } else {
+            // Items are claimed two ahead (claims number items from 2G on).
+            uint32_t bases = 0u;
+            do {
+                uint32_t ndec;
+                int after = step(cur, nxt, 0, b0, b1, 0u, ndec, bases);
+                cur = nxt;
+                nxt = after;
+                after = step(cur, nxt, 0, b1, b0, 0u, ndec, bases);
+                cur = nxt;
+                nxt = after;
+            } while (cur < end);
+        }
     }
 
     // ---- 5. this workgroup's share of the layer is done ----
@@ -898,6 +1169,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     return P.status & kStatusTimeout;
 }
 
+template <bool kCodec>
 __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     // A local copy: the helpers take it by reference, which must not force
     // the kernel-argument block into private memory.
@@ -906,7 +1178,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     __shared__ Plan P;
     // This call's number, from the count of finished workgroups (DecodeSync).
     const unsigned long long finished = ld_agent64(&a.sync->finished);
-    const int32_t timeout = decode_layer<false>(a, P, dyn, finished, 0, [] {});
+    const int32_t timeout = decode_layer<false, kCodec>(a, P, dyn, finished, 0, [] {});
     if (threadIdx.x == 0) {
         if (timeout) atomicOr(a.status, kStatusTimeout);
         __hip_atomic_fetch_add(&a.sync->finished, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -924,6 +1196,7 @@ struct ChainState {
 // Several decode layers in one launch, with a grid barrier between layers
 // (every workgroup is resident).  Layer l is decode call c + l, with c the
 // call number read at the start (DecodeSync).
+template <bool kCodec>
 __global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
     __shared__ Plan P;
@@ -962,6 +1235,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
         a.sh_down = w.sh_down;
         a.shared_expert_gate = w.shared_expert_gate;
         a.norm = w.norm;
+        a.codec = w.codec;
         // The chain always routes with the layer's router.
         a.logits_in = nullptr;
         a.indices_in = nullptr;
@@ -992,7 +1266,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
                 __syncthreads();
             }
         };
-        const int32_t timeout = decode_layer<true>(a, P, dyn, finished, l, wait_input);
+        const int32_t timeout = decode_layer<true, kCodec>(a, P, dyn, finished, l, wait_input);
         if (threadIdx.x == 0) {
             S.timeout |= timeout;
             if (l + 1 < c.layers) {
@@ -1065,24 +1339,43 @@ hipError_t persistent_grid(Kernel kernel, LaunchSetup (&setup)[64], int* grid) {
 hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
     if (a.tokens > kMaxT) return hipErrorInvalidValue;
-    static LaunchSetup setup[64];
+    // The codec kernel carries the tile-choice pipeline; calls without codec
+    // tables run the kernel without it.
+    static LaunchSetup setup[2][64];
+    const bool codec = a.codec != nullptr;
     int grid = 0;
-    const hipError_t err = persistent_grid(moe_decode, setup, &grid);
+    const hipError_t err = codec ? persistent_grid(moe_decode<true>, setup[1], &grid)
+                                 : persistent_grid(moe_decode<false>, setup[0], &grid);
     if (err != hipSuccess) return err;
     const StageEvents ev = timing_events(kStageLayer);
-    LRMOE_LAUNCH(moe_decode, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start, ev.stop, a);
+    if (codec) {
+        LRMOE_LAUNCH(moe_decode<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start,
+                     ev.stop, a);
+    } else {
+        LRMOE_LAUNCH(moe_decode<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start,
+                     ev.stop, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_moe_chain(const ChainArgs& a, hipStream_t stream) {
     if (a.base.tokens <= 0 || a.layers <= 0) return hipSuccess;
     if (a.base.tokens > kMaxT) return hipErrorInvalidValue;
-    static LaunchSetup setup[64];
+    static LaunchSetup setup[2][64];
+    bool codec = false;
+    for (int l = 0; l < a.layers; ++l) codec |= a.layer[l].codec != nullptr;
     int grid = 0;
-    const hipError_t err = persistent_grid(moe_chain, setup, &grid);
+    const hipError_t err = codec ? persistent_grid(moe_chain<true>, setup[1], &grid)
+                                 : persistent_grid(moe_chain<false>, setup[0], &grid);
     if (err != hipSuccess) return err;
     const StageEvents ev = timing_events(kStageLayer);
-    LRMOE_LAUNCH(moe_chain, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start, ev.stop, a);
+    if (codec) {
+        LRMOE_LAUNCH(moe_chain<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start,
+                     ev.stop, a);
+    } else {
+        LRMOE_LAUNCH(moe_chain<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start,
+                     ev.stop, a);
+    }
     return hipGetLastError();
 }
 

@@ -153,6 +153,27 @@ __device__ __forceinline__ float fma8(uint4 w, const float* x, float acc) {
 // LDS counter too, so every LDS access would wait for all weight loads.
 typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
 
+// Eight values of a codec tile (format in codec.hip): the low bytes of
+// values 0..3 in `low0` and of 4..7 in `low1`, the code of value j in nibble
+// j / 4 of byte j % 4 of `codes`, base4 = base * 0x01010101.  Returns the
+// eight bf16 values in order (value 2i in the low half of component i).  A
+// high byte is (base + (code & 7)) | (sign << 7): four at a time, one per
+// byte (a value's field base + (code & 7) <= 127, so no byte carries into the
+// next), then v_perm_b32 interleaves them with the low bytes (byte i of the
+// result is byte sel_i of {first operand : second operand}, the second
+// operand holding bytes 0..3).
+__device__ __forceinline__ uint4 codec_decode8(uint32_t low0, uint32_t low1, uint32_t codes, uint32_t base4) {
+    const uint32_t h0 = ((codes & 0x07070707u) + base4) | ((codes << 4) & 0x80808080u);
+    const uint32_t h1 = (((codes >> 4) & 0x07070707u) + base4) | (codes & 0x80808080u);
+    return make_uint4(__builtin_amdgcn_perm(h0, low0, 0x05010400u), __builtin_amdgcn_perm(h0, low0, 0x07030602u),
+                      __builtin_amdgcn_perm(h1, low1, 0x05010400u), __builtin_amdgcn_perm(h1, low1, 0x07030602u));
+}
+
+// 2-byte load through a global pointer (see ldg16), zero-extended.
+__device__ __forceinline__ uint32_t ldg_u16(const void* p) {
+    return *reinterpret_cast<__attribute__((address_space(1))) const uint16_t*>(reinterpret_cast<uintptr_t>(p));
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) {
     const u32x4 v = *reinterpret_cast<global_u32x4*>(reinterpret_cast<uintptr_t>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -195,10 +216,10 @@ __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
 // then the eight probabilities are renormalised by their sum in rank order
 // and rounded to bf16.  Lane k < 8 receives the expert and weight bits of
 // rank k.  Same arithmetic and order as the oracle.  topk8_waves does this
-// for N tokens at once, their steps interleaved.
+// for N tokens at once, their steps interleaved.  `lane` is the caller's lane
+// index (threadIdx.x % 64).
 template <int N>
-__device__ __forceinline__ void topk8_waves(const uint64_t* packed, int* expert, uint32_t* weight_bits) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void topk8_waves(const uint64_t* packed, int* expert, uint32_t* weight_bits, int lane) {
     uint32_t bits[N][4], k[N][4];
 #pragma unroll
     for (int n = 0; n < N; ++n) {
@@ -265,15 +286,16 @@ __device__ __forceinline__ void topk8_waves(const uint64_t* packed, int* expert,
     }
 }
 
-__device__ __forceinline__ void topk8_wave(uint64_t packed, int& expert, uint32_t& weight_bits) {
-    topk8_waves<1>(&packed, &expert, &weight_bits);
+__device__ __forceinline__ void topk8_wave(uint64_t packed, int& expert, uint32_t& weight_bits, int lane) {
+    topk8_waves<1>(&packed, &expert, &weight_bits, lane);
 }
 
-// Exclusive scan over threads 0..255 (all threads call; others contribute 0).
-__device__ __forceinline__ uint32_t block_scan256(uint32_t value, uint32_t* scratch, uint32_t* total) {
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    if (threadIdx.x >= kExperts) value = 0;
+// Exclusive scan over threads 0..255 (all threads call, tid = threadIdx.x;
+// others contribute 0).
+__device__ __forceinline__ uint32_t block_scan256(uint32_t value, uint32_t* scratch, uint32_t* total, int tid) {
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    if (tid >= kExperts) value = 0;
     uint32_t inclusive = value;
 #pragma unroll
     for (int offset = 1; offset < kWave; offset <<= 1) {
@@ -286,7 +308,7 @@ __device__ __forceinline__ uint32_t block_scan256(uint32_t value, uint32_t* scra
     for (int w = 0; w < wave && w < 4; ++w) before += scratch[w];
     *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
     __syncthreads();
-    return threadIdx.x < kExperts ? before + inclusive - value : 0u;
+    return tid < kExperts ? before + inclusive - value : 0u;
 }
 
 }  // namespace lrmoe

@@ -22,6 +22,10 @@ constexpr int kDecodeMaxTokens = 16;
 constexpr int kDecodeSlots = 8 * kDecodeMaxTokens + 1;  // unique routed experts + the shared expert
 constexpr int kSyncStride = 64;  // counters 256 bytes apart (separate memory channels)
 constexpr int kPassTok = 128;    // prefill: tokens of one expert per work unit
+constexpr int kCodecTile = 256;        // values per codec tile
+constexpr int kCodecTileBytes = 384;   // packed bytes per tile (low bytes, then 4-bit codes)
+constexpr int kCodecTableColumns = 10;  // int64 per expert in a decode codec table
+constexpr int kCodecMisfit = 255;      // base of a tile whose exponent fields span more than 8 values
 
 // Cross-workgroup counter of one decode call.
 struct DecodeCounters {
@@ -219,6 +223,9 @@ struct DecodeArgs {
     const uint16_t* sh_up;        // [512][2048]
     const uint16_t* sh_down;      // [2048][512]
     const int64_t* expert_ptrs;   // [256][2] (gate_up, down)
+    const int64_t* codec;         // [257][10] per expert, row 256 the shared expert: tile-codec addresses
+                                  // (packed gate_up, packed down, gate_up bases, down bases), then 48 bytes of
+                                  // per-(item, wave) raw flags; a zero row reads raw; or null
     uint16_t* out;                // [T][2048]
     int64_t* indices_out;         // [T][8] or null
     uint16_t* weights_out;        // [T][8] or null
@@ -243,6 +250,7 @@ struct ChainLayer {
     const uint16_t* sh_down;             // [2048][512]
     const uint16_t* shared_expert_gate;  // [2048]
     const uint16_t* norm;                // [2048] RMSNorm weight, or null (no norm, no residual)
+    const int64_t* codec;                // [257][10] tile-codec table (DecodeArgs::codec), or null
 };
 constexpr int kChainMaxLayers = 48;  // the arguments stay under 4 KiB
 struct ChainArgs {
@@ -315,6 +323,10 @@ hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in
                                const Workspace& ws, const Plan& plan, hipStream_t stream);
 hipError_t launch_prefill_experts(const ExpertArgs& args, hipStream_t stream);
 size_t decode_lds_bytes(int tokens);
+hipError_t launch_codec_pack(const uint16_t* w, int64_t rows, int cols, uint8_t* packed, uint8_t* bases,
+                             unsigned long long* misfit, hipStream_t stream);
+hipError_t launch_codec_unpack(const uint8_t* packed, const uint8_t* bases, int64_t rows, int cols, uint16_t* w,
+                               hipStream_t stream);
 hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
                               int64_t first, hipStream_t stream);
 

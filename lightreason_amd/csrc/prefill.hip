@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void pf_topk(const uint16_t* logits, const int
         if (indices_in == nullptr) {
             const uint64_t packed = *reinterpret_cast<const uint64_t*>(logits + static_cast<size_t>(t) * kExperts + 4 * lane);
             uint32_t w = 0;
-            topk8_wave(packed, e, w);
+            topk8_wave(packed, e, w, static_cast<int>(threadIdx.x & 63));
             if (lane < kTopK) {
                 indices[t * kTopK + lane] = e;
                 weights[t * kTopK + lane] = static_cast<uint16_t>(w);
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void pf_scan(int nblk, Workspace ws, Plan plan
     uint32_t local = 0;
     for (int b = b0; b < b1; ++b) local += __popc(row[b]);
     uint32_t total = 0;
-    uint32_t running = block_scan256(local, scratch, &total);
+    uint32_t running = block_scan256(local, scratch, &total, static_cast<int>(threadIdx.x));
     for (int b = b0; b < b1; ++b) {
         ws.blk_base[static_cast<size_t>(e) * ws.nblk_pad + b] = running;
         running += __popc(row[b]);
@@ -139,8 +139,8 @@ __global__ __launch_bounds__(256) void pf_fill(const int64_t* indices, int token
     }
     const uint32_t count = ws.counts[e];
     uint32_t pairs = 0, unique = 0;
-    const uint32_t pair0 = block_scan256(count, scratch, &pairs);
-    const uint32_t rank = block_scan256(count ? 1u : 0u, scratch, &unique);
+    const uint32_t pair0 = block_scan256(count, scratch, &pairs, static_cast<int>(threadIdx.x));
+    const uint32_t rank = block_scan256(count ? 1u : 0u, scratch, &unique, static_cast<int>(threadIdx.x));
     off[e] = pair0;
     if (blk == 0) {
         if (count) {
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void pf_fill(const int64_t* indices, int token
         const uint32_t passes = (count + kPassTok - 1) / kPassTok;
         uint32_t unit_total = 0;
         const uint32_t shared_units = shared_present ? (tokens + kPassTok - 1) / kPassTok : 0u;
-        const uint32_t first_unit = shared_units + block_scan256(passes, scratch, &unit_total);
+        const uint32_t first_unit = shared_units + block_scan256(passes, scratch, &unit_total, static_cast<int>(threadIdx.x));
         // A unit names its expert and pair range directly, so an expert
         // workgroup reaches its weight addresses in two dependent loads.
         for (uint32_t j = threadIdx.x; j < shared_units; j += 256) {

@@ -162,6 +162,135 @@ class ExpertBank:
         return self.bank.numel() * 2
 
 
+# ---- lossless BF16 tile codec --------------------------------------------------
+
+CODEC_TILE = 256
+CODEC_TILE_BYTES = 384
+CODEC_MISFIT = 255
+CODEC_GU_PACKED = 2 * INNER * (HIDDEN // CODEC_TILE) * CODEC_TILE_BYTES   # 3 MiB
+CODEC_DN_PACKED = HIDDEN * (INNER // CODEC_TILE) * CODEC_TILE_BYTES       # 1.5 MiB
+CODEC_GU_BASES = 2 * INNER * (HIDDEN // CODEC_TILE)                        # 8 KiB
+CODEC_DN_BASES = HIDDEN * (INNER // CODEC_TILE)                            # 4 KiB
+# One expert's block: packed gate_up, packed down, their bases, and room for
+# the 16-byte base loads that read past the last row.
+CODEC_EXPERT_BYTES = (CODEC_GU_PACKED + CODEC_DN_PACKED + CODEC_GU_BASES + CODEC_DN_BASES + 256 + 4095) // 4096 * 4096
+
+
+def codec_pack(w: torch.Tensor, packed: torch.Tensor, bases: torch.Tensor,
+               misfit: torch.Tensor | None = None) -> None:
+    """Pack a [rows, cols] bf16 matrix (cols a multiple of 256; row stride
+    cols) into tile-codec form: ``packed`` uint8 [rows * cols / 256 * 384],
+    ``bases`` uint8 [rows * cols / 256]; ``misfit`` (int64 [1]) is increased
+    by the number of tiles that do not fit (lrmoe_codec_pack)."""
+    rows, cols = w.shape
+    if w.dtype != torch.bfloat16 or w.stride() != (cols, 1):
+        raise ValueError("codec_pack takes a row-contiguous bf16 matrix")
+    tiles = rows * cols // CODEC_TILE
+    if packed.numel() < tiles * CODEC_TILE_BYTES or bases.numel() < tiles:
+        raise ValueError("codec_pack output buffers are too small")
+    _native.call("lrmoe_codec_pack", w.data_ptr(), rows, cols, packed.data_ptr(), bases.data_ptr(), _opt(misfit),
+                 _stream(w.device))
+
+
+def codec_unpack(packed: torch.Tensor, bases: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=packed.device)
+    _native.call("lrmoe_codec_unpack", packed.data_ptr(), bases.data_ptr(), rows, cols, out.data_ptr(),
+                 _stream(packed.device))
+    return out
+
+
+CODEC_TABLE_COLUMNS = _native.CODEC_TABLE_COLUMNS   # 4 addresses + 48 bytes of per-(item, wave) raw flags
+
+
+def codec_unit_flags(gu_bases: torch.Tensor, dn_bases: torch.Tensor) -> torch.Tensor:
+    """Raw flags of the decode kernel's (item, wave) units from an expert's
+    tile bases: byte i (0..31) for gate/up item i, byte 32 + i (0..15) for
+    down item i; bit w is set when a tile read by wave w of that item does
+    not fit the codec.  Gate/up item i, wave w reads tiles 2(w%4), 2(w%4)+1
+    of gate rows and up rows 16i + 8(w/4) .. +7; down item i, wave w reads
+    both tiles of down rows 128i + 16w .. +15.  Leading dimensions of the
+    bases ([..., 8192] and [..., 4096]) are kept: the result is [..., 48]."""
+    lead = gu_bases.shape[:-1]
+    gu = gu_bases.reshape(*lead, 2, 32, 2, 8, 4, 2) == CODEC_MISFIT   # [gate/up, item, w/4, row, w%4, tile]
+    a = gu.any(dim=-1).any(dim=-2).any(dim=-4)                         # [item, w/4, w%4]
+    a = a.reshape(*lead, 32, 8).to(torch.int32)
+    dn = (dn_bases.reshape(*lead, 16, 8, 16, 2) == CODEC_MISFIT).any(dim=-1).any(dim=-1).to(torch.int32)
+    weights = 1 << torch.arange(8, dtype=torch.int32, device=a.device)   # bit w for wave w
+    return torch.cat([(a * weights).sum(dim=-1), (dn * weights).sum(dim=-1)], dim=-1).to(torch.uint8)
+
+
+class CodecBank:
+    """Tile-codec copies of an ExpertBank's experts (and of each layer's
+    shared expert) for the decode kernel.  ``tables[l]`` is a device int64
+    [257, 10] table per expert (row 256 the shared expert): the addresses of
+    the packed gate_up, packed down, gate_up bases and down bases, then 48
+    bytes of raw flags (codec_unit_flags).  A wave whose unit has a tile that
+    does not fit (its exponent fields span more than 8 values) reads that
+    unit's raw rows; an all-zero row reads the whole expert raw."""
+
+    def __init__(self, bank: ExpertBank, shared=None):
+        """``shared``: per layer (gate_proj [512,2048], up_proj [512,2048],
+        down_proj [2048,512]) or None."""
+        self.layers = bank.layers
+        self.device = bank.device
+        slots = EXPERTS + 1
+        self.blob = torch.zeros((bank.layers, slots, CODEC_EXPERT_BYTES), dtype=torch.uint8, device=self.device)
+        misfit = torch.zeros((bank.layers, slots), dtype=torch.int64, device=self.device)
+        present = torch.ones((bank.layers, slots), dtype=torch.bool)
+        for layer in range(bank.layers):
+            for e in range(EXPERTS):
+                gate_up, down = bank.expert(layer, e)
+                self._pack(layer, e, gate_up[:INNER], gate_up[INNER:], down, misfit[layer, e:e + 1])
+            if shared is not None and shared[layer] is not None:
+                g, u, d = shared[layer]
+                self._pack(layer, EXPERTS, g, u, d, misfit[layer, EXPERTS:EXPERTS + 1])
+            else:
+                present[layer, EXPERTS] = False
+        self.misfit = misfit.cpu()   # tiles that do not fit, per expert
+        gu0 = CODEC_GU_PACKED + CODEC_DN_PACKED
+        dn0 = gu0 + CODEC_GU_BASES
+        flags = codec_unit_flags(self.blob[:, :, gu0:gu0 + CODEC_GU_BASES],
+                                 self.blob[:, :, dn0:dn0 + CODEC_DN_BASES]).cpu()      # [L, 257, 48]
+        bits = (flags[present].to(torch.int32).unsqueeze(-1) >> torch.arange(8, dtype=torch.int32)) & 1
+        self.raw_units = int(bits.sum())
+        self.units = bits.numel()
+        base = self.blob.data_ptr()
+        tables = torch.zeros((bank.layers, slots, CODEC_TABLE_COLUMNS), dtype=torch.int64)
+        tables[:, :, 4:] = flags.cpu().view(torch.int64).view(bank.layers, slots, 6)
+        for layer in range(bank.layers):
+            for e in range(slots):
+                if not present[layer, e]:
+                    tables[layer, e] = 0
+                    continue
+                start = base + (layer * slots + e) * CODEC_EXPERT_BYTES
+                tables[layer, e, :4] = torch.tensor([start, start + CODEC_GU_PACKED, start + gu0, start + dn0])
+        self.tables = tables.to(self.device)
+
+    def _pack(self, layer, e, gate, up, down, misfit):
+        block = self.blob[layer, e]
+        gu_packed = block[:CODEC_GU_PACKED]
+        dn_packed = block[CODEC_GU_PACKED:CODEC_GU_PACKED + CODEC_DN_PACKED]
+        gu_bases = block[CODEC_GU_PACKED + CODEC_DN_PACKED:CODEC_GU_PACKED + CODEC_DN_PACKED + CODEC_GU_BASES]
+        dn_bases = block[CODEC_GU_PACKED + CODEC_DN_PACKED + CODEC_GU_BASES:
+                         CODEC_GU_PACKED + CODEC_DN_PACKED + CODEC_GU_BASES + CODEC_DN_BASES]
+        half_packed, half_bases = CODEC_GU_PACKED // 2, CODEC_GU_BASES // 2
+        codec_pack(gate, gu_packed[:half_packed], gu_bases[:half_bases], misfit)
+        codec_pack(up, gu_packed[half_packed:], gu_bases[half_bases:], misfit)
+        codec_pack(down, dn_packed, dn_bases, misfit)
+
+    def table(self, layer: int) -> torch.Tensor:
+        return self.tables[layer]
+
+    @property
+    def packed_fraction(self) -> float:
+        """Share of the (item, wave) units read from the codec form."""
+        return 1.0 - self.raw_units / max(self.units, 1)
+
+    @property
+    def nbytes(self) -> int:
+        return self.blob.numel()
+
+
 @dataclass
 class LayerWeights:
     """Everything one sparse MoE block reads besides the routed experts."""
@@ -174,6 +303,7 @@ class LayerWeights:
     shared_expert_gate: torch.Tensor | None = None  # [2048] (Linear(2048, 1).weight flattened)
     norm_weight: torch.Tensor | None = None    # [2048] RMSNorm weight (scale 1 + w)
     eps: float = 1e-6
+    codec: torch.Tensor | None = None          # [257, 10] int64 tile-codec table (CodecBank.table), or None
 
     def check(self, device) -> None:
         _check(self.router, "router", torch.bfloat16, (EXPERTS, HIDDEN), device)
@@ -188,6 +318,8 @@ class LayerWeights:
             _check(self.shared_expert_gate, "shared_expert_gate", torch.bfloat16, (HIDDEN,), device)
         if self.norm_weight is not None:
             _check(self.norm_weight, "norm_weight", torch.bfloat16, (HIDDEN,), device)
+        if self.codec is not None:
+            _check(self.codec, "codec", torch.int64, (EXPERTS + 1, CODEC_TABLE_COLUMNS), device)
 
 
 # ---- the hot path ---------------------------------------------------------------
@@ -274,6 +406,7 @@ def moe_layer(hidden: torch.Tensor, layer: LayerWeights, *, out: torch.Tensor | 
         out = torch.empty_like(hidden)
     router = None if logits_in is not None else layer.router.data_ptr()
     _native.call("lrmoe_moe_layer", hidden.data_ptr(), tokens, router, _opt(logits_in), layer.expert_ptrs.data_ptr(),
+                 _opt(layer.codec),
                  _opt(layer.shared_gate_proj), _opt(layer.shared_up_proj), _opt(layer.shared_down_proj),
                  _opt(layer.shared_expert_gate), _opt(layer.norm_weight), float(layer.eps), out.data_ptr(),
                  _opt(indices), _opt(weights), ws.ptr, ws.nbytes, _stream(device))
@@ -287,7 +420,7 @@ def chain_table(layers) -> "C.Array":
     table = (C.c_int64 * (_native.CHAIN_PTRS * len(layers)))()
     for l, w in enumerate(layers):
         row = [w.router.data_ptr(), w.expert_ptrs.data_ptr(), _opt(w.shared_gate_proj), _opt(w.shared_up_proj),
-               _opt(w.shared_down_proj), _opt(w.shared_expert_gate), _opt(w.norm_weight), 0]
+               _opt(w.shared_down_proj), _opt(w.shared_expert_gate), _opt(w.norm_weight), _opt(w.codec)]
         for i, v in enumerate(row):
             table[_native.CHAIN_PTRS * l + i] = v or 0
     return table

@@ -451,3 +451,80 @@ void lro_moe_layer(const uint16_t *x, int tokens, const uint16_t *router,
     free(logits);
     free(normed);
 }
+
+/* ---- lossless BF16 tile codec, in the decode kernel's layout ----------------
+ *
+ * Format of edge35b/cpu_bf16_reads.h:16-52 (pack_cpu_read_tiles) and
+ * bf16_gather_ada.cu:117-123 (unpack_cpu_tile_pair): a row is cut into tiles
+ * of 256 values.  base = the smallest 7-bit field (bits 14..8) of the tile's
+ * values; a tile whose fields span more than 8 values does not fit (base 255,
+ * the reference's raw marker).  Each value keeps its low byte (bits 7..0) and
+ * the 4-bit code (field - base) | (sign << 3).
+ *
+ * Byte order (the decode kernel's MFMA lane mapping; the reference stores
+ * values in index order): value k = 8g + 32s + j of a tile (g 0..3, s 0..7,
+ * j 0..7) has its low byte at LRO_CODEC_LOW(g, s, j) = 64(s/2) + 16g +
+ * 8(s%2) + j and its code in the nibble j/4 (low nibble first) of byte
+ * LRO_CODEC_CODE(g, s, j) = 256 + 64(s/4) + 16g + 4(s%4) + j%4.  The six
+ * 16-byte blocks of a k-group g then sit at 16g + 64i (i = 0..5), and those of
+ * the next tile continue at 16g + 64i for i = 6..11.  A tile is 384 bytes; the
+ * base of tile t of row r is bases[r * (cols / 256) + t].
+ */
+#define LRO_CODEC_LOW(g, s, j) (64 * ((s) >> 1) + 16 * (g) + 8 * ((s) & 1) + (j))
+#define LRO_CODEC_CODE(g, s, j) (256 + 64 * ((s) >> 2) + 16 * (g) + 4 * ((s) & 3) + ((j) & 3))
+#define LRO_CODEC_TILE 256
+#define LRO_CODEC_TILE_BYTES 384
+
+int64_t lro_codec_pack(const uint16_t *w, int64_t rows, int cols, uint8_t *packed, uint8_t *bases) {
+    const int tiles = cols / LRO_CODEC_TILE;
+    int64_t misfit = 0;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int t = 0; t < tiles; ++t) {
+            const uint16_t *v = w + r * cols + (int64_t)t * LRO_CODEC_TILE;
+            uint8_t *out = packed + (r * tiles + t) * LRO_CODEC_TILE_BYTES;
+            int low = 127, high = 0;
+            for (int k = 0; k < LRO_CODEC_TILE; ++k) {
+                const int field = (v[k] >> 8) & 127;
+                if (field < low) low = field;
+                if (field > high) high = field;
+            }
+            memset(out, 0, LRO_CODEC_TILE_BYTES);
+            if (high - low > 7) {
+                bases[r * tiles + t] = 255;
+                ++misfit;
+                continue;
+            }
+            bases[r * tiles + t] = (uint8_t)low;
+            for (int k = 0; k < LRO_CODEC_TILE; ++k) {
+                const int g = (k >> 3) & 3, s = k >> 5, j = k & 7;
+                const int code = (((v[k] >> 8) & 127) - low) | ((v[k] >> 15) << 3);
+                out[LRO_CODEC_LOW(g, s, j)] = (uint8_t)(v[k] & 255);
+                out[LRO_CODEC_CODE(g, s, j)] |= (uint8_t)(code << (4 * (j >> 2)));
+            }
+        }
+    }
+    return misfit;
+}
+
+/* Inverse of lro_codec_pack for tiles that fit; a tile with base 255 decodes
+ * to 0xffff in every position. */
+void lro_codec_unpack(const uint8_t *packed, const uint8_t *bases, int64_t rows, int cols, uint16_t *w) {
+    const int tiles = cols / LRO_CODEC_TILE;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int t = 0; t < tiles; ++t) {
+            const uint8_t *in = packed + (r * tiles + t) * LRO_CODEC_TILE_BYTES;
+            const int base = bases[r * tiles + t];
+            uint16_t *v = w + r * cols + (int64_t)t * LRO_CODEC_TILE;
+            for (int k = 0; k < LRO_CODEC_TILE; ++k) {
+                if (base == 255) {
+                    v[k] = 0xffff;
+                    continue;
+                }
+                const int g = (k >> 3) & 3, s = k >> 5, j = k & 7;
+                const int code = (in[LRO_CODEC_CODE(g, s, j)] >> (4 * (j >> 2))) & 15;
+                const int high = (base + (code & 7)) | ((code & 8) << 4);
+                v[k] = (uint16_t)((high << 8) | in[LRO_CODEC_LOW(g, s, j)]);
+            }
+        }
+    }
+}

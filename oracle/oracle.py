@@ -24,6 +24,7 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "_build" / "liblro.so"
 REF = HERE / "_ref" / "libcpu_experts.so"
 REF_WORKERS = HERE / "_ref" / "libpacked_workers.so"
+REF_TILE_CODEC = HERE / "_ref" / "libref_tile_codec.so"
 HIDDEN, INNER, EXPERTS, TOPK = 2048, 512, 256, 8
 EXPERT_ELEMENTS = 3 * INNER * HIDDEN
 
@@ -72,6 +73,10 @@ def lib() -> C.CDLL:
     so.lro_bucket.restype = C.c_int
     so.lro_combine.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
     so.lro_moe_layer.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P]
+    so.lro_codec_pack.argtypes = [_P, C.c_int64, C.c_int, _P, _P]
+    so.lro_codec_pack.restype = C.c_int64
+    so.lro_codec_unpack.argtypes = [_P, _P, C.c_int64, C.c_int, _P]
+    so.lro_codec_unpack.restype = None
     for name in ("lro_fill_normal_bf16", "lro_expert_pair", "lro_expert_rows", "lro_expert_block_rows",
                  "lro_route", "lro_shared_gate", "lro_rmsnorm", "lro_combine", "lro_moe_layer"):
         getattr(so, name).restype = None
@@ -253,6 +258,46 @@ def moe_layer(x, router, gate_up, down, shared=None, norm_weight=None, eps: floa
                         _ptr(sg_proj), _ptr(su_proj), _ptr(sd_proj), _ptr(sgate), _ptr(norm_weight), float(eps),
                         _ptr(out), _ptr(indices), _ptr(weights))
     return out, indices, weights
+
+
+CODEC_TILE = 256
+CODEC_TILE_BYTES = 384
+
+
+def codec_pack(w: np.ndarray):
+    """Tile-codec packing of a [rows, cols] bf16-bit array (cols a multiple of
+    256) in the decode kernel's byte order.  Returns (packed [rows, tiles,
+    384] u8, bases [rows, tiles] u8, number of tiles that do not fit)."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    rows, cols = w.shape
+    tiles = cols // CODEC_TILE
+    packed = np.empty((rows, tiles, CODEC_TILE_BYTES), dtype=np.uint8)
+    bases = np.empty((rows, tiles), dtype=np.uint8)
+    misfit = lib().lro_codec_pack(_ptr(w), rows, cols, _ptr(packed), _ptr(bases))
+    return packed, bases, int(misfit)
+
+
+def codec_unpack(packed: np.ndarray, bases: np.ndarray) -> np.ndarray:
+    rows, tiles, _ = packed.shape
+    out = np.empty((rows, tiles * CODEC_TILE), dtype=np.uint16)
+    lib().lro_codec_unpack(_ptr(np.ascontiguousarray(packed)), _ptr(np.ascontiguousarray(bases)), rows,
+                           tiles * CODEC_TILE, _ptr(out))
+    return out
+
+
+@lru_cache(maxsize=1)
+def reference_tile_codec() -> C.CDLL | None:
+    """The reference's own tile packer (edge35b/cpu_bf16_reads.h:16-52), built
+    into oracle/_ref by oracle/Makefile where /root/reference is present."""
+    if not REF_TILE_CODEC.exists():
+        if Path("/root/reference/edge35b/cpu_bf16_reads.h").exists():
+            build(ref=True)
+        else:
+            return None
+    so = C.CDLL(str(REF_TILE_CODEC))
+    so.ref_pack_cpu_read_tiles.argtypes = [_P, _P, _P, C.c_size_t]
+    so.ref_pack_cpu_read_tiles.restype = C.c_int64
+    return so
 
 
 def physical_cores() -> int:

@@ -1,0 +1,163 @@
+"""Lossless BF16 tile codec on an MI355X: packing against the oracle, and
+decode layers reading codec experts against the same layers reading raw
+rows.
+
+Bar: packed bytes, tile bases and misfit counts bit-identical to the oracle
+(oracle/lro.c lro_codec_pack, itself checked against the reference's tile
+packer in tests/test_oracle.py); unpacking restores the raw bits; a decode
+layer or chain reading codec experts gives bit-identical outputs and routes
+to the same call reading the raw rows (each MFMA sees the same operands in
+the same order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import to_u16
+
+pytestmark = pytest.mark.gpu
+
+
+def _mixed_matrix(rows: int, cols: int, seed: int) -> np.ndarray:
+    """bf16 bits whose tiles mostly fit the codec; every 5th tile spans the
+    whole exponent range (does not fit)."""
+    rng = np.random.default_rng(seed)
+    tiles = rows * cols // 256
+    base = rng.integers(0, 121, size=(tiles, 1))
+    field = base + rng.integers(0, 8, size=(tiles, 256))
+    bits = (rng.integers(0, 2, size=(tiles, 256)) << 15) | (field << 8) | rng.integers(0, 256, size=(tiles, 256))
+    bits[::5] = rng.integers(0, 65536, size=bits[::5].shape)
+    return bits.astype(np.uint16).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (200, 512), (3, 256)])
+def test_codec_pack_matches_oracle(device, oracle, rows, cols):
+    from lightreason_amd.moe import codec_pack, codec_unpack
+
+    bits = _mixed_matrix(rows, cols, seed=rows + cols)
+    w = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)
+    tiles = rows * cols // 256
+    packed = torch.full((tiles * 384,), 0x5A, dtype=torch.uint8, device=device)
+    bases = torch.full((tiles,), 0x5A, dtype=torch.uint8, device=device)
+    misfit = torch.zeros(1, dtype=torch.int64, device=device)
+    codec_pack(w, packed, bases, misfit)
+    back = codec_unpack(packed, bases, rows, cols)
+    torch.cuda.synchronize()
+    o_packed, o_bases, o_misfit = oracle.codec_pack(bits)
+    assert int(misfit.item()) == o_misfit > 0
+    np.testing.assert_array_equal(bases.cpu().numpy(), o_bases.ravel())
+    np.testing.assert_array_equal(packed.cpu().numpy(), o_packed.ravel())
+    np.testing.assert_array_equal(to_u16(back), oracle.codec_unpack(o_packed, o_bases))
+
+
+@pytest.fixture(scope="module")
+def codec_bank(model):
+    from lightreason_amd.moe import CodecBank
+
+    layer = model.layers[0]
+    bank = CodecBank(model.bank, [(layer.shared_gate_proj, layer.shared_up_proj, layer.shared_down_proj)])
+    torch.cuda.synchronize()
+    return bank
+
+
+def test_codec_bank_round_trips_experts(model, codec_bank):
+    from lightreason_amd.moe import CODEC_DN_PACKED, CODEC_GU_BASES, CODEC_GU_PACKED, CODEC_MISFIT, codec_unpack
+
+    # Gaussian weights: about 1% of tiles hold a value too small for their
+    # tile's window; every expert has some, and most units still read packed.
+    assert int((codec_bank.misfit[0] > 0).sum()) == 257
+    assert 0.5 < codec_bank.packed_fraction < 1.0
+    blob = codec_bank.blob[0]
+    gu0 = CODEC_GU_PACKED + CODEC_DN_PACKED
+    for e in (0, 77, 255, 256):
+        if e == 256:
+            layer = model.layers[0]
+            gate_up = torch.cat([layer.shared_gate_proj, layer.shared_up_proj])
+            down = layer.shared_down_proj
+        else:
+            gate_up, down = model.bank.expert(0, e)
+        block = blob[e]
+        gu = codec_unpack(block[:CODEC_GU_PACKED], block[gu0:gu0 + CODEC_GU_BASES], 1024, 2048)
+        dn = codec_unpack(block[CODEC_GU_PACKED:gu0], block[gu0 + CODEC_GU_BASES:], 2048, 512)
+        torch.cuda.synchronize()
+        # Tiles that fit restore exactly; the others decode to 0xffff.
+        misfit = 0
+        for got, want, bases, cols in ((gu, gate_up, block[gu0:gu0 + CODEC_GU_BASES], 2048),
+                                       (dn, down, block[gu0 + CODEC_GU_BASES:gu0 + CODEC_GU_BASES + 4096], 512)):
+            fits = (bases != CODEC_MISFIT).view(-1, cols // 256, 1).expand(-1, -1, 256).reshape(-1, cols)
+            g16, w16 = got.view(torch.int16), want.reshape(-1, cols).view(torch.int16)
+            assert torch.equal(g16[fits], w16[fits]), e
+            assert bool((g16[~fits] == -1).all()), e
+            misfit += int((~fits[:, ::256]).sum())
+        assert int(codec_bank.misfit[0, e]) == misfit, e
+
+
+def _layer_pair(model, codec_bank, norm: bool):
+    from lightreason_amd.moe import LayerWeights
+
+    base = model.layers[0]
+    raw = LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None, "codec": None})
+    packed = LayerWeights(**{**raw.__dict__, "codec": codec_bank.table(0)})
+    return raw, packed
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 16])
+@pytest.mark.parametrize("norm,logits", [(True, False), (False, True)])
+def test_codec_layer_equals_raw_layer(model, codec_bank, tokens, norm, logits):
+    from lightreason_amd.moe import Workspace, moe_layer
+
+    raw, packed = _layer_pair(model, codec_bank, norm)
+    x = model.hidden(tokens, step=700 + tokens)
+    lg = None
+    if logits:
+        lg = (x.float() @ raw.router.float().T).to(torch.bfloat16)
+    ws = Workspace(x.device, tokens)
+    results = []
+    for layer in (raw, packed, raw):
+        idx = torch.empty((tokens, 8), dtype=torch.int64, device=x.device)
+        out = moe_layer(x, layer, indices=idx, logits_in=lg, workspace=ws)
+        results.append((out, idx))
+    torch.cuda.synchronize()
+    print(f"codec layer T={tokens} norm={norm} logits={logits}", flush=True)
+    assert torch.equal(results[0][1], results[1][1])
+    assert torch.equal(results[0][0].view(torch.int16), results[1][0].view(torch.int16))
+    assert torch.equal(results[0][0].view(torch.int16), results[2][0].view(torch.int16))
+    assert ws.status() == 0
+
+
+def test_codec_mixed_raw_and_packed_experts(model, codec_bank):
+    """Experts whose codec row is zero are read raw inside the same call."""
+    from lightreason_amd.moe import LayerWeights, Workspace, moe_layer
+
+    raw, packed = _layer_pair(model, codec_bank, True)
+    table = codec_bank.table(0).clone()
+    table[1::3] = 0          # every third routed expert raw
+    table[256] = 0           # and the shared expert
+    mixed = LayerWeights(**{**packed.__dict__, "codec": table})
+    tokens = 8
+    x = model.hidden(tokens, step=750)
+    ws = Workspace(x.device, tokens)
+    want = moe_layer(x, raw, workspace=ws)
+    got = moe_layer(x, mixed, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_codec_chain_equals_raw_chain(model, codec_bank):
+    from lightreason_amd.moe import Workspace, moe_chain
+
+    raw, packed = _layer_pair(model, codec_bank, True)
+    tokens = 8
+    x = model.hidden(tokens, step=760)
+    ws = Workspace(x.device, tokens)
+    idx_raw = torch.empty((3, tokens, 8), dtype=torch.int64, device=x.device)
+    idx_pk = torch.empty_like(idx_raw)
+    want = moe_chain(x, [raw] * 3, indices=idx_raw, workspace=ws)
+    got = moe_chain(x, [packed] * 3, indices=idx_pk, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(idx_raw, idx_pk)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert ws.status() == 0

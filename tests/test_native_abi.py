@@ -55,7 +55,8 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     null = None
     assert lib.lrmoe_route_topk(null, 1, null, null, null, 1e-6, null, null, null, null, null, null, null, 0,
                                 null) == -1
-    assert lib.lrmoe_moe_layer(null, 1, null, null, null, null, null, null, null, null, 1e-6, null, null, null, null,
+    assert lib.lrmoe_moe_layer(null, 1, null, null, null, null, null, null, null, null, null, 1e-6, null, null, null,
+                               null,
                                0, null) == -1
     dummy = C.c_void_p(16)
     # both a router and logits: refused
@@ -100,3 +101,18 @@ def test_product_does_not_reach_the_oracle():
             text = path.read_text()
             assert "import oracle" not in text and "from oracle" not in text, path
             assert "liblro" not in text and "lro_" not in text, path
+
+
+def test_header_constants_match_the_bindings():
+    from lightreason_amd import _native
+
+    text = (ROOT / "include" / "lrmoe.h").read_text()
+    defines = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define LRMOE_(\w+) \(?(-?\d+)\)?", text)}
+    pairs = {"OK": _native.LRMOE_OK, "E_ARG": _native.LRMOE_E_ARG, "E_WORKSPACE": _native.LRMOE_E_WORKSPACE,
+             "E_DEVICE": _native.LRMOE_E_DEVICE, "WS_STATUS_OFFSET": _native.WS_STATUS_OFFSET,
+             "STATUS_BAD_EXPERT": _native.STATUS_BAD_EXPERT,
+             "STATUS_REPEATED_EXPERT": _native.STATUS_REPEATED_EXPERT,
+             "STATUS_CODEC_ROW": _native.STATUS_CODEC_ROW, "CHAIN_PTRS": _native.CHAIN_PTRS,
+             "CHAIN_MAX_LAYERS": _native.CHAIN_MAX_LAYERS, "CODEC_TABLE_COLUMNS": _native.CODEC_TABLE_COLUMNS}
+    for name, value in pairs.items():
+        assert defines.get(name) == value, name

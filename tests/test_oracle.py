@@ -366,3 +366,79 @@ def test_moe_layer_against_float32_torch(oracle):
     got = torch.from_numpy(oracle.bf16_to_f32(out))
     moe_got, moe_exp = got - xf, expected - xf
     assert (moe_got - moe_exp).abs().max() <= 3e-2 * moe_exp.abs().max()
+
+
+# ---- lossless BF16 tile codec ---------------------------------------------------
+
+def _fitting_tiles(rng, count):
+    """Tiles whose 7-bit exponent fields lie in an 8-value window."""
+    base = rng.integers(0, 121, size=(count, 1))
+    field = base + rng.integers(0, 8, size=(count, 256))
+    sign = rng.integers(0, 2, size=(count, 256))
+    low = rng.integers(0, 256, size=(count, 256))
+    return ((sign << 15) | (field << 8) | low).astype(np.uint16)
+
+
+def test_codec_round_trips_every_bf16_pattern(oracle):
+    # 256 consecutive patterns share bits 15..8, so each of these tiles fits.
+    values = np.arange(65536, dtype=np.uint16).reshape(256, 256)
+    packed, bases, misfit = oracle.codec_pack(values)
+    assert misfit == 0
+    np.testing.assert_array_equal(bases[:, 0], (np.arange(256) & 127).astype(np.uint8))
+    np.testing.assert_array_equal(oracle.codec_unpack(packed, bases), values)
+    # Shuffled, most tiles span more than 8 fields: exactly those are marked.
+    shuffled = np.random.default_rng(5).permutation(values.ravel()).reshape(64, 1024)
+    packed, bases, misfit = oracle.codec_pack(shuffled)
+    fields = ((shuffled.reshape(64, 4, 256) >> 8) & 127).astype(np.int32)
+    wide = fields.max(axis=2) - fields.min(axis=2) > 7
+    assert misfit == int(wide.sum()) > 0
+    np.testing.assert_array_equal(bases == 255, wide)
+    restored = oracle.codec_unpack(packed, bases).reshape(64, 4, 256)
+    np.testing.assert_array_equal(restored[~wide], shuffled.reshape(64, 4, 256)[~wide])
+
+
+def test_codec_matches_the_reference_packer(oracle):
+    ref = oracle.reference_tile_codec()
+    if ref is None:
+        pytest.skip("the reference's cpu_bf16_reads.h is not present")
+    rng = np.random.default_rng(11)
+    tiles = np.concatenate([_fitting_tiles(rng, 48), rng.integers(0, 65536, (16, 256), dtype=np.uint16),
+                            np.full((1, 256), 0x3F80, dtype=np.uint16),          # one field, no sign
+                            np.full((1, 256), 0x8000, dtype=np.uint16),          # negative zeros
+                            np.tile(np.array([0x7F80, 0x0001], dtype=np.uint16), (1, 128))])  # inf and a denormal: 127 fields apart
+    n = tiles.shape[0]
+    ref_packed = np.zeros((n, 384), dtype=np.uint8)
+    ref_bases = np.zeros(n, dtype=np.uint8)
+    encoded = ref.ref_pack_cpu_read_tiles(tiles.ctypes.data, ref_packed.ctypes.data, ref_bases.ctypes.data, n)
+    packed, bases, misfit = oracle.codec_pack(tiles)
+    assert encoded == n - misfit
+    np.testing.assert_array_equal(bases[:, 0], ref_bases)
+    # Value k of the reference tile: low byte at k, code in nibble k of bytes
+    # 256..383 (index order).  Here, for k = 8g + 32s + j: low byte at
+    # 64(s/2) + 16g + 8(s%2) + j, code in nibble j/4 of byte
+    # 256 + 64(s/4) + 16g + 4(s%4) + j%4.
+    k = np.arange(256)
+    g, s, j = (k >> 3) & 3, k >> 5, k & 7
+    low_at = 64 * (s >> 1) + 16 * g + 8 * (s & 1) + j
+    code_at = 256 + 64 * (s >> 2) + 16 * g + 4 * (s & 3) + (j & 3)
+    # Every byte of the tile is used once (low bytes) or twice (code nibbles).
+    assert sorted(low_at.tolist()) == list(range(256))
+    assert np.all(np.bincount(code_at - 256, minlength=128) == 2)
+    for t in np.flatnonzero(ref_bases != 255):
+        ref_low = ref_packed[t, :256]
+        ref_code = (ref_packed[t, 256 + k // 2] >> (4 * (k & 1))) & 15
+        ours = packed[t, 0]
+        np.testing.assert_array_equal(ours[low_at], ref_low)
+        np.testing.assert_array_equal((ours[code_at] >> (4 * (j >> 2))) & 15, ref_code)
+    assert (ref_bases == 255).sum() >= 17   # the random tiles and the inf/denormal tile
+
+
+def test_codec_closed_forms(oracle):
+    # 1.0 everywhere: field 63, no sign, low byte 0x80; code 0 in every nibble.
+    one = np.full((1, 256), 0x3F80, dtype=np.uint16)
+    packed, bases, misfit = oracle.codec_pack(one)
+    assert misfit == 0 and bases[0, 0] == 63
+    assert np.all(packed[0, 0, :256] == 0x80) and np.all(packed[0, 0, 256:] == 0)
+    # -2.0 (0xC000): field 64, sign set -> code 8 in every nibble.
+    packed, bases, _ = oracle.codec_pack(np.full((1, 256), 0xC000, dtype=np.uint16))
+    assert bases[0, 0] == 64 and np.all(packed[0, 0, 256:] == 0x88) and np.all(packed[0, 0, :256] == 0)
