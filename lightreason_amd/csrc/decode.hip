@@ -372,11 +372,16 @@ __device__ constexpr int raw_reg(int s) {
     return (s & 8) + j;
 }
 
-// a where mask is all ones, b where it is zero, as bit operations (a
-// conditional would let the compiler branch around the computation of a).
+// a where mask is all ones, b where it is zero: v_bfi_b32 per word (a
+// conditional would let the compiler branch around the computation of a;
+// the same bit operations in C become two instructions).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ uint4 pick(uint32_t mask, const uint4& a, const uint4& b) {
-    return make_uint4((a.x & mask) | (b.x & ~mask), (a.y & mask) | (b.y & ~mask), (a.z & mask) | (b.z & ~mask),
-                      (a.w & mask) | (b.w & ~mask));
+    return make_uint4(bfi(mask, a.x, b.x), bfi(mask, a.y, b.y), bfi(mask, a.z, b.z), bfi(mask, a.w, b.w));
 }
 
 // A bases pair of two tiles that do not fit the codec: the dummy source of
@@ -934,6 +939,25 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
 
     auto stale_word = [&](uint64_t w) { return tag_of(w) != tag; };
 
+    // The MFMAs of an item of a codec slot (B operand rows at bp, bb = the
+    // byte of the lane's first tile base in its bases block): per tile the
+    // decoded packed values or the raw row's.  (A second copy without the
+    // pick for waves that read every tile packed needs more registers than
+    // the kernel has.)
+    auto codec_mfmas = [&](const uint4* buf, const uint16_t* bp, uint32_t dec, int bb, f32x4& acc0,
+                           f32x4& acc1) __attribute__((always_inline)) {
+        const uint32_t base0 = byte_of(buf[6], bb) * 0x01010101u;
+        const uint32_t base1 = byte_of(buf[14], bb + 1) * 0x01010101u;
+#pragma unroll
+        for (int q = 0; q < kLoads; q += 2) {
+            const uint32_t base = q < kLoads / 2 ? base0 : base1;
+            const uint32_t pk = 0u - ((dec >> (q >> 3)) & 1u);
+            acc0 = mfma16x16x32(pick(pk, packed_operand(buf, q, base), buf[raw_reg(q)]),
+                                *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+            acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
+                                *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+        }
+    };
     // Runs item kk, whose weights are in buf (tile choice `dec`), prefetches
     // item kn into nbuf (tile choice from `bases`, its tile bases, which
     // become those of kn2) and loads the tile bases of kn2.  Returns the item
@@ -1015,19 +1039,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
             if (kCodec && s.pk_gu != nullptr) {
-                // Per tile: the decoded packed values or the raw row's.
-                const int bb = packed_lane(s, it, wave, lane).base_byte;
-                const uint32_t base0 = byte_of(buf[6], bb) * 0x01010101u;
-                const uint32_t base1 = byte_of(buf[14], bb + 1) * 0x01010101u;
-#pragma unroll
-                for (int q = 0; q < kLoads; q += 2) {
-                    const uint32_t base = q < kLoads / 2 ? base0 : base1;
-                    const uint32_t pk = 0u - ((dec >> (q >> 3)) & 1u);
-                    acc0 = mfma16x16x32(pick(pk, packed_operand(buf, q, base), buf[raw_reg(q)]),
-                                        *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
-                    acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
-                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
-                }
+                codec_mfmas(buf, bp, dec, packed_lane(s, it, wave, lane).base_byte, acc0, acc1);
             } else {
 #pragma unroll
                 for (int q = 0; q < kLoads; q += 2) {
@@ -1060,19 +1072,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
             if (kCodec && s.pk_gu != nullptr) {
-                // Per tile: the decoded packed values or the raw row's.
-                const int bb = packed_lane(s, it, wave, lane).base_byte;
-                const uint32_t base0 = byte_of(buf[6], bb) * 0x01010101u;
-                const uint32_t base1 = byte_of(buf[14], bb + 1) * 0x01010101u;
-#pragma unroll
-                for (int q = 0; q < kLoads; q += 2) {
-                    const uint32_t base = q < kLoads / 2 ? base0 : base1;
-                    const uint32_t pk = 0u - ((dec >> (q >> 3)) & 1u);
-                    acc0 = mfma16x16x32(pick(pk, packed_operand(buf, q, base), buf[raw_reg(q)]),
-                                        *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
-                    acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
-                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
-                }
+                codec_mfmas(buf, bp, dec, packed_lane(s, it, wave, lane).base_byte, acc0, acc1);
             } else {
 #pragma unroll
                 for (int q = 0; q < kLoads; q += 2) {
