@@ -184,19 +184,25 @@ struct SlotInfo {
     const uint16_t* gate;  // gate rows [512][2048]
     const uint16_t* up;    // up rows [512][2048]
     const uint16_t* down;  // [2048][512]
+    uint32_t tok[4];       // token of column n in byte n
+    int32_t count;         // tokens (columns), <= 16
+    int32_t pair0;         // first act/y row
+    int32_t pad[2];
+};
+
+// The tile-codec rows of a slot's expert (codec calls only).
+struct SlotCodec {
     const uint8_t* pk_gu;  // tile-codec gate_up [1024 rows][8 tiles][384 B], or null (raw expert)
     const uint8_t* pk_dn;  // tile-codec down [2048][2][384]
     const uint8_t* b_gu;   // tile bases of gate_up [1024][8]
     const uint8_t* b_dn;   // tile bases of down [2048][2]
-    uint32_t tok[4];       // token of column n in byte n
-    int32_t count;         // tokens (columns), <= 16
-    int32_t pair0;         // first act/y row
-    int32_t crow;          // row of Plan::ecodec holding the expert's raw flags (codec slots)
+    int32_t crow;          // row of Plan::ecodec holding the expert's raw flags
     int32_t pad;
 };
 
 struct Plan {
     SlotInfo slot[kDecodeSlots];
+    SlotCodec scodec[kDecodeSlots];   // codec calls
     int16_t comb_pair[kMaxT][kTopK];  // per token: pair of the k-th smallest expert
     float comb_w[kMaxT][kTopK];       // its routing weight
     float sg[kMaxT];                  // shared-expert gate per token
@@ -250,22 +256,25 @@ __device__ __forceinline__ float lane_dot32(const uint4* w, const uint16_t* row,
     return acc;
 }
 
-// Weight addresses of a slot: the raw rows, and the tile-codec rows when the
-// expert has them (codec = {packed gate_up, packed down, gate_up bases, down
-// bases} as two uint4, or null; crow = its row of Plan::ecodec).
-__device__ __forceinline__ void set_slot_weights(SlotInfo& s, const uint16_t* gate, const uint16_t* up,
-                                                 const uint16_t* down, const uint4* codec, int crow) {
+// Weight addresses of a slot: the raw rows, and (sc not null) the tile-codec
+// rows when the expert has them (codec = {packed gate_up, packed down,
+// gate_up bases, down bases} as two uint4, or null; crow = its row of
+// Plan::ecodec).
+__device__ __forceinline__ void set_slot_weights(SlotInfo& s, SlotCodec* sc, const uint16_t* gate,
+                                                 const uint16_t* up, const uint16_t* down, const uint4* codec,
+                                                 int crow) {
     auto ptr = [](uint32_t lo, uint32_t hi) {
         return reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(lo) | (static_cast<uintptr_t>(hi) << 32));
     };
     s.gate = gate;
     s.up = up;
     s.down = down;
-    s.pk_gu = codec != nullptr ? ptr(codec[0].x, codec[0].y) : nullptr;
-    s.pk_dn = codec != nullptr ? ptr(codec[0].z, codec[0].w) : nullptr;
-    s.b_gu = codec != nullptr ? ptr(codec[1].x, codec[1].y) : nullptr;
-    s.b_dn = codec != nullptr ? ptr(codec[1].z, codec[1].w) : nullptr;
-    s.crow = crow;
+    if (sc == nullptr) return;
+    sc->pk_gu = codec != nullptr ? ptr(codec[0].x, codec[0].y) : nullptr;
+    sc->pk_dn = codec != nullptr ? ptr(codec[0].z, codec[0].w) : nullptr;
+    sc->b_gu = codec != nullptr ? ptr(codec[1].x, codec[1].y) : nullptr;
+    sc->b_dn = codec != nullptr ? ptr(codec[1].z, codec[1].w) : nullptr;
+    sc->crow = crow;
 }
 
 // ---- item geometry ------------------------------------------------------------
@@ -329,7 +338,7 @@ struct PackedLane {
     int base_byte;           // byte of the first base in that block
 };
 
-__device__ __forceinline__ PackedLane packed_lane(const SlotInfo& s, const Item& it, int wave, int lane) {
+__device__ __forceinline__ PackedLane packed_lane(const SlotCodec& s, const Item& it, int wave, int lane) {
     const int m = lane & 15;
     PackedLane p;
     uintptr_t b;
@@ -717,7 +726,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // loaded one step before the item's own loads (tile_choice).
     auto unit_choice = [&](const Item& it) __attribute__((always_inline)) -> uint32_t {
         if (it.kind > 1) return 0u;
-        const SlotInfo& s = P.slot[it.slot];
+        const SlotCodec& s = P.scodec[it.slot];
         if (s.pk_gu == nullptr) return 0u;
         const uint8_t* flags = reinterpret_cast<const uint8_t*>(&P.ecodec[s.crow][2]);
         return ((flags[(it.kind == 1 ? 32 : 0) + it.tile] >> wave) & 1u) == 0u ? 3u : 0u;
@@ -730,7 +739,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     auto load_bases = [&](const Item& it) __attribute__((always_inline)) -> uint32_t {
         const void* at = &kBothMisfit;
         if (it.kind == 0 || it.kind == 1) {
-            const SlotInfo& s = P.slot[it.slot];
+            const SlotCodec& s = P.scodec[it.slot];
             if (s.pk_gu != nullptr) at = packed_lane(s, it, wave, lane).bases2;
         }
         return ldg_u16(at);
@@ -756,8 +765,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         const uint8_t* pk = raw;
         const uint8_t* bases = raw;
         if (it.kind == 0 || it.kind == 1) {
-            const SlotInfo& s = P.slot[it.slot];
-            raw = reinterpret_cast<const uint8_t*>(item_base(s, it, wave, lane));
+            raw = reinterpret_cast<const uint8_t*>(item_base(P.slot[it.slot], it, wave, lane));
+            const SlotCodec& s = P.scodec[it.slot];
             if (s.pk_gu != nullptr) {
                 const PackedLane p = packed_lane(s, it, wave, lane);
                 pk = p.tile0 + 16 * (lane >> 4);
@@ -785,33 +794,49 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                          (c[1].z | c[1].w) != 0u;
         return all ? c : nullptr;
     };
-    // Slots 0..8 -- the shared expert and token 0's experts in rank order,
-    // the first slots in discovery order -- get their weight addresses now.
-    if (tid <= kTopK) {
+    // Codec calls: slots 0..8 -- the shared expert and token 0's experts in
+    // rank order, the first slots in discovery order -- get their weight
+    // addresses now, for the first item's tile choice.  (Raw calls address
+    // the first item straight from the expert table, one barrier sooner.)
+    if (kCodec && tid <= kTopK) {
         if (tid == 0) {
-            set_slot_weights(P.slot[0], a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
+            set_slot_weights(P.slot[0], &P.scodec[0], a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
         } else {
             const int e = P.ids[0][tid - 1];
             const uint4 ptrs = P.eptr[e];
             const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
                                                                         (static_cast<uintptr_t>(ptrs.y) << 32));
-            set_slot_weights(P.slot[tid], gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
+            set_slot_weights(P.slot[tid], &P.scodec[tid], gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
                              reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) |
                                                                (static_cast<uintptr_t>(ptrs.w) << 32)),
                              codec_of(e), e);
         }
     }
-    __syncthreads();
+    if constexpr (kCodec) __syncthreads();
     const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
     int cur = (block - offset + G) % G;
-    uint32_t dec;  // tile choice of the item being run
-    {
+    uint32_t dec = 0u;  // tile choice of the item being run
+    if constexpr (kCodec) {
         Item first;
         first.kind = 0;
         first.slot = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
         first.tile = cur % kATiles;
-        dec = kCodec ? unit_choice(first) : 0u;
+        dec = unit_choice(first);
         issue_item(first, b0, dec);
+    } else {
+        // item_base's A geometry for tile cur % 32 of slot s0.
+        const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
+        const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
+        const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
+                                                                    (static_cast<uintptr_t>(ptrs.y) << 32));
+        const uint16_t* gate = s0 == 0 ? a.sh_gate : gate_up;
+        const uint16_t* up = s0 == 0 ? a.sh_up : gate_up + static_cast<size_t>(kInner) * kHidden;
+        const int m = lane & 15;
+        const int row = 16 * (cur % kATiles) + 8 * (wave >> 2) + (m & 7);
+        const uint16_t* p =
+            (m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * i);
     }
 
     if (block == 0 && tid < T * kTopK) {
@@ -842,10 +867,11 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         if (opens) {
             P.poff[e] = pair0;
             SlotInfo& s = P.slot[1 + rank];
+            SlotCodec* sc = kCodec ? &P.scodec[1 + rank] : nullptr;
             const uint4 ptrs = P.eptr[e];
             const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
                                                                         (static_cast<uintptr_t>(ptrs.y) << 32));
-            set_slot_weights(s, gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
+            set_slot_weights(s, sc, gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
                              reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) |
                                                                (static_cast<uintptr_t>(ptrs.w) << 32)),
                              codec_of(e), e);
@@ -869,7 +895,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         if (tid == 0) {
             const bool shared = a.sh_down != nullptr && routes_ok;
             SlotInfo& s = P.slot[0];
-            set_slot_weights(s, a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
+            set_slot_weights(s, kCodec ? &P.scodec[0] : nullptr, a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts),
+                             kExperts);
             uint32_t tok[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int j = 0; j < kMaxT; ++j) {
@@ -1038,8 +1065,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const int tok = column_token(s, m < s.count ? m : 0);
             const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (kCodec && s.pk_gu != nullptr) {
-                codec_mfmas(buf, bp, dec, packed_lane(s, it, wave, lane).base_byte, acc0, acc1);
+            if (kCodec && P.scodec[it.slot].pk_gu != nullptr) {
+                codec_mfmas(buf, bp, dec, packed_lane(P.scodec[it.slot], it, wave, lane).base_byte, acc0, acc1);
             } else {
 #pragma unroll
                 for (int q = 0; q < kLoads; q += 2) {
@@ -1071,8 +1098,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         } else if (it.kind == 1) {
             const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (kCodec && s.pk_gu != nullptr) {
-                codec_mfmas(buf, bp, dec, packed_lane(s, it, wave, lane).base_byte, acc0, acc1);
+            if (kCodec && P.scodec[it.slot].pk_gu != nullptr) {
+                codec_mfmas(buf, bp, dec, packed_lane(P.scodec[it.slot], it, wave, lane).base_byte, acc0, acc1);
             } else {
 #pragma unroll
                 for (int q = 0; q < kLoads; q += 2) {
