@@ -122,10 +122,12 @@ int lrmoe_moe_experts(const uint16_t *hidden, int tokens, const int64_t *indices
  * i < 32 for gate_up item i, byte 32 + i for down item i, bit w set when a
  * tile that wave w of the item reads has base 255 (gate_up item i, wave w:
  * tiles 2(w%4), 2(w%4)+1 of gate_proj and up_proj rows 16i + 8(w/4) .. +7;
- * down item i, wave w: both tiles of rows 128i + 16w .. +15).  For tokens
- * <= 16 an expert whose four addresses are non-zero is read from its codec
- * form, except the flagged (item, wave) units, which read the raw rows;
- * results are identical to the raw rows'.  The raw pointers stay required.
+ * down item i, wave w: both tiles of rows 128i + 16w .. +15).  For 8 <=
+ * tokens <= 16 an expert whose four addresses are non-zero is read from its
+ * codec form, tile by tile, with the raw row's tile where a tile's base is
+ * 255; fewer tokens read the raw rows (too few items per workgroup for the
+ * codec to pay).  Results are identical to the raw rows' either way.  The
+ * raw pointers stay required.
  * Replaces Transformers
  * Qwen3_5MoeSparseMoeBlock.forward + the residual add of
  * Qwen3_5MoeDecoderLayer.forward, as driven by edge35b/expert_stream.py:457-526

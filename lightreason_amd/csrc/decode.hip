@@ -15,7 +15,8 @@
 //   4. walks its share of one list of 128 KiB work items, each item's
 //      weights prefetched one item ahead (the first two items of a workgroup
 //      are fixed by its index, later ones are claimed from a counter two
-//      items ahead, so faster workgroups take more of them):
+//      items ahead -- three with codec experts, the first three fixed -- so
+//      faster workgroups take more of them):
 //        A (slot, 16-row tile): gate and up rows 16i..16i+15 of an expert over
 //          k = 2048 -> SwiGLU with the cpu_experts.c:59-62 rounding points ->
 //          act rows;
@@ -720,10 +721,11 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // row 0, in cache after the first read.
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
     // Which of the lane's two tiles of an item it reads packed: bit t of
-    // `dec`.  A workgroup's first two items take it from the codec table's
-    // per-(item, wave) flags (both tiles packed when every tile of the
-    // wave's share fits; wave-uniform), later items from their tile bases,
-    // loaded one step before the item's own loads (tile_choice).
+    // `dec`.  A workgroup's first item is read raw; its second takes the
+    // choice from the codec table's per-(item, wave) flags (both tiles packed
+    // when every tile of the wave's share fits; wave-uniform), later items
+    // from their tile bases, loaded one step before the item's own loads
+    // (tile_choice).
     auto unit_choice = [&](const Item& it) __attribute__((always_inline)) -> uint32_t {
         if (it.kind > 1) return 0u;
         const SlotCodec& s = P.scodec[it.slot];
@@ -794,36 +796,12 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                          (c[1].z | c[1].w) != 0u;
         return all ? c : nullptr;
     };
-    // Codec calls: slots 0..8 -- the shared expert and token 0's experts in
-    // rank order, the first slots in discovery order -- get their weight
-    // addresses now, for the first item's tile choice.  (Raw calls address
-    // the first item straight from the expert table, one barrier sooner.)
-    if (kCodec && tid <= kTopK) {
-        if (tid == 0) {
-            set_slot_weights(P.slot[0], &P.scodec[0], a.sh_gate, a.sh_up, a.sh_down, codec_of(kExperts), kExperts);
-        } else {
-            const int e = P.ids[0][tid - 1];
-            const uint4 ptrs = P.eptr[e];
-            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
-                                                                        (static_cast<uintptr_t>(ptrs.y) << 32));
-            set_slot_weights(P.slot[tid], &P.scodec[tid], gate_up, gate_up + static_cast<size_t>(kInner) * kHidden,
-                             reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.z) |
-                                                               (static_cast<uintptr_t>(ptrs.w) << 32)),
-                             codec_of(e), e);
-        }
-    }
-    if constexpr (kCodec) __syncthreads();
     const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
     int cur = (block - offset + G) % G;
+    // The first item (read raw, tile choice 0) is addressed straight from
+    // the expert table.
     uint32_t dec = 0u;  // tile choice of the item being run
-    if constexpr (kCodec) {
-        Item first;
-        first.kind = 0;
-        first.slot = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
-        first.tile = cur % kATiles;
-        dec = unit_choice(first);
-        issue_item(first, b0, dec);
-    } else {
+    {
         // item_base's A geometry for tile cur % 32 of slot s0.
         const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
         const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
@@ -836,7 +814,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         const uint16_t* p =
             (m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4);
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * i);
+        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * (kCodec ? (i & 8) + kRawStep[i & 7] : i));
     }
 
     if (block == 0 && tid < T * kTopK) {
@@ -1324,6 +1302,11 @@ size_t decode_lds_bytes(int tokens) {
 
 namespace {
 
+// Below this many tokens a workgroup runs one or two items per layer, which
+// the codec's tile choice (one step ahead) does not reach; its pipeline then
+// only costs (T=1 chain: 35 instead of 30 us per layer).
+constexpr int kCodecMinTokens = 8;
+
 // Per device and kernel: the CU count, and whether the LDS limit was raised
 // and the occupancy checked.
 struct LaunchSetup {
@@ -1367,9 +1350,11 @@ hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
     if (a.tokens <= 0) return hipSuccess;
     if (a.tokens > kMaxT) return hipErrorInvalidValue;
     // The codec kernel carries the tile-choice pipeline; calls without codec
-    // tables run the kernel without it.
+    // tables, and calls of fewer than kCodecMinTokens tokens, run the kernel
+    // without it (the codec is lossless and the raw rows are always given,
+    // so either gives the same results).
     static LaunchSetup setup[2][64];
-    const bool codec = a.codec != nullptr;
+    const bool codec = a.codec != nullptr && a.tokens >= kCodecMinTokens;
     int grid = 0;
     const hipError_t err = codec ? persistent_grid(moe_decode<true>, setup[1], &grid)
                                  : persistent_grid(moe_decode<false>, setup[0], &grid);
@@ -1391,6 +1376,7 @@ hipError_t launch_moe_chain(const ChainArgs& a, hipStream_t stream) {
     static LaunchSetup setup[2][64];
     bool codec = false;
     for (int l = 0; l < a.layers; ++l) codec |= a.layer[l].codec != nullptr;
+    codec = codec && a.base.tokens >= kCodecMinTokens;  // as in launch_moe_decode
     int grid = 0;
     const hipError_t err = codec ? persistent_grid(moe_chain<true>, setup[1], &grid)
                                  : persistent_grid(moe_chain<false>, setup[0], &grid);
