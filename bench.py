@@ -442,15 +442,16 @@ def main() -> int:
         bank = CodecBank(model.bank, [(ly.shared_gate_proj, ly.shared_up_proj, ly.shared_down_proj)
                                       for ly in model.layers])
         torch.cuda.synchronize()
-        packed_frac = bank.packed_fraction
         misfit_tiles = float(bank.misfit.sum()) / (bank.misfit.numel() * (CODEC_GU_BASES + CODEC_DN_BASES))
-        # Bytes a unit reads: 3/4 of its raw bytes when packed (plus 16 bytes
-        # of bases per lane, 1/64 of the packed bytes), all of them when raw.
-        read_frac = packed_frac * 0.75 * (1 + 1 / 64) + (1 - packed_frac)
+        # Weight bytes read per raw byte: a fitting tile is 384 bytes and its
+        # base byte instead of 512; a tile that does not fit is read raw.  (A
+        # workgroup's first item is read raw, its second with the
+        # per-(item, wave) flags: units_packed of them pack.)
+        read_frac = (1 - misfit_tiles) * 385 / 512 + misfit_tiles
         log(f"[bench] C5 codec bank in {time.perf_counter() - t0:.1f}s: {bank.nbytes / 2**30:.1f} GiB, "
-            f"units packed {packed_frac:.3f}, tiles misfit {misfit_tiles:.4f}")
-        res = dict(units_packed=round(packed_frac, 4), tiles_misfit=round(misfit_tiles, 5),
-                   weight_bytes_read_frac=round(read_frac, 4))
+            f"tiles misfit {misfit_tiles:.4f}, weight bytes read x{read_frac:.3f}")
+        res = dict(tiles_misfit=round(misfit_tiles, 5), weight_bytes_read_frac=round(read_frac, 4),
+                   units_packed=round(bank.packed_fraction, 4), bank_gib=round(bank.nbytes / 2**30, 1))
         c5 = Case(model, 8, logits=logits, codec=bank)
         assert c5.unique_counts() == uniques
         ms5 = bench_case(c5, replays, warm) / L
