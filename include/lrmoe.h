@@ -205,6 +205,23 @@ int lrmoe_gather(const int64_t *descriptors, const int64_t *destinations, const 
                  int banks, int max_copies, int stripes, int threads, int keep_in_l2, int32_t *status,
                  void *stream);
 
+/* Tile-codec row gather, the launch protocol of lrmoe_gather: descriptors
+ * [banks][experts][3] = (packed, bases, raw).  bases == 0: copy sizes[b]
+ * bytes from raw.  Otherwise, per 512-byte tile t of the row, in the
+ * reference's tile format and byte order (cpu_bf16_reads.h:16-52: value k's
+ * low byte at byte k, its 4-bit code in nibble k of bytes 256..383): base
+ * bases[t], 384 packed bytes at packed + 384t, decoded; base 255: the tile is
+ * copied from raw + 512t.  With compact != 0, a descriptor whose raw is -1 is
+ * a compact row: bases holds uint32 headers (raw tiles before t) << 8 | base
+ * and tile t's bytes (512 for a raw tile) start at packed + 384t + 128 * (raw
+ * tiles before t).  sizes[b] a multiple of 512.  Replaces
+ * edge35b/bf16_gather_ada.cu:127-201 (gather_bf16_cpu_tiles, and
+ * gather_bf16_resident with compact), launched by native_bf16_gather.py:71-77
+ * with the "cpu-tiles" / "resident" policies. */
+int lrmoe_gather_tiles(const int64_t *descriptors, const int64_t *destinations, const int64_t *sizes,
+                       const int32_t *src_ids, const int32_t *dst_ids, const int64_t *count, int experts, int banks,
+                       int max_copies, int stripes, int threads, int compact, void *stream);
+
 /* Batched matvec with the _matvec protocol: for e < experts and r < N,
  * result[e*N + r] = bf16(sum_k W_e[r,k] x_e[k]), W_e = table[stride*e + column]
  * (rows skipped when that address is 0 and stride != 3), x_e = x when

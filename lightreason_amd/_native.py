@@ -36,6 +36,7 @@ _SIGNATURES = {
     "lrmoe_bucket": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_experts": ([_P, _I, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
+    "lrmoe_gather_tiles": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "lrmoe_moe_chain": ([_P, _I, _I, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_codec_pack": ([_P, C.c_int64, _I, _P, _P, _P, _P], _I),
     "lrmoe_codec_unpack": ([_P, _P, C.c_int64, _I, _P, _P], _I),

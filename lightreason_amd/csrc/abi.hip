@@ -284,6 +284,19 @@ int lrmoe_gather(const int64_t* descriptors, const int64_t* destinations, const 
                                           max_copies, stripes, threads, keep_in_l2, status, as_stream(stream)));
 }
 
+int lrmoe_gather_tiles(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                       const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts, int banks,
+                       int max_copies, int stripes, int threads, int compact, void* stream) {
+    if (!descriptors || !destinations || !sizes || !src_ids || !dst_ids || !count) return LRMOE_E_ARG;
+    if (experts <= 0 || banks <= 0 || banks > 65535 || max_copies < 0 || max_copies > 65535 || stripes <= 0 ||
+        stripes > 65535 || threads < 64 || threads > 256 || threads % 64 != 0)
+        return LRMOE_E_ARG;
+    if (max_copies == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_gather_tiles(descriptors, destinations, sizes, src_ids, dst_ids, count, experts,
+                                                banks, max_copies, stripes, threads, compact, as_stream(stream)));
+}
+
 int lrmoe_matvec(const int64_t* table, const uint16_t* x, uint16_t* result, int K, int N, int column, int shared_x,
                  int stride, int experts, void* stream) {
     if (!table || !x || !result || K <= 0 || K % 512 != 0 || N <= 0 || experts <= 0 || experts > 65535 ||

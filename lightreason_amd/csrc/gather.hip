@@ -63,6 +63,77 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors,
     for (; i < end; i += blockDim.x) dst[i] = src[i];
 }
 
+// Eight values of a codec tile in the reference's byte order
+// (cpu_bf16_reads.h:16-52): the low bytes of values 0..3 in low0 and of 4..7
+// in low1, the codes of values 2i and 2i+1 in the low and high nibble of byte
+// i of `codes`, base4 = base * 0x01010101.  The high bytes of the even and
+// of the odd values come four at a time (no byte carries: a field is at most
+// 127), v_perm_b32 puts them in value order and then beside the low bytes.
+__device__ __forceinline__ u32x4 ref_tile_decode8(uint32_t low0, uint32_t low1, uint32_t codes, uint32_t base4) {
+    const uint32_t even = ((codes & 0x07070707u) + base4) | ((codes << 4) & 0x80808080u);
+    const uint32_t odd = (((codes >> 4) & 0x07070707u) + base4) | (codes & 0x80808080u);
+    const uint32_t h03 = __builtin_amdgcn_perm(odd, even, 0x05010400u);
+    const uint32_t h47 = __builtin_amdgcn_perm(odd, even, 0x07030602u);
+    u32x4 v;
+    v.x = __builtin_amdgcn_perm(h03, low0, 0x05010400u);
+    v.y = __builtin_amdgcn_perm(h03, low0, 0x07030602u);
+    v.z = __builtin_amdgcn_perm(h47, low1, 0x05010400u);
+    v.w = __builtin_amdgcn_perm(h47, low1, 0x07030602u);
+    return v;
+}
+
+// Rows in the tile codec (edge35b/bf16_gather_ada.cu:127-180,
+// gather_cpu_tiles), with the launch protocol of gather_kernel.  Descriptor
+// (packed, bases, raw): bases 0 copies the raw row; otherwise tile t of the
+// row (512 bytes) has base bases[t] (one byte) and 384 packed bytes at
+// packed + 384t, or is copied from raw + 512t when its base is 255.  With
+// kCompact and raw == -1 (the reference's "resident" rows): bases holds a
+// 32-bit header per tile, (tiles read raw before it) << 8 | base, the tile's
+// bytes start at packed + 384t + 128 * (tiles read raw before it), and a raw
+// tile's 512 bytes are stored there.  Half a wave per tile, 16 bytes per
+// lane; every tile of the row is covered (stripes of ceil(tiles / stripes)).
+template <bool kCompact>
+__global__ __launch_bounds__(256) void gather_tiles_kernel(const int64_t* descriptors, const int64_t* destinations,
+                                                           const int64_t* sizes, const int32_t* src_ids,
+                                                           const int32_t* dst_ids, const int64_t* count,
+                                                           int experts) {
+    const int stripe = blockIdx.x;
+    const int bank = blockIdx.y;
+    const int row = blockIdx.z;
+    if (row >= *count) return;
+    const int64_t* desc = descriptors + (static_cast<int64_t>(bank) * experts + src_ids[row]) * 3;
+    const uint8_t* packed = reinterpret_cast<const uint8_t*>(desc[0]);
+    const uint8_t* bases = reinterpret_cast<const uint8_t*>(desc[1]);
+    const int64_t raw_at = desc[2];
+    const int64_t row_bytes = sizes[bank];
+    u32x4* dst = reinterpret_cast<u32x4*>(destinations[bank] + static_cast<int64_t>(dst_ids[row]) * row_bytes);
+    const int64_t tiles = row_bytes / 512;
+    const int64_t per = (tiles + gridDim.x - 1) / gridDim.x;
+    const int64_t begin = stripe * per;
+    const int64_t end = begin + per < tiles ? begin + per : tiles;
+    if (bases == nullptr) {
+        const u32x4* raw = reinterpret_cast<const u32x4*>(raw_at);
+        for (int64_t i = begin * 32 + threadIdx.x; i < end * 32; i += blockDim.x) dst[i] = raw[i];
+        return;
+    }
+    const bool compact = kCompact && raw_at == -1;
+    const u32x4* raw = reinterpret_cast<const u32x4*>(raw_at);
+    const int lane = threadIdx.x & 31;
+    for (int64_t tile = begin + (threadIdx.x >> 5); tile < end; tile += blockDim.x >> 5) {
+        const uint32_t header = compact ? reinterpret_cast<const uint32_t*>(bases)[tile] : bases[tile];
+        const uint32_t base = compact ? header & 255u : header;
+        const uint8_t* data = packed + tile * 384 + (compact ? static_cast<int64_t>(header >> 8) * 128 : 0);
+        const int64_t i = tile * 32 + lane;
+        if (base == 255u) {
+            dst[i] = compact ? reinterpret_cast<const u32x4*>(data)[lane] : raw[i];
+            continue;
+        }
+        const uint2 low = *reinterpret_cast<const uint2*>(data + 8 * lane);
+        const uint32_t codes = *reinterpret_cast<const uint32_t*>(data + 256 + 4 * lane);
+        dst[i] = ref_tile_decode8(low.x, low.y, codes, base * 0x01010101u);
+    }
+}
+
 // Counter-based synthetic bf16 ~N(0, sigma): h = splitmix64(key + index),
 // key = splitmix64(seed * 0x9E3779B97F4A7C15 + stream); Irwin-Hall sum of the
 // four 16-bit fields of h, centred and scaled to unit variance in double,
@@ -109,6 +180,22 @@ hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations
     } else {
         LRMOE_LAUNCH(gather_kernel<true>, grid, dim3(threads), 0, stream, ev.start, ev.stop, descriptors,
                      destinations, sizes, src_ids, dst_ids, count, experts, status);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_tiles(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                               const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts,
+                               int banks, int max_copies, int stripes, int threads, int compact, hipStream_t stream) {
+    if (max_copies <= 0 || banks <= 0) return hipSuccess;
+    const StageEvents ev = timing_events(kStageGather);
+    const dim3 grid(stripes, banks, max_copies);
+    if (compact) {
+        LRMOE_LAUNCH(gather_tiles_kernel<true>, grid, dim3(threads), 0, stream, ev.start, ev.stop, descriptors,
+                     destinations, sizes, src_ids, dst_ids, count, experts);
+    } else {
+        LRMOE_LAUNCH(gather_tiles_kernel<false>, grid, dim3(threads), 0, stream, ev.start, ev.stop, descriptors,
+                     destinations, sizes, src_ids, dst_ids, count, experts);
     }
     return hipGetLastError();
 }

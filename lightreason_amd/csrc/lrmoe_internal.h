@@ -296,6 +296,9 @@ StageEvents timing_events(int stage);
         }                                                                                                     \
     } while (0)
 
+hipError_t launch_gather_tiles(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,
+                               const int32_t* src_ids, const int32_t* dst_ids, const int64_t* count, int experts,
+                               int banks, int max_copies, int stripes, int threads, int compact, hipStream_t stream);
 hipError_t launch_route(const RouteArgs& args, hipStream_t stream);
 hipError_t launch_bucket(const int64_t* indices, int tokens, const Workspace& ws, const Plan& plan, hipStream_t stream);
 hipError_t launch_gather(const int64_t* descriptors, const int64_t* destinations, const int64_t* sizes,

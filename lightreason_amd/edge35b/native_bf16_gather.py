@@ -10,11 +10,14 @@ device, grid (stripes, banks, max_copies), torch's current stream, no host
 synchronisation (graph-capturable; a replay picks up new counts and
 descriptors).
 
-Raw BF16 rows (base < 0) are copied bit for bit.  The lossless codec rows
-(base >= 0) and the codec tile layouts behind ``cpu-tiles``,
-``stage_primary`` and ``copy_compact_tail`` are not implemented: a codec
-descriptor is skipped and flagged in ``status`` (STATUS_CODEC_ROW), and the
-codec entry points raise NotImplementedError.
+Policies "default" and "l2" copy raw BF16 rows (base < 0) bit for bit
+(lrmoe_gather); their escape-codec rows (base >= 0) are not implemented: such
+a descriptor is skipped and flagged in ``status`` (STATUS_CODEC_ROW).
+Policies "cpu-tiles" and "resident" decode the tile codec (descriptors
+(packed, bases, raw), "resident" also compact rows with raw = -1;
+lrmoe_gather_tiles), like bf16_gather_ada.cu:127-201.  ``stage_primary`` and
+``copy_compact_tail`` (the reference's host-cache staging) raise
+NotImplementedError.
 """
 
 from __future__ import annotations
@@ -60,9 +63,8 @@ class NativeBf16Gather:
 
     def copy(self, descriptors, destinations, sizes, src, dst, count, *, max_copies, experts, geometry):
         stripes, threads, policy = geometry
-        if policy not in ("default", "l2"):
-            raise NotImplementedError(f"gather policy {policy!r} decodes a codec tile layout (not built); "
-                                      "raw rows use 'default' or 'l2'")
+        if policy not in ("default", "l2", "cpu-tiles", "resident"):
+            raise ValueError(f"Unknown gather policy {policy!r}.")
         banks = destinations.numel()
         if descriptors.numel() < banks * int(experts) * 3 or sizes.numel() < banks:
             raise ValueError("descriptors must be [banks, experts, 3] and sizes [banks]")
@@ -71,6 +73,13 @@ class NativeBf16Gather:
         if self.status.device != destinations.device:
             self.status = torch.zeros(1, dtype=torch.int32, device=destinations.device)
         try:
+            if policy in ("cpu-tiles", "resident"):
+                _native.call("lrmoe_gather_tiles", pointer(descriptors, torch.int64, "descriptors"),
+                             pointer(destinations, torch.int64, "destinations"), pointer(sizes, torch.int64, "sizes"),
+                             pointer(src, torch.int32, "src"), pointer(dst, torch.int32, "dst"),
+                             pointer(count, torch.int64, "count"), int(experts), banks, int(max_copies),
+                             int(stripes), int(threads), int(policy == "resident"), stream_of(destinations))
+                return
             _native.call("lrmoe_gather", pointer(descriptors, torch.int64, "descriptors"),
                          pointer(destinations, torch.int64, "destinations"), pointer(sizes, torch.int64, "sizes"),
                          pointer(src, torch.int32, "src"), pointer(dst, torch.int32, "dst"),
@@ -84,10 +93,12 @@ class NativeBf16Gather:
         return bool(int(self.status.item()) & _native.STATUS_CODEC_ROW)
 
     def stage_primary(self, *args, **kwargs):
-        raise NotImplementedError("stage_primary decodes codec-packed rows; the codec is not built")
+        raise NotImplementedError("stage_primary fills the reference's host-side expert caches; experts are "
+                                  "resident in HBM here (tile-codec rows: copy() with 'cpu-tiles'/'resident')")
 
     def copy_compact_tail(self, *args, **kwargs):
-        raise NotImplementedError("copy_compact_tail decodes compact codec tails; the codec is not built")
+        raise NotImplementedError("copy_compact_tail fills the reference's host-side expert caches; experts are "
+                                  "resident in HBM here (tile-codec rows: copy() with 'cpu-tiles'/'resident')")
 
 
 def expert_descriptors(expert_ptrs: torch.Tensor) -> torch.Tensor:

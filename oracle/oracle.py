@@ -285,6 +285,71 @@ def codec_unpack(packed: np.ndarray, bases: np.ndarray) -> np.ndarray:
     return out
 
 
+def _reference_order():
+    """Byte positions in codec_pack's tile of the reference's bytes: value k's
+    low byte (reference byte k) and the byte and nibble holding its code
+    (reference nibble k of bytes 256..383)."""
+    k = np.arange(CODEC_TILE)
+    g, s, j = (k >> 3) & 3, k >> 5, k & 7
+    low_at = 64 * (s >> 1) + 16 * g + 8 * (s & 1) + j
+    code_at = 256 + 64 * (s >> 2) + 16 * g + 4 * (s & 3) + (j & 3)
+    return k, low_at, code_at, 4 * (j >> 2)
+
+
+def codec_pack_reference_order(w: np.ndarray):
+    """Tile-codec packing in the reference's byte order
+    (edge35b/cpu_bf16_reads.h:16-52, pack_cpu_read_tiles): per tile value k's
+    low byte at byte k and its code in nibble k (low nibble first) of bytes
+    256..383; tiles that do not fit (base 255) are all zero.  The bytes of
+    codec_pack, rearranged.  Returns (packed [rows, tiles, 384], bases [rows,
+    tiles], number of tiles that do not fit)."""
+    ours, bases, misfit = codec_pack(w)
+    k, low_at, code_at, shift = _reference_order()
+    out = np.zeros_like(ours)
+    out[..., :CODEC_TILE] = ours[..., low_at]
+    codes = (ours[..., code_at] >> shift) & 15
+    out[..., CODEC_TILE:] = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+    return out, bases, misfit
+
+
+def compact_rows(w: np.ndarray):
+    """The reference's compact resident row (edge35b/gpu_resident_experts.py:
+    22-45, encode) of the tiles of a bf16-bit array, in reading order: a
+    fitting tile's 384 packed bytes (reference order) or a raw tile's 512
+    bytes, and per tile the header (raw tiles before it) << 8 | base.
+    Returns (data u8, headers u32, tiles encoded, tiles raw); data is the raw
+    bytes and headers None when the compact form would not be smaller."""
+    raw = np.ascontiguousarray(w, dtype=np.uint16).reshape(-1, CODEC_TILE)
+    packed, bases, _ = codec_pack_reference_order(raw)
+    packed, bases = packed[:, 0], bases[:, 0]
+    fits = bases != 255
+    raw_before = np.cumsum(~fits, dtype=np.uint32) - (~fits)
+    headers = (raw_before << 8) | bases.astype(np.uint32)
+    raw_bytes = raw.view(np.uint8).reshape(len(raw), 2 * CODEC_TILE)
+    if int(np.where(fits, CODEC_TILE_BYTES, 2 * CODEC_TILE).sum()) + headers.nbytes >= raw_bytes.nbytes:
+        return raw_bytes.reshape(-1), None, 0, len(raw)
+    parts = [packed[t] if fits[t] else raw_bytes[t] for t in range(len(raw))]
+    return np.concatenate(parts), headers, int(fits.sum()), int((~fits).sum())
+
+
+def decode_compact_rows(data: np.ndarray, headers: np.ndarray) -> np.ndarray:
+    """Inverse of compact_rows (bf16 bits, tiles in order), in plain numpy
+    from the reference layout: a check of the encoder independent of the
+    device decoder."""
+    out = np.empty((len(headers), CODEC_TILE), dtype=np.uint16)
+    k = np.arange(CODEC_TILE)
+    for t, h in enumerate(headers.tolist()):
+        base, before = h & 255, h >> 8
+        at = t * CODEC_TILE_BYTES + before * 128
+        if base == 255:
+            out[t] = data[at:at + 2 * CODEC_TILE].view(np.uint16)
+            continue
+        tile = data[at:at + CODEC_TILE_BYTES].astype(np.uint16)
+        code = (tile[CODEC_TILE + k // 2] >> (4 * (k & 1))) & 15
+        out[t] = (((base + (code & 7)) | ((code & 8) << 4)) << 8) | tile[k]
+    return out
+
+
 @lru_cache(maxsize=1)
 def reference_tile_codec() -> C.CDLL | None:
     """The reference's own tile packer (edge35b/cpu_bf16_reads.h:16-52), built

@@ -101,3 +101,20 @@ def oracle_experts(oracle, x_bits: np.ndarray, indices: np.ndarray, weights_bits
         y_shared = np.stack([oracle.expert_pair(g, u_, d, x_bits[t]) for t in range(tokens)])
     return oracle.combine(y, plan["route_pair"], plan["pair_slot"], np.ascontiguousarray(weights_bits),
                           y_shared, sg_bits, residual_bits)
+
+
+def resident_fixture_words():
+    """The input of the reference's resident-row fixture
+    (edge35b/test_gpu_resident_experts.py:14-20): 32 tiles of bf16 bits,
+    every fourth with exponents 0..127 (does not fit the tile codec), the
+    others within 8 exponents."""
+    import numpy as np
+    import torch
+
+    gen = torch.Generator().manual_seed(7091)
+    words = torch.randint(0, 128, (32, 256), generator=gen, dtype=torch.int32)
+    words |= torch.randint(0, 2, words.shape, generator=gen, dtype=torch.int32) << 15
+    exponents = 118 + torch.randint(0, 8, words.shape, generator=gen, dtype=torch.int32)
+    exponents[1::4] = torch.arange(256) % 128
+    words |= exponents << 7
+    return words.to(torch.int16).numpy().view(np.uint16)

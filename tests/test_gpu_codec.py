@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import to_u16
+from helpers import resident_fixture_words, to_u16
 
 pytestmark = pytest.mark.gpu
 
@@ -161,3 +161,94 @@ def test_codec_chain_equals_raw_chain(model, codec_bank):
     assert torch.equal(idx_raw, idx_pk)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert ws.status() == 0
+
+
+def test_gather_resident_rows_reference_fixture(device, oracle):
+    """edge35b/test_gpu_resident_experts.py:12-57 on lrmoe_gather_tiles: a
+    compact row (24 packed tiles, 8 raw ones inline) and a raw row, the
+    descriptors swapped between graph replays, counts 2, 0, 1."""
+    from lightreason_amd.edge35b.native_bf16_gather import NativeBf16Gather
+
+    bits = resident_fixture_words()
+    data, headers, encoded, fallback = oracle.compact_rows(bits)
+    assert (encoded, fallback) == (24, 8)
+    packed = torch.from_numpy(data).to(device)
+    meta = torch.from_numpy(headers.view(np.uint8)).to(device)
+    original = torch.from_numpy(bits.view(np.int16))
+    other = original ^ 31
+    raw = other.to(device)
+    descriptors = torch.tensor([[[packed.data_ptr(), meta.data_ptr(), -1], [0, 0, raw.data_ptr()]]],
+                               device=device, dtype=torch.int64)
+    output = torch.full((4, 32, 256), -123, device=device, dtype=torch.int16)
+    destinations = torch.tensor([output.data_ptr()], device=device, dtype=torch.int64)
+    sizes = torch.tensor([original.numel() * 2], device=device, dtype=torch.int64)
+    ids = torch.tensor([0, 1], device=device, dtype=torch.int32)
+    slots = torch.tensor([1, 3], device=device, dtype=torch.int32)
+    count = torch.tensor([2], device=device, dtype=torch.int64)
+    native = NativeBf16Gather()
+
+    def copy():
+        native.copy(descriptors, destinations, sizes, ids, slots, count, max_copies=2, experts=2,
+                    geometry=(4, 256, "resident"))
+
+    copy()
+    torch.cuda.synchronize()
+    assert torch.equal(output[1].cpu(), original) and torch.equal(output[3].cpu(), other)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        copy()
+    references = [original, other]
+    for n in (2, 0, 1):
+        descriptors.copy_(descriptors.flip(1))
+        references.reverse()
+        output.fill_(-123)
+        count.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = torch.full_like(output.cpu(), -123)
+        for slot, reference in zip((1, 3)[:n], references[:n]):
+            expected[slot] = reference
+        print(f"resident fixture replay count={n}", flush=True)
+        assert torch.equal(output.cpu(), expected)
+
+
+@pytest.mark.parametrize("geometry", [(4, 256, "cpu-tiles"), (8, 128, "cpu-tiles"), (16, 128, "cpu-tiles"),
+                                      (4, 256, "resident")])
+def test_gather_codec_expert_rows(model, device, oracle, geometry):
+    """Whole expert rows (gate_up 4 MiB, down 2 MiB) of Gaussian weights in
+    the reference tile layout, each tile that does not fit read from the raw
+    row; a descriptor with bases 0 copies its raw row."""
+    from lightreason_amd.edge35b.native_bf16_gather import NativeBf16Gather
+
+    experts = (3, 200, 77)
+    keep = []
+    desc = torch.zeros((2, len(experts), 3), dtype=torch.int64)
+    misfit = 0
+    for i, e in enumerate(experts):
+        for bank, w in enumerate(model.bank.expert(0, e)):
+            bits = w.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, 256)
+            packed, bases, m = oracle.codec_pack_reference_order(bits)
+            misfit += m
+            pk = torch.from_numpy(packed.reshape(-1)).to(device)
+            bs = torch.from_numpy(bases.reshape(-1)).to(device)
+            keep += [pk, bs]
+            desc[bank, i] = torch.tensor([pk.data_ptr(), bs.data_ptr() if e != 77 else 0, w.data_ptr()])
+    assert misfit > 0
+    desc = desc.to(device)
+    gate_dst = torch.full((4, 1024, 2048), -123, dtype=torch.int16, device=device)
+    down_dst = torch.full((4, 2048, 512), -123, dtype=torch.int16, device=device)
+    destinations = torch.tensor([gate_dst.data_ptr(), down_dst.data_ptr()], dtype=torch.int64, device=device)
+    sizes = torch.tensor([1024 * 2048 * 2, 2048 * 512 * 2], dtype=torch.int64, device=device)
+    src = torch.tensor([0, 1, 2], dtype=torch.int32, device=device)
+    dst = torch.tensor([2, 0, 3], dtype=torch.int32, device=device)
+    count = torch.tensor([3], dtype=torch.int64, device=device)
+    NativeBf16Gather().copy(desc, destinations, sizes, src, dst, count, max_copies=3, experts=len(experts),
+                            geometry=geometry)
+    torch.cuda.synchronize()
+    print(f"codec expert rows {geometry}", flush=True)
+    for i, e in enumerate(experts):
+        gu, dn = model.bank.expert(0, e)
+        slot = int(dst[i])
+        assert torch.equal(gate_dst[slot], gu.view(torch.int16)), e
+        assert torch.equal(down_dst[slot], dn.view(torch.int16)), e
+    assert bool((gate_dst[1] == -123).all()) and bool((down_dst[1] == -123).all())

@@ -280,9 +280,10 @@ def test_native_gather_copy(model, device, geometry):
                 geometry=select_geometry(geometry))
     assert gather.codec_rows_seen()
     assert bool((gate_dst[1] == -123.0).all())
-    with pytest.raises(NotImplementedError):
+    # An unknown policy is refused on the host, before any launch.
+    with pytest.raises(ValueError):
         gather.copy(desc, destinations, sizes, src, dst, count, max_copies=8, experts=256,
-                    geometry=(4, 256, "cpu-tiles"))
+                    geometry=(4, 256, "no-such-policy"))
 
 
 def _hf_experts(model, device):

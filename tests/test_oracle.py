@@ -433,6 +433,42 @@ def test_codec_matches_the_reference_packer(oracle):
     assert (ref_bases == 255).sum() >= 17   # the random tiles and the inf/denormal tile
 
 
+def test_codec_reference_order_equals_the_reference_packer(oracle):
+    """codec_pack_reference_order gives the reference packer's bytes for
+    every tile that fits (the reference leaves the others unspecified)."""
+    ref = oracle.reference_tile_codec()
+    if ref is None:
+        pytest.skip("the reference's cpu_bf16_reads.h is not present")
+    rng = np.random.default_rng(12)
+    tiles = np.concatenate([_fitting_tiles(rng, 40), rng.integers(0, 65536, (8, 256), dtype=np.uint16)])
+    n = len(tiles)
+    ref_packed = np.zeros((n, 384), dtype=np.uint8)
+    ref_bases = np.zeros(n, dtype=np.uint8)
+    ref.ref_pack_cpu_read_tiles(tiles.ctypes.data, ref_packed.ctypes.data, ref_bases.ctypes.data, n)
+    packed, bases, misfit = oracle.codec_pack_reference_order(tiles)
+    np.testing.assert_array_equal(bases[:, 0], ref_bases)
+    fit = ref_bases != 255
+    assert misfit == int((~fit).sum()) >= 8
+    np.testing.assert_array_equal(packed[fit, 0], ref_packed[fit])
+
+
+def test_compact_rows_reference_fixture(oracle):
+    from helpers import resident_fixture_words
+
+    bits = resident_fixture_words()
+    data, headers, encoded, fallback = oracle.compact_rows(bits)
+    # The reference fixture's own expectation (test_gpu_resident_experts.py:22).
+    assert (encoded, fallback) == (24, 8)
+    assert data.nbytes == 24 * 384 + 8 * 512 and headers.dtype == np.uint32
+    # Raw tiles 1, 5, 9, ...: header base 255, later headers count them.
+    assert [h & 255 for h in headers[1::4].tolist()] == [255] * 8
+    assert [h >> 8 for h in headers.tolist()] == [(t + 2) // 4 for t in range(32)]
+    np.testing.assert_array_equal(oracle.decode_compact_rows(data, headers), bits)
+    # Nothing to gain: the raw bytes and no headers.
+    data, headers, encoded, fallback = oracle.compact_rows(np.arange(512, dtype=np.uint16) * 127)
+    assert headers is None and (encoded, fallback) == (0, 2) and data.nbytes == 1024
+
+
 def test_codec_closed_forms(oracle):
     # 1.0 everywhere: field 63, no sign, low byte 0x80; code 0 in every nibble.
     one = np.full((1, 256), 0x3F80, dtype=np.uint16)
