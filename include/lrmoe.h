@@ -189,16 +189,20 @@ int lrmoe_codec_pack(const uint16_t *w, int64_t rows, int cols, uint8_t *packed,
 int lrmoe_codec_unpack(const uint8_t *packed, const uint8_t *bases, int64_t rows, int cols, uint16_t *w,
                        void *stream);
 
-/* Raw BF16 row gather: for row < *count and bank b < banks, copy sizes[b]
- * bytes from descriptors[(b*experts + src_ids[row])*3] to
- * destinations[b] + dst_ids[row]*sizes[b]; a descriptor whose second field is
- * >= 0 (a codec row) is skipped and LRMOE_STATUS_CODEC_ROW is or-ed into
- * *status (may be NULL).  Grid (stripes, banks, max_copies) of `threads`
- * (64, 128, 192 or 256) threads; keep_in_l2 = 0 streams the rows with
- * nontemporal accesses, 1 uses cached accesses (the reference geometries'
- * "default" and "l2" policies).  Sizes and addresses are multiples of 16 bytes.
- * Replaces edge35b/bf16_gather_ada.cu:36-66 (gather_bf16 raw path) launched
- * by native_bf16_gather.py:71-77 (NativeBf16Gather.copy), and the staging copy
+/* BF16 row gather: for row < *count and bank b < banks, fill sizes[b] bytes
+ * at destinations[b] + dst_ids[row]*sizes[b] from the descriptor
+ * descriptors[(b*experts + src_ids[row])*3] = (address, base, escapes).
+ * base < 0: a raw row, copied.  base >= 0: an escape-codec row of n =
+ * sizes[b]/2 values (edge35b/bf16_expert_codec.py pack_row): n sign|fraction
+ * bytes, n/2 bytes of 4-bit exponent deltas from base, then `escapes` sorted
+ * int32 indices and their raw 16-bit values; it is decoded, and
+ * LRMOE_STATUS_CODEC_ROW is or-ed into *status (may be NULL).  Grid
+ * (stripes, banks, max_copies) of `threads` (64, 128, 192 or 256) threads;
+ * keep_in_l2 = 0 streams the rows with nontemporal accesses, 1 uses cached
+ * accesses (the reference geometries' "default" and "l2" policies).  Sizes
+ * and addresses are multiples of 16 bytes.  Replaces
+ * edge35b/bf16_gather_ada.cu:36-112 (gather_bf16, gather_bf16_l2) launched by
+ * native_bf16_gather.py:71-77 (NativeBf16Gather.copy), and the staging copy
  * of scheduled_graph.py:14-26 (_stage). */
 int lrmoe_gather(const int64_t *descriptors, const int64_t *destinations, const int64_t *sizes,
                  const int32_t *src_ids, const int32_t *dst_ids, const int64_t *count, int experts,

@@ -1,11 +1,13 @@
 // HBM-resident expert gather (raw BF16 rows) and the synthetic generator.
 //
-// Gather semantics: edge35b/bf16_gather_ada.cu:36-66 (raw path, base < 0) as
-// launched by edge35b/native_bf16_gather.py:71-77: for every copy row below
-// the device-resident *count, for every bank b, copy sizes[b] bytes from
-// descriptors[(b*experts + src_ids[row])*3 + 0] to
-// destinations[b] + dst_ids[row]*sizes[b].  The count stays on the device, so
-// a captured graph replays with new counts and descriptors.
+// Gather semantics: edge35b/bf16_gather_ada.cu:36-112 as launched by
+// edge35b/native_bf16_gather.py:71-77: for every copy row below the
+// device-resident *count, for every bank b, fill sizes[b] bytes at
+// destinations[b] + dst_ids[row]*sizes[b] from the descriptor
+// descriptors[(b*experts + src_ids[row])*3] = (address, base, escapes): a raw
+// row (base < 0) is copied; an escape-codec row (edge35b/bf16_expert_codec.py
+// pack_row) is decoded.  The count stays on the device, so a captured graph
+// replays with new counts and descriptors.
 //
 // On MI355X every expert row is resident in HBM, so the copy is HBM->HBM.
 // Each workgroup owns one contiguous stripe of one row of one bank and moves
@@ -21,6 +23,66 @@ constexpr int kGatherUnroll = 8;
 // kStream = true: nontemporal loads and stores (the rows stream past the
 // caches, the "default" policy); false: ordinary cached accesses that leave
 // the rows in L2 ("l2").
+// Two values of an escape-codec row: their sign|fraction bytes in bits 0..7
+// and 8..15 of sf, their exponent deltas in nibbles 0 and 1 of nib, base_pair
+// = base * 0x10001.  A value is sign << 15 | (base + delta) << 7 | fraction;
+// base + delta <= 255, so the two halves never carry into each other.
+__device__ __forceinline__ uint32_t escape_pair(uint32_t sf, uint32_t nib, uint32_t base_pair) {
+    const uint32_t bytes = (sf & 0xffu) | ((sf & 0xff00u) << 8);
+    const uint32_t delta = (nib & 0x0fu) | ((nib & 0xf0u) << 12);
+    return ((bytes & 0x00800080u) << 8) | (bytes & 0x007f007fu) | ((base_pair + delta) << 7);
+}
+
+// First index in the sorted escape list not below value.
+__device__ __forceinline__ int escape_lower_bound(const int32_t* indices, int count, int64_t value) {
+    int lo = 0, hi = count;
+    while (lo < hi) {
+        const int mid = lo + (hi - lo) / 2;
+        if (indices[mid] < value) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo;
+}
+
+// Escape-codec row of n = row_bytes / 2 values (bf16_expert_codec.py:37-60):
+// bytes [0, n) sign|fraction, [n, 3n/2) exponent deltas from base (value 2i
+// in the low nibble of byte i), then `escapes` sorted int32 indices and their
+// raw 16-bit values.  The workgroup decodes its units [begin, end) (8 values
+// each), waits for those stores, then writes the escapes inside its units.
+template <bool kStream>
+__device__ __forceinline__ void gather_escape_row(const uint8_t* src, int base, int escapes, int64_t row_bytes,
+                                                  u32x4* dst, int64_t begin, int64_t end) {
+    const int64_t n = row_bytes / 2;
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2* sf = reinterpret_cast<const u32x2*>(src);
+    const uint32_t* deltas = reinterpret_cast<const uint32_t*>(src + n);
+    const uint32_t base_pair = static_cast<uint32_t>(base) * 0x10001u;
+    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        const u32x2 s = kStream ? __builtin_nontemporal_load(sf + i) : sf[i];
+        const uint32_t d = kStream ? __builtin_nontemporal_load(deltas + i) : deltas[i];
+        u32x4 v;
+        v.x = escape_pair(s.x, d, base_pair);
+        v.y = escape_pair(s.x >> 16, d >> 8, base_pair);
+        v.z = escape_pair(s.y, d >> 16, base_pair);
+        v.w = escape_pair(s.y >> 16, d >> 24, base_pair);
+        dst[i] = v;
+    }
+    if (escapes <= 0) return;
+    const int32_t* indices = reinterpret_cast<const int32_t*>(src + n + n / 2);
+    const uint16_t* values = reinterpret_cast<const uint16_t*>(indices + escapes);
+    __shared__ int range[2];
+    if (threadIdx.x == 0) {
+        range[0] = escape_lower_bound(indices, escapes, begin * 8);
+        range[1] = escape_lower_bound(indices, escapes, end * 8);
+    }
+    __syncthreads();  // also orders this workgroup's decoded stores before the escapes
+    uint16_t* out = reinterpret_cast<uint16_t*>(dst);
+    for (int j = range[0] + static_cast<int>(threadIdx.x); j < range[1]; j += blockDim.x) out[indices[j]] = values[j];
+}
+
 template <bool kStream>
 __global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors, const int64_t* destinations,
                                                      const int64_t* sizes, const int32_t* src_ids,
@@ -32,17 +94,18 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* descriptors,
     if (row >= *count) return;
     const int64_t* desc = descriptors + (static_cast<int64_t>(bank) * experts + src_ids[row]) * 3;
     const u32x4* src = reinterpret_cast<const u32x4*>(desc[0]);
-    if (desc[1] >= 0) {
-        // A codec-packed row: not a raw BF16 row, so nothing is copied.
-        if (threadIdx.x == 0 && stripe == 0 && status != nullptr) atomicOr(status, kStatusCodecRow);
-        return;
-    }
     const int64_t row_bytes = sizes[bank];
     u32x4* dst = reinterpret_cast<u32x4*>(destinations[bank] + static_cast<int64_t>(dst_ids[row]) * row_bytes);
     const int64_t units = row_bytes >> 4;
     const int64_t per = (units + gridDim.x - 1) / gridDim.x;
     const int64_t begin = stripe * per;
     const int64_t end = begin + per < units ? begin + per : units;
+    if (desc[1] >= 0) {
+        if (threadIdx.x == 0 && stripe == 0 && status != nullptr) atomicOr(status, kStatusCodecRow);
+        gather_escape_row<kStream>(reinterpret_cast<const uint8_t*>(desc[0]), static_cast<int>(desc[1]),
+                                   static_cast<int>(desc[2]), row_bytes, dst, begin, end);
+        return;
+    }
     const int64_t step = static_cast<int64_t>(blockDim.x) * kGatherUnroll;
     int64_t i = begin + threadIdx.x;
     for (; i + (kGatherUnroll - 1) * blockDim.x < end; i += step) {

@@ -14,7 +14,7 @@ namespace lrmoe {
 // Bits of the device status word (workspace control block).
 constexpr int32_t kStatusBadExpert = 1;     // expert id outside [0, 256)
 constexpr int32_t kStatusRepeatedExpert = 2;  // a token routes to one expert twice
-constexpr int32_t kStatusCodecRow = 4;      // gather met a codec descriptor (not a raw row)
+constexpr int32_t kStatusCodecRow = 4;      // gather met (and decoded) an escape-codec descriptor
 constexpr int32_t kStatusTimeout = 8;       // a bounded cross-workgroup wait expired (results invalid)
 
 // Decode layer (one persistent kernel) limits.

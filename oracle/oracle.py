@@ -350,6 +350,82 @@ def decode_compact_rows(data: np.ndarray, headers: np.ndarray) -> np.ndarray:
     return out
 
 
+# ---- the escape codec of the gather (edge35b/bf16_expert_codec.py:27-78) ----
+
+ESCAPE_WINDOW = 16
+
+
+def escape_window(bits: np.ndarray):
+    """(base, escapes) of a flat row of bf16 bits (bf16_expert_codec.py:27-35):
+    base starts the window of 16 consecutive 8-bit exponents (bits 14..7)
+    that holds the most values, the first such window on ties; escapes =
+    values outside it."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    if bits.ndim != 1 or bits.size % 8 or not 0 < bits.size < 2**31:
+        raise ValueError("Expected a flat, aligned BF16 bit array")
+    counts = np.bincount((bits >> 7) & 255, minlength=256).astype(np.int64)
+    upto = np.concatenate([[0], np.cumsum(counts)])
+    inside = upto[ESCAPE_WINDOW:] - upto[:-ESCAPE_WINDOW]   # window b covers exponents b .. b+15
+    base = int(np.argmax(inside))
+    return base, int(bits.size - inside[base])
+
+
+def escape_row_bytes(n: int, escapes: int) -> int:
+    """n sign|fraction bytes, n/2 delta bytes, 4 + 2 bytes per escape."""
+    return 3 * n // 2 + 6 * escapes
+
+
+def escape_pack(bits: np.ndarray, base: int, escapes: int) -> np.ndarray:
+    """Packed row (bf16_expert_codec.py:42-55): per value its sign and
+    fraction in one byte (sign at bit 7), its exponent - base in a nibble
+    (value 2i in the low nibble of byte i; escaped values keep the low four
+    bits), then the escapes' int32 indices in order and their raw bits."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    n = bits.size
+    delta = ((bits >> 7) & 255).astype(np.int32) - base
+    escaped = np.flatnonzero((delta < 0) | (delta >= ESCAPE_WINDOW))
+    if escaped.size != escapes:
+        raise ValueError("escape count disagrees with the row")
+    out = np.zeros(escape_row_bytes(n, escapes), dtype=np.uint8)
+    out[:n] = ((bits & 0x7F) | ((bits >> 8) & 0x80)).astype(np.uint8)
+    nib = (delta & 15).astype(np.uint8)
+    out[n:3 * n // 2] = nib[0::2] | (nib[1::2] << 4)
+    tail = 3 * n // 2
+    out[tail:tail + 4 * escapes] = escaped.astype("<i4").view(np.uint8)
+    out[tail + 4 * escapes:] = bits[escaped].astype("<u2").view(np.uint8)
+    return out
+
+
+def escape_restore(packed: np.ndarray, n: int, base: int, escapes: int) -> np.ndarray:
+    """Inverse of escape_pack (bf16_expert_codec.py:58-67)."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    sf = packed[:n].astype(np.uint16)
+    nib = packed[n:3 * n // 2]
+    delta = np.empty(n, dtype=np.uint16)
+    delta[0::2] = nib & 15
+    delta[1::2] = nib >> 4
+    bits = ((sf & 0x80) << 8) | (sf & 0x7F) | ((delta + base) << 7)
+    tail = 3 * n // 2
+    idx = packed[tail:tail + 4 * escapes].view("<i4")
+    bits[idx] = packed[tail + 4 * escapes:tail + 6 * escapes].view("<u2")
+    return bits.astype(np.uint16)
+
+
+def escape_plan(rows: np.ndarray):
+    """Layout of a bank of packed rows (bf16_expert_codec.py:70-81): per row
+    (offset, base, escapes), or None where more than 1% of its values escape
+    (that row stays raw); offsets 16-byte aligned.  Returns (plans, bytes)."""
+    plans, size = [], 0
+    for row in rows:
+        base, escapes = escape_window(row)
+        if escapes * 100 > row.size:
+            plans.append(None)
+            continue
+        plans.append((size, base, escapes))
+        size = (size + escape_row_bytes(row.size, escapes) + 15) & ~15
+    return plans, size
+
+
 @lru_cache(maxsize=1)
 def reference_tile_codec() -> C.CDLL | None:
     """The reference's own tile packer (edge35b/cpu_bf16_reads.h:16-52), built

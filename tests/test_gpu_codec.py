@@ -252,3 +252,44 @@ def test_gather_codec_expert_rows(model, device, oracle, geometry):
         assert torch.equal(gate_dst[slot], gu.view(torch.int16)), e
         assert torch.equal(down_dst[slot], dn.view(torch.int16)), e
     assert bool((gate_dst[1] == -123).all()) and bool((down_dst[1] == -123).all())
+
+
+@pytest.mark.parametrize("geometry", [(4, 256, "default"), (16, 128, "default"), (8, 256, "l2"), (16, 128, "l2")])
+def test_gather_escape_codec_rows(model, device, oracle, geometry):
+    """Escape-codec rows (bf16_expert_codec.py pack_row, decoded by
+    bf16_gather_ada.cu:36-100): Gaussian expert rows with their few escapes,
+    a row of every bf16 pattern (mostly escapes), and raw rows beside them."""
+    from lightreason_amd.edge35b.native_bf16_gather import NativeBf16Gather
+
+    rng = np.random.default_rng(5)
+    patterns = rng.permutation(np.arange(65536, dtype=np.uint16))
+    rows = [model.bank.expert(0, 9)[0], model.bank.expert(0, 41)[0],
+            torch.from_numpy(np.tile(patterns, 32).view(np.int16)).to(device).view(torch.bfloat16).view(1024, 2048)]
+    keep = []
+    desc = torch.zeros((1, 4, 3), dtype=torch.int64)
+    escapes_seen = []
+    for i, w in enumerate(rows):
+        bits = w.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        base, escapes = oracle.escape_window(bits)
+        escapes_seen.append(escapes)
+        pk = torch.from_numpy(oracle.escape_pack(bits, base, escapes)).to(device)
+        keep.append(pk)
+        desc[0, i] = torch.tensor([pk.data_ptr(), base, escapes])
+    desc[0, 3] = torch.tensor([model.bank.expert(0, 50)[0].data_ptr(), -1, 0])
+    assert escapes_seen[0] > 0 and escapes_seen[2] > 1_000_000
+    desc = desc.to(device)
+    out = torch.full((5, 1024, 2048), -123, dtype=torch.int16, device=device)
+    destinations = torch.tensor([out.data_ptr()], dtype=torch.int64, device=device)
+    sizes = torch.tensor([1024 * 2048 * 2], dtype=torch.int64, device=device)
+    src = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device=device)
+    dst = torch.tensor([4, 0, 2, 1], dtype=torch.int32, device=device)
+    count = torch.tensor([4], dtype=torch.int64, device=device)
+    gather = NativeBf16Gather()
+    gather.copy(desc, destinations, sizes, src, dst, count, max_copies=4, experts=4, geometry=geometry)
+    torch.cuda.synchronize()
+    print(f"escape codec rows {geometry}", flush=True)
+    expected = [rows[0], rows[1], rows[2], model.bank.expert(0, 50)[0]]
+    for i, w in enumerate(expected):
+        assert torch.equal(out[int(dst[i])], w.view(torch.int16)), i
+    assert bool((out[3] == -123).all())
+    assert gather.codec_rows_seen()

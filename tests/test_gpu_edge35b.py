@@ -274,12 +274,20 @@ def test_native_gather_copy(model, device, geometry):
         assert torch.equal(down_dst[slot].view(torch.int16), dn.view(torch.int16))
     assert bool((gate_dst[5] == -123.0).all()) and bool((down_dst[5] == -123.0).all())
     assert not gather.codec_rows_seen()
-    desc[0, 100, 1] = 7  # a codec row: skipped and flagged
+    # Expert 100's gate_up as an escape-codec row (bf16_expert_codec.py):
+    # decoded into its slot, and flagged.
+    from oracle import oracle as O
+
+    bits = model.bank.expert(0, 100)[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    base, escapes = O.escape_window(bits)
+    packed = torch.from_numpy(O.escape_pack(bits, base, escapes)).to(device)
+    desc[0, 100] = torch.tensor([packed.data_ptr(), base, escapes])
     gate_dst.fill_(-123.0)
     gather.copy(desc, destinations, sizes, src, dst, count, max_copies=8, experts=256,
                 geometry=select_geometry(geometry))
+    torch.cuda.synchronize()
     assert gather.codec_rows_seen()
-    assert bool((gate_dst[1] == -123.0).all())
+    assert torch.equal(gate_dst[1].view(torch.int16), model.bank.expert(0, 100)[0].view(torch.int16))
     # An unknown policy is refused on the host, before any launch.
     with pytest.raises(ValueError):
         gather.copy(desc, destinations, sizes, src, dst, count, max_copies=8, experts=256,

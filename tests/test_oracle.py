@@ -469,6 +469,43 @@ def test_compact_rows_reference_fixture(oracle):
     assert headers is None and (encoded, fallback) == (0, 2) and data.nbytes == 1024
 
 
+def test_escape_codec_reference_fixture(oracle):
+    """edge35b/test_freetoken_packed_transfer.py:15-25: every bf16 pattern
+    round-trips; a bank plan keeps the all-patterns row raw (it escapes far
+    more than 1%) and packs the constant rows without escapes."""
+    values = np.arange(65536, dtype=np.uint16)
+    base, escapes = oracle.escape_window(values)
+    packed = oracle.escape_pack(values, base, escapes)
+    assert packed.size == oracle.escape_row_bytes(values.size, escapes)
+    np.testing.assert_array_equal(oracle.escape_restore(packed, values.size, base, escapes), values)
+    common = np.full(values.shape, 0x3F80, dtype=np.uint16)
+    plans, size = oracle.escape_plan(np.stack([common, values, common]))
+    assert plans[1] is None
+    assert plans[0][2] == 0
+    assert plans[2][0] == oracle.escape_row_bytes(common.size, 0)
+    assert size == 2 * oracle.escape_row_bytes(common.size, 0)
+
+
+def test_escape_codec_closed_forms(oracle):
+    # 1.0 (exponent 127): the first window holding it starts at 112; delta 15.
+    one = np.full(64, 0x3F80, dtype=np.uint16)
+    assert oracle.escape_window(one) == (112, 0)
+    packed = oracle.escape_pack(one, 112, 0)
+    assert np.all(packed[:64] == 0) and np.all(packed[64:96] == 0xFF)
+    # Every pattern: the 16 exponents 0..15 hold 16 x 128 x 2 values, tied
+    # with every other window; the first one wins.
+    assert oracle.escape_window(np.arange(65536, dtype=np.uint16)) == (0, 65536 - 16 * 256)
+    # One value escapes below the window, one above: indices in order.
+    row = np.full(32, 0x4000, dtype=np.uint16)     # 2.0, exponent 128
+    row[5], row[20] = 0x0001, 0x7F80               # exponent 0, +inf (255)
+    base, escapes = oracle.escape_window(row)
+    assert (base, escapes) == (113, 2)
+    packed = oracle.escape_pack(row, base, escapes)
+    assert packed[48:56].view("<i4").tolist() == [5, 20]
+    assert packed[56:60].view("<u2").tolist() == [0x0001, 0x7F80]
+    np.testing.assert_array_equal(oracle.escape_restore(packed, 32, base, escapes), row)
+
+
 def test_codec_closed_forms(oracle):
     # 1.0 everywhere: field 63, no sign, low byte 0x80; code 0 in every nibble.
     one = np.full((1, 256), 0x3F80, dtype=np.uint16)
