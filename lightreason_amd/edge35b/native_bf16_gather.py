@@ -10,9 +10,9 @@ device, grid (stripes, banks, max_copies), torch's current stream, no host
 synchronisation (graph-capturable; a replay picks up new counts and
 descriptors).
 
-Policies "default" and "l2" copy raw BF16 rows (base < 0) bit for bit
-(lrmoe_gather); their escape-codec rows (base >= 0) are not implemented: such
-a descriptor is skipped and flagged in ``status`` (STATUS_CODEC_ROW).
+Policies "default" and "l2" copy raw BF16 rows (base < 0) bit for bit and
+decode escape-codec rows (base >= 0, bf16_expert_codec.py; flagged in
+``status`` as STATUS_CODEC_ROW) with lrmoe_gather.
 Policies "cpu-tiles" and "resident" decode the tile codec (descriptors
 (packed, bases, raw), "resident" also compact rows with raw = -1;
 lrmoe_gather_tiles), like bf16_gather_ada.cu:127-201.  ``stage_primary`` and
@@ -89,7 +89,7 @@ class NativeBf16Gather:
             raise RuntimeError(str(exc)) from exc
 
     def codec_rows_seen(self) -> bool:
-        """True when a copy met a codec descriptor (reads the device)."""
+        """True when a copy decoded an escape-codec row (reads the device)."""
         return bool(int(self.status.item()) & _native.STATUS_CODEC_ROW)
 
     def stage_primary(self, *args, **kwargs):
