@@ -146,17 +146,20 @@ def test_codec_mixed_raw_and_packed_experts(model, codec_bank):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
-def test_codec_chain_equals_raw_chain(model, codec_bank):
+@pytest.mark.parametrize("tokens,pattern", [(8, "ccc"), (16, "ccc"), (8, "crc"), (16, "rcr")])
+def test_codec_chain_equals_raw_chain(model, codec_bank, tokens, pattern):
+    """Chains of codec (c) and raw (r) layers: the codec kernel instance
+    runs the raw layers too, whose codec rows are left from earlier layers."""
     from lightreason_amd.moe import Workspace, moe_chain
 
     raw, packed = _layer_pair(model, codec_bank, True)
-    tokens = 8
-    x = model.hidden(tokens, step=760)
+    x = model.hidden(tokens, step=760 + tokens)
     ws = Workspace(x.device, tokens)
     idx_raw = torch.empty((3, tokens, 8), dtype=torch.int64, device=x.device)
     idx_pk = torch.empty_like(idx_raw)
     want = moe_chain(x, [raw] * 3, indices=idx_raw, workspace=ws)
-    got = moe_chain(x, [packed] * 3, indices=idx_pk, workspace=ws)
+    got = moe_chain(x, [packed if c == "c" else raw for c in pattern], indices=idx_pk, workspace=ws)
+    print(f"codec chain T={tokens} {pattern}", flush=True)
     torch.cuda.synchronize()
     assert torch.equal(idx_raw, idx_pk)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
