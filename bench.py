@@ -188,6 +188,58 @@ class GatherCase:
                    max_copies=self.max_copies, experts=256, stripes=48)
 
 
+class CodecGatherCase:
+    """C1 with codec rows: per layer, gather its selected experts' 6 MiB rows
+    from the tile codec ("cpu-tiles": lrmoe_gather_tiles) or the escape codec
+    (lrmoe_gather), packed on the device from the resident experts."""
+
+    def __init__(self, model, per_layer, staging, device, codec: str):
+        from lightreason_amd.moe import pack_escape_row, pack_tiles_reference_order
+
+        self.codec = codec
+        self.keep = []
+        self.descs = []
+        self.read_bytes = 0
+        for l, sel in enumerate(per_layer):
+            ptrs = model.bank.tables[l][:, 0].cpu()
+            desc = torch.zeros((1, 256, 3), dtype=torch.int64)
+            desc[0, :, 2 if codec == "tile" else 0] = ptrs
+            if codec == "escape":
+                desc[0, :, 1] = -1
+            for e in sel:
+                row = model.bank.bank[l, e]
+                if codec == "tile":
+                    packed, bases, _ = pack_tiles_reference_order(row.view(-1, 256))
+                    self.keep += [packed, bases]
+                    desc[0, e, 0], desc[0, e, 1] = packed.data_ptr(), bases.data_ptr()
+                    self.read_bytes += packed.numel() + bases.numel()
+                else:
+                    packed, base, escapes = pack_escape_row(row)
+                    self.keep.append(packed)
+                    desc[0, e] = torch.tensor([packed.data_ptr(), base, escapes])
+                    self.read_bytes += packed.numel()
+            self.descs.append(desc.to(device))
+        self.read_bytes /= len(per_layer)
+        self.srcs = [torch.tensor(sel + [0] * (128 - len(sel)), dtype=torch.int32, device=device) for sel in per_layer]
+        self.dst = torch.arange(128, dtype=torch.int32, device=device)
+        self.counts = [torch.tensor([len(sel)], device=device) for sel in per_layer]
+        self.dests = torch.tensor([staging.data_ptr()], device=device)
+        self.sizes = torch.tensor([EXPERT_BYTES], device=device)
+        self.max_copies = max(len(sel) for sel in per_layer)
+        self.stream = torch.cuda.current_stream(device).cuda_stream
+
+    def run(self):
+        for l in range(len(self.descs)):
+            if self.codec == "tile":
+                _native.call("lrmoe_gather_tiles", self.descs[l].data_ptr(), self.dests.data_ptr(),
+                             self.sizes.data_ptr(), self.srcs[l].data_ptr(), self.dst.data_ptr(),
+                             self.counts[l].data_ptr(), 256, 1, self.max_copies, 48, 256, 0,
+                             torch.cuda.current_stream().cuda_stream)
+            else:
+                gather(self.descs[l], self.dests, self.sizes, self.srcs[l], self.dst, self.counts[l],
+                       max_copies=self.max_copies, experts=256, stripes=48)
+
+
 def bench_case(case: Case, replays: int, warmup: int, spread: dict | None = None) -> float:
     """Milliseconds per graph replay (one pass over the case's layers).  With
     `spread`, also fills it with per-layer percentiles from a separate pass."""
@@ -416,6 +468,21 @@ def main() -> int:
             moved = 2 * u * EXPERT_BYTES
             gather_res[f"t{T}"] = dict(unique=round(u, 1), us=round(msg * 1e3, 2),
                                        gbs_moved=round(moved / (msg * 1e-3) / 1e9, 1))
+            if T == 8:
+                t8_layers = per_layer
+        # Codec rows, T=8 selections of the first 8 layers: raw-equivalent
+        # GB/s (6 MiB read + 6 MiB written per row) and the bytes read.
+        for codec in ("tile", "escape"):
+            sel8 = t8_layers[:min(L, 8)]
+            ccase = CodecGatherCase(model, sel8, staging, device, codec)
+            msc = bench_case(ccase, replays, warm) / len(sel8)
+            u = float(np.mean([len(sel) for sel in sel8]))
+            gather_res[f"t8_{codec}_codec"] = dict(
+                unique=round(u, 1), us=round(msc * 1e3, 2),
+                gbs_raw_equivalent=round(2 * u * EXPERT_BYTES / (msc * 1e-3) / 1e9, 1),
+                read_fraction=round(ccase.read_bytes / (u * EXPERT_BYTES), 4),
+                gbs_moved=round((ccase.read_bytes + u * EXPERT_BYTES) / (msc * 1e-3) / 1e9, 1))
+            del ccase
         configs["c1_gather"] = gather_res
         log(f"[bench] C1 gather: {gather_res}")
         del staging

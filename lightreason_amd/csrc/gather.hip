@@ -60,15 +60,32 @@ __device__ __forceinline__ void gather_escape_row(const uint8_t* src, int base, 
     const u32x2* sf = reinterpret_cast<const u32x2*>(src);
     const uint32_t* deltas = reinterpret_cast<const uint32_t*>(src + n);
     const uint32_t base_pair = static_cast<uint32_t>(base) * 0x10001u;
-    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
-        const u32x2 s = kStream ? __builtin_nontemporal_load(sf + i) : sf[i];
-        const uint32_t d = kStream ? __builtin_nontemporal_load(deltas + i) : deltas[i];
+    auto decode = [&](const u32x2& s, uint32_t d) {
         u32x4 v;
         v.x = escape_pair(s.x, d, base_pair);
         v.y = escape_pair(s.x >> 16, d >> 8, base_pair);
         v.z = escape_pair(s.y, d >> 16, base_pair);
         v.w = escape_pair(s.y >> 16, d >> 24, base_pair);
-        dst[i] = v;
+        return v;
+    };
+    // Four units' loads in flight per lane, then the rest one at a time.
+    constexpr int kUnits = 4;
+    int64_t i = begin + threadIdx.x;
+    for (; i + (kUnits - 1) * blockDim.x < end; i += kUnits * blockDim.x) {
+        u32x2 s[kUnits];
+        uint32_t d[kUnits];
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            s[u] = kStream ? __builtin_nontemporal_load(sf + i + u * blockDim.x) : sf[i + u * blockDim.x];
+            d[u] = kStream ? __builtin_nontemporal_load(deltas + i + u * blockDim.x) : deltas[i + u * blockDim.x];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) dst[i + u * blockDim.x] = decode(s[u], d[u]);
+    }
+    for (; i < end; i += blockDim.x) {
+        const u32x2 s = kStream ? __builtin_nontemporal_load(sf + i) : sf[i];
+        const uint32_t d = kStream ? __builtin_nontemporal_load(deltas + i) : deltas[i];
+        dst[i] = decode(s, d);
     }
     if (escapes <= 0) return;
     const int32_t* indices = reinterpret_cast<const int32_t*>(src + n + n / 2);
@@ -182,7 +199,31 @@ __global__ __launch_bounds__(256) void gather_tiles_kernel(const int64_t* descri
     const bool compact = kCompact && raw_at == -1;
     const u32x4* raw = reinterpret_cast<const u32x4*>(raw_at);
     const int lane = threadIdx.x & 31;
-    for (int64_t tile = begin + (threadIdx.x >> 5); tile < end; tile += blockDim.x >> 5) {
+    const int64_t step = blockDim.x >> 5;
+    int64_t tile = begin + (threadIdx.x >> 5);
+    if (!compact) {
+        // Every tile has its 384 bytes at packed + 384t, so a tile's loads do
+        // not wait for its base: four tiles' loads in flight per lane.
+        constexpr int kTiles = 4;
+        for (; tile + (kTiles - 1) * step < end; tile += kTiles * step) {
+            uint32_t base[kTiles], codes[kTiles];
+            uint2 low[kTiles];
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) {
+                const int64_t t = tile + u * step;
+                base[u] = bases[t];
+                low[u] = *reinterpret_cast<const uint2*>(packed + t * 384 + 8 * lane);
+                codes[u] = *reinterpret_cast<const uint32_t*>(packed + t * 384 + 256 + 4 * lane);
+            }
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) {
+                const int64_t i = (tile + u * step) * 32 + lane;
+                dst[i] = base[u] == 255u ? raw[i]
+                                         : ref_tile_decode8(low[u].x, low[u].y, codes[u], base[u] * 0x01010101u);
+            }
+        }
+    }
+    for (; tile < end; tile += step) {
         const uint32_t header = compact ? reinterpret_cast<const uint32_t*>(bases)[tile] : bases[tile];
         const uint32_t base = compact ? header & 255u : header;
         const uint8_t* data = packed + tile * 384 + (compact ? static_cast<int64_t>(header >> 8) * 128 : 0);

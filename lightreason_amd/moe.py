@@ -199,6 +199,68 @@ def codec_unpack(packed: torch.Tensor, bases: torch.Tensor, rows: int, cols: int
     return out
 
 
+def _reference_tile_order(device):
+    """Byte positions, in lrmoe_codec_pack's tile, of the reference tile
+    layout's bytes (value k: low byte k, code nibble k of bytes 256..383)."""
+    k = torch.arange(CODEC_TILE, device=device)
+    g, s, j = (k >> 3) & 3, k >> 5, k & 7
+    low_at = 64 * (s >> 1) + 16 * g + 8 * (s & 1) + j
+    code_at = 256 + 64 * (s >> 2) + 16 * g + 4 * (s & 3) + (j & 3)
+    return low_at, code_at, 4 * (j >> 2)
+
+
+def pack_tiles_reference_order(w: torch.Tensor):
+    """A [rows, cols] bf16 matrix in the reference's tile-codec layout
+    (edge35b/cpu_bf16_reads.h:16-52; decoded by lrmoe_gather_tiles): returns
+    (packed uint8 [tiles, 384], bases uint8 [tiles], tiles that do not fit).
+    lrmoe_codec_pack on the device, then its bytes rearranged."""
+    rows, cols = w.shape
+    tiles = rows * cols // CODEC_TILE
+    ours = torch.empty((tiles, CODEC_TILE_BYTES), dtype=torch.uint8, device=w.device)
+    bases = torch.empty(tiles, dtype=torch.uint8, device=w.device)
+    misfit = torch.zeros(1, dtype=torch.int64, device=w.device)
+    codec_pack(w, ours.view(-1), bases, misfit)
+    low_at, code_at, shift = _reference_order_cached(w.device)
+    codes = (ours[:, code_at] >> shift.to(torch.uint8)) & 15
+    packed = torch.cat([ours[:, low_at], codes[:, 0::2] | (codes[:, 1::2] << 4)], dim=1)
+    return packed, bases, int(misfit.item())
+
+
+_ORDER = {}
+
+
+def _reference_order_cached(device):
+    key = str(device)
+    if key not in _ORDER:
+        _ORDER[key] = _reference_tile_order(device)
+    return _ORDER[key]
+
+
+def pack_escape_row(w: torch.Tensor):
+    """A bf16 row (any shape, flattened) in the gather's escape-codec format
+    (edge35b/bf16_expert_codec.py:27-55; decoded by lrmoe_gather): returns
+    (packed uint8, base, escapes).  base starts the first window of 16
+    consecutive exponents holding the most values; per value one
+    sign|fraction byte and a 4-bit exponent delta, then the escapes' sorted
+    int32 indices and raw bits."""
+    bits = w.reshape(-1).view(torch.int16).to(torch.int32) & 0xFFFF
+    n = bits.numel()
+    exponent = (bits >> 7) & 255
+    counts = torch.bincount(exponent, minlength=256)
+    upto = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)])
+    inside = upto[16:] - upto[:-16]
+    base = int(torch.argmax(inside).item())   # torch.argmax returns the first maximum
+    delta = exponent - base
+    escaped = torch.nonzero((delta < 0) | (delta >= 16)).reshape(-1)
+    escapes = escaped.numel()
+    sf = ((bits & 0x7F) | ((bits >> 8) & 0x80)).to(torch.uint8)
+    nib = (delta & 15).to(torch.uint8)
+    deltas = nib[0::2] | (nib[1::2] << 4)
+    index_bytes = escaped.to(torch.int32).view(torch.uint8)
+    value_bytes = bits[escaped].to(torch.int16).view(torch.uint8)
+    return torch.cat([sf, deltas, index_bytes, value_bytes]), base, escapes
+
+
 CODEC_TABLE_COLUMNS = _native.CODEC_TABLE_COLUMNS   # 4 addresses + 48 bytes of per-(item, wave) raw flags
 
 

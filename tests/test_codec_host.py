@@ -62,3 +62,20 @@ def test_unit_flags_extremes():
     every = codec_unit_flags(torch.full((8192,), CODEC_MISFIT, dtype=torch.uint8),
                              torch.full((4096,), CODEC_MISFIT, dtype=torch.uint8))
     assert f.dtype == torch.uint8 and every.tolist() == [255] * 48
+
+
+def test_escape_packer_matches_the_oracle(oracle):
+    """moe.pack_escape_row (torch, here on the CPU) against the oracle's
+    restatement of bf16_expert_codec.py: every bf16 pattern, Gaussian
+    weights, and a constant row."""
+    import numpy as np
+
+    from lightreason_amd.moe import pack_escape_row
+
+    rng = np.random.default_rng(3)
+    gauss = (rng.standard_normal(8192).astype(np.float32) * 0.02).view(np.uint32) >> 16
+    for bits in (np.arange(65536, dtype=np.uint16), gauss.astype(np.uint16), np.full(64, 0x3F80, np.uint16)):
+        w = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+        packed, base, escapes = pack_escape_row(w)
+        assert (base, escapes) == oracle.escape_window(bits)
+        np.testing.assert_array_equal(packed.numpy(), oracle.escape_pack(bits, base, escapes))

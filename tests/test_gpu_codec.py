@@ -296,3 +296,18 @@ def test_gather_escape_codec_rows(model, device, oracle, geometry):
         assert torch.equal(out[int(dst[i])], w.view(torch.int16)), i
     assert bool((out[3] == -123).all())
     assert gather.codec_rows_seen()
+
+
+def test_reference_order_tile_packer(model, device, oracle):
+    """moe.pack_tiles_reference_order (lrmoe_codec_pack, bytes rearranged on
+    the device) against the oracle's reference-order packing."""
+    from lightreason_amd.moe import pack_tiles_reference_order
+
+    gate_up, _ = model.bank.expert(0, 12)
+    packed, bases, misfit = pack_tiles_reference_order(gate_up)
+    torch.cuda.synchronize()
+    bits = gate_up.view(torch.int16).cpu().numpy().view(np.uint16)
+    o_packed, o_bases, o_misfit = oracle.codec_pack_reference_order(bits)
+    assert misfit == o_misfit > 0
+    np.testing.assert_array_equal(bases.cpu().numpy(), o_bases.reshape(-1))
+    np.testing.assert_array_equal(packed.cpu().numpy(), o_packed.reshape(-1, 384))
