@@ -17,16 +17,16 @@ int status_of(hipError_t err) { return err == hipSuccess ? LRMOE_OK : static_cas
 
 // gfx950 check of the current device, cached per device ordinal.
 int check_device() {
-    static int verdict[64] = {0};  // 0 unknown, 1 ok, 2 wrong device
+    static int device_state[64] = {0};  // 0 unknown, 1 ok, 2 wrong device
     int device = 0;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return static_cast<int>(err);
-    if (device >= 0 && device < 64 && verdict[device] != 0) return verdict[device] == 1 ? LRMOE_OK : LRMOE_E_DEVICE;
+    if (device >= 0 && device < 64 && device_state[device] != 0) return device_state[device] == 1 ? LRMOE_OK : LRMOE_E_DEVICE;
     hipDeviceProp_t prop;
     err = hipGetDeviceProperties(&prop, device);
     if (err != hipSuccess) return static_cast<int>(err);
     const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-    if (device >= 0 && device < 64) verdict[device] = ok ? 1 : 2;
+    if (device >= 0 && device < 64) device_state[device] = ok ? 1 : 2;
     return ok ? LRMOE_OK : LRMOE_E_DEVICE;
 }
 
