@@ -19,7 +19,16 @@
  *     token routed twice to one expert) set bits in the int32 status word at
  *     byte offset LRMOE_WS_STATUS_OFFSET of the workspace; the affected call
  *     then writes zeros (plus the residual, where one is given) instead of
- *     reading out of bounds.
+ *     reading out of bounds;
+ *   - the decode layer and chain (lrmoe_moe_layer and lrmoe_moe_experts at
+ *     tokens <= 16, lrmoe_moe_chain) run one
+ *     persistent workgroup per CU whose workgroups wait for each other's
+ *     results, so all of them must be resident at once: a kernel running
+ *     concurrently on another stream of the same device can keep some of
+ *     them off the GPU.  Every such wait is bounded (50 ms); on expiry the
+ *     call still ends, sets LRMOE_STATUS_TIMEOUT in the status word, and
+ *     its outputs are invalid.  Callers that share the device with other
+ *     streams read the status word after such calls.
  *
  * Fixed model shape: hidden 2048, 256 routed experts, top-8, expert
  * intermediate 512, one shared expert with intermediate 512.  A routed
@@ -52,6 +61,7 @@ extern "C" {
 #define LRMOE_STATUS_BAD_EXPERT 1
 #define LRMOE_STATUS_REPEATED_EXPERT 2
 #define LRMOE_STATUS_CODEC_ROW 4
+#define LRMOE_STATUS_TIMEOUT 8  /* a bounded cross-workgroup wait expired: the call's outputs are invalid */
 
 /* Library version string.  No reference counterpart. */
 const char *lrmoe_version(void);
@@ -291,6 +301,14 @@ int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t
 #define LRMOE_STAGE_GATHER 16
 int lrmoe_timing_enable(int mask, int launches);
 int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
+
+/* Measurement support, no reference counterpart: the best time of `reps`
+ * launches of a read-only stream kernel over `bytes` (a multiple of 16) at
+ * the device address `src` (16-byte nontemporal loads, nothing written but
+ * possibly the 4-byte device word `sink`), in *best_ms.  Synchronises on
+ * the stream.  bytes / best_ms is the HBM read rate a weight-streaming
+ * kernel can reach on this device. */
+int lrmoe_read_bandwidth(const void *src, int64_t bytes, int reps, uint32_t *sink, double *best_ms, void *stream);
 
 #ifdef __cplusplus
 }

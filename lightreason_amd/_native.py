@@ -20,6 +20,7 @@ WS_STATUS_OFFSET = 4
 STATUS_BAD_EXPERT = 1
 STATUS_REPEATED_EXPERT = 2
 STATUS_CODEC_ROW = 4
+STATUS_TIMEOUT = 8       # a bounded cross-workgroup wait of the decode kernel expired: outputs invalid
 
 CHAIN_PTRS = 8           # int64 addresses per layer in a chain's layer table
 CHAIN_MAX_LAYERS = 48    # layers per lrmoe_moe_chain call
@@ -50,6 +51,7 @@ _SIGNATURES = {
     "lrmoe_fill_normal_bf16": ([_P, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_int64, _P], _I),
     "lrmoe_timing_enable": ([_I, _I], _I),
     "lrmoe_timing_collect": ([_I, C.POINTER(C.c_double), C.POINTER(_I)], _I),
+    "lrmoe_read_bandwidth": ([_P, C.c_int64, _I, _P, C.POINTER(C.c_double), _P], _I),
 }
 
 STAGE_ROUTE = 1

@@ -5,6 +5,7 @@
 // stream is being captured into a graph.
 #include <vector>
 
+#include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
 namespace lrmoe {
@@ -27,6 +28,31 @@ int stage_index(int stage) {
         if (stage == (1 << i)) return i;
     }
     return -1;
+}
+
+// Read-only stream: every byte of src read once with 16-byte nontemporal
+// loads, 8 in flight per lane; nothing is written unless the xor of all words
+// happens to equal a constant (keeps the loads live).  Measures the HBM read
+// rate a weight-streaming kernel can reach, beside a copy's read + write rate.
+constexpr int kReadThreads = 256;
+constexpr int kReadUnroll = 8;
+
+__global__ __launch_bounds__(kReadThreads) void read_stream(const u32x4* src, int64_t n16, uint32_t* sink) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kReadThreads;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * kReadThreads + threadIdx.x;
+    uint32_t acc = 0u;
+    for (; i + (kReadUnroll - 1) * stride < n16; i += kReadUnroll * stride) {
+        u32x4 v[kReadUnroll];
+#pragma unroll
+        for (int j = 0; j < kReadUnroll; ++j) v[j] = __builtin_nontemporal_load(src + i + j * stride);
+#pragma unroll
+        for (int j = 0; j < kReadUnroll; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    for (; i < n16; i += stride) {
+        const u32x4 v = __builtin_nontemporal_load(src + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
 }
 
 }  // namespace
@@ -96,6 +122,40 @@ int lrmoe_timing_collect(int stage, double* total_ms, int* launches) {
     *total_ms = sum;
     *launches = pairs;
     t.used[i] = 0;
+    return LRMOE_OK;
+}
+
+// Best time of `reps` launches of the read-only stream over `bytes` (a
+// multiple of 16) at `src`; `sink` is 4 bytes of device memory.  Synchronises.
+int lrmoe_read_bandwidth(const void* src, int64_t bytes, int reps, uint32_t* sink, double* best_ms, void* stream) {
+    if (!src || !sink || !best_ms || bytes <= 0 || (bytes & 15) || reps <= 0) return LRMOE_E_ARG;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int device = 0, cus = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return static_cast<int>(err);
+    hipEvent_t start, stop;
+    if ((err = hipEventCreate(&start)) != hipSuccess) return static_cast<int>(err);
+    if ((err = hipEventCreate(&stop)) != hipSuccess) {
+        (void)hipEventDestroy(start);
+        return static_cast<int>(err);
+    }
+    const int64_t n16 = bytes / 16;
+    const dim3 grid(static_cast<unsigned>(8 * cus));
+    double best = 1e30;
+    for (int r = 0; r < reps && err == hipSuccess; ++r) {
+        hipExtLaunchKernelGGL(lrmoe::read_stream, grid, dim3(lrmoe::kReadThreads), 0, s, start, stop, 0,
+                              static_cast<const lrmoe::u32x4*>(src), n16, sink);
+        err = hipGetLastError();
+        if (err == hipSuccess) err = hipEventSynchronize(stop);
+        float ms = 0.0f;
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, start, stop);
+        if (err == hipSuccess && ms < best) best = ms;
+    }
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+    if (err != hipSuccess) return static_cast<int>(err);
+    *best_ms = best;
     return LRMOE_OK;
 }
 

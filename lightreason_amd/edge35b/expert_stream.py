@@ -180,8 +180,13 @@ def expert_table(layer) -> torch.Tensor:
 
 
 def raise_on_bad_routes(workspace: moe.Workspace, message: str) -> None:
-    """Reads the device route status of the last call (a host sync)."""
-    if workspace.status() & (moe._native.STATUS_BAD_EXPERT | moe._native.STATUS_REPEATED_EXPERT):
+    """Reads the device status of the last call (a host sync): ValueError
+    with the reference's message for bad routes, RuntimeError when a
+    bounded wait of the decode kernel expired (the outputs are invalid)."""
+    status = workspace.status()
+    if status & moe._native.STATUS_TIMEOUT:
+        moe.check_status(status, "experts forward")
+    if status & (moe._native.STATUS_BAD_EXPERT | moe._native.STATUS_REPEATED_EXPERT):
         raise ValueError(message)
 
 

@@ -72,6 +72,10 @@ class NativeBf16Gather:
             raise ValueError("src and dst need max_copies entries and count one")
         if self.status.device != destinations.device:
             self.status = torch.zeros(1, dtype=torch.int32, device=destinations.device)
+        else:
+            # Per-copy flag: cleared by a fill kernel on the device's current
+            # stream, the copy's stream (stream-ordered, graph-capturable).
+            self.status.zero_()
         try:
             if policy in ("cpu-tiles", "resident"):
                 _native.call("lrmoe_gather_tiles", pointer(descriptors, torch.int64, "descriptors"),
@@ -89,7 +93,9 @@ class NativeBf16Gather:
             raise RuntimeError(str(exc)) from exc
 
     def codec_rows_seen(self) -> bool:
-        """True when a copy decoded an escape-codec row (reads the device)."""
+        """True when the last copy decoded an escape-codec row (reads the
+        device).  Copies on the "cpu-tiles"/"resident" policies leave it
+        False."""
         return bool(int(self.status.item()) & _native.STATUS_CODEC_ROW)
 
     def stage_primary(self, *args, **kwargs):

@@ -84,6 +84,24 @@ class Workspace:
         word = self.buffer[_native.WS_STATUS_OFFSET:_native.WS_STATUS_OFFSET + 4]
         return int(word.view(torch.int32).item())
 
+    def check(self, what: str = "lrmoe call") -> int:
+        """Raise for the last call's status (reads the device: synchronises):
+        RuntimeError when a bounded wait of the decode kernel expired (its
+        outputs are invalid: some of its workgroups were kept off the GPU),
+        ValueError for bad routes (an expert id outside [0, 256) or a token
+        routed twice to one expert).  Returns the status word otherwise."""
+        return check_status(self.status(), what)
+
+
+def check_status(status: int, what: str = "lrmoe call") -> int:
+    """The mapping of Workspace.check: status bits to exceptions."""
+    if status & _native.STATUS_TIMEOUT:
+        raise RuntimeError(f"{what}: a cross-workgroup wait timed out; the outputs are invalid (the decode kernel "
+                           "needs every workgroup resident: is another kernel running on the device?)")
+    if status & (_native.STATUS_BAD_EXPERT | _native.STATUS_REPEATED_EXPERT):
+        raise ValueError(f"{what}: routes hold an expert id outside [0, 256) or repeat an expert within a token")
+    return status
+
 
 _workspaces: dict = {}
 
@@ -432,9 +450,12 @@ def bucket(indices: torch.Tensor, workspace: Workspace | None = None) -> dict:
 
 
 def moe_experts(hidden: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, expert_ptrs: torch.Tensor, *,
-                out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, workspace: Workspace | None = None,
+                check: bool = False) -> torch.Tensor:
     """Routed experts for given routes (the Transformers experts forward):
-    hidden [T,2048] bf16, indices [T,8] int64, weights [T,8] bf16 -> [T,2048]."""
+    hidden [T,2048] bf16, indices [T,8] int64, weights [T,8] bf16 -> [T,2048].
+    ``check`` reads the status word after the call (a host sync) and raises
+    as Workspace.check does."""
     tokens = hidden.shape[0]
     device = hidden.device
     _check(hidden, "hidden", torch.bfloat16, (tokens, HIDDEN))
@@ -448,15 +469,20 @@ def moe_experts(hidden: torch.Tensor, indices: torch.Tensor, weights: torch.Tens
         _check(out, "out", torch.bfloat16, (tokens, HIDDEN), device)
     _native.call("lrmoe_moe_experts", hidden.data_ptr(), tokens, indices.data_ptr(), weights.data_ptr(),
                  expert_ptrs.data_ptr(), out.data_ptr(), ws.ptr, ws.nbytes, _stream(device))
+    if check:
+        ws.check("moe_experts")
     return out
 
 
 def moe_layer(hidden: torch.Tensor, layer: LayerWeights, *, out: torch.Tensor | None = None,
               indices: torch.Tensor | None = None, weights: torch.Tensor | None = None,
-              logits_in: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+              logits_in: torch.Tensor | None = None, workspace: Workspace | None = None,
+              check: bool = False) -> torch.Tensor:
     """Whole sparse MoE block (router, experts, shared expert); with
     ``layer.norm_weight`` the decoder MLP half: hidden + MoE(RMSNorm(hidden)).
-    ``logits_in`` [T,256] replaces the router GEMV (top-k runs on it)."""
+    ``logits_in`` [T,256] replaces the router GEMV (top-k runs on it).
+    ``check`` reads the status word after the call (a host sync) and raises
+    as Workspace.check does."""
     tokens = hidden.shape[0]
     device = hidden.device
     _check(hidden, "hidden", torch.bfloat16, (tokens, HIDDEN))
@@ -472,6 +498,8 @@ def moe_layer(hidden: torch.Tensor, layer: LayerWeights, *, out: torch.Tensor | 
                  _opt(layer.shared_gate_proj), _opt(layer.shared_up_proj), _opt(layer.shared_down_proj),
                  _opt(layer.shared_expert_gate), _opt(layer.norm_weight), float(layer.eps), out.data_ptr(),
                  _opt(indices), _opt(weights), ws.ptr, ws.nbytes, _stream(device))
+    if check:
+        ws.check("moe_layer")
     return out
 
 
@@ -489,11 +517,14 @@ def chain_table(layers) -> "C.Array":
 
 
 def moe_chain(hidden: torch.Tensor, layers, *, out: torch.Tensor | None = None, indices: torch.Tensor | None = None,
-              weights: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+              weights: torch.Tensor | None = None, workspace: Workspace | None = None,
+              check: bool = False) -> torch.Tensor:
     """Decode (T <= 16) through a stack of MoE layers in persistent launches
     of up to 48 layers each: h = moe_layer(h, layer) for every layer in
     order, with results identical to those successive calls.  ``indices`` /
-    ``weights``, when given, receive every layer's routes ([L, T, 8])."""
+    ``weights``, when given, receive every layer's routes ([L, T, 8]).
+    ``check`` reads the status word after each launch (a host sync) and
+    raises as Workspace.check does."""
     tokens = hidden.shape[0]
     device = hidden.device
     layers = list(layers)
@@ -530,6 +561,8 @@ def moe_chain(hidden: torch.Tensor, layers, *, out: torch.Tensor | None = None, 
                      float(layers[0].eps), dst.data_ptr(),
                      None if indices is None else indices[first].data_ptr(),
                      None if weights is None else weights[first].data_ptr(), ws.ptr, ws.nbytes, _stream(device))
+        if check:
+            ws.check(f"moe_chain layers {first}..{first + len(group) - 1}")
         src = dst
     return out
 

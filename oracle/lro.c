@@ -221,17 +221,16 @@ static uint32_t route_key(uint16_t bits, int expert) {
     return (ordered << 8) | (uint32_t)(255 - expert);
 }
 
-/* Router for one token: logits = bf16(x . Wr^T) (fixed order), softmax in fp32
- * over 256 experts, top-8 by (logit desc, id asc), renormalised over the 8 in
- * fp32 (sequential sum in rank order), weights rounded to bf16.  Indices are
- * written in rank order, like torch.topk(sorted=True). */
-static void route_token(const float *x, const uint16_t *router, uint16_t *logits,
-                        int64_t *indices, uint16_t *weights) {
+/* Top-8 of one token's bf16 router logits, [HF] Qwen3_5MoeTopKRouter.forward
+ * 768-777 after the GEMV: softmax in fp32 over 256 experts, top-8 by (logit
+ * desc, id asc), renormalised over the 8 in fp32 (sequential sum in rank
+ * order), weights rounded to bf16.  Indices are written in rank order, like
+ * torch.topk(sorted=True).  softmax is monotonic, so ranking the logits ranks
+ * the probabilities; its sum runs over 64 partials of 4 terms, then a
+ * butterfly (the device order). */
+static void topk_token(const uint16_t *logits, int64_t *indices, uint16_t *weights) {
     float value[LRO_EXPERTS];
-    for (int e = 0; e < LRO_EXPERTS; ++e) {
-        logits[e] = lro_bf16_round(lro_canon_dot(router + (size_t)e * LRO_HIDDEN, x, LRO_HIDDEN));
-        value[e] = lro_bf16_value(logits[e]);
-    }
+    for (int e = 0; e < LRO_EXPERTS; ++e) value[e] = lro_bf16_value(logits[e]);
     int chosen[LRO_TOPK];
     uint8_t taken[LRO_EXPERTS] = {0};
     for (int k = 0; k < LRO_TOPK; ++k) {
@@ -265,6 +264,23 @@ static void route_token(const float *x, const uint16_t *router, uint16_t *logits
     for (int k = 0; k < LRO_TOPK; ++k) {
         indices[k] = chosen[k];
         weights[k] = lro_bf16_round(prob[k] / sum);
+    }
+}
+
+/* Router for one token: logits = bf16(x . Wr^T) (fixed order), then
+ * topk_token. */
+static void route_token(const float *x, const uint16_t *router, uint16_t *logits,
+                        int64_t *indices, uint16_t *weights) {
+    for (int e = 0; e < LRO_EXPERTS; ++e) {
+        logits[e] = lro_bf16_round(lro_canon_dot(router + (size_t)e * LRO_HIDDEN, x, LRO_HIDDEN));
+    }
+    topk_token(logits, indices, weights);
+}
+
+/* Top-8 on caller logits [tokens, 256] (the decode kernel's logits_in path). */
+void lro_route_logits(const uint16_t *logits, int tokens, int64_t *indices, uint16_t *weights) {
+    for (int t = 0; t < tokens; ++t) {
+        topk_token(logits + (size_t)t * LRO_EXPERTS, indices + (size_t)t * LRO_TOPK, weights + (size_t)t * LRO_TOPK);
     }
 }
 

@@ -67,6 +67,7 @@ def lib() -> C.CDLL:
     so.lro_expert_rows.argtypes = [_P, _P, _P, _P, C.c_int]
     so.lro_expert_block_rows.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int]
     so.lro_route.argtypes = [_P, _P, C.c_int, _P, _P, _P]
+    so.lro_route_logits.argtypes = [_P, C.c_int, _P, _P]
     so.lro_shared_gate.argtypes = [_P, _P, C.c_int, _P]
     so.lro_rmsnorm.argtypes = [_P, _P, C.c_int, C.c_float, _P]
     so.lro_bucket.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P]
@@ -78,7 +79,7 @@ def lib() -> C.CDLL:
     so.lro_codec_unpack.argtypes = [_P, _P, C.c_int64, C.c_int, _P]
     so.lro_codec_unpack.restype = None
     for name in ("lro_fill_normal_bf16", "lro_expert_pair", "lro_expert_rows", "lro_expert_block_rows",
-                 "lro_route", "lro_shared_gate", "lro_rmsnorm", "lro_combine", "lro_moe_layer"):
+                 "lro_route", "lro_route_logits", "lro_shared_gate", "lro_rmsnorm", "lro_combine", "lro_moe_layer"):
         getattr(so, name).restype = None
     return so
 
@@ -206,6 +207,18 @@ def route(x: np.ndarray, router: np.ndarray):
     weights = np.empty((tokens, TOPK), dtype=np.uint16)
     lib().lro_route(_ptr(x), _ptr(router), tokens, _ptr(logits), _ptr(indices), _ptr(weights))
     return logits, indices, weights
+
+
+def route_logits(logits: np.ndarray):
+    """Top-8 with softmax renormalisation of given bf16 logits [T, 256]
+    ([HF] Qwen3_5MoeTopKRouter.forward 768-777 after the GEMV): (indices
+    [T, 8] int64 in rank order, weights [T, 8] bf16 bits)."""
+    logits = np.ascontiguousarray(logits, dtype=np.uint16)
+    tokens = logits.shape[0]
+    indices = np.empty((tokens, TOPK), dtype=np.int64)
+    weights = np.empty((tokens, TOPK), dtype=np.uint16)
+    lib().lro_route_logits(_ptr(logits), tokens, _ptr(indices), _ptr(weights))
+    return indices, weights
 
 
 def shared_gate(x: np.ndarray, gate_weight: np.ndarray) -> np.ndarray:

@@ -84,23 +84,87 @@ class HostExperts:
         return self.cache[e]
 
 
+def _pool():
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    global _POOL
+    if _POOL is None:
+        _POOL = ThreadPoolExecutor(max_workers=max(1, min(16, len(os.sched_getaffinity(0)))))
+    return _POOL
+
+
+_POOL = None
+
+
 def oracle_experts(oracle, x_bits: np.ndarray, indices: np.ndarray, weights_bits: np.ndarray, host: HostExperts,
                    shared=None, sg_bits=None, residual_bits=None) -> np.ndarray:
-    """Routed experts (+ shared, + residual) through the oracle."""
+    """Routed experts (+ shared, + residual) through the oracle.  Each token's
+    result depends only on its own row, routes and weights, so any subset of
+    a batch's tokens gives those tokens' rows of the whole batch's result.
+    The per-pair expert products run on a thread pool (the oracle's ctypes
+    calls release the GIL)."""
     plan = oracle.bucket(indices)
     tokens = x_bits.shape[0]
     y = np.zeros((8 * tokens, 2048), dtype=np.uint16)
+    jobs = []
     for u, e in enumerate(plan["expert"].tolist()):
         gu, dn = host(e)
         for p in range(plan["offset"][u], plan["offset"][u + 1]):
-            t = plan["pair_token"][p]
-            y[p] = oracle.expert_pair(gu[:512], gu[512:], dn, x_bits[t])
+            jobs.append((p, gu, dn, plan["pair_token"][p]))
+
+    def pair(job):
+        p, gu, dn, t = job
+        y[p] = oracle.expert_pair(gu[:512], gu[512:], dn, x_bits[t])
+
+    list(_pool().map(pair, jobs))
     y_shared = None
     if shared is not None:
         g, u_, d = shared
-        y_shared = np.stack([oracle.expert_pair(g, u_, d, x_bits[t]) for t in range(tokens)])
+        y_shared = np.stack(list(_pool().map(lambda t: oracle.expert_pair(g, u_, d, x_bits[t]), range(tokens))))
     return oracle.combine(y, plan["route_pair"], plan["pair_slot"], np.ascontiguousarray(weights_bits),
                           y_shared, sg_bits, residual_bits)
+
+
+def oracle_layer_rows(oracle, layer, x_bits: np.ndarray, host: HostExperts, rows=None, logits_bits=None):
+    """The oracle's sparse MoE block for the tokens ``rows`` (all when None)
+    of the batch ``x_bits`` [T, 2048]: RMSNorm when ``layer.norm_weight`` is
+    set, the router (or top-8 of ``logits_bits`` [T, 256]), routed experts,
+    shared expert and gate, ordered combine and residual.  Returns (out bits
+    [R, 2048], indices [T, 8], weights bits [T, 8]) with the routes of every
+    token, so that they can be compared in full."""
+    norm = layer.norm_weight is not None
+    xin = oracle.rmsnorm(x_bits, to_u16(layer.norm_weight), layer.eps) if norm else x_bits
+    if logits_bits is None:
+        _, idx, wts = oracle.route(xin, to_u16(layer.router))
+    else:
+        idx, wts = oracle.route_logits(logits_bits)
+    sel = np.arange(x_bits.shape[0]) if rows is None else np.asarray(rows)
+    shared = sg = None
+    if layer.shared_down_proj is not None:
+        shared = (to_u16(layer.shared_gate_proj), to_u16(layer.shared_up_proj), to_u16(layer.shared_down_proj))
+        sg = oracle.shared_gate(np.ascontiguousarray(xin[sel]), to_u16(layer.shared_expert_gate))
+    want = oracle_experts(oracle, np.ascontiguousarray(xin[sel]), np.ascontiguousarray(idx[sel]),
+                          np.ascontiguousarray(wts[sel]), host, shared, sg,
+                          np.ascontiguousarray(x_bits[sel]) if norm else None)
+    return want, idx, wts
+
+
+def assert_layer_close(got_bits: np.ndarray, want_bits: np.ndarray, x_bits: np.ndarray | None, what: str = "") -> None:
+    """Output bar of a MoE block.  Without a residual (x_bits None):
+    assert_close_bf16.  With one (out = bf16(h + moe)): every element within
+    1e-2 of its row's MoE magnitude plus one bf16 ulp of the output for the
+    final residual rounding."""
+    if x_bits is None:
+        assert_close_bf16(got_bits, want_bits, what=what)
+        return
+    got, exp_, h = bf16_f32(got_bits), bf16_f32(want_bits), bf16_f32(x_bits)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    moe_scale = np.abs(exp_ - h).max(axis=1, keepdims=True)
+    excess = np.abs(got - exp_) - (1e-2 * moe_scale + 2.0 ** -7 * np.abs(exp_))
+    worst = np.unravel_index(int(np.argmax(excess)), excess.shape)
+    print(f"{what}: worst excess {excess.max():.3e} at {worst}, exact {float((got == exp_).mean()):.3f}")
+    assert excess.max() <= 0, f"{what}: element {worst} off by {np.abs(got - exp_)[worst]:.3e}"
 
 
 def resident_fixture_words():

@@ -139,3 +139,49 @@ def test_install_as_edge35b():
     assert sys.modules["edge35b"] is pkg
     assert fe is fused_experts
     assert sys.modules["edge35b.native_bf16_gather"] is native_bf16_gather
+
+
+def _forged_workspace(status: int):
+    """A workspace whose status word (byte offset WS_STATUS_OFFSET) holds
+    ``status``, in host memory: what a decode call leaves behind."""
+    from lightreason_amd import _native, moe
+
+    ws = moe.Workspace.__new__(moe.Workspace)
+    ws.device = torch.device("cpu")
+    ws.max_tokens = 1
+    ws.buffer = torch.zeros(64, dtype=torch.uint8)
+    ws.buffer[_native.WS_STATUS_OFFSET:_native.WS_STATUS_OFFSET + 4].view(torch.int32)[0] = status
+    return ws
+
+
+def test_status_word_maps_to_errors():
+    """The timeout bit (a bounded cross-workgroup wait of the decode kernel
+    expired) raises RuntimeError on every checked path; bad routes raise the
+    reference's ValueError; a clean word passes."""
+    from lightreason_amd import _native, moe
+
+    assert _native.STATUS_TIMEOUT == 8
+    assert _forged_workspace(0).check() == 0
+    assert _forged_workspace(_native.STATUS_CODEC_ROW).check() == _native.STATUS_CODEC_ROW
+    with pytest.raises(RuntimeError, match="timed out"):
+        _forged_workspace(_native.STATUS_TIMEOUT).check()
+    with pytest.raises(RuntimeError, match="timed out"):   # timeout wins over bad routes
+        _forged_workspace(_native.STATUS_TIMEOUT | _native.STATUS_BAD_EXPERT).check()
+    for bits in (_native.STATUS_BAD_EXPERT, _native.STATUS_REPEATED_EXPERT):
+        with pytest.raises(ValueError, match="expert id"):
+            _forged_workspace(bits).check()
+    # the edge35b validate=True paths (fused_forward, grouped_block,
+    # routed_forward, the patched experts forward) all go through this check
+    with pytest.raises(RuntimeError, match="timed out"):
+        expert_stream.raise_on_bad_routes(_forged_workspace(_native.STATUS_TIMEOUT), "bad routes")
+    with pytest.raises(ValueError, match="^bad routes$"):
+        expert_stream.raise_on_bad_routes(_forged_workspace(_native.STATUS_REPEATED_EXPERT), "bad routes")
+    expert_stream.raise_on_bad_routes(_forged_workspace(0), "bad routes")
+    assert moe.check_status(0) == 0
+
+
+def test_header_declares_the_timeout_bit():
+    from pathlib import Path
+
+    header = (Path(__file__).resolve().parents[1] / "include" / "lrmoe.h").read_text()
+    assert "#define LRMOE_STATUS_TIMEOUT 8" in header

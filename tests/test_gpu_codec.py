@@ -166,6 +166,60 @@ def test_codec_chain_equals_raw_chain(model, codec_bank, tokens, pattern):
     assert ws.status() == 0
 
 
+@pytest.mark.parametrize("tokens", [8, 16])
+@pytest.mark.parametrize("norm,logits", [(True, False), (False, True)])
+def test_codec_layer_against_oracle(model, codec_bank, oracle, host_experts, tokens, norm, logits):
+    """A decode layer reading codec experts (the codec instance runs from 8
+    tokens up) against the oracle on the raw weights: routes bit-exact,
+    output within the layer bar."""
+    from helpers import assert_layer_close, oracle_layer_rows
+    from lightreason_amd.moe import Workspace, moe_layer
+
+    _, packed = _layer_pair(model, codec_bank, norm)
+    x = model.hidden(tokens, step=780 + tokens)
+    lg = (x.float() @ packed.router.float().T).to(torch.bfloat16) if logits else None
+    ws = Workspace(x.device, tokens)
+    idx = torch.empty((tokens, 8), dtype=torch.int64, device=x.device)
+    wts = torch.empty((tokens, 8), dtype=torch.bfloat16, device=x.device)
+    print(f"codec layer vs oracle T={tokens} norm={norm} logits={logits}", flush=True)
+    out = moe_layer(x, packed, indices=idx, weights=wts, logits_in=lg, workspace=ws)
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    xb = to_u16(x)
+    want, o_idx, o_w = oracle_layer_rows(oracle, packed, xb, host_experts,
+                                         logits_bits=None if lg is None else to_u16(lg))
+    np.testing.assert_array_equal(idx.cpu().numpy(), o_idx)
+    np.testing.assert_array_equal(to_u16(wts), o_w)
+    assert_layer_close(to_u16(out), want, xb if norm else None, what=f"codec layer T={tokens}")
+
+
+@pytest.mark.parametrize("tokens", [8, 16])
+def test_codec_chain_against_oracle(model, codec_bank, oracle, host_experts, tokens):
+    """Three chained codec layers (RMSNorm + residual): the chain equals
+    successive codec layer calls bit for bit, and every layer matches the
+    oracle applied to that layer's input."""
+    from helpers import assert_layer_close, oracle_layer_rows
+    from lightreason_amd.moe import Workspace, moe_chain, moe_layer
+
+    _, packed = _layer_pair(model, codec_bank, True)
+    x = model.hidden(tokens, step=790 + tokens)
+    ws = Workspace(x.device, tokens)
+    idx = torch.empty((3, tokens, 8), dtype=torch.int64, device=x.device)
+    print(f"codec chain vs oracle T={tokens}", flush=True)
+    out = moe_chain(x, [packed] * 3, indices=idx, workspace=ws)
+    inputs = [x]
+    for _ in range(3):
+        inputs.append(moe_layer(inputs[-1], packed, workspace=ws))
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    assert torch.equal(out.view(torch.int16), inputs[-1].view(torch.int16))
+    for l in range(3):
+        xb = to_u16(inputs[l])
+        want, o_idx, _ = oracle_layer_rows(oracle, packed, xb, host_experts)
+        np.testing.assert_array_equal(idx[l].cpu().numpy(), o_idx)
+        assert_layer_close(to_u16(inputs[l + 1]), want, xb, what=f"codec chain T={tokens} layer {l}")
+
+
 def test_gather_resident_rows_reference_fixture(device, oracle):
     """edge35b/test_gpu_resident_experts.py:12-57 on lrmoe_gather_tiles: a
     compact row (24 packed tiles, 8 raw ones inline) and a raw row, the

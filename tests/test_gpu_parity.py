@@ -264,3 +264,62 @@ def test_decode_layer_reuses_workspace_and_replays(model, oracle, host_experts):
         torch.cuda.synchronize()
         _check_layer(oracle, host_experts, layer, x, idx_out, w_out, out, f"replay {r}")
         assert ws.status() == 0
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 16])
+@pytest.mark.parametrize("norm", [False, True])
+def test_moe_layer_caller_logits_parity(model, oracle, host_experts, tokens, norm):
+    """The headline step's routing: the decode kernel's top-8 on caller logits
+    (Zipf(1.1) Gumbel logits rounded to bf16, as the T=8 verify workload
+    draws them) against the oracle's top-8 of the same logits.  Indices and
+    weights bit-exact; outputs within the layer bar."""
+    from helpers import assert_layer_close, oracle_layer_rows
+    from lightreason_amd.moe import LayerWeights, Workspace, moe_layer
+
+    base = model.layers[0]
+    layer = LayerWeights(**{**base.__dict__, "norm_weight": base.norm_weight if norm else None})
+    rng = np.random.default_rng(8100 + tokens)
+    ranks = rng.permutation(256) + 1
+    raw = (-1.1 * np.log(ranks)[None, :] + rng.gumbel(size=(tokens, 256))).astype(np.float32)
+    lg_bits = oracle.f32_to_bf16(raw)
+    x = model.hidden(tokens, step=8100 + tokens)
+    lg = from_u16(lg_bits, x.device)
+    ws = Workspace(x.device, tokens)
+    idx_out = torch.empty((tokens, 8), dtype=torch.int64, device=x.device)
+    w_out = torch.empty((tokens, 8), dtype=torch.bfloat16, device=x.device)
+    out = moe_layer(x, layer, indices=idx_out, weights=w_out, logits_in=lg, workspace=ws)
+    torch.cuda.synchronize()
+    assert ws.status() == 0
+    xb = to_u16(x)
+    want, o_idx, o_w = oracle_layer_rows(oracle, layer, xb, host_experts, logits_bits=lg_bits)
+    np.testing.assert_array_equal(idx_out.cpu().numpy(), o_idx)
+    np.testing.assert_array_equal(to_u16(w_out), o_w)
+    assert_layer_close(to_u16(out), want, xb if norm else None, what=f"caller logits T={tokens} norm={norm}")
+
+
+def test_gather_t16_selection_bit_exact(model, device):
+    """C1 at T=16: the unique experts of 16 tokens x 8 distinct uniform
+    experts (about 102 copies, max_copies 128) gathered into staging; every
+    copied byte equals its source, unused staging rows keep the sentinel."""
+    from lightreason_amd.moe import EXPERT_BYTES, EXPERT_ELEMENTS, gather
+
+    rng = np.random.default_rng(16)
+    sel = sorted(set(np.concatenate([rng.choice(256, 8, replace=False) for _ in range(16)]).tolist()))
+    assert 90 <= len(sel) <= 115, len(sel)
+    bank = model.bank
+    staging = torch.full((128, EXPERT_ELEMENTS), 0x5A5A, dtype=torch.int16, device=device)
+    ptrs = bank.expert_ptrs(0).cpu()
+    desc = torch.stack([ptrs[:, 0], torch.full((256,), -1), torch.zeros(256, dtype=torch.int64)], 1)[None]
+    desc = desc.contiguous().to(device)
+    order = rng.permutation(len(sel))             # staging slot of each copy, not in expert order
+    src = torch.tensor(sel + [0] * (128 - len(sel)), dtype=torch.int32, device=device)
+    dst = torch.tensor(order.tolist() + [0] * (128 - len(sel)), dtype=torch.int32, device=device)
+    count = torch.tensor([len(sel)], device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    gather(desc, torch.tensor([staging.data_ptr()], device=device), torch.tensor([EXPERT_BYTES], device=device),
+           src, dst, count, max_copies=128, experts=256, stripes=48, status=status)
+    torch.cuda.synchronize()
+    for i, e in enumerate(sel):
+        assert torch.equal(staging[int(order[i])], bank.bank[0, e].view(torch.int16)), (i, e)
+    assert bool((staging[len(sel):] == 0x5A5A).all())
+    assert int(status.item()) == 0

@@ -308,6 +308,42 @@ def test_router_against_torch(oracle):
     assert np.all(oracle.bf16_to_f32(w) == np.float32(0.125))
 
 
+def test_route_logits_against_torch(oracle):
+    """Top-8 on given logits (the decode layer's logits_in path) against
+    torch CPU softmax + topk + renormalisation on bf16 Zipf(1.1) Gumbel
+    logits, the headline workload's routing input."""
+    tokens = 256
+    rng = np.random.default_rng(77)
+    ranks = rng.permutation(256) + 1
+    raw = (-1.1 * np.log(ranks)[None, :] + rng.gumbel(size=(tokens, 256))).astype(np.float32)
+    logits = oracle.f32_to_bf16(raw)
+    indices, weights = oracle.route_logits(logits)
+    lt = _torch_bf16(logits)
+    probs = torch.softmax(lt.float(), dim=-1)
+    top, t_idx = torch.topk(probs, 8, dim=-1)
+    top = (top / top.sum(dim=-1, keepdim=True)).to(torch.bfloat16).float().numpy()
+    values = oracle.bf16_to_f32(logits)
+    checked = 0
+    for t in range(tokens):
+        row = np.sort(values[t])[::-1]
+        if len(set(row[:9].tolist())) < 9:
+            continue  # equal logits among the top 9: torch's order is not pinned there
+        checked += 1
+        assert indices[t].tolist() == t_idx[t].tolist()   # rank order, not just the set
+        got = oracle.bf16_to_f32(weights[t])
+        assert np.all(np.abs(got - top[t]) <= np.abs(top[t]) * 2 ** -8), (t, got, top[t])
+    assert checked > tokens // 2
+    # equal logits: the lower expert id first, uniform weights
+    idx, w = oracle.route_logits(np.full((1, 256), 0x3F80, dtype=np.uint16))
+    assert idx[0].tolist() == list(range(8)) and np.all(oracle.bf16_to_f32(w) == np.float32(0.125))
+    # -0 ranks with +0; a larger logit wins over a lower id
+    row = np.zeros((1, 256), dtype=np.uint16)
+    row[0, 3] = 0x8000
+    row[0, 200] = 0x3F80
+    idx, _ = oracle.route_logits(row)
+    assert idx[0].tolist() == [200, 0, 1, 2, 3, 4, 5, 6]
+
+
 def test_shared_gate_and_rmsnorm_against_torch(oracle):
     x = oracle.normal_bf16((32, 2048), 12, 1, 1.0)
     gate_w = oracle.normal_bf16((2048,), 12, 2, 0.02)
