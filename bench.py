@@ -347,16 +347,17 @@ def torch_block_rows(model, layer: int, x: torch.Tensor, idx: torch.Tensor, w: t
 
 def parity_gate(model, layer: int, x, out, idx, w, rows, rel: float = 1e-2) -> dict:
     """The bench's own correctness gate for a timed case: sampled output
-    rows against torch_block_rows, each row within `rel` of its max |ref|
-    (elementwise) and in L2."""
+    rows against torch_block_rows, with the tests' output bar (bf16 storage,
+    fp32 accumulation): max |got - ref| <= rel * max |ref| over the sample,
+    and every row's L2 error <= rel of the row's norm.  The fp32 reference
+    skips the bf16 rounding points of the kernel's arithmetic, which the
+    tolerance covers."""
     want = torch_block_rows(model, layer, x, idx, w, rows)
     got = out[list(rows)].float()
-    diff = (got - want).abs()
-    row_max = diff.max(dim=1).values / want.abs().max(dim=1).values.clamp_min(1e-30)
-    row_l2 = (got - want).norm(dim=1) / want.norm(dim=1).clamp_min(1e-30)
-    worst = float(torch.maximum(row_max, row_l2).max())
-    return {"tokens_checked": len(rows), "worst_rel": round(worst, 5), "tolerance": rel,
-            "ok": bool(worst <= rel and torch.isfinite(got).all())}
+    tensor_rel = float((got - want).abs().max() / want.abs().max().clamp_min(1e-30))
+    row_l2 = float(((got - want).norm(dim=1) / want.norm(dim=1).clamp_min(1e-30)).max())
+    return {"tokens_checked": len(rows), "max_rel": round(tensor_rel, 5), "worst_row_l2_rel": round(row_l2, 5),
+            "tolerance": rel, "ok": bool(tensor_rel <= rel and row_l2 <= rel and torch.isfinite(got).all())}
 
 
 # ---- CPU baseline: the reference kernel in a pinned child process ---------------
