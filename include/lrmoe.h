@@ -150,6 +150,27 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
                     uint16_t *out, int64_t *indices_out, uint16_t *weights_out, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* lrmoe_moe_layer for decode sizes (1 <= tokens <= LRMOE_STATIC_MAX_TOKENS)
+ * without a workspace: no counterpart in the reference.  For callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * lrmoe_moe_layer, minus the workspace; the route status word (the
+ * LRMOE_STATUS_* bits of that call) goes to *status_out when status_out (a
+ * device int32) is given.  Its scratch (3 MiB: counters and tagged rows) is
+ * a static device array of the library, one per GPU, held until the process
+ * ends; the first call on a GPU looks up its address and zeroes it with a
+ * kernel on that call's stream.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, or two host threads)
+ * race, as calls sharing one workspace do.  Calls nothing that allocates.
+ * Returns LRMOE_E_ARG for tokens > LRMOE_STATIC_MAX_TOKENS. */
+#define LRMOE_STATIC_MAX_TOKENS 16
+int lrmoe_moe_layer_static(const uint16_t *hidden, int tokens, const uint16_t *router_weight,
+                           const uint16_t *logits_in, const int64_t *expert_ptrs, const int64_t *expert_codec,
+                           const uint16_t *shared_gate_proj, const uint16_t *shared_up_proj,
+                           const uint16_t *shared_down_proj, const uint16_t *shared_expert_gate,
+                           const uint16_t *norm_weight, float eps, uint16_t *out, int64_t *indices_out,
+                           uint16_t *weights_out, int32_t *status_out, void *stream);
+
 /* Several MoE decode layers (tokens <= 16) chained in one persistent launch:
  * h_0 = hidden, h_{l+1} = MoE layer l applied to h_l exactly as
  * lrmoe_moe_layer with that layer's router and weights, out = h_layers

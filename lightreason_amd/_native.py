@@ -22,6 +22,7 @@ STATUS_REPEATED_EXPERT = 2
 STATUS_CODEC_ROW = 4
 STATUS_TIMEOUT = 8       # a bounded cross-workgroup wait of the decode kernel expired: outputs invalid
 
+STATIC_MAX_TOKENS = 16  # tokens per lrmoe_moe_layer_static call
 CHAIN_PTRS = 8           # int64 addresses per layer in a chain's layer table
 CHAIN_MAX_LAYERS = 48    # layers per lrmoe_moe_chain call
 CODEC_TABLE_COLUMNS = 10  # int64 per expert in a decode codec table (4 addresses, 48 flag bytes)
@@ -38,6 +39,7 @@ _SIGNATURES = {
     "lrmoe_moe_experts": ([_P, _I, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_moe_layer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_gather_tiles": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "lrmoe_moe_layer_static": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P], _I),
     "lrmoe_moe_chain": ([_P, _I, _I, _P, C.c_float, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_codec_pack": ([_P, C.c_int64, _I, _P, _P, _P, _P], _I),
     "lrmoe_codec_unpack": ([_P, _P, C.c_int64, _I, _P, _P], _I),

@@ -2,6 +2,8 @@
 // Host-side argument checks happen here; nothing is launched when they fail.
 #include <string.h>
 
+#include <mutex>
+
 #include "lrmoe_internal.h"
 
 namespace {
@@ -31,6 +33,61 @@ int check_device() {
 }
 
 bool bad_tokens(int tokens) { return tokens < 0 || tokens > kMaxTokens; }
+
+// ---- the no-allocation decode layer (lrmoe_moe_layer_static) ----------------
+//
+// Its scratch is this file-scope device array: one copy per GPU, held until the
+// process ends, shared by every call on that GPU (it keeps the last call's
+// counters and tagged rows).  Host code never uses the array's name as an
+// address: the per-device address comes from hipGetSymbolAddress once per
+// device (static_scratch()), and only that address is handed to kernels.
+constexpr size_t kStaticScratchBytes = 3u << 20;  // >= lrmoe::workspace_bytes(16)
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+// Zeroes the scratch on its first use on a device (a fill kernel, not a
+// memset node, so that a caller capturing its first call records a kernel).
+__global__ __launch_bounds__(256) void clear_scratch(uint4* p, size_t n16) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n16; i += static_cast<size_t>(gridDim.x) * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+struct StaticScratch {
+    std::mutex lock;
+    void* ptr[64] = {};     // device address of `scratch`, per device
+    bool cleared[64] = {};  // clear_scratch enqueued on that device
+};
+
+StaticScratch& static_state() {
+    static StaticScratch s;
+    return s;
+}
+
+// The scratch address on the current device, looked up (and the scratch
+// zeroed on `stream`) on the device's first call.
+int static_scratch(void** out, hipStream_t stream) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return static_cast<int>(err);
+    if (device < 0 || device >= 64) return static_cast<int>(hipErrorInvalidDevice);
+    StaticScratch& s = static_state();
+    std::lock_guard<std::mutex> guard(s.lock);
+    if (!s.ptr[device]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return static_cast<int>(err);
+        if (!p) return static_cast<int>(hipErrorInvalidSymbol);
+        s.ptr[device] = p;
+    }
+    if (!s.cleared[device]) {
+        hipLaunchKernelGGL(clear_scratch, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(s.ptr[device]),
+                           kStaticScratchBytes / 16);
+        err = hipGetLastError();
+        if (err != hipSuccess) return static_cast<int>(err);
+        s.cleared[device] = true;
+    }
+    *out = s.ptr[device];
+    return LRMOE_OK;
+}
 
 }  // namespace
 
@@ -206,6 +263,51 @@ int lrmoe_moe_layer(const uint16_t* hidden, int tokens, const uint16_t* router_w
     a.plan = ws.plan;
     a.ws = ws;
     return status_of(lrmoe::launch_experts(a, s));
+}
+
+int lrmoe_moe_layer_static(const uint16_t* hidden, int tokens, const uint16_t* router_weight,
+                           const uint16_t* logits_in, const int64_t* expert_ptrs, const int64_t* expert_codec,
+                           const uint16_t* shared_gate_proj, const uint16_t* shared_up_proj,
+                           const uint16_t* shared_down_proj, const uint16_t* shared_expert_gate,
+                           const uint16_t* norm_weight, float eps, uint16_t* out, int64_t* indices_out,
+                           uint16_t* weights_out, int32_t* status_out, void* stream) {
+    if (tokens < 0 || tokens > LRMOE_STATIC_MAX_TOKENS) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!hidden || !expert_ptrs || !out || (!router_weight == !logits_in)) return LRMOE_E_ARG;
+    const bool any_shared = shared_gate_proj || shared_up_proj || shared_down_proj || shared_expert_gate;
+    const bool all_shared = shared_gate_proj && shared_up_proj && shared_down_proj && shared_expert_gate;
+    if (any_shared && !all_shared) return LRMOE_E_ARG;
+    if (lrmoe::workspace_bytes(LRMOE_STATIC_MAX_TOKENS) > kStaticScratchBytes) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    hipStream_t s = as_stream(stream);
+    void* base = nullptr;
+    if (int e = static_scratch(&base, s)) return e;
+    // The decode layer's scratch (counters, tagged rows) sits at fixed
+    // offsets of a 16-token workspace, whatever the call's token count.
+    const Workspace ws = lrmoe::carve(base, LRMOE_STATIC_MAX_TOKENS);
+    lrmoe::DecodeArgs d{};
+    d.x = hidden;
+    d.norm = norm_weight;
+    d.eps = eps;
+    d.router = logits_in ? nullptr : router_weight;
+    d.logits_in = logits_in;
+    d.shared_expert_gate = shared_expert_gate;
+    d.sh_gate = shared_gate_proj;
+    d.sh_up = shared_up_proj;
+    d.sh_down = shared_down_proj;
+    d.expert_ptrs = expert_ptrs;
+    d.codec = expert_codec;
+    d.out = out;
+    d.indices_out = indices_out;
+    d.weights_out = weights_out;
+    d.logits = ws.dlogits;
+    d.act = ws.dact;
+    d.y = ws.dy;
+    d.sync = ws.sync;
+    d.status = status_out ? status_out : ws.plan.status;
+    d.tokens = tokens;
+    d.residual = norm_weight != nullptr;
+    return status_of(lrmoe::launch_moe_decode(d, s));
 }
 
 int lrmoe_moe_chain(const uint16_t* hidden, int tokens, int layers, const int64_t* layer_table, float eps,

@@ -53,6 +53,14 @@ def test_host_side_queries(lib):
 
 def test_argument_errors_are_reported_before_any_launch(lib):
     null = None
+    # the no-allocation decode layer: sizes beyond its maximum and missing
+    # pointers are rejected on the host
+    assert lib.lrmoe_moe_layer_static(null, 17, null, null, null, null, null, null, null, null, null, 1e-6, null,
+                                      null, null, null, null) == -1
+    assert lib.lrmoe_moe_layer_static(null, 1, null, null, null, null, null, null, null, null, null, 1e-6, null,
+                                      null, null, null, null) == -1
+    assert lib.lrmoe_moe_layer_static(null, 0, null, null, null, null, null, null, null, null, null, 1e-6, null,
+                                      null, null, null, null) == 0
     assert lib.lrmoe_route_topk(null, 1, null, null, null, 1e-6, null, null, null, null, null, null, null, 0,
                                 null) == -1
     assert lib.lrmoe_moe_layer(null, 1, null, null, null, null, null, null, null, null, null, 1e-6, null, null, null,
