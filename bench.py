@@ -557,7 +557,7 @@ def main() -> int:
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=1.0, help="scale of the CPU legs' time budgets")
-    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5 to run besides the headline "
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6 to run besides the headline "
                                                    "(default all)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
@@ -579,7 +579,7 @@ def main() -> int:
         f"in {time.perf_counter() - t0:.1f}s")
     L = args.layers
     aux = max(2, min(10, args.steps // L))  # graph replays of the secondary configs
-    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5"}
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6"}
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
@@ -704,6 +704,49 @@ def main() -> int:
                                             for j in range(min(L, 4))]
                 log(f"[bench] C3 T={T} {'chain' if one_launch else 'per-layer'}: {ms3:.3f} ms/step over {L} layers, "
                     f"{configs[key]['gbs']} GB/s")
+
+    # ---- C6: verify widths (speculative-verify blocks of 1-16 positions) ----
+    if "c6" in only:
+        from lightreason_amd.verify import VerifyGraphs
+
+        sweep = {}
+        for W in (1, 2, 4, 6, 8, 10, 12, 14, 16):
+            lgw = [bf16_from_f64(zipf_logits(W, args.seed * 1000 + 500 + l), device) for l in range(L)]
+            cw = Case(model, W, logits=lgw)
+            uw = cw.unique_counts()
+            msw = bench_case(cw, aux, 1) / L
+            bw = float(np.mean(uw)) * EXPERT_BYTES + SHARED_BYTES
+            sweep[f"t{W}"] = dict(us_per_layer=round(msw * 1e3, 2), unique_experts=round(float(np.mean(uw)), 1),
+                                  gbs=round(bw / (msw * 1e-3) / 1e9, 1), status=cw.status())
+            del cw
+        stacks = {}
+        layers_n = [LayerWeights(**ly.__dict__) for ly in model.layers]
+        vg = VerifyGraphs(layers_n, widths=(4, 8, 12, 16))
+        for W in (4, 8, 12, 16):
+            xw = model.hidden(W, step=700 + W)
+            vg.verify(xw)
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = max(3, aux)
+            start.record()
+            for _ in range(reps):
+                vg.verify(xw)
+            stop.record()
+            torch.cuda.synchronize()
+            msv = start.elapsed_time(stop) / reps
+            idx_v, _ = vg.routes(W)
+            uv = [len(set(i.ravel().tolist())) for i in idx_v.cpu().numpy()]
+            bv = sum(u * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 2 * HIDDEN for u in uv)
+            stacks[f"t{W}"] = dict(ms_per_pass=round(msv, 4), positions_per_s=round(W / (msv * 1e-3), 1),
+                                   gbs=round(bv / (msv * 1e-3) / 1e9, 1), mean_unique=round(float(np.mean(uv)), 1),
+                                   status=vg.status())
+        del vg
+        configs["c6_verify_widths"] = dict(
+            layer_zipf=sweep, stack_40_graphs=stacks,
+            note="layer_zipf: one decode layer per width with Zipf(1.1) Gumbel logits, graph replays rotating over "
+                 "the resident layers; stack_40_graphs: the 40-layer stack (router, RMSNorm, residual) as one "
+                 "captured graph per width (lightreason_amd.verify.VerifyGraphs), one replay per verify pass")
+        log(f"[bench] C6 verify widths: {sweep}; 40-layer graphs {stacks}")
 
     # ---- C5: the decode layers reading tile-codec experts ----
     if "c5" in only:

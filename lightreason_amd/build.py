@@ -3,7 +3,9 @@
 Every source is compiled with -ffp-contract=off (rounding points must match
 the reference's, so only explicit fmaf contracts) and with packed fp32 math
 disabled.  Objects go to lightreason_amd/_build/, the library to
-lightreason_amd/liblrmoe.so.
+lightreason_amd/liblrmoe.so.  `--timeline` builds the measurement variant
+liblrmoe_timeline.so instead (-DLRMOE_TIMELINE: the decode kernel stamps the
+wall clock at its phases; read by lightreason_amd.timeline).
 """
 
 from __future__ import annotations
@@ -19,6 +21,7 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "liblrmoe.so"
+TIMELINE_LIBRARY = PACKAGE / "liblrmoe_timeline.so"
 INCLUDE = PACKAGE.parent / "include"
 ARCH = os.environ.get("LRMOE_ARCH", "gfx950")
 
@@ -46,9 +49,9 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(source: Path) -> Path:
-    obj = BUILD / (source.stem + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(source: Path, build_dir: Path = BUILD, extra=()) -> Path:
+    obj = build_dir / (source.stem + ".o")
+    cmd = [hipcc(), *FLAGS, *extra, "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     stderr = "\n".join(line for line in result.stderr.splitlines() if noise not in line)
@@ -59,18 +62,21 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def build(jobs: int = 4) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int = 4, timeline: bool = False) -> Path:
+    build_dir = BUILD if not timeline else PACKAGE / "_build_timeline"
+    library = LIBRARY if not timeline else TIMELINE_LIBRARY
+    extra = ("-DLRMOE_TIMELINE",) if timeline else ()
+    build_dir.mkdir(exist_ok=True)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(_compile, sources()))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda src: _compile(src, build_dir, extra), sources()))
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, library)
+    return library
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(timeline="--timeline" in sys.argv[1:]))

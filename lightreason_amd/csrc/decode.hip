@@ -47,9 +47,51 @@
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
+// Timeline build (compiled with -DLRMOE_TIMELINE into liblrmoe_timeline.so
+// by `python -m lightreason_amd.build --timeline`; the product library has
+// none of it): thread 0 of every workgroup stamps the 100 MHz wall clock at
+// the phases of a single decode layer into LDS and, at the end, copies the
+// stamps to the buffer given by lrmoe_timeline_set (kTimelineWords per
+// workgroup).  Word 0 launch entry, 1 top-8 in the plan, 2 first item's
+// loads issued (wave 0), 3 plan done, 4 items done, 5 first item's loads
+// issued (wave 7), 6 token rows staged; 8 + 5n the n-th item step: start,
+// its weights in, its inputs in, end, and item code (kind + 1) * 1e6 +
+// slot * 1e3 + tile.
+#ifdef LRMOE_TIMELINE
+__device__ unsigned long long* g_timeline;
+extern "C" int lrmoe_timeline_set(void* p) {
+    return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &p, sizeof(p)));
+}
+#define TL_DECLARE __shared__ unsigned long long tl_stamps[lrmoe::kTimelineWords]
+#define TL(k, thread)                                                                                  \
+    do {                                                                                               \
+        if (threadIdx.x == (thread) && (k) < lrmoe::kTimelineWords) tl_stamps[(k)] = wall_clock64();   \
+    } while (0)
+#define TL_WORD(k, v)                                                                \
+    do {                                                                             \
+        if (threadIdx.x == 0 && (k) < lrmoe::kTimelineWords) tl_stamps[(k)] = (v);   \
+    } while (0)
+#define TL_CLEAR                                                                     \
+    do {                                                                             \
+        if (threadIdx.x < lrmoe::kTimelineWords) tl_stamps[threadIdx.x] = 0ull;      \
+    } while (0)
+#define TL_FLUSH(layer)                                                                                    \
+    do {                                                                                                   \
+        if ((layer) == 0 && g_timeline != nullptr && threadIdx.x < lrmoe::kTimelineWords)                  \
+            g_timeline[blockIdx.x * lrmoe::kTimelineWords + threadIdx.x] = tl_stamps[threadIdx.x];         \
+    } while (0)
+#else
+#define TL_DECLARE
+#define TL(k, thread)
+#define TL_WORD(k, v)
+#define TL_CLEAR
+#define TL_FLUSH(layer)
+#endif
+
 namespace lrmoe {
 namespace {
 
+[[maybe_unused]] constexpr int kTimelineWords = 128;  // timeline build: stamps per workgroup
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxT = kDecodeMaxTokens;
@@ -516,6 +558,9 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
     DecodeSync* sync = a.sync;
+    TL_DECLARE;
+    TL_CLEAR;
+    TL(0, 0);
 
     // ---- 1. every load that depends on nothing, issued first ----
     // In order of need: the caller's logits rows of this wave's tokens
@@ -710,6 +755,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     }
     __syncthreads();
 
+    TL(1, 0);
     // ---- the first item's weights, before the rest of the plan ----
     // Slots are numbered in discovery order (token 0's routes first, in rank
     // order), so a workgroup's first item -- A tile k % 32 of slot
@@ -817,6 +863,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * (kCodec ? (i & 8) + kRawStep[i & 7] : i));
     }
 
+    TL(2, 0);
+    TL(5, 7 * kWave);
     if (block == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
@@ -916,6 +964,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     }
     __syncthreads();
 
+    TL(3, 0);
     const int n_slots = P.n_slots;
     const int first_slot = P.first_slot;
     const int total = (kATiles + kBTiles) * n_slots;          // A and B items
@@ -941,6 +990,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     const uint32_t claim_lanes = wave == 0 ? 1u : 0u;
     int par = 0;              // A partial-sum buffer
     int cpar = 0;             // claim buffer
+    [[maybe_unused]] int tl_step = 0;  // timeline build: steps taken
 
     auto stale_word = [&](uint64_t w) { return tag_of(w) != tag; };
 
@@ -969,6 +1019,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // claimed for the step after kn2; ndec receives kn's tile choice.
     auto step = [&](int kk, int kn, int kn2, uint4* buf, uint4* nbuf, uint32_t dec, uint32_t& ndec,
                     uint32_t& bases) __attribute__((always_inline)) -> int {
+        [[maybe_unused]] const int tl_at = 8 + 5 * tl_step;
+        TL(tl_at, 0);
         const Item it = item_at(kk, total, n_slots, first_slot);
         const Item nx = item_at(kn, total, n_slots, first_slot);
         const Item nx2 = item_at(kn2, total, n_slots, first_slot);
@@ -1001,6 +1053,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         // what it completed.
         __builtin_amdgcn_s_waitcnt(kWaitVm16);
         __builtin_amdgcn_sched_barrier(0);
+        TL(tl_at + 1, 0);
         bases = next_bases;
         if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + (kCodec ? 3 : 2) * G;
         const int m = lane & 15;
@@ -1038,6 +1091,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                                 static_cast<uint32_t>(stg[6]), static_cast<uint32_t>(stg[7]));
             __syncthreads();
         }
+        TL(tl_at + 2, 0);
         // (c) the item itself.
         if (it.kind == 0) {
             const int tok = column_token(s, m < s.count ? m : 0);
@@ -1105,6 +1159,9 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             // No item; the barrier publishes the claim.
             __syncthreads();
         }
+        TL(tl_at + 3, 0);
+        TL_WORD(tl_at + 4, static_cast<unsigned long long>((it.kind + 1) * 1000000 + it.slot * 1000 + it.tile));
+        ++tl_step;
         const int after = P.claim[cpar];
         cpar ^= 1;
         return after;
@@ -1119,6 +1176,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             // Token rows staged while the first weights stream in.
             stage_rows();
             __syncthreads();
+            TL(6, 0);
         }
         // Everything but the first item's 16 loads is complete by now; the
         // wait tells the compiler so, which keeps it from draining the
@@ -1168,6 +1226,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         }
     }
 
+    TL(4, 0);
+    TL_FLUSH(layer);
     // ---- 5. this workgroup's share of the layer is done ----
     __builtin_amdgcn_s_waitcnt(0);  // also the first-item loads of a call without items
     __syncthreads();

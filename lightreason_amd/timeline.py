@@ -1,0 +1,112 @@
+"""Per-workgroup timeline of one decode layer (lrmoe_moe_layer, T <= 16),
+from the timeline build of the library (`python -m lightreason_amd.build
+--timeline`: liblrmoe_timeline.so, whose decode kernel stamps the wall clock
+at its phases).
+
+Runs the workload the benchmark times -- 40 resident seeded layers (seed
+2026), T tokens, with Zipf(1.1) Gumbel logits (T > 1) or the router (T = 1)
+-- twice over the layers so that no call finds its experts in the Infinity
+Cache, stamps every 5th call of the second pass, and prints, per stamped
+call, the median and maximum over workgroups of each phase (microseconds
+from the first workgroup's entry) and per item step the median start, wait
+for the step's weights, wait for its inputs, and end.
+
+Usage: python -m lightreason_amd.timeline [--tokens T] [--layers L]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import sys
+
+import numpy as np
+import torch
+
+from . import _native
+
+WORDS = 128  # stamps per workgroup (kTimelineWords)
+PHASES = (("entry", 0), ("top8", 1), ("first_issued_w0", 2), ("first_issued_w7", 5), ("plan", 3),
+          ("rows_staged", 6), ("end", 4))
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--tokens", type=int, default=8)
+    parser.add_argument("--layers", type=int, default=40)
+    parser.add_argument("--seed", type=int, default=2026)
+    args = parser.parse_args(argv)
+    from .build import TIMELINE_LIBRARY
+    if not TIMELINE_LIBRARY.exists():
+        print(f"{TIMELINE_LIBRARY} is missing: python -m lightreason_amd.build --timeline", file=sys.stderr)
+        return 2
+    _native.LIBRARY = TIMELINE_LIBRARY
+    lib = _native.library()
+    lib.lrmoe_timeline_set.argtypes = [C.c_void_p]
+    lib.lrmoe_timeline_set.restype = C.c_int
+
+    from .moe import Workspace, moe_layer
+    from .synthetic import SyntheticModel
+
+    T, L = args.tokens, args.layers
+    device = torch.device("cuda:0")
+    model = SyntheticModel(layers=L, device=device, seed=args.seed, shared=True, norm="normal")
+    G = torch.cuda.get_device_properties(0).multi_processor_count
+    stamps = torch.zeros(256 * WORDS, dtype=torch.int64, device=device)
+    if lib.lrmoe_timeline_set(C.c_void_p(stamps.data_ptr())) != 0:
+        raise RuntimeError("lrmoe_timeline_set failed")
+    rng_logits = []
+    for l in range(L):
+        if T == 1:
+            rng_logits.append(None)
+            continue
+        rng = np.random.default_rng(args.seed * 1000 + l)
+        ranks = rng.permutation(256) + 1
+        raw = (-1.1 * np.log(ranks)[None, :] + rng.gumbel(size=(T, 256))).astype(np.float32)
+        bits = raw.view(np.uint32).astype(np.uint64)
+        b16 = (((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+        rng_logits.append(torch.from_numpy(b16.view(np.int16)).view(torch.bfloat16).to(device))
+    xs = [model.hidden(T, step=100 + l) for l in range(L)]
+    idx = [torch.empty((T, 8), dtype=torch.int64, device=device) for _ in range(L)]
+    ws = Workspace(device, T)
+    traces = []
+    for rep in range(2):
+        for l in range(L):
+            stamps.zero_()
+            moe_layer(xs[l], model.layers[l], logits_in=rng_logits[l], indices=idx[l], workspace=ws)
+            if rep == 1 and l % 5 == 0:
+                torch.cuda.synchronize()
+                traces.append((l, stamps.view(256, WORDS)[:G].cpu().numpy().astype(np.int64)))
+    torch.cuda.synchronize()
+    ws.check("timeline run")
+    print(f"decode layer T={T} ({'router' if T == 1 else 'Zipf(1.1) logits'}), {G} workgroups; "
+          "times in us from the first workgroup's entry (wall clock, 10 ns)")
+    for l, t in traces:
+        t0 = t[:, 0].min()
+        f = lambda a: np.where(a > 0, (a - t0) / 100.0, np.nan)  # noqa: E731
+        unique = len(set(idx[l].cpu().numpy().ravel().tolist()))
+        print(f"\nlayer {l}: {unique} unique experts")
+        cells = []
+        for name, i in PHASES:
+            v = f(t[:, i])
+            cells.append(f"{name} {np.nanmedian(v):.2f}/{np.nanmax(v):.2f}" if (~np.isnan(v)).any() else f"{name} -")
+        print("  " + " | ".join(cells) + "   (median/max)")
+        for n in range(24):
+            b = 8 + 5 * n
+            if b + 4 >= WORDS:
+                break
+            s0, s1, s2, s3 = (f(t[:, b + i]) for i in range(4))
+            ok = ~np.isnan(s0)
+            if not ok.any():
+                break
+            kinds = (t[ok, b + 4] // 1000000).tolist()
+            names = {1: "A", 2: "B", 3: "C", 0: "-"}
+            mix = ", ".join(f"{names[k]}:{kinds.count(k)}" for k in sorted(set(kinds)))
+            print(f"  step {n:2d}: {int(ok.sum()):3d} wgs  start {np.nanmedian(s0):6.2f}  weights-wait "
+                  f"{np.nanmedian(s1 - s0):5.2f}  input-wait {np.nanmedian(s2 - s1):5.2f} (max {np.nanmax(s2 - s1):5.2f})"
+                  f"  end {np.nanmedian(s3):6.2f} (max {np.nanmax(s3):6.2f})  items {mix}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
