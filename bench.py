@@ -154,6 +154,8 @@ class Case:
         self.out = [torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=device) for _ in self.layer_ids]
         self.idx_all = torch.empty((len(self.layer_ids), tokens, 8), dtype=torch.int64, device=device)
         self.idx = list(self.idx_all)
+        self.wts_all = torch.empty((len(self.layer_ids), tokens, 8), dtype=torch.bfloat16, device=device)
+        self.wts = list(self.wts_all)
         self.logits = logits
         self.chain = chain
         self.one_launch = one_launch
@@ -166,11 +168,12 @@ class Case:
     def run(self):
         if self.one_launch:
             # The whole stack as persistent chain launches (48 layers each).
-            moe_chain(self.x[0], self.layers, out=self.out[-1], indices=self.idx_all, workspace=self.ws)
+            moe_chain(self.x[0], self.layers, out=self.out[-1], indices=self.idx_all, weights=self.wts_all,
+                      workspace=self.ws)
             return
         for j, layer in enumerate(self.layers):
             x = self.out[j - 1] if (self.chain and j > 0) else self.x[j]
-            moe_layer(x, layer, out=self.out[j], indices=self.idx[j],
+            moe_layer(x, layer, out=self.out[j], indices=self.idx[j], weights=self.wts[j],
                       logits_in=None if self.logits is None else self.logits[j], workspace=self.ws)
 
     def run_steps(self, steps: int):
@@ -178,7 +181,7 @@ class Case:
         i % L for call i); for cases without a chain."""
         for i in range(steps):
             j = i % len(self.layers)
-            moe_layer(self.x[j], self.layers[j], out=self.out[j], indices=self.idx[j],
+            moe_layer(self.x[j], self.layers[j], out=self.out[j], indices=self.idx[j], weights=self.wts[j],
                       logits_in=None if self.logits is None else self.logits[j], workspace=self.ws)
 
     def unique_counts(self) -> list[int]:
@@ -325,23 +328,33 @@ def read_peak_gbs(device, nbytes: int = 1 << 30, reps: int = 10) -> float:
 # ---- fp32 parity gates (torch on the GPU; no oracle in the timed legs) -----------
 
 def torch_block_rows(model, layer: int, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, rows) -> torch.Tensor:
-    """fp32 evaluation of the sparse MoE block without RMSNorm for the tokens
-    `rows`, given its routes: sum_k w_k down_e(silu(gate_e x) * up_e x) +
-    sigmoid(x . w_sg) * shared(x).  Matrix-vector products in fp32."""
+    """The sparse MoE block without RMSNorm for the tokens `rows`, given its
+    routes (indices and bf16 weights), in torch on the GPU with the rounding
+    points of the reference's CPU expert kernel and ordered combine: gate,
+    up, SiLU and their product rounded to bf16, the down projection to bf16,
+    then per token over its routes in ascending expert order
+    acc = bf16(acc + bf16(y * w)), plus bf16(sigmoid(bf16(x . w_sg))) times
+    the shared expert.  Matrix-vector products in fp32."""
     f = torch.nn.functional
     ly = model.layers[layer]
-    sg_w = ly.shared_expert_gate.float()
-    s_gate, s_up, s_down = ly.shared_gate_proj.float(), ly.shared_up_proj.float(), ly.shared_down_proj.float()
+
+    def r(t):
+        return t.to(torch.bfloat16).float()
+
+    def expert(gate, up, down, xf):
+        g, u = r(torch.mv(gate.float(), xf)), r(torch.mv(up.float(), xf))
+        return r(torch.mv(down.float(), r(r(f.silu(g)) * u)))
+
     out = []
     for t in rows:
         xf = x[t].float()
         acc = torch.zeros(HIDDEN, dtype=torch.float32, device=x.device)
-        for k in range(8):
+        for k in sorted(range(8), key=lambda k: int(idx[t, k])):
             gu, dn = model.bank.expert(layer, int(idx[t, k]))
-            h = torch.mv(gu.float(), xf)
-            acc += w[t, k].float() * torch.mv(dn.float(), f.silu(h[:INNER]) * h[INNER:])
-        shared = torch.mv(s_down, f.silu(torch.mv(s_gate, xf)) * torch.mv(s_up, xf))
-        out.append(acc + torch.sigmoid(torch.dot(sg_w, xf)) * shared)
+            acc = r(acc + r(expert(gu[:INNER], gu[INNER:], dn, xf) * w[t, k].float()))
+        shared = expert(ly.shared_gate_proj, ly.shared_up_proj, ly.shared_down_proj, xf)
+        gate = r(torch.sigmoid(r(torch.dot(ly.shared_expert_gate.float(), xf))))
+        out.append(r(acc + r(gate * shared)))
     return torch.stack(out)
 
 
@@ -349,9 +362,7 @@ def parity_gate(model, layer: int, x, out, idx, w, rows, rel: float = 1e-2) -> d
     """The bench's own correctness gate for a timed case: sampled output
     rows against torch_block_rows, with the tests' output bar (bf16 storage,
     fp32 accumulation): max |got - ref| <= rel * max |ref| over the sample,
-    and every row's L2 error <= rel of the row's norm.  The fp32 reference
-    skips the bf16 rounding points of the kernel's arithmetic, which the
-    tolerance covers."""
+    and every row's L2 error <= rel of the row's norm."""
     want = torch_block_rows(model, layer, x, idx, w, rows)
     got = out[list(rows)].float()
     tensor_rel = float((got - want).abs().max() / want.abs().max().clamp_min(1e-30))
@@ -597,7 +608,7 @@ def main() -> int:
     logits = [bf16_from_f64(zipf_logits(8, args.seed * 1000 + l), device) for l in range(L)]
     c2 = Case(model, 8, logits=logits)
     uniques = c2.unique_counts()
-    gate2 = parity_gate(model, 0, c2.x[0], c2.out[0], c2.idx[0], _routing_weights(c2, 0), range(8))
+    gate2 = parity_gate(model, 0, c2.x[0], c2.out[0], c2.idx[0], c2.wts[0], range(8))
     log(f"[bench] C2 parity gate (fp32 torch, layer 0, 8 tokens): {gate2}")
     warm_graph = capture(lambda: c2.run_steps(args.warmup)) if args.warmup else None
     step_graph = capture(lambda: c2.run_steps(args.steps))
@@ -813,7 +824,7 @@ def main() -> int:
         for start in range(0, len(hot_tokens), 128):
             sample |= {int(hot_tokens[p]) for p in (start - 1, start, start + 64) if 0 <= p < len(hot_tokens)}
         rows = sorted(sample)
-        gate4 = parity_gate(model, 0, c4.x[0], c4.out[0], c4.idx[0], _routing_weights(c4, 0), rows)
+        gate4 = parity_gate(model, 0, c4.x[0], c4.out[0], c4.idx[0], c4.wts[0], rows)
         log(f"[bench] C4 parity gate (fp32 torch, {len(rows)} tokens): {gate4}")
         ms4 = bench_case(c4, 3, 1) / len(layer_ids)
         statuses["c4"] = c4.status()
@@ -880,15 +891,6 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
-
-
-def _routing_weights(case: Case, j: int) -> torch.Tensor:
-    """Routing weights of layer j's last call: the top-8 of its logits as the
-    kernel computed them (recomputed here from the logits in fp32, which
-    the gate's tolerance covers)."""
-    lg = case.logits[j].float()
-    top = torch.softmax(lg, dim=-1).gather(1, case.idx[j])
-    return top / top.sum(dim=-1, keepdim=True)
 
 
 if __name__ == "__main__":
