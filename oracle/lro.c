@@ -544,3 +544,221 @@ void lro_codec_unpack(const uint8_t *packed, const uint8_t *bases, int64_t rows,
         }
     }
 }
+
+/* ---- Gated DeltaNet decode ---------------------------------------------------
+ *
+ * The single-step linear-attention mixer of the 35B runner's Gated DeltaNet
+ * layers ([HF] Qwen3_5MoeGatedDeltaNet.forward 430-543 with a cached state)
+ * with the recurrence of edge35b/delta_decode.py:11-36 (_delta: one token at
+ * a time, the state rounded to the cache dtype after every token).  Floating
+ * point throughout: sums run in ascending index order in fp32. */
+
+/* [HF] l2norm 243-247 on a bf16 vector: every op rounds to bf16 (x*x, the
+ * sum, + eps, rsqrt, x * inv). */
+static void l2norm_bf16(const uint16_t *x, int n, float *out) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        float v = lro_bf16_value(x[i]);
+        sum += rbf(v * v);
+    }
+    float s = rbf(rbf(sum) + 1e-6f);
+    float inv = rbf(1.0f / sqrtf(s));
+    for (int i = 0; i < n; ++i) out[i] = rbf(lro_bf16_value(x[i]) * inv);
+}
+
+static float state_get(const void *s, int bf16, size_t i) {
+    return bf16 ? lro_bf16_value(((const uint16_t *)s)[i]) : ((const float *)s)[i];
+}
+
+static void state_put(void *s, int bf16, size_t i, float v) {
+    if (bf16) ((uint16_t *)s)[i] = lro_bf16_round(v);
+    else ((float *)s)[i] = v;
+}
+
+/* The gated delta rule over T tokens and H heads (edge35b/delta_decode.py:
+ * 11-36 _delta, 38-55 _run): q, k [T][H][D] bf16; v [T][H][E] bf16;
+ * G [T][H] fp32 (= exp(g)); beta [T][H] bf16; state_in [H][D][E] (fp32, or
+ * bf16 when state_bf16).  normalize: q and k through l2norm first.  Per
+ * token and head: state *= G; mem[e] = sum_d state[d][e] k[d]; delta[e] =
+ * (v[e] - mem[e]) beta; state[d][e] += k[d] delta[e]; out[e] = sum_d
+ * state[d][e] (q[d] D^-1/2), stored as bf16; then the state is rounded to
+ * its dtype.  states_out [T][H][D][E] with record, else [H][D][E] (the
+ * final state), in the state dtype. */
+void lro_delta_rule(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *G, const uint16_t *beta,
+                    const void *state_in, int state_bf16, int T, int H, int D, int E, int normalize, int record,
+                    uint16_t *out, void *states_out) {
+    float *state = (float *)malloc(sizeof(float) * (size_t)D * E);
+    float *qf = (float *)malloc(sizeof(float) * D);
+    float *kf = (float *)malloc(sizeof(float) * D);
+    float *mem = (float *)malloc(sizeof(float) * E);
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int h = 0; h < H; ++h) {
+        for (size_t i = 0; i < (size_t)D * E; ++i) state[i] = state_get(state_in, state_bf16, (size_t)h * D * E + i);
+        for (int t = 0; t < T; ++t) {
+            const uint16_t *qt = q + ((size_t)t * H + h) * D;
+            const uint16_t *kt = k + ((size_t)t * H + h) * D;
+            const uint16_t *vt = v + ((size_t)t * H + h) * E;
+            if (normalize) {
+                l2norm_bf16(qt, D, qf);
+                l2norm_bf16(kt, D, kf);
+            } else {
+                for (int d = 0; d < D; ++d) qf[d] = lro_bf16_value(qt[d]), kf[d] = lro_bf16_value(kt[d]);
+            }
+            for (int d = 0; d < D; ++d) qf[d] = qf[d] * scale;
+            const float g = G[(size_t)t * H + h];
+            const float b = lro_bf16_value(beta[(size_t)t * H + h]);
+            for (size_t i = 0; i < (size_t)D * E; ++i) state[i] = state[i] * g;
+            for (int e = 0; e < E; ++e) {
+                float m = 0.0f;
+                for (int d = 0; d < D; ++d) m += state[(size_t)d * E + e] * kf[d];
+                mem[e] = (lro_bf16_value(vt[e]) - m) * b;
+            }
+            for (int d = 0; d < D; ++d)
+                for (int e = 0; e < E; ++e) state[(size_t)d * E + e] = state[(size_t)d * E + e] + kf[d] * mem[e];
+            for (int e = 0; e < E; ++e) {
+                float o = 0.0f;
+                for (int d = 0; d < D; ++d) o += state[(size_t)d * E + e] * qf[d];
+                out[((size_t)t * H + h) * E + e] = lro_bf16_round(o);
+            }
+            if (state_bf16)
+                for (size_t i = 0; i < (size_t)D * E; ++i) state[i] = rbf(state[i]);
+            if (record)
+                for (size_t i = 0; i < (size_t)D * E; ++i)
+                    state_put(states_out, state_bf16, (((size_t)t * H + h) * D) * E + i, state[i]);
+        }
+        if (!record)
+            for (size_t i = 0; i < (size_t)D * E; ++i) state_put(states_out, state_bf16, (size_t)h * D * E + i, state[i]);
+    }
+    free(state);
+    free(qf);
+    free(kf);
+    free(mem);
+}
+
+#define LRO_DN_KH 16      /* key heads */
+#define LRO_DN_VH 32      /* value heads */
+#define LRO_DN_D 128      /* key / value head width */
+#define LRO_DN_KEY (LRO_DN_KH * LRO_DN_D)     /* 2048 */
+#define LRO_DN_VAL (LRO_DN_VH * LRO_DN_D)     /* 4096 */
+#define LRO_DN_CONV (2 * LRO_DN_KEY + LRO_DN_VAL)  /* 8192 */
+#define LRO_DN_K 4        /* conv kernel */
+
+static inline float silu_f(float x) { return x / (1.0f + lro_exp(-x)); }
+static inline float softplus_f(float x) { return x > 20.0f ? x : log1pf(lro_exp(x)); }
+
+/* The Gated DeltaNet mixer for T tokens with a cached state ([HF]
+ * Qwen3_5MoeGatedDeltaNet.forward 430-543; dims of the 35B model: 16 key
+ * heads, 32 value heads, width 128, conv kernel 4):
+ *   mixed = bf16(x W_qkv^T), z = bf16(x W_z^T), b = bf16(x W_b^T),
+ *   a = bf16(x W_a^T) (fixed fp32 order, lro_canon_dot);
+ *   per channel c the sequence [conv_state[c][0..3], mixed[0..T-1][c]],
+ *   token t: bf16(silu(bf16(sum_j w[c][j] seq[t + 1 + j]))) (causal_conv1d
+ *   201-218 / 221-240 with the cached left context), conv_state <- the last
+ *   4 of the sequence;
+ *   q = channels 0..2047 (16 heads), k = 2048..4095, v = 4096..8191 (32
+ *   heads); value head h reads key head h / 2 (repeat_interleave);
+ *   beta = bf16(sigmoid(b)); g = -exp(A_log) softplus(a + dt_bias) in fp32,
+ *   G = exp(g);
+ *   lro_delta_rule(normalize = 1) on the cached state (fp32 or bf16);
+ *   per token and value head the gated RMSNorm (Qwen3_5MoeRMSNormGated
+ *   169-185): n = bf16(o rsqrt(mean(o^2) + eps)), bf16(bf16(w n) silu(z));
+ *   out = bf16(normed W_out^T) (fixed fp32 order over 4096).
+ * conv_state [8192][4] and state [32][128][128] are updated in place;
+ * states_record ([T][32][128][128], state dtype) may be NULL. */
+void lro_delta_mixer(const uint16_t *x, int T, const uint16_t *w_qkv, const uint16_t *w_z, const uint16_t *w_b,
+                     const uint16_t *w_a, const uint16_t *conv_w, const uint16_t *A_log, const uint16_t *dt_bias,
+                     const uint16_t *norm_w, float eps, const uint16_t *w_out, uint16_t *conv_state, void *state,
+                     int state_bf16, void *states_record, uint16_t *out) {
+    const size_t H = LRO_HIDDEN;
+    uint16_t *mixed = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_CONV);
+    uint16_t *z = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    uint16_t *bb = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VH);
+    uint16_t *aa = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VH);
+    float *xf = (float *)malloc(sizeof(float) * LRO_DN_VAL);
+    for (int t = 0; t < T; ++t) {
+        to_floats(x + t * H, xf, (int)H);
+        for (int r = 0; r < LRO_DN_CONV; ++r) mixed[(size_t)t * LRO_DN_CONV + r] = lro_bf16_round(lro_canon_dot(w_qkv + r * H, xf, (int)H));
+        for (int r = 0; r < LRO_DN_VAL; ++r) z[(size_t)t * LRO_DN_VAL + r] = lro_bf16_round(lro_canon_dot(w_z + r * H, xf, (int)H));
+        for (int r = 0; r < LRO_DN_VH; ++r) bb[t * LRO_DN_VH + r] = lro_bf16_round(lro_canon_dot(w_b + r * H, xf, (int)H));
+        for (int r = 0; r < LRO_DN_VH; ++r) aa[t * LRO_DN_VH + r] = lro_bf16_round(lro_canon_dot(w_a + r * H, xf, (int)H));
+    }
+    /* causal conv with the cached context, SiLU */
+    uint16_t *act = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_CONV);
+    float *seq = (float *)malloc(sizeof(float) * (LRO_DN_K + T));
+    uint16_t *seqb = (uint16_t *)malloc(sizeof(uint16_t) * (LRO_DN_K + T));
+    for (int c = 0; c < LRO_DN_CONV; ++c) {
+        for (int j = 0; j < LRO_DN_K; ++j) seqb[j] = conv_state[c * LRO_DN_K + j];
+        for (int t = 0; t < T; ++t) seqb[LRO_DN_K + t] = mixed[(size_t)t * LRO_DN_CONV + c];
+        for (int i = 0; i < LRO_DN_K + T; ++i) seq[i] = lro_bf16_value(seqb[i]);
+        for (int t = 0; t < T; ++t) {
+            float acc = 0.0f;
+            for (int j = 0; j < LRO_DN_K; ++j) acc = fmaf(lro_bf16_value(conv_w[c * LRO_DN_K + j]), seq[t + 1 + j], acc);
+            act[(size_t)t * LRO_DN_CONV + c] = lro_bf16_round(silu_f(rbf(acc)));
+        }
+        for (int j = 0; j < LRO_DN_K; ++j) conv_state[c * LRO_DN_K + j] = seqb[T + j];
+    }
+    /* q, k (value heads' copies), v, beta, G */
+    uint16_t *q = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    uint16_t *k = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    uint16_t *v = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    uint16_t *beta = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VH);
+    float *G = (float *)malloc(sizeof(float) * T * LRO_DN_VH);
+    for (int t = 0; t < T; ++t) {
+        const uint16_t *row = act + (size_t)t * LRO_DN_CONV;
+        for (int h = 0; h < LRO_DN_VH; ++h) {
+            for (int d = 0; d < LRO_DN_D; ++d) {
+                q[((size_t)t * LRO_DN_VH + h) * LRO_DN_D + d] = row[(h / 2) * LRO_DN_D + d];
+                k[((size_t)t * LRO_DN_VH + h) * LRO_DN_D + d] = row[LRO_DN_KEY + (h / 2) * LRO_DN_D + d];
+                v[((size_t)t * LRO_DN_VH + h) * LRO_DN_D + d] = row[2 * LRO_DN_KEY + h * LRO_DN_D + d];
+            }
+            const float bv = lro_bf16_value(bb[t * LRO_DN_VH + h]);
+            beta[t * LRO_DN_VH + h] = lro_bf16_round(1.0f / (1.0f + lro_exp(-bv)));
+            const float gv = -lro_exp(lro_bf16_value(A_log[h])) *
+                             softplus_f(lro_bf16_value(aa[t * LRO_DN_VH + h]) + lro_bf16_value(dt_bias[h]));
+            G[t * LRO_DN_VH + h] = lro_exp(gv);
+        }
+    }
+    uint16_t *core = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    const size_t state_elems = (size_t)LRO_DN_VH * LRO_DN_D * LRO_DN_D;
+    const size_t esz = state_bf16 ? 2 : 4;
+    void *rec = states_record ? states_record : malloc(esz * state_elems * T);
+    lro_delta_rule(q, k, v, G, beta, state, state_bf16, T, LRO_DN_VH, LRO_DN_D, LRO_DN_D, 1, 1, core, rec);
+    memcpy(state, (const char *)rec + esz * state_elems * (T - 1), esz * state_elems);
+    if (!states_record) free(rec);
+    /* gated RMSNorm per token and value head */
+    uint16_t *normed = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_DN_VAL);
+    for (int t = 0; t < T; ++t) {
+        for (int h = 0; h < LRO_DN_VH; ++h) {
+            const uint16_t *o = core + ((size_t)t * LRO_DN_VH + h) * LRO_DN_D;
+            float var = 0.0f;
+            for (int e = 0; e < LRO_DN_D; ++e) var += lro_bf16_value(o[e]) * lro_bf16_value(o[e]);
+            var = var / (float)LRO_DN_D;
+            const float r = 1.0f / sqrtf(var + eps);
+            for (int e = 0; e < LRO_DN_D; ++e) {
+                const float n = rbf(lro_bf16_value(o[e]) * r);
+                const float wn = rbf(lro_bf16_value(norm_w[e]) * n);
+                const float zz = lro_bf16_value(z[(size_t)t * LRO_DN_VAL + h * LRO_DN_D + e]);
+                normed[(size_t)t * LRO_DN_VAL + h * LRO_DN_D + e] = lro_bf16_round(wn * silu_f(zz));
+            }
+        }
+    }
+    for (int t = 0; t < T; ++t) {
+        to_floats(normed + (size_t)t * LRO_DN_VAL, xf, LRO_DN_VAL);
+        for (size_t r = 0; r < H; ++r) out[t * H + r] = lro_bf16_round(lro_canon_dot(w_out + r * LRO_DN_VAL, xf, LRO_DN_VAL));
+    }
+    free(normed);
+    free(core);
+    free(G);
+    free(beta);
+    free(v);
+    free(k);
+    free(q);
+    free(seqb);
+    free(seq);
+    free(act);
+    free(xf);
+    free(aa);
+    free(bb);
+    free(z);
+    free(mixed);
+}

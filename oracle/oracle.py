@@ -74,6 +74,11 @@ def lib() -> C.CDLL:
     so.lro_bucket.restype = C.c_int
     so.lro_combine.argtypes = [_P, _P, _P, _P, _P, _P, _P, C.c_int, _P]
     so.lro_moe_layer.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P]
+    so.lro_delta_rule.argtypes = [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                  C.c_int, _P, _P]
+    so.lro_delta_rule.restype = None
+    so.lro_delta_mixer.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, C.c_int, _P, _P]
+    so.lro_delta_mixer.restype = None
     so.lro_codec_pack.argtypes = [_P, C.c_int64, C.c_int, _P, _P]
     so.lro_codec_pack.restype = C.c_int64
     so.lro_codec_unpack.argtypes = [_P, _P, C.c_int64, C.c_int, _P]
@@ -271,6 +276,56 @@ def moe_layer(x, router, gate_up, down, shared=None, norm_weight=None, eps: floa
                         _ptr(sg_proj), _ptr(su_proj), _ptr(sd_proj), _ptr(sgate), _ptr(norm_weight), float(eps),
                         _ptr(out), _ptr(indices), _ptr(weights))
     return out, indices, weights
+
+
+# ---- Gated DeltaNet decode (linear-attention mixer) ------------------------
+
+DN_KEY_HEADS, DN_VALUE_HEADS, DN_WIDTH, DN_CONV_K = 16, 32, 128, 4
+DN_CONV = 2 * DN_KEY_HEADS * DN_WIDTH + DN_VALUE_HEADS * DN_WIDTH   # 8192 channels
+
+
+def delta_rule(q, k, v, G, beta, state, *, normalize: bool, record: bool):
+    """edge35b/delta_decode.py:11-55 restated (lro_delta_rule): q, k [T, H, D]
+    and v [T, H, E] bf16 bits, G [T, H] float32 (= exp(g)), beta [T, H] bf16
+    bits, state [H, D, E] float32 or bf16 bits (uint16).  Returns (out [T, H,
+    E] bf16 bits, states [T or 1, H, D, E] in the state's dtype)."""
+    q, k, v, beta = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v, beta))
+    G = np.ascontiguousarray(G, dtype=np.float32)
+    state = np.ascontiguousarray(state)
+    bf16_state = state.dtype == np.uint16
+    if not bf16_state and state.dtype != np.float32:
+        raise ValueError("state must be float32 or bf16 bits")
+    T, H, D = q.shape
+    E = v.shape[-1]
+    out = np.empty((T, H, E), dtype=np.uint16)
+    states = np.empty((T if record else 1, H, D, E), dtype=state.dtype)
+    lib().lro_delta_rule(_ptr(q), _ptr(k), _ptr(v), _ptr(G), _ptr(beta), _ptr(state), int(bf16_state), T, H, D, E,
+                         int(normalize), int(record), _ptr(out), _ptr(states))
+    return out, states
+
+
+def delta_mixer(x, weights: dict, conv_state, state, eps: float = 1e-6, record: bool = False):
+    """The Gated DeltaNet mixer step for x [T, 2048] (lro_delta_mixer).
+    weights: in_proj_qkv [8192, 2048], in_proj_z [4096, 2048], in_proj_b and
+    in_proj_a [32, 2048], conv1d [8192, 4], A_log [32], dt_bias [32], norm
+    [128], out_proj [2048, 4096], all bf16 bits.  conv_state [8192, 4] bf16
+    bits and state [32, 128, 128] (float32 or bf16 bits) are copied; returns
+    (out [T, 2048], new conv_state, new state, per-token states or None)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    T = x.shape[0]
+    w = {name: np.ascontiguousarray(weights[name], dtype=np.uint16)
+         for name in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "conv1d", "A_log", "dt_bias", "norm",
+                      "out_proj")}
+    conv = np.array(conv_state, dtype=np.uint16, copy=True, order="C")
+    st = np.array(state, copy=True, order="C")
+    bf16_state = st.dtype == np.uint16
+    rec = np.empty((T, DN_VALUE_HEADS, DN_WIDTH, DN_WIDTH), dtype=st.dtype) if record else None
+    out = np.empty((T, HIDDEN), dtype=np.uint16)
+    lib().lro_delta_mixer(_ptr(x), T, _ptr(w["in_proj_qkv"]), _ptr(w["in_proj_z"]), _ptr(w["in_proj_b"]),
+                          _ptr(w["in_proj_a"]), _ptr(w["conv1d"]), _ptr(w["A_log"]), _ptr(w["dt_bias"]),
+                          _ptr(w["norm"]), float(eps), _ptr(w["out_proj"]), _ptr(conv), _ptr(st), int(bf16_state),
+                          _ptr(rec), _ptr(out))
+    return out, conv, st, rec
 
 
 CODEC_TILE = 256
