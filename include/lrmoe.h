@@ -320,6 +320,10 @@ int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t
 #define LRMOE_STAGE_DOWN 4
 #define LRMOE_STAGE_COMBINE 8
 #define LRMOE_STAGE_GATHER 16
+#define LRMOE_STAGE_LAYER 32       /* lrmoe_moe_layer / lrmoe_moe_chain decode kernel */
+#define LRMOE_STAGE_DELTA_IN 64    /* lrmoe_delta_mixer: in_proj + conv */
+#define LRMOE_STAGE_DELTA_RULE 128 /* lrmoe_delta_rule, and the rule inside lrmoe_delta_mixer */
+#define LRMOE_STAGE_DELTA_OUT 256  /* lrmoe_delta_mixer: gated RMSNorm + out_proj */
 int lrmoe_timing_enable(int mask, int launches);
 int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
 
@@ -330,6 +334,57 @@ int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
  * the stream.  bytes / best_ms is the HBM read rate a weight-streaming
  * kernel can reach on this device. */
 int lrmoe_read_bandwidth(const void *src, int64_t bytes, int reps, uint32_t *sink, double *best_ms, void *stream);
+
+/* ---- Gated DeltaNet decode (the linear-attention mixer before each of the
+ * 30 linear-attention layers' MoE) ------------------------------------------ */
+
+/* The gated delta rule over a block of `tokens` tokens and `heads` heads,
+ * the recurrence of edge35b/delta_decode.py:11-36 (_delta) with the calling
+ * convention of :38-55 (_run): q, k [tokens][heads][key_width] bf16 (value
+ * head h reads q/k head h; repeat grouped key heads before the call),
+ * v [tokens][heads][value_width] bf16, G [tokens][heads] fp32 = exp(g),
+ * beta [tokens][heads] bf16, initial [heads][key_width][value_width] fp32
+ * (state_bf16 = 0) or bf16.  normalize != 0 applies l2norm to q and k first
+ * (Transformers l2norm on bf16: every step rounded).  Per token and head:
+ * state *= G; delta = (v - state^T k) beta; state += k delta^T;
+ * out = bf16(state^T q / sqrt(key_width)); the state is rounded to its dtype
+ * after every token.  record != 0: states [tokens][heads][kw][vw] receives
+ * the state after every token; else states [heads][kw][vw] the final state
+ * (states may equal initial then: updated in place).  key_width 64, 128 or
+ * 256, value_width a multiple of 16; q, k 16-byte aligned (8 for width 64),
+ * v and out 8-byte, initial and states 16-byte aligned. */
+int lrmoe_delta_rule(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *G, const uint16_t *beta,
+                     const void *initial, int state_bf16, int tokens, int heads, int key_width, int value_width,
+                     int normalize, int record, uint16_t *out, void *states, void *stream);
+
+/* Bytes of workspace lrmoe_delta_mixer needs for `tokens` tokens (1..16;
+ * 0 outside that range).  No reference counterpart. */
+#define LRMOE_DELTA_MAX_TOKENS 16
+size_t lrmoe_delta_workspace_bytes(int tokens);
+
+/* One cached step of the Gated DeltaNet mixer of the 35B model (hidden 2048,
+ * 16 key heads and 32 value heads of width 128, conv kernel 4) for 1..16
+ * tokens that follow the cached state: [HF] Qwen3_5MoeGatedDeltaNet.forward
+ * 430-543 with cache_params holding a previous state, the short-block path
+ * that edge35b/delta_decode.py:84-126 (fused_delta) routes through its
+ * _delta kernel, and the single-token step that edge35b/packed_native.py:
+ * 96-149 (mixer_graphs) replays.  Weights as the module holds them, bf16:
+ * in_proj_qkv [8192][2048], in_proj_z [4096][2048], in_proj_b and in_proj_a
+ * [32][2048], conv_weight [8192][4] (conv1d.weight without its middle
+ * axis), A_log, dt_bias [32], norm_weight [128], out_proj [2048][4096].
+ * conv_state [8192][4] bf16 and state [32][128][128] (fp32, or bf16 when
+ * state_bf16) are updated in place.  conv_record [tokens][8192][4] and
+ * state_record [tokens][32][128][128] (may be NULL) receive both states
+ * after every token, for rolling back to an accepted prefix.  out
+ * [tokens][2048] bf16.  Workspace of lrmoe_delta_workspace_bytes(tokens),
+ * 256-byte aligned.  Rounding points: those of the Transformers forward in
+ * bf16 (see lrmoe_delta_rule for the recurrence). */
+int lrmoe_delta_mixer(const uint16_t *hidden, int tokens, const uint16_t *in_proj_qkv, const uint16_t *in_proj_z,
+                      const uint16_t *in_proj_b, const uint16_t *in_proj_a, const uint16_t *conv_weight,
+                      const uint16_t *A_log, const uint16_t *dt_bias, const uint16_t *norm_weight, float eps,
+                      const uint16_t *out_proj, uint16_t *conv_state, void *state, int state_bf16,
+                      uint16_t *conv_record, void *state_record, uint16_t *out, void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,10 @@ _SIGNATURES = {
     "lrmoe_timing_enable": ([_I, _I], _I),
     "lrmoe_timing_collect": ([_I, C.POINTER(C.c_double), C.POINTER(_I)], _I),
     "lrmoe_read_bandwidth": ([_P, C.c_int64, _I, _P, C.POINTER(C.c_double), _P], _I),
+    "lrmoe_delta_workspace_bytes": ([_I], C.c_size_t),
+    "lrmoe_delta_rule": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
+    "lrmoe_delta_mixer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _I, _P, _P, _P, _P,
+                           C.c_size_t, _P], _I),
 }
 
 STAGE_ROUTE = 1
@@ -62,6 +66,10 @@ STAGE_DOWN = 4
 STAGE_COMBINE = 8
 STAGE_GATHER = 16
 STAGE_LAYER = 32
+STAGE_DELTA_IN = 64
+STAGE_DELTA_RULE = 128
+STAGE_DELTA_OUT = 256
+DELTA_MAX_TOKENS = 16    # tokens per lrmoe_delta_mixer call
 
 
 class NativeError(RuntimeError):

@@ -34,6 +34,9 @@ int check_device() {
 
 bool bad_tokens(int tokens) { return tokens < 0 || tokens > kMaxTokens; }
 
+// A non-null pointer that is not a multiple of `bytes`.
+bool misaligned(const void* p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) != 0; }
+
 // ---- the no-allocation decode layer (lrmoe_moe_layer_static) ----------------
 //
 // Its scratch is this file-scope device array: one copy per GPU, held until the
@@ -454,6 +457,86 @@ int lrmoe_fill_normal_bf16(uint16_t* out, int64_t count, uint64_t seed, uint64_t
     if (count == 0) return LRMOE_OK;
     if (int d = check_device()) return d;
     return status_of(lrmoe::launch_fill_normal(out, count, seed, stream_id, sigma, first, as_stream(stream)));
+}
+
+// ---- Gated DeltaNet decode ----
+
+size_t lrmoe_delta_workspace_bytes(int tokens) {
+    if (tokens < 1 || tokens > lrmoe::kDeltaMaxTokens) return 0;
+    return lrmoe::delta_workspace_bytes(tokens);
+}
+
+int lrmoe_delta_rule(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* G, const uint16_t* beta,
+                     const void* initial, int state_bf16, int tokens, int heads, int key_width, int value_width,
+                     int normalize, int record, uint16_t* out, void* states, void* stream) {
+    if (bad_tokens(tokens) || heads <= 0 || heads > 65535 ||
+        (key_width != 64 && key_width != 128 && key_width != 256) || value_width <= 0 || value_width % 16 != 0 ||
+        value_width / 16 > 65535 || !initial || !states)
+        return LRMOE_E_ARG;
+    if (tokens > 0 && (!q || !k || !v || !G || !beta || !out)) return LRMOE_E_ARG;
+    const size_t qk_align = key_width == 64 ? 8 : 16;
+    if ((tokens > 0 && (misaligned(q, qk_align) || misaligned(k, qk_align) || misaligned(v, 8) || misaligned(out, 8))) ||
+        misaligned(initial, 16) || misaligned(states, 16))
+        return LRMOE_E_ARG;
+    if (tokens == 0 && record) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    lrmoe::DnRuleArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.qk_stride = static_cast<int64_t>(heads) * key_width;
+    a.v_stride = static_cast<int64_t>(heads) * value_width;
+    a.kv_shift = 0;
+    a.G = G;
+    a.beta = beta;
+    a.initial = initial;
+    a.final_state = record ? nullptr : states;
+    a.record = record ? states : nullptr;
+    a.out = out;
+    a.sumsq = nullptr;
+    a.tokens = tokens;
+    a.heads = heads;
+    a.width = value_width;
+    a.normalize = normalize ? 1 : 0;
+    return status_of(lrmoe::launch_delta_rule(a, key_width, state_bf16 != 0, as_stream(stream)));
+}
+
+int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_proj_qkv, const uint16_t* in_proj_z,
+                      const uint16_t* in_proj_b, const uint16_t* in_proj_a, const uint16_t* conv_weight,
+                      const uint16_t* A_log, const uint16_t* dt_bias, const uint16_t* norm_weight, float eps,
+                      const uint16_t* out_proj, uint16_t* conv_state, void* state, int state_bf16,
+                      uint16_t* conv_record, void* state_record, uint16_t* out, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (tokens < 0 || tokens > lrmoe::kDeltaMaxTokens) return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!hidden || !in_proj_qkv || !in_proj_z || !in_proj_b || !in_proj_a || !conv_weight || !A_log || !dt_bias ||
+        !norm_weight || !out_proj || !conv_state || !state || !out || !workspace)
+        return LRMOE_E_ARG;
+    if (misaligned(hidden, 16) || misaligned(in_proj_qkv, 16) || misaligned(in_proj_z, 16) ||
+        misaligned(in_proj_b, 16) || misaligned(in_proj_a, 16) || misaligned(out_proj, 16) ||
+        misaligned(norm_weight, 16) || misaligned(state, 16) || misaligned(state_record, 16) ||
+        misaligned(conv_record, 8) || misaligned(workspace, 256))
+        return LRMOE_E_ARG;
+    if (workspace_bytes < lrmoe::delta_workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    lrmoe::DnProjectArgs p{};
+    p.x = hidden;
+    p.w_qkv = in_proj_qkv;
+    p.w_z = in_proj_z;
+    p.w_b = in_proj_b;
+    p.w_a = in_proj_a;
+    p.conv_w = conv_weight;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.norm_w = norm_weight;
+    p.w_out = out_proj;
+    p.eps = eps;
+    p.conv_state = conv_state;
+    p.conv_record = conv_record;
+    p.out = out;
+    p.tokens = tokens;
+    const lrmoe::DeltaWorkspace w = lrmoe::carve_delta(workspace, tokens);
+    return status_of(lrmoe::launch_delta_mixer(p, state, state_bf16 != 0, state_record, w, as_stream(stream)));
 }
 
 }  // extern "C"

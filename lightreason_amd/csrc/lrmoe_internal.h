@@ -277,6 +277,9 @@ enum Stage : int {
     kStageCombine = 8,
     kStageGather = 16,
     kStageLayer = 32,
+    kStageDeltaIn = 64,     // Gated DeltaNet: in_proj + conv
+    kStageDeltaRule = 128,  // Gated DeltaNet: the delta rule
+    kStageDeltaOut = 256,   // Gated DeltaNet: gated norm + out_proj
 };
 struct StageEvents {
     hipEvent_t start = nullptr;
@@ -332,5 +335,73 @@ hipError_t launch_codec_unpack(const uint8_t* packed, const uint8_t* bases, int6
                                hipStream_t stream);
 hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint64_t stream_id, double sigma,
                               int64_t first, hipStream_t stream);
+
+// ---- Gated DeltaNet decode (delta.hip) ----
+
+// Arguments of the mixer's two projection kernels (in_proj with the conv /
+// beta / G epilogue, and the gated norm + out_proj).
+struct DnProjectArgs {
+    const uint16_t* x;        // hidden [T][2048]
+    const uint16_t* w_qkv;    // in_proj_qkv [8192][2048]
+    const uint16_t* w_z;      // in_proj_z [4096][2048]
+    const uint16_t* w_b;      // in_proj_b [32][2048]
+    const uint16_t* w_a;      // in_proj_a [32][2048]
+    const uint16_t* conv_w;   // conv1d weight [8192][4]
+    const uint16_t* A_log;    // [32]
+    const uint16_t* dt_bias;  // [32]
+    const uint16_t* norm_w;   // gated RMSNorm weight [128]
+    const uint16_t* w_out;    // out_proj [2048][4096]
+    float eps;
+    uint16_t* conv_state;     // [8192][4], updated in place
+    uint16_t* conv_record;    // [T][8192][4] per-token conv states, or null
+    uint16_t* act;            // [T][8192] conv + SiLU outputs (q | k | v)
+    uint16_t* z;              // [T][4096]
+    const uint16_t* z_in;     // the same z, read by out_proj
+    uint16_t* beta;           // [T][32]
+    float* G;                 // [T][32] exp(g)
+    const uint16_t* o;        // [T][4096] delta-rule output
+    const float* sumsq;       // [T][32][8] sums of o^2 per 16-column block
+    uint16_t* out;            // [T][2048]
+    int tokens;
+};
+
+// The delta rule over `tokens` tokens for `heads` value heads of state
+// width `width` (E); q/k head of value head h is h >> kv_shift.
+struct DnRuleArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t qk_stride;  // elements between consecutive tokens of q and k
+    int64_t v_stride;   // elements between consecutive tokens of v
+    int kv_shift;
+    const float* G;         // [T][H]
+    const uint16_t* beta;   // [T][H]
+    const void* initial;    // [H][D][E]
+    void* final_state;      // [H][D][E] or null (may equal initial)
+    void* record;           // [T][H][D][E] or null
+    uint16_t* out;          // [T][H][E]
+    float* sumsq;           // [T][H][E/16] or null
+    int tokens;
+    int heads;
+    int width;
+    int normalize;
+};
+
+struct DeltaWorkspace {
+    uint16_t* act;
+    uint16_t* z;
+    uint16_t* beta;
+    float* G;
+    uint16_t* o;
+    float* sumsq;
+    size_t bytes;
+};
+
+constexpr int kDeltaMaxTokens = 16;
+DeltaWorkspace carve_delta(void* base, int tokens);
+size_t delta_workspace_bytes(int tokens);
+hipError_t launch_delta_rule(const DnRuleArgs& a, int key_width, bool state_bf16, hipStream_t stream);
+hipError_t launch_delta_mixer(DnProjectArgs p, const void* state, bool state_bf16, void* state_record,
+                              const DeltaWorkspace& w, hipStream_t stream);
 
 }  // namespace lrmoe

@@ -11,11 +11,13 @@
 namespace lrmoe {
 namespace {
 
+constexpr int kStages = 9;  // LRMOE_STAGE_* bits 0..8
+
 struct Timing {
     int mask = 0;
     int capacity = 0;
-    std::vector<hipEvent_t> events[6];  // per stage: start, stop, start, stop, ...
-    int used[6] = {0, 0, 0, 0, 0, 0};
+    std::vector<hipEvent_t> events[kStages];  // per stage: start, stop, start, stop, ...
+    int used[kStages] = {};
 };
 
 Timing& timing() {
@@ -24,7 +26,7 @@ Timing& timing() {
 }
 
 int stage_index(int stage) {
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < kStages; ++i) {
         if (stage == (1 << i)) return i;
     }
     return -1;
@@ -86,8 +88,8 @@ int lrmoe_timing_enable(int mask, int launches) {
     t.mask = 0;
     t.capacity = 0;
     if (mask == 0) return LRMOE_OK;
-    if (launches <= 0 || launches > (1 << 20) || (mask & ~63)) return LRMOE_E_ARG;
-    for (int i = 0; i < 6; ++i) {
+    if (launches <= 0 || launches > (1 << 20) || (mask & ~((1 << lrmoe::kStages) - 1))) return LRMOE_E_ARG;
+    for (int i = 0; i < lrmoe::kStages; ++i) {
         if (!(mask & (1 << i))) continue;
         t.events[i].resize(2 * static_cast<size_t>(launches));
         for (auto& e : t.events[i]) {

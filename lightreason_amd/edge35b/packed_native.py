@@ -14,15 +14,15 @@ reduce to:
 
 The captured graphs read the routes and weights from fixed device buffers
 (the device table is rebuilt in place before each replay), so a call never
-reads the routes on the host.  ``mixer_graphs`` captures single-token mixer
-forwards (Gated DeltaNet in the reference model) per layer and replays them
-with the request's cache states copied in and out (82-149).
+reads the routes on the host.  The reference's ``mixer_graphs`` (82-149), a
+replay of the eager single-token mixer, is replaced by the native Gated
+DeltaNet step in ``lightreason_amd.delta`` (``native_mixers``), which updates
+the live cache in place and needs no captured copy of it.
 """
 
 from __future__ import annotations
 
 from contextlib import contextmanager
-from types import SimpleNamespace
 
 import torch
 
@@ -76,78 +76,6 @@ def native_library():
     CPU expert workers; here the plan is built on the device and no expert
     runs on the host."""
     return _native.library()
-
-
-class StaticMixerCache:
-    """A one-layer cache with the fixed-address state buffers a captured
-    mixer forward reads and writes (packed_native.py:82-95)."""
-
-    def __init__(self, layer_index, source):
-        self.layers = {layer_index: SimpleNamespace(conv_states=torch.empty_like(source.conv_states),
-                                                    recurrent_states=torch.empty_like(source.recurrent_states))}
-
-    def has_previous_state(self, _index):
-        return True
-
-    def update_recurrent_state(self, state, index):
-        target = self.layers[index].recurrent_states
-        target.copy_(state)
-        return target
-
-
-@contextmanager
-def mixer_graphs(model, pool):
-    """Replay each layer's single-token mixer (``layer.linear_attn``) as a
-    captured graph; anything else (prefill, no cache, a mask) runs eagerly."""
-    graphs = getattr(pool, "mixer_graphs", None)
-    if graphs is None:
-        graphs = pool.mixer_graphs = {}
-        pool.mixer_graph_memory = torch.cuda.graph_pool_handle()
-    restore = []
-
-    def replayed(original, index):
-        def forward(hidden_states, cache_params=None, attention_mask=None):
-            if (hidden_states.shape[:2] != (1, 1) or cache_params is None or attention_mask is not None
-                    or not cache_params.has_previous_state(index)):
-                return original(hidden_states, cache_params=cache_params, attention_mask=attention_mask)
-            live = cache_params.layers[index]
-            entry = graphs.get(index)
-            if entry is None:
-                cache = StaticMixerCache(index, live)
-                static_in = hidden_states.clone()
-                state = cache.layers[index]
-                state.conv_states.copy_(live.conv_states)
-                state.recurrent_states.copy_(live.recurrent_states)
-                original(static_in, cache_params=cache, attention_mask=None)
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, pool=pool.mixer_graph_memory):
-                    static_out = original(static_in, cache_params=cache, attention_mask=None)
-                entry = graphs[index] = (graph, static_in, cache, static_out)
-            graph, static_in, cache, static_out = entry
-            state = cache.layers[index]
-            static_in.copy_(hidden_states)
-            state.conv_states.copy_(live.conv_states)
-            state.recurrent_states.copy_(live.recurrent_states)
-            graph.replay()
-            live.conv_states.copy_(state.conv_states)
-            live.recurrent_states.copy_(state.recurrent_states)
-            return static_out
-        return forward
-
-    try:
-        for index, layer in enumerate(model.model.layers):
-            mixer = getattr(layer, "linear_attn", None)
-            if mixer is None:
-                continue
-            restore.append((mixer, mixer.__dict__.get("forward")))
-            mixer.forward = replayed(mixer.forward, index)
-        yield
-    finally:
-        for mixer, previous in restore:
-            if previous is None:
-                del mixer.forward
-            else:
-                mixer.forward = previous
 
 
 @contextmanager
