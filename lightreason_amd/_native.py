@@ -69,6 +69,7 @@ STAGE_LAYER = 32
 STAGE_DELTA_IN = 64
 STAGE_DELTA_RULE = 128
 STAGE_DELTA_OUT = 256
+STAGE_DELTA_NORM = 512
 DELTA_MAX_TOKENS = 16    # tokens per lrmoe_delta_mixer call
 
 

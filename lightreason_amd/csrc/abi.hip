@@ -471,7 +471,7 @@ int lrmoe_delta_rule(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
                      int normalize, int record, uint16_t* out, void* states, void* stream) {
     if (bad_tokens(tokens) || heads <= 0 || heads > 65535 ||
         (key_width != 64 && key_width != 128 && key_width != 256) || value_width <= 0 || value_width % 16 != 0 ||
-        value_width / 16 > 65535 || !initial || !states)
+        value_width / 4 > 65535 || !initial || !states)
         return LRMOE_E_ARG;
     if (tokens > 0 && (!q || !k || !v || !G || !beta || !out)) return LRMOE_E_ARG;
     const size_t qk_align = key_width == 64 ? 8 : 16;
@@ -493,7 +493,6 @@ int lrmoe_delta_rule(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
     a.final_state = record ? nullptr : states;
     a.record = record ? states : nullptr;
     a.out = out;
-    a.sumsq = nullptr;
     a.tokens = tokens;
     a.heads = heads;
     a.width = value_width;
@@ -515,7 +514,7 @@ int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_pro
     if (misaligned(hidden, 16) || misaligned(in_proj_qkv, 16) || misaligned(in_proj_z, 16) ||
         misaligned(in_proj_b, 16) || misaligned(in_proj_a, 16) || misaligned(out_proj, 16) ||
         misaligned(norm_weight, 16) || misaligned(state, 16) || misaligned(state_record, 16) ||
-        misaligned(conv_record, 8) || misaligned(workspace, 256))
+        misaligned(conv_weight, 8) || misaligned(conv_record, 8) || misaligned(workspace, 256))
         return LRMOE_E_ARG;
     if (workspace_bytes < lrmoe::delta_workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
     if (int d = check_device()) return d;

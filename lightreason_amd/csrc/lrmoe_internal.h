@@ -279,7 +279,8 @@ enum Stage : int {
     kStageLayer = 32,
     kStageDeltaIn = 64,     // Gated DeltaNet: in_proj + conv
     kStageDeltaRule = 128,  // Gated DeltaNet: the delta rule
-    kStageDeltaOut = 256,   // Gated DeltaNet: gated norm + out_proj
+    kStageDeltaOut = 256,   // Gated DeltaNet: out_proj
+    kStageDeltaNorm = 512,  // Gated DeltaNet: gated RMSNorm
 };
 struct StageEvents {
     hipEvent_t start = nullptr;
@@ -339,9 +340,9 @@ hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint6
 // ---- Gated DeltaNet decode (delta.hip) ----
 
 // Arguments of the mixer's two projection kernels (in_proj with the conv /
-// beta / G epilogue, and the gated norm + out_proj).
+// beta / G epilogue, and out_proj).
 struct DnProjectArgs {
-    const uint16_t* x;        // hidden [T][2048]
+    const uint16_t* x;        // input [T][K]: hidden (in_proj), the gated-norm output (out_proj)
     const uint16_t* w_qkv;    // in_proj_qkv [8192][2048]
     const uint16_t* w_z;      // in_proj_z [4096][2048]
     const uint16_t* w_b;      // in_proj_b [32][2048]
@@ -356,11 +357,8 @@ struct DnProjectArgs {
     uint16_t* conv_record;    // [T][8192][4] per-token conv states, or null
     uint16_t* act;            // [T][8192] conv + SiLU outputs (q | k | v)
     uint16_t* z;              // [T][4096]
-    const uint16_t* z_in;     // the same z, read by out_proj
     uint16_t* beta;           // [T][32]
     float* G;                 // [T][32] exp(g)
-    const uint16_t* o;        // [T][4096] delta-rule output
-    const float* sumsq;       // [T][32][8] sums of o^2 per 16-column block
     uint16_t* out;            // [T][2048]
     int tokens;
 };
@@ -380,7 +378,6 @@ struct DnRuleArgs {
     void* final_state;      // [H][D][E] or null (may equal initial)
     void* record;           // [T][H][D][E] or null
     uint16_t* out;          // [T][H][E]
-    float* sumsq;           // [T][H][E/16] or null
     int tokens;
     int heads;
     int width;
@@ -393,7 +390,7 @@ struct DeltaWorkspace {
     uint16_t* beta;
     float* G;
     uint16_t* o;
-    float* sumsq;
+    uint16_t* core;
     size_t bytes;
 };
 

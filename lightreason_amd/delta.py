@@ -98,7 +98,7 @@ def _workspace(device: torch.device) -> torch.Tensor:
     ws = _WORKSPACES.get(key)
     if ws is None:
         nbytes = int(_native.library().lrmoe_delta_workspace_bytes(MAX_TOKENS))
-        ws = _WORKSPACES[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws = _WORKSPACES[key] = torch.zeros(nbytes, dtype=torch.uint8, device=device)
     return ws
 
 
