@@ -10,8 +10,10 @@ not Infinity-Cache resident; the steps run as HIP-graph replays.
 Also reported under "configs": T=1 decode layer with the router (latency and
 GB/s), the raw expert gather at T in {1,4,8,16}, the 40-layer decode chain
 with RMSNorm + residual at T=1 and T=16 (one persistent launch, and for
-comparison one launch per layer in a graph), and the T=2048 prefill
-(TFLOPS).
+comparison one launch per layer in a graph), the T=2048 prefill (TFLOPS),
+and (C7) the Gated DeltaNet mixer step of the 30 linear-attention layers at
+T=1 and T=16 (µs and GB/s on its weight and state bytes, per-kernel times,
+a torch gate, and the oracle's C step timed on one core beside it).
 
 `roofline` is for moe_decode, the one kernel of the headline step, timed
 with HIP events stamped by its own dispatches, against the 8 TB/s spec and,
@@ -371,6 +373,54 @@ def parity_gate(model, layer: int, x, out, idx, w, rows, rel: float = 1e-2) -> d
             "tolerance": rel, "ok": bool(tensor_rel <= rel and row_l2 <= rel and torch.isfinite(got).all())}
 
 
+def torch_mixer_step(m, x, conv, state):
+    """The Gated DeltaNet mixer step in torch on the GPU, fp32 arithmetic with
+    the Transformers forward's bf16 rounding points ([HF]
+    Qwen3_5MoeGatedDeltaNet.forward 430-543, causal_conv1d_update,
+    torch_recurrent_gated_delta_rule, Qwen3_5MoeRMSNormGated): the bench's
+    gate for the mixer case.  x [T, 2048] bf16, conv [8192, 4] bf16, state
+    [32, 128, 128] fp32 (not modified).  Returns out [T, 2048] fp32."""
+    r = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    xf = x.float()
+    mixed = r(xf @ m.in_proj_qkv.float().T)                       # [T, 8192]
+    z = r(xf @ m.in_proj_z.float().T)
+    b = r(xf @ m.in_proj_b.float().T)
+    a = r(xf @ m.in_proj_a.float().T)
+    T = x.shape[0]
+    seq = torch.cat([conv.float(), mixed.T], dim=1)                # [8192, 4 + T]
+    w = m.conv1d.float()
+    act = torch.empty_like(mixed)
+    for t in range(T):
+        acc = torch.zeros(seq.shape[0], device=x.device)
+        for j in range(4):
+            acc = torch.addcmul(acc, w[:, j], seq[:, t + 1 + j])
+        act[t] = r(torch.nn.functional.silu(r(acc)))
+    beta = r(torch.sigmoid(b))
+    g = -m.A_log.float().exp() * torch.nn.functional.softplus(a + m.dt_bias.float())
+    G = g.exp()
+
+    def l2(v):  # torch l2norm on bf16 tensors: every step rounded
+        vb = v.to(torch.bfloat16)
+        inv = torch.rsqrt((vb * vb).sum(-1, keepdim=True) + 1e-6)
+        return (vb * inv).float()
+
+    S = state.float().clone()
+    core = torch.empty(T, 32, 128, device=x.device)
+    for t in range(T):
+        q = l2(act[t, :2048].view(16, 128)).repeat_interleave(2, 0) * (128 ** -0.5)
+        k = l2(act[t, 2048:4096].view(16, 128)).repeat_interleave(2, 0)
+        v = act[t, 4096:].view(32, 128)
+        S = S * G[t][:, None, None]
+        mem = (S * k[:, :, None]).sum(1)
+        delta = (v - mem) * beta[t][:, None]
+        S = S + k[:, :, None] * delta[:, None, :]
+        core[t] = r((S * q[:, :, None]).sum(1))
+    var = (core * core).mean(-1, keepdim=True)
+    n = r(core * torch.rsqrt(var + m.eps))
+    normed = r(r(m.norm.float() * n) * torch.nn.functional.silu(z.view(T, 32, 128)))
+    return normed.view(T, 4096) @ m.out_proj.float().T
+
+
 # ---- CPU baseline: the reference kernel in a pinned child process ---------------
 
 def cpu_placement(limit: int = 16) -> tuple[list[int], int]:
@@ -554,6 +604,92 @@ def cpu_workers_t1(model, legs_t1, budget_s: float = 3.0) -> dict | None:
                       f"packed_workers with {threads} threads"}
 
 
+MIXER_LAYERS = 30  # linear-attention layers of the 35B model
+MIXER_WEIGHT_BYTES = ((8192 + 4096 + 2 * 32) * HIDDEN + HIDDEN * 4096) * 2
+MIXER_IN_BYTES = (8192 + 4096 + 2 * 32) * HIDDEN * 2
+MIXER_OUT_BYTES = HIDDEN * 4096 * 2
+
+
+def mixer_bytes(tokens: int) -> int:
+    """Algorithmic HBM bytes of one mixer step: the weights once, the fp32
+    recurrent state and the conv state read and written, per token the
+    hidden row in and the output row out."""
+    return MIXER_WEIGHT_BYTES + 2 * (32 * 128 * 128 * 4) + 2 * (8192 * 4 * 2) + tokens * 2 * HIDDEN * 2
+
+
+def bench_mixers(device, seed: int, passes: int, skip_cpu: bool) -> dict:
+    """C7: one cached Gated DeltaNet mixer step (lrmoe_delta_mixer: in_proj +
+    conv, the delta rule, the gated RMSNorm, out_proj) at T = 1 (decode) and
+    T = 16 (a verify block, no state records), rotating over 30 resident
+    layers (1.9 GiB of weights, so no step finds its weights in the Infinity
+    Cache), as graph replays; per-kernel times from event pairs stamped by the
+    kernels' own dispatches; a torch gate on layer 0 before timing."""
+    from lightreason_amd.synthetic import SyntheticMixers
+
+    mix = SyntheticMixers(MIXER_LAYERS, device, seed)
+    out = {}
+    for T in (1, 16):
+        xs = [mix.hidden(T, step=l) for l in range(MIXER_LAYERS)]
+        outs = [torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=device) for _ in range(MIXER_LAYERS)]
+        conv0, state0 = mix.conv[0].clone(), mix.state[0].clone()
+        want = torch_mixer_step(mix.mixers[0], xs[0], conv0, state0)
+        got = mix.mixers[0].step(xs[0], conv0, state0).float()
+        tensor_rel = float((got - want).abs().max() / want.abs().max().clamp_min(1e-30))
+        row_l2 = float(((got - want).norm(dim=1) / want.norm(dim=1).clamp_min(1e-30)).max())
+        gate = {"tokens_checked": T, "max_rel": round(tensor_rel, 5), "worst_row_l2_rel": round(row_l2, 5),
+                "tolerance": 1e-2, "ok": bool(tensor_rel <= 1e-2 and row_l2 <= 1e-2 and torch.isfinite(got).all())}
+
+        def run(n, T=T, xs=xs, outs=outs):
+            for i in range(n):
+                l = i % MIXER_LAYERS
+                mix.mixers[l].step(xs[l], mix.conv[l], mix.state[l], out=outs[l])
+
+        steps = MIXER_LAYERS * passes
+        graph = capture(lambda: run(steps))
+        graph.replay()
+        ms = timed_replays(graph, 1) / steps
+        del graph
+        stages = {}
+        mask = _native.STAGE_DELTA_IN | _native.STAGE_DELTA_RULE | _native.STAGE_DELTA_NORM | _native.STAGE_DELTA_OUT
+        torch.cuda.synchronize()
+        _native.timing_enable(mask, 2 * MIXER_LAYERS + 8)
+        run(2 * MIXER_LAYERS)
+        for name, st in (("dn_project_in", _native.STAGE_DELTA_IN), ("dn_rule", _native.STAGE_DELTA_RULE),
+                         ("dn_gate_norm", _native.STAGE_DELTA_NORM), ("dn_project_out", _native.STAGE_DELTA_OUT)):
+            total, n = _native.timing_collect(st)
+            stages[name] = round(total / max(n, 1) * 1e3, 2)
+        _native.timing_enable(0)
+        nbytes = mixer_bytes(T)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        in_gbs = MIXER_IN_BYTES / (stages["dn_project_in"] * 1e-6) / 1e9
+        out_gbs = MIXER_OUT_BYTES / (stages["dn_project_out"] * 1e-6) / 1e9
+        out[f"t{T}"] = dict(us_per_layer=round(ms * 1e3, 2), algorithmic_bytes=nbytes, gbs=round(gbs, 1),
+                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stages,
+                            dn_project_in_gbs=round(in_gbs, 1), dn_project_out_gbs=round(out_gbs, 1), parity=gate)
+    if not skip_cpu:
+        out["cpu_reference"] = mixer_cpu_leg(mix)
+    return out
+
+
+def mixer_cpu_leg(mix, budget_s: float = 3.0) -> dict:
+    """The oracle's C mixer step (oracle/lro.c lro_delta_mixer, one thread:
+    the reference has no CPU implementation of this step) at T = 1 on layer
+    0's weights, as many calls as fit in `budget_s`."""
+    from oracle import oracle as O
+
+    m = mix.mixers[0]
+    w = {name: bits(getattr(m, name)) for name in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "conv1d",
+                                                   "A_log", "dt_bias", "norm", "out_proj")}
+    x, conv, state = bits(mix.hidden(1, step=0)), bits(mix.conv[0]), mix.state[0].cpu().numpy()
+    calls, t0 = 0, time.perf_counter()
+    while calls < 2 or time.perf_counter() - t0 < budget_s:
+        O.delta_mixer(x, w, conv, state, eps=m.eps)
+        calls += 1
+    sec = (time.perf_counter() - t0) / calls
+    return {"value": round(sec * 1e6, 1), "unit": "us per T=1 mixer step", "cores": 1, "kind": "port",
+            "sample": f"{calls} calls of the oracle's C mixer step on one layer"}
+
+
 def bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
@@ -568,7 +704,7 @@ def main() -> int:
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=1.0, help="scale of the CPU legs' time budgets")
-    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6 to run besides the headline "
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6,c7 to run besides the headline "
                                                    "(default all)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
@@ -590,7 +726,7 @@ def main() -> int:
         f"in {time.perf_counter() - t0:.1f}s")
     L = args.layers
     aux = max(2, min(10, args.steps // L))  # graph replays of the secondary configs
-    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6"}
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6", "c7"}
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
@@ -840,6 +976,11 @@ def main() -> int:
         cpu_routes["c4"] = (0, idx0, bits(c4.x[0]))
         log(f"[bench] C4 T=2048: {ms4:.3f} ms/layer, {tflops:.1f} TFLOPS, hit {hit}, max/mean {skew:.2f}")
         del c4
+
+    # ---- C7: Gated DeltaNet mixer step (the 30 linear-attention layers) ----
+    if "c7" in only:
+        configs["c7_delta_mixer"] = bench_mixers(device, args.seed, aux, args.skip_cpu)
+        log(f"[bench] C7 mixer: {configs['c7_delta_mixer']}")
 
     cpu = {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference", "sample": "skipped"}
     if not args.skip_cpu:

@@ -93,12 +93,13 @@ _WORKSPACES: dict = {}
 
 def _workspace(device: torch.device) -> torch.Tensor:
     """Scratch for lrmoe_delta_mixer on the current stream of `device`
-    (sized for 16 tokens, so its address never changes)."""
+    (sized for 16 tokens, so its address never changes; one per stream, as
+    calls sharing a workspace must not overlap)."""
     key = (device, _stream(device))
     ws = _WORKSPACES.get(key)
     if ws is None:
         nbytes = int(_native.library().lrmoe_delta_workspace_bytes(MAX_TOKENS))
-        ws = _WORKSPACES[key] = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        ws = _WORKSPACES[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
     return ws
 
 

@@ -58,3 +58,40 @@ class SyntheticModel:
 
     def hidden(self, tokens: int, step: int = 0, sigma: float = 1.0) -> torch.Tensor:
         return _tensor((tokens, HIDDEN), self.device, self.seed, STREAM_HIDDEN + step, sigma)
+
+
+STREAM_MIXER = 20000  # + 16 * layer + field
+STREAM_MIXER_HIDDEN = 40000
+
+
+class SyntheticMixers:
+    """``layers`` Gated DeltaNet mixers of the 35B shape (the model's 30
+    linear-attention layers) with decode states, all seeded: projections
+    ~N(0, 0.02), conv1d ~N(0, 0.3), A_log 1.5 + N(0, 0.5), dt_bias
+    ~N(0, 0.5), norm 1 + N(0, 0.1); conv states ~N(0, 1) and recurrent
+    states ~N(0, 0.05) in ``state_dtype``."""
+
+    def __init__(self, layers: int = 30, device="cuda", seed: int = 0, state_dtype=torch.float32):
+        from .delta import CONV_DIM, CONV_TAPS, HEAD_WIDTH, VALUE_HEADS, DeltaMixer
+
+        self.seed = seed
+        self.device = torch.device(device)
+        self.mixers, self.conv, self.state = [], [], []
+        for layer in range(layers):
+            base = STREAM_MIXER + 16 * layer
+
+            def t(shape, field, sigma, shift=0.0):
+                x = _tensor(shape, device, seed, base + field, sigma)
+                return x.add_(shift) if shift else x
+
+            self.mixers.append(DeltaMixer(
+                in_proj_qkv=t((CONV_DIM, HIDDEN), 0, WEIGHT_SIGMA), in_proj_z=t((VALUE_HEADS * HEAD_WIDTH, HIDDEN), 1, WEIGHT_SIGMA),
+                in_proj_b=t((VALUE_HEADS, HIDDEN), 2, WEIGHT_SIGMA), in_proj_a=t((VALUE_HEADS, HIDDEN), 3, WEIGHT_SIGMA),
+                conv1d=t((CONV_DIM, CONV_TAPS), 4, 0.3), A_log=t((VALUE_HEADS,), 5, 0.5, 1.5),
+                dt_bias=t((VALUE_HEADS,), 6, 0.5), norm=t((HEAD_WIDTH,), 7, 0.1, 1.0),
+                out_proj=t((HIDDEN, VALUE_HEADS * HEAD_WIDTH), 8, WEIGHT_SIGMA)))
+            self.conv.append(t((CONV_DIM, CONV_TAPS), 9, 1.0))
+            self.state.append(t((VALUE_HEADS, HEAD_WIDTH, HEAD_WIDTH), 10, 0.05).to(state_dtype))
+
+    def hidden(self, tokens: int, step: int = 0, sigma: float = 1.0) -> torch.Tensor:
+        return _tensor((tokens, HIDDEN), self.device, self.seed, STREAM_MIXER_HIDDEN + step, sigma)
