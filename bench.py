@@ -606,8 +606,6 @@ def cpu_workers_t1(model, legs_t1, budget_s: float = 3.0) -> dict | None:
 
 MIXER_LAYERS = 30  # linear-attention layers of the 35B model
 MIXER_WEIGHT_BYTES = ((8192 + 4096 + 2 * 32) * HIDDEN + HIDDEN * 4096) * 2
-MIXER_IN_BYTES = (8192 + 4096 + 2 * 32) * HIDDEN * 2
-MIXER_OUT_BYTES = HIDDEN * 4096 * 2
 
 
 def mixer_bytes(tokens: int) -> int:
@@ -624,6 +622,7 @@ def bench_mixers(device, seed: int, passes: int, skip_cpu: bool) -> dict:
     layers (1.9 GiB of weights, so no step finds its weights in the Infinity
     Cache), as graph replays; per-kernel times from event pairs stamped by the
     kernels' own dispatches; a torch gate on layer 0 before timing."""
+    from lightreason_amd.delta import mixer_status
     from lightreason_amd.synthetic import SyntheticMixers
 
     mix = SyntheticMixers(MIXER_LAYERS, device, seed)
@@ -649,23 +648,18 @@ def bench_mixers(device, seed: int, passes: int, skip_cpu: bool) -> dict:
         graph.replay()
         ms = timed_replays(graph, 1) / steps
         del graph
-        stages = {}
-        mask = _native.STAGE_DELTA_IN | _native.STAGE_DELTA_RULE | _native.STAGE_DELTA_NORM | _native.STAGE_DELTA_OUT
         torch.cuda.synchronize()
-        _native.timing_enable(mask, 2 * MIXER_LAYERS + 8)
+        _native.timing_enable(_native.STAGE_DELTA_MIXER, 2 * MIXER_LAYERS + 8)
         run(2 * MIXER_LAYERS)
-        for name, st in (("dn_project_in", _native.STAGE_DELTA_IN), ("dn_rule", _native.STAGE_DELTA_RULE),
-                         ("dn_gate_norm", _native.STAGE_DELTA_NORM), ("dn_project_out", _native.STAGE_DELTA_OUT)):
-            total, n = _native.timing_collect(st)
-            stages[name] = round(total / max(n, 1) * 1e3, 2)
+        total, n = _native.timing_collect(_native.STAGE_DELTA_MIXER)
         _native.timing_enable(0)
+        kernel_us = total / max(n, 1) * 1e3
         nbytes = mixer_bytes(T)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        in_gbs = MIXER_IN_BYTES / (stages["dn_project_in"] * 1e-6) / 1e9
-        out_gbs = MIXER_OUT_BYTES / (stages["dn_project_out"] * 1e-6) / 1e9
         out[f"t{T}"] = dict(us_per_layer=round(ms * 1e3, 2), algorithmic_bytes=nbytes, gbs=round(gbs, 1),
-                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), stage_us=stages,
-                            dn_project_in_gbs=round(in_gbs, 1), dn_project_out_gbs=round(out_gbs, 1), parity=gate)
+                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), dn_mixer_us=round(kernel_us, 2),
+                            dn_mixer_gbs=round(nbytes / (kernel_us * 1e-6) / 1e9, 1), parity=gate,
+                            status=mixer_status(device))
     if not skip_cpu:
         out["cpu_reference"] = mixer_cpu_leg(mix)
     return out

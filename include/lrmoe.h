@@ -321,10 +321,8 @@ int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t
 #define LRMOE_STAGE_COMBINE 8
 #define LRMOE_STAGE_GATHER 16
 #define LRMOE_STAGE_LAYER 32       /* lrmoe_moe_layer / lrmoe_moe_chain decode kernel */
-#define LRMOE_STAGE_DELTA_IN 64    /* lrmoe_delta_mixer: in_proj + conv */
-#define LRMOE_STAGE_DELTA_RULE 128 /* lrmoe_delta_rule, and the rule inside lrmoe_delta_mixer */
-#define LRMOE_STAGE_DELTA_OUT 256  /* lrmoe_delta_mixer: out_proj */
-#define LRMOE_STAGE_DELTA_NORM 512 /* lrmoe_delta_mixer: gated RMSNorm */
+#define LRMOE_STAGE_DELTA_MIXER 64 /* lrmoe_delta_mixer (one launch) */
+#define LRMOE_STAGE_DELTA_RULE 128 /* lrmoe_delta_rule */
 int lrmoe_timing_enable(int mask, int launches);
 int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
 
@@ -378,9 +376,17 @@ size_t lrmoe_delta_workspace_bytes(int tokens);
  * state_record [tokens][32][128][128] (may be NULL) receive both states
  * after every token, for rolling back to an accepted prefix.  out
  * [tokens][2048] bf16.  Workspace of lrmoe_delta_workspace_bytes(tokens),
- * 256-byte aligned, used by one stream at a time.  Rounding points: those
- * of the Transformers forward in bf16 (see lrmoe_delta_rule for the
- * recurrence). */
+ * 256-byte aligned, zeroed once after allocation (its counters never need
+ * a reset), used by one stream at a time.  One persistent launch of 256
+ * workgroups, one per CU, which wait for each other at two grid barriers:
+ * all must be resident (a device with fewer than 256 CUs gets
+ * hipErrorNotSupported; a kernel running on another stream can keep some
+ * off the GPU).  Waits are bounded (50 ms); on expiry the call still ends,
+ * sets LRMOE_STATUS_TIMEOUT in the int32 status word at byte offset
+ * LRMOE_DELTA_WS_STATUS_OFFSET of the workspace, and its outputs are
+ * invalid.  Rounding points: those of the Transformers forward in bf16
+ * (see lrmoe_delta_rule for the recurrence). */
+#define LRMOE_DELTA_WS_STATUS_OFFSET 0
 int lrmoe_delta_mixer(const uint16_t *hidden, int tokens, const uint16_t *in_proj_qkv, const uint16_t *in_proj_z,
                       const uint16_t *in_proj_b, const uint16_t *in_proj_a, const uint16_t *conv_weight,
                       const uint16_t *A_log, const uint16_t *dt_bias, const uint16_t *norm_weight, float eps,

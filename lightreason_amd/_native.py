@@ -66,10 +66,9 @@ STAGE_DOWN = 4
 STAGE_COMBINE = 8
 STAGE_GATHER = 16
 STAGE_LAYER = 32
-STAGE_DELTA_IN = 64
+STAGE_DELTA_MIXER = 64
 STAGE_DELTA_RULE = 128
-STAGE_DELTA_OUT = 256
-STAGE_DELTA_NORM = 512
+DELTA_WS_STATUS_OFFSET = 0  # int32 status word of a mixer workspace
 DELTA_MAX_TOKENS = 16    # tokens per lrmoe_delta_mixer call
 
 

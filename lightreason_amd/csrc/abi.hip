@@ -514,7 +514,8 @@ int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_pro
     if (misaligned(hidden, 16) || misaligned(in_proj_qkv, 16) || misaligned(in_proj_z, 16) ||
         misaligned(in_proj_b, 16) || misaligned(in_proj_a, 16) || misaligned(out_proj, 16) ||
         misaligned(norm_weight, 16) || misaligned(state, 16) || misaligned(state_record, 16) ||
-        misaligned(conv_weight, 8) || misaligned(conv_record, 8) || misaligned(workspace, 256))
+        misaligned(conv_weight, 8) || misaligned(conv_state, 8) || misaligned(conv_record, 8) ||
+        misaligned(workspace, 256))
         return LRMOE_E_ARG;
     if (workspace_bytes < lrmoe::delta_workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
     if (int d = check_device()) return d;

@@ -107,23 +107,8 @@ constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
 // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14.
 constexpr int kWaitVm16 = (16 & 15) | (7 << 4) | (15 << 8) | ((16 >> 4) << 14);
 
-// ---- agent-scope memory operations (coherent across XCDs) -------------------
+// ---- agent-scope memory operations (coherent across XCDs): lrmoe_device.h ----
 
-typedef __attribute__((address_space(1))) uint64_t g_u64;
-typedef __attribute__((address_space(1))) uint32_t g_u32;
-
-__device__ __forceinline__ g_u64* as_g64(const void* p) {
-    return reinterpret_cast<g_u64*>(reinterpret_cast<uintptr_t>(p));
-}
-__device__ __forceinline__ g_u32* as_g32(const void* p) {
-    return reinterpret_cast<g_u32*>(reinterpret_cast<uintptr_t>(p));
-}
-__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
-    __hip_atomic_store(as_g64(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
-    return __hip_atomic_load(as_g64(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // Four agent-scope (sc1) 8-byte loads at a uniform base plus a per-lane byte
 // offset.  Written as assembly so that the compiler's wait insertion does not
 // tie the next prefetch to them; the caller's "s_waitcnt vmcnt(16)" after
@@ -137,17 +122,6 @@ __device__ __forceinline__ void ld_agent64x4_async(uint64_t* out, const void* ba
         : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
         : "v"(byte_offset), "s"(base)
         : "memory");
-}
-__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
-    __hip_atomic_store(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// A wave-uniform copy of a 64-bit value (each half through readfirstlane,
-// whose int result is taken as unsigned before widening).
-__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
-    return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
 }
 
 // Claims a work item: one agent-scope fetch-add by the lanes in `lanes`
@@ -186,13 +160,7 @@ __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
 template <bool kChained>
 __device__ __forceinline__ uint4 ld_row16(const uint16_t* base, uint32_t byte_offset) {
     if constexpr (kChained) {
-        // Raw buffer over 2 GiB from base; dword 3 = gfx9 untyped 32-bit data format.
-        const __amdgpu_buffer_rsrc_t rsrc =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff, 0x00020000);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        constexpr int kSc1 = 16;  // cache policy: sc1 (agent scope)
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(byte_offset), 0, kSc1);
-        return make_uint4(v.x, v.y, v.z, v.w);
+        return ld_agent16(base, byte_offset);
     } else {
         return ldg16(reinterpret_cast<const uint8_t*>(base) + byte_offset);
     }

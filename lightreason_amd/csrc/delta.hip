@@ -1,20 +1,10 @@
 // Gated DeltaNet decode on gfx950: the gated delta rule over a short block
-// of tokens (edge35b/delta_decode.py:11-55, _delta and _run), and the whole
-// cached-decode step of the 35B model's linear-attention mixer ([HF]
-// Qwen3_5MoeGatedDeltaNet.forward 430-543: 16 key heads and 32 value heads
-// of width 128, conv kernel 4) as four kernels on one stream:
-//
-//   dn_project<kProjIn>   hidden [T, 2048] times in_proj_qkv / _z / _b / _a
-//                         (12352 rows, MFMA with the T <= 16 tokens as the
-//                         16 columns), with the causal conv + SiLU and the
-//                         conv-state update (qkv channels), beta (b rows) and
-//                         G = exp(g) (a rows) in the epilogue;
-//   dn_rule               per (value head, block of 4 state columns): the
-//                         block's q, k, v, g, beta staged in LDS, l2norm of q
-//                         and k, the recurrence over the T tokens with the
-//                         state slab in registers, the bf16 output;
-//   dn_gate_norm          the gated RMSNorm per (token, value head);
-//   dn_project<kProjOut>  out_proj [2048, 4096].
+// of tokens (edge35b/delta_decode.py:11-55, _delta and _run: dn_rule), and
+// the whole cached-decode step of the 35B model's linear-attention mixer
+// ([HF] Qwen3_5MoeGatedDeltaNet.forward 430-543: 16 key heads and 32 value
+// heads of width 128, conv kernel 4) as one persistent launch (dn_mixer):
+// in_proj with the causal conv + SiLU, the conv-state update, beta and
+// G = exp(g); the delta rule; the gated RMSNorm; out_proj.
 //
 // Rounding points follow the Transformers forward in bf16: projections and
 // conv outputs rounded to bf16, SiLU of the rounded conv output rounded,
@@ -38,175 +28,10 @@ constexpr int kDnConv = 2 * kDnKey + kDnValue;      // 8192
 constexpr int kDnTaps = 4;
 constexpr int kDnZRow = kDnConv;                    // first in_proj_z row
 constexpr int kDnBRow = kDnZRow + kDnValue;         // first in_proj_b row
-constexpr int kDnARow = kDnBRow + kDnValueHeads;    // first in_proj_a row
-constexpr int kDnProjRows = kDnARow + kDnValueHeads;  // 12352
-
-enum ProjMode : int { kProjIn = 0, kProjOut = 1 };
-
-// Per mode: workgroup waves (each owns a 512-wide slice of the reduction
-// dimension), tiles per workgroup (each wave multiplies its slice of every
-// tile with the same input fragments) and rows per tile (16: every MFMA row
-// is a weight row; 8: half the rows are zero so out_proj still has 256
-// workgroups).  in_proj: 386 workgroups of 2 x 16 rows, all resident at
-// once (two per CU at 2 waves per SIMD), so no tile waits for a second round.
-template <int MODE> struct ProjShape;
-template <> struct ProjShape<kProjIn> {
-    static constexpr int kWaves = 4, kTiles = 2, kRows = 16, kK = 2048;
-};
-template <> struct ProjShape<kProjOut> {
-    static constexpr int kWaves = 8, kTiles = 1, kRows = 8, kK = 4096;
-};
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + lr_exp(-x)); }
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(lr_exp(x)); }
-
-// out[t][n] = bf16(sum_k X[t][k] W[n][k]) for kTiles tiles of kRows weight
-// rows (workgroup blockIdx.x), T <= 16 tokens.  Wave w multiplies k in
-// [512w, 512w + 512): per 128-wide step s, lane l (token l % 16, group
-// g = l / 16) holds the eight values at 128s + 32j + 8g (j = 0..3) of its
-// row's weights (A, per tile) and of its token's input (B, shared by the
-// tiles), so each load instruction reads 64 contiguous bytes per row.  The
-// waves' 16x16 partial tiles are summed in LDS in wave order, then the
-// mode's epilogue runs on (row, token) = (tid / 16 % 16, tid % 16).
-template <int MODE>
-__global__ __launch_bounds__(ProjShape<MODE>::kWaves * 64) void dn_project(DnProjectArgs a) {
-    constexpr int kWaves = ProjShape<MODE>::kWaves;
-    constexpr int kTiles = ProjShape<MODE>::kTiles;
-    constexpr int kRows = ProjShape<MODE>::kRows;
-    constexpr int kK = ProjShape<MODE>::kK;
-    __shared__ float red[kTiles][kWaves][16][17];
-    __shared__ uint16_t seq[16][kDnTaps + 16];  // conv: per row the cached context, then the projections
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int t = lane & 15;
-    const int g = lane >> 4;
-    const int T = a.tokens;
-    const int n0 = blockIdx.x * kRows * kTiles;
-    const int k0 = 512 * wave + 8 * g;
-
-    // the weight rows of this workgroup's tiles (no tile pair straddles two
-    // matrices: every boundary is a multiple of 32 rows)
-    const uint16_t* W;
-    int seg = 0;
-    if constexpr (MODE == kProjIn) {
-        if (n0 < kDnZRow) {
-            W = a.w_qkv + static_cast<int64_t>(n0) * kK;
-        } else if (n0 < kDnBRow) {
-            W = a.w_z + static_cast<int64_t>(n0 - kDnZRow) * kK;
-            seg = 1;
-        } else if (n0 < kDnARow) {
-            W = a.w_b + static_cast<int64_t>(n0 - kDnBRow) * kK;
-            seg = 2;
-        } else {
-            W = a.w_a + static_cast<int64_t>(n0 - kDnARow) * kK;
-            seg = 3;
-        }
-    } else {
-        W = a.w_out + static_cast<int64_t>(n0) * kK;
-    }
-
-    // the epilogue's small operands, fetched before the weights stream
-    const int tid = threadIdx.x;
-    const int row = (tid >> 4) & 15;
-    const int tt = tid & 15;
-    uint2 conv_w[kTiles] = {};
-    uint32_t conv_old[kTiles] = {};
-    float A[kTiles] = {}, dt[kTiles] = {};
-    if constexpr (MODE == kProjIn) {
-        if (seg == 0 && tid < 256) {
-#pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                const int n = n0 + u * kRows + row;
-                conv_w[u] = *reinterpret_cast<const uint2*>(a.conv_w + n * kDnTaps);
-                if (tt < kDnTaps) conv_old[u] = ldg_u16(a.conv_state + n * kDnTaps + tt);
-            }
-        } else if (seg == 3 && tid < 256) {
-#pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                const int h = n0 + u * kRows + row - kDnARow;
-                A[u] = bf2f(ldg_u16(a.A_log + h));
-                dt[u] = bf2f(ldg_u16(a.dt_bias + h));
-            }
-        }
-    }
-
-    uint4 wa[kTiles][16];
-    const bool row_live = t < kRows;
-#pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        const uint16_t* wrow = W + static_cast<int64_t>(u * kRows + t) * kK + k0;
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                wa[u][4 * s + j] = row_live ? ldg16(wrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    uint4 xb[16];
-    const uint16_t* xrow = a.x + static_cast<int64_t>(t) * kK + k0;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xb[4 * s + j] = t < T ? ldg16(xrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
-
-#pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc = mfma16x16x32(wa[u][i], xb[i], acc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[u][wave][4 * g + i][t] = acc[i];
-    }
-    __syncthreads();
-
-#pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        float p = 0.0f;
-        if (tid < 256) {
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) p += red[u][w][row][tt];
-        }
-        const int n = n0 + u * kRows + row;
-        if constexpr (MODE == kProjOut) {
-            if (tid < 256 && row < kRows && tt < T) a.out[static_cast<int64_t>(tt) * kHidden + n] = static_cast<uint16_t>(f2bf(p));
-        } else {
-            if (seg == 0) {
-                // causal conv over [cached 4 inputs, the T projections], SiLU;
-                // the cache keeps the last 4 (channel n belongs to this tile)
-                if (u > 0) __syncthreads();  // the previous tile's conv has read seq
-                seq[row][kDnTaps + tt] = static_cast<uint16_t>(f2bf(p));
-                if (tt < kDnTaps) seq[row][tt] = static_cast<uint16_t>(conv_old[u]);
-                __syncthreads();
-                if (tt < T) {
-                    const float w[kDnTaps] = {lo_bf(conv_w[u].x), hi_bf(conv_w[u].x), lo_bf(conv_w[u].y), hi_bf(conv_w[u].y)};
-                    float c = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < kDnTaps; ++j) c = __builtin_fmaf(w[j], bf2f(seq[row][tt + 1 + j]), c);
-                    a.act[static_cast<int64_t>(tt) * kDnConv + n] = static_cast<uint16_t>(f2bf(silu(rbf(c))));
-                    if (a.conv_record) {
-                        uint16_t* rec = a.conv_record + (static_cast<int64_t>(tt) * kDnConv + n) * kDnTaps;
-#pragma unroll
-                        for (int j = 0; j < kDnTaps; ++j) rec[j] = seq[row][tt + 1 + j];
-                    }
-                }
-                if (tt < kDnTaps) a.conv_state[n * kDnTaps + tt] = seq[row][T + tt];
-            } else if (tt < T) {
-                const uint32_t pb = f2bf(p);
-                if (seg == 1) {
-                    a.z[static_cast<int64_t>(tt) * kDnValue + (n - kDnZRow)] = static_cast<uint16_t>(pb);
-                } else if (seg == 2) {
-                    const int h = n - kDnBRow;
-                    a.beta[tt * kDnValueHeads + h] = static_cast<uint16_t>(f2bf(1.0f / (1.0f + lr_exp(-bf2f(pb)))));
-                } else {
-                    const int h = n - kDnARow;
-                    const float gv = -lr_exp(A[u]) * softplus(bf2f(pb) + dt[u]);
-                    a.G[tt * kDnValueHeads + h] = lr_exp(gv);
-                }
-            }
-        }
-    }
-}
 
 // Sum over the 16 lanes of a DPP row, the same total in every lane: xor
 // butterflies 1 and 2 (quad permutes), then the half-row and row mirrors,
@@ -398,25 +223,6 @@ __global__ __launch_bounds__(64) void dn_rule(DnRuleArgs a) {
     }
 }
 
-// The gated RMSNorm of the mixer ([HF] Qwen3_5MoeRMSNormGated 169-185) for
-// token blockIdx.y, value head blockIdx.x, one thread per element e:
-// n = bf16(o rsqrt(mean(o^2) + eps)), core = bf16(bf16(w n) silu(z)).  The
-// sum of squares: a butterfly per wave, then wave 0's sum plus wave 1's.
-__global__ __launch_bounds__(kDnWidth) void dn_gate_norm(const uint16_t* o, const uint16_t* z, const uint16_t* norm_w,
-                                                         float eps, uint16_t* core) {
-    __shared__ float part[kDnWidth / 64];
-    const int e = threadIdx.x;
-    const int64_t at = static_cast<int64_t>(blockIdx.y) * kDnValue + blockIdx.x * kDnWidth + e;
-    const float ov = bf2f(ldg_u16(o + at));
-    const float zv = bf2f(ldg_u16(z + at));
-    const float wv = bf2f(ldg_u16(norm_w + e));
-    const float s = wave_butterfly_sum(ov * ov);
-    if ((e & 63) == 0) part[e >> 6] = s;
-    __syncthreads();
-    const float r = 1.0f / __builtin_sqrtf((part[0] + part[1]) / static_cast<float>(kDnWidth) + eps);
-    core[at] = static_cast<uint16_t>(f2bf(rbf(wv * rbf(ov * r)) * silu(zv)));
-}
-
 template <int D>
 hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
     const StageEvents ev = timing_events(kStageDeltaRule);
@@ -427,6 +233,455 @@ hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
         LRMOE_LAUNCH((dn_rule<D, false, 1>), grid, dim3(64), 0, stream, ev.start, ev.stop, a);
     }
     return hipGetLastError();
+}
+
+// ---- the mixer step in one persistent launch (dn_mixer) ---------------------
+//
+// 256 workgroups of 8 waves, one per CU, all resident (the grid barriers
+// rely on it).  Everything that comes from HBM is requested at the start
+// or streamed in phase A, so the later phases touch only rows the launch
+// wrote itself:
+//
+//   start    the rule's state slab (waves 0-3), A_log and dt_bias;
+//   phase A  in_proj's qkv and z rows in 768 units of 16 rows, units
+//            b, b + 256, b + 512 requested at once (192 KiB per CU), each
+//            load instruction reading 1 KiB of one row (5.4 TB/s for the
+//            48 MiB on this part, against 3.9 TB/s when an instruction
+//            gathers the MFMA layout's 64 bytes from each of 16 rows); a
+//            unit passes through LDS into the MFMA layout, wave w
+//            multiplying k in [256 w, 256 w + 256); per unit the causal conv
+//            + SiLU, the conv-state update and z, written with agent-scope
+//            stores; into the registers of consumed units, head b / 8's
+//            in_proj_b and in_proj_a rows (its beta and G go to LDS: no
+//            other workgroup needs them) and out_proj rows 8b .. 8b + 7 (A
+//            operands of phase D);
+//   barrier
+//   phase B  the rule for (head b / 8, columns 16 (b % 8) .. +15): q and k
+//            staged and l2norm'd by the workgroup, waves 0-3 four columns
+//            each (dn_rule's arithmetic); outputs through LDS to agent-scope
+//            rows; the last of a head's 8 workgroups to count itself in
+//            (a monotonic counter, 8 per call) forms the head's gated
+//            RMSNorm (phase C);
+//   barrier
+//   phase D  out_proj rows 8b .. 8b + 7 from the registers loaded at the
+//            start and the normed rows.
+//
+// Barriers: one arrival counter (2 x 256 per call, never reset) and a
+// release word set by the arrival that completes a barrier, as moe_chain's.
+// Waits are bounded (50 ms); on expiry the launch still ends and sets
+// LRMOE_STATUS_TIMEOUT in the status word.
+
+constexpr int kMixGrid = 256;
+constexpr int kMixWaves = 8;
+constexpr int kMixThreads = 64 * kMixWaves;
+constexpr int kMixRows = 8;                                        // out_proj rows per workgroup
+constexpr int kMixInRows = 16;                                     // rows per in_proj unit
+constexpr int kMixInUnits = kDnBRow / kMixInRows;                  // 768: qkv and z rows
+constexpr int kMixUnitsPerWg = kMixInUnits / 256;                   // 3, all in flight at once
+constexpr int kMixRuleWaves = 4;
+constexpr int kMixHeadGroups = kDnWidth / (4 * kMixRuleWaves);    // 8 workgroups per head
+constexpr uint64_t kMixSpinTicks = 5000000;                        // 50 ms of the 100 MHz wall clock
+static_assert(kMixGrid == kDnValueHeads * kMixHeadGroups, "one rule unit per workgroup");
+static_assert(kMixGrid == kHidden / kMixRows, "one out_proj unit per workgroup");
+static_assert(kMixUnitsPerWg * kMixGrid == kMixInUnits && kMixUnitsPerWg == 3, "three in_proj units each");
+
+__device__ __forceinline__ const uint16_t* mix_row_ptr(const DnProjectArgs& a, int n) {
+    return n < kDnZRow ? a.w_qkv + static_cast<int64_t>(n) * kHidden : a.w_z + static_cast<int64_t>(n - kDnZRow) * kHidden;
+}
+
+template <bool BF16>
+__device__ __forceinline__ float state_at(const void* base, int64_t i) {
+    if constexpr (BF16) return bf2f(static_cast<const uint16_t*>(base)[i]);
+    else return static_cast<const float*>(base)[i];
+}
+
+template <bool BF16>
+__device__ __forceinline__ void state_put(void* base, int64_t i, float v) {
+    if constexpr (BF16) static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(f2bf(v));
+    else static_cast<float*>(base)[i] = v;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
+    const DnProjectArgs& a = m.p;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kMixInRows][kHidden + 8];  // one in_proj unit, row-major
+    __shared__ float red[kMixWaves][16][17];
+    __shared__ float red_ba[kMixWaves][2][16];
+    __shared__ uint16_t seq[kMixInRows][kDnTaps + 16];
+    __shared__ uint2 conv_lds[2][2][kMixInRows];  // [unit parity] per unit row: conv weights, cached conv inputs
+    __shared__ float gate_lds[2][kDnValueHeads];  // A_log, dt_bias
+    __shared__ float qs[kRuleStage][kDnWidth];
+    __shared__ float ks[kRuleStage][kDnWidth];
+    __shared__ float vs[kMixRuleWaves][kRuleStage][4];
+    __shared__ float gs[kRuleStage];
+    __shared__ float bs[kRuleStage];
+    __shared__ uint16_t os[kRuleStage][4 * kMixRuleWaves];
+    __shared__ unsigned long long base_s;
+    __shared__ int timeout_s;
+    __shared__ int last_s;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int t = lane & 15;
+    const int g = lane >> 4;
+    const int T = a.tokens;
+    const int b = blockIdx.x;
+    const bool live = t < kMixRows;  // this lane's MFMA row holds a weight row
+
+    // conv weights and cached inputs of a unit's rows (threads 0-31)
+    auto load_conv = [&](int v) -> uint2 {
+        const int n0 = kMixInRows * v;
+        if (tid < 2 * kMixInRows && n0 < kDnZRow)
+            return *reinterpret_cast<const uint2*>((tid < kMixInRows ? a.conv_w : a.conv_state) + (n0 + (tid & 15)) * kDnTaps);
+        return make_uint2(0u, 0u);
+    };
+    // A unit's rows as the memory system streams them best: each load
+    // instruction of a wave reads 1 KiB of one row (wave w: rows 2w, 2w + 1;
+    // load i: row 2w + i / 4, k from 512 (i % 4) + 8 lane).
+    auto load_unit = [&](uint4 (&w)[8], uint2& cv, int v) {
+        const uint16_t* row0 = mix_row_ptr(a, kMixInRows * v + 2 * wave) + 8 * lane;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
+        cv = load_conv(v);
+    };
+    // the three in_proj units first: nothing else is in the memory queue ahead of them
+    uint4 w0[8], w1[8], w2[8];
+    uint2 c0, c1, c2;
+    const int v0 = b, v1 = b + kMixGrid, v2 = b + 2 * kMixGrid;
+    load_unit(w0, c0, v0);
+    load_unit(w1, c1, v1);
+    load_unit(w2, c2, v2);
+
+    if (tid == 0) {
+        base_s = ld_agent64(m.arrive) / kMixGrid * kMixGrid;
+        timeout_s = 0;
+    }
+    if (tid < 2 * kDnValueHeads) gate_lds[tid >> 5][tid & 31] = bf2f(ldg_u16((tid < 32 ? a.A_log : a.dt_bias) + (tid & 31)));
+
+    // the rule's state: head rh, column rc, rows 8 rg .. 8 rg + 7 (waves 0-3)
+    const int rg = lane & 15;
+    const int cq = lane >> 4;
+    const int rh = b / kMixHeadGroups;
+    const int rc0 = 16 * (b % kMixHeadGroups);
+    const int rc = rc0 + 4 * wave + cq;
+    const int64_t slab = static_cast<int64_t>(rh) * kDnWidth * kDnWidth;
+    float S[8];
+    if (wave < kMixRuleWaves) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S[i] = state_at<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc);
+    }
+
+    // ---- phase A: in_proj (wave w multiplies k in [256 w, 256 w + 256)) ----
+    uint4 xb[8];
+    {
+        const uint16_t* xrow = a.x + static_cast<int64_t>(t) * kHidden + 256 * wave + 8 * g;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xb[4 * s + j] = t < T ? ldg16(xrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    auto load_rows = [&](uint4 (&w)[8], const uint16_t* row0, bool have) {
+        const uint16_t* wrow = row0 + 256 * wave + 8 * g;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[4 * s + j] = have ? ldg16(wrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    // The unit's rows through LDS into the MFMA layout, its partial tile
+    // into red (rows 4 g + i, token t).  The caller's next barrier (the
+    // epilogue's first) ends the reads of `tile`.
+    auto unit_mfma = [&](const uint4 (&w)[8], uint2 cv, int v, int slot) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&tile[2 * wave + (i >> 2)][512 * (i & 3) + 8 * lane]) = w[i];
+        __syncthreads();
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = mfma16x16x32(*reinterpret_cast<const uint4*>(&tile[t][256 * wave + 128 * s + 32 * j + 8 * g]),
+                                   xb[4 * s + j], acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][4 * g + i][t] = acc[i];
+        if (tid < 2 * kMixInRows && kMixInRows * v < kDnZRow) conv_lds[slot][tid >> 4][tid & 15] = cv;
+    };
+    auto unit_epilogue = [&](int v, int slot) {
+        const int n0 = kMixInRows * v;
+        __syncthreads();
+        if (tid < 16 * kMixInRows) {
+            const int row = tid >> 4;
+            const int tt = tid & 15;
+            float p = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < kMixWaves; ++ww) p += red[ww][row][tt];
+            seq[row][kDnTaps + tt] = static_cast<uint16_t>(f2bf(p));
+            if (n0 < kDnZRow && tt < kDnTaps) {
+                const uint2 old = conv_lds[slot][1][row];
+                seq[row][tt] = static_cast<uint16_t>(((tt < 2 ? old.x : old.y) >> (16 * (tt & 1))) & 0xffffu);
+            }
+        }
+        __syncthreads();
+        // waves 0-1: rows in pairs (one 4-byte store per token and pair).
+        // The next unit writes red and seq only after its own first barrier,
+        // which these waves reach after this, and the other conv_lds slot.
+        if (tid < 8 * 16) {
+            const int rp = tid >> 4;
+            const int tt = tid & 15;
+            if (tt < T) {
+                if (n0 < kDnZRow) {
+                    uint32_t pair = 0;
+#pragma unroll
+                    for (int r2 = 0; r2 < 2; ++r2) {
+                        const int rr = 2 * rp + r2;
+                        const uint2 cw = conv_lds[slot][0][rr];
+                        const float wv[kDnTaps] = {lo_bf(cw.x), hi_bf(cw.x), lo_bf(cw.y), hi_bf(cw.y)};
+                        float c = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < kDnTaps; ++j) c = __builtin_fmaf(wv[j], bf2f(seq[rr][tt + 1 + j]), c);
+                        pair |= f2bf(silu(rbf(c))) << (16 * r2);
+                        if (a.conv_record) {
+                            uint16_t* rec = a.conv_record + (static_cast<int64_t>(tt) * kDnConv + n0 + rr) * kDnTaps;
+#pragma unroll
+                            for (int j = 0; j < kDnTaps; ++j) rec[j] = seq[rr][tt + 1 + j];
+                        }
+                    }
+                    st_agent32(a.act + static_cast<int64_t>(tt) * kDnConv + n0 + 2 * rp, pair);
+                } else {
+                    st_agent32(a.z + static_cast<int64_t>(tt) * kDnValue + (n0 - kDnZRow) + 2 * rp,
+                               static_cast<uint32_t>(seq[2 * rp][kDnTaps + tt]) |
+                                   (static_cast<uint32_t>(seq[2 * rp + 1][kDnTaps + tt]) << 16));
+                }
+            }
+        }
+        if (n0 < kDnZRow && tid >= 128 && tid < 128 + kMixInRows * kDnTaps) {
+            const int rr = (tid - 128) >> 2;
+            const int j = tid & 3;
+            a.conv_state[(n0 + rr) * kDnTaps + j] = seq[rr][T + j];
+        }
+    };
+    uint4 wo[16];  // out_proj rows 8b + t (t < 8), k in [512 wave, 512 wave + 512): phase D's A operands
+    {
+        unit_mfma(w0, c0, v0, 0);
+        // head rh's b row (MFMA row 0) and a row (row 1), into w0's registers
+        load_rows(w0, (t == 0 ? a.w_b : a.w_a) + static_cast<int64_t>(rh) * kHidden, t < 2);
+        unit_epilogue(v0, 0);
+        unit_mfma(w1, c1, v1, 1);
+        unit_epilogue(v1, 1);
+        unit_mfma(w2, c2, v2, 0);
+        // every in_proj load is issued and w1, w2 are consumed: out_proj's
+        // rows stream from here on
+        {
+            const uint16_t* wrow = a.w_out + static_cast<int64_t>(kMixRows * b + (live ? t : 0)) * kDnValue + 512 * wave + 8 * g;
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wo[4 * s + j] = live ? ldg16(wrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        unit_epilogue(v2, 0);
+        {
+            // beta and G of head rh for every token, from its b and a rows
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc = mfma16x16x32(w0[i], xb[i], acc);
+            if (g == 0) {
+                red_ba[wave][0][t] = acc[0];
+                red_ba[wave][1][t] = acc[1];
+            }
+            __syncthreads();
+            if (tid < 2 * 16) {
+                const int row = tid >> 4;  // 0: b, 1: a
+                const int tt = tid & 15;
+                float p = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < kMixWaves; ++ww) p += red_ba[ww][row][tt];
+                const float pb = rbf(p);
+                if (row == 0) bs[tt] = rbf(1.0f / (1.0f + lr_exp(-pb)));
+                else gs[tt] = lr_exp(-lr_exp(gate_lds[0][rh]) * softplus(pb + gate_lds[1][rh]));
+            }
+        }
+    }
+
+    auto grid_sync = [&](unsigned long long target) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's agent-scope stores are complete
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned long long before =
+                __hip_atomic_fetch_add(m.arrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (before + 1 == target) st_agent64(m.release, target);
+            const uint64_t start = wall_clock64();
+            while (ld_agent64(m.release) < target) {
+                if (wall_clock64() - start > kMixSpinTicks) {
+                    timeout_s = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+    };
+    const unsigned long long base = base_s;
+    grid_sync(base + kMixGrid);
+
+    // ---- phase B: the rule for head rh, columns rc0 .. rc0 + 15 ----
+    {
+        const int kh = rh >> 1;  // value head h reads key head h / 2
+        if (tid < 16 * T) {
+            const int tt = tid >> 4;
+            const int ch = tid & 15;
+            const uint32_t qoff = static_cast<uint32_t>((tt * kDnConv + kh * kDnWidth + ch * 8) * 2);
+            unpack8(ld_agent16(a.act, qoff), &qs[tt][ch * 8]);
+            unpack8(ld_agent16(a.act, qoff + kDnKey * 2), &ks[tt][ch * 8]);
+        } else if (tid >= 256 && tid < 256 + kMixRuleWaves * T) {
+            const int i = tid - 256;
+            const int w = i & 3;
+            const int tt = i >> 2;
+            const uint64_t v4 = ld_agent64(a.act + static_cast<int64_t>(tt) * kDnConv + 2 * kDnKey + rh * kDnWidth + rc0 + 4 * w);
+            const uint32_t lo = static_cast<uint32_t>(v4), hi = static_cast<uint32_t>(v4 >> 32);
+            vs[w][tt][0] = lo_bf(lo); vs[w][tt][1] = hi_bf(lo); vs[w][tt][2] = lo_bf(hi); vs[w][tt][3] = hi_bf(hi);
+        }
+        __syncthreads();
+        {
+            const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kDnWidth));
+            const int tt = tid >> 4;  // one DPP row per token
+            if (tt < T) {
+                float* qrow = &qs[tt][8 * rg];
+                float* krow = &ks[tt][8 * rg];
+                float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    sq += rbf(qrow[i] * qrow[i]);
+                    sk += rbf(krow[i] * krow[i]);
+                }
+                sq = row_sum16(sq);
+                sk = row_sum16(sk);
+                const float iq = rbf(1.0f / __builtin_sqrtf(rbf(rbf(sq) + 1e-6f)));
+                const float ik = rbf(1.0f / __builtin_sqrtf(rbf(rbf(sk) + 1e-6f)));
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    qrow[i] = rbf(qrow[i] * iq) * scale;
+                    krow[i] = rbf(krow[i] * ik);
+                }
+            }
+        }
+        __syncthreads();
+        if (wave < kMixRuleWaves) {
+            for (int tt = 0; tt < T; ++tt) {
+                float q[8], k[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    q[i] = qs[tt][8 * rg + i];
+                    k[i] = ks[tt][8 * rg + i];
+                }
+                const float G = gs[tt];
+                const float beta = bs[tt];
+                float mem = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    S[i] = S[i] * G;
+                    mem = mem + S[i] * k[i];
+                }
+                const float delta = (vs[wave][tt][cq] - row_sum16(mem)) * beta;
+                float o = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    S[i] = S[i] + k[i] * delta;
+                    o = o + S[i] * q[i];
+                }
+                o = row_sum16(o);
+                if (rg == 0) os[tt][4 * wave + cq] = static_cast<uint16_t>(f2bf(o));
+                if constexpr (BF16) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) S[i] = rbf(S[i]);
+                }
+                if (m.state_record) {
+                    const int64_t rec = static_cast<int64_t>(tt) * kDnValueHeads * kDnWidth * kDnWidth + slab;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) state_put<BF16>(m.state_record, rec + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc, S[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) state_put<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc, S[i]);
+        }
+        __syncthreads();
+        if (tid < 4 * T) {
+            const int tt = tid >> 2;
+            const int q4 = tid & 3;
+            const uint64_t w4 = static_cast<uint64_t>(os[tt][4 * q4]) | (static_cast<uint64_t>(os[tt][4 * q4 + 1]) << 16) |
+                                (static_cast<uint64_t>(os[tt][4 * q4 + 2]) << 32) |
+                                (static_cast<uint64_t>(os[tt][4 * q4 + 3]) << 48);
+            st_agent64(m.o + static_cast<int64_t>(tt) * kDnValue + rh * kDnWidth + rc0 + 4 * q4, w4);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned long long before =
+                __hip_atomic_fetch_add(m.heads + rh, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = (before + 1) % kMixHeadGroups == 0;
+        }
+        __syncthreads();
+        // ---- phase C (the head's last workgroup): gated RMSNorm of head rh ----
+        if (last_s) {
+            const int tt = tid >> 5;
+            const int q4 = tid & 31;
+            const bool act_t = tt < T;
+            const int64_t at = static_cast<int64_t>(tt) * kDnValue + rh * kDnWidth + 4 * q4;
+            float ov[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (act_t) {
+                const uint64_t o4 = ld_agent64(m.o + at);
+                ov[0] = lo_bf(static_cast<uint32_t>(o4)); ov[1] = hi_bf(static_cast<uint32_t>(o4));
+                ov[2] = lo_bf(static_cast<uint32_t>(o4 >> 32)); ov[3] = hi_bf(static_cast<uint32_t>(o4 >> 32));
+            }
+            float sq = ov[0] * ov[0] + ov[1] * ov[1] + ov[2] * ov[2] + ov[3] * ov[3];
+            sq = sq + __int_as_float(lane_xor<1>(__float_as_int(sq)));
+            sq = sq + __int_as_float(lane_xor<2>(__float_as_int(sq)));
+            sq = sq + __int_as_float(lane_xor<4>(__float_as_int(sq)));
+            sq = sq + __int_as_float(lane_xor<8>(__float_as_int(sq)));
+            sq = sq + __int_as_float(lane_xor<16>(__float_as_int(sq)));
+            if (act_t) {
+                const float r = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kDnWidth) + a.eps);
+                const uint64_t z4 = ld_agent64(a.z + at);
+                const uint2 w4 = *reinterpret_cast<const uint2*>(a.norm_w + 4 * q4);
+                const float zv[4] = {lo_bf(static_cast<uint32_t>(z4)), hi_bf(static_cast<uint32_t>(z4)),
+                                     lo_bf(static_cast<uint32_t>(z4 >> 32)), hi_bf(static_cast<uint32_t>(z4 >> 32))};
+                const float wv[4] = {lo_bf(w4.x), hi_bf(w4.x), lo_bf(w4.y), hi_bf(w4.y)};
+                uint64_t c4 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    c4 |= static_cast<uint64_t>(f2bf(rbf(wv[i] * rbf(ov[i] * r)) * silu(zv[i]))) << (16 * i);
+                st_agent64(m.core + at, c4);
+            }
+        }
+    }
+    grid_sync(base + 2 * kMixGrid);
+
+    // ---- phase D: out_proj rows 8b .. 8b + 7 ----
+    {
+        uint4 cb[16];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                cb[4 * s + j] = t < T ? ld_agent16(m.core, static_cast<uint32_t>((t * kDnValue + 512 * wave + 128 * s + 32 * j + 8 * g) * 2))
+                                      : make_uint4(0u, 0u, 0u, 0u);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = mfma16x16x32(wo[i], cb[i], acc);
+        if (g < 2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][4 * g + i][t] = acc[i];
+        }
+        __syncthreads();
+        if (tid < 16 * kMixRows) {
+            const int row = tid >> 4;
+            const int tt = tid & 15;
+            float p = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < kMixWaves; ++ww) p += red[ww][row][tt];
+            if (tt < T) a.out[static_cast<int64_t>(tt) * kHidden + kMixRows * b + row] = static_cast<uint16_t>(f2bf(p));
+        }
+    }
+    if (tid == 0 && timeout_s) atomicOr(m.status, LRMOE_STATUS_TIMEOUT);
 }
 
 }  // namespace
@@ -447,11 +702,17 @@ size_t delta_workspace_bytes(int tokens) {
 
 DeltaWorkspace carve_delta(void* base, int tokens) {
     DeltaWorkspace w{};
-    size_t off = 0;
+    uint8_t* p = static_cast<uint8_t*>(base);
+    // control block (fixed offsets whatever the token count; zero at allocation)
+    w.status = reinterpret_cast<int32_t*>(p + kDeltaWsStatus);
+    w.arrive = reinterpret_cast<unsigned long long*>(p + kDeltaWsArrive);
+    w.release = reinterpret_cast<unsigned long long*>(p + kDeltaWsRelease);
+    w.heads = reinterpret_cast<unsigned long long*>(p + kDeltaWsHeads);
+    size_t off = kDeltaWsControl;
     auto take = [&](size_t bytes) {
         const size_t at = off;
         off += (bytes + 255) & ~static_cast<size_t>(255);
-        return static_cast<uint8_t*>(base) + at;
+        return p + at;
     };
     const size_t T = static_cast<size_t>(tokens);
     w.act = reinterpret_cast<uint16_t*>(take(T * kDnConv * 2));
@@ -464,50 +725,38 @@ DeltaWorkspace carve_delta(void* base, int tokens) {
     return w;
 }
 
-hipError_t launch_delta_mixer(DnProjectArgs p, const void* state, bool state_bf16, void* state_record,
+hipError_t launch_delta_mixer(DnProjectArgs p, void* state, bool state_bf16, void* state_record,
                               const DeltaWorkspace& w, hipStream_t stream) {
+    static int cus[64] = {0};
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    if (cus[device] == 0) {
+        err = hipDeviceGetAttribute(&cus[device], hipDeviceAttributeMultiprocessorCount, device);
+        if (err != hipSuccess) return err;
+    }
+    // one workgroup per CU, all resident: the grid barriers need 256 CUs
+    if (cus[device] < kMixGrid) return hipErrorNotSupported;
+    DnMixerArgs m{};
     p.act = w.act;
     p.z = w.z;
     p.beta = w.beta;
     p.G = w.G;
-    {
-        const StageEvents ev = timing_events(kStageDeltaIn);
-        LRMOE_LAUNCH((dn_project<kProjIn>), dim3(kDnProjRows / (ProjShape<kProjIn>::kRows * ProjShape<kProjIn>::kTiles)),
-                     dim3(ProjShape<kProjIn>::kWaves * 64), 0, stream, ev.start, ev.stop, p);
-        const hipError_t err = hipGetLastError();
-        if (err != hipSuccess) return err;
-    }
-    DnRuleArgs r{};
-    r.q = w.act;
-    r.k = w.act + kDnKey;
-    r.v = w.act + 2 * kDnKey;
-    r.qk_stride = kDnConv;
-    r.v_stride = kDnConv;
-    r.kv_shift = 1;  // value head h reads key head h / 2 (repeat_interleave by 2)
-    r.G = w.G;
-    r.beta = w.beta;
-    r.initial = state;
-    r.final_state = const_cast<void*>(state);
-    r.record = state_record;
-    r.out = w.o;
-    r.tokens = p.tokens;
-    r.heads = kDnValueHeads;
-    r.width = kDnWidth;
-    r.normalize = 1;
-    hipError_t err = launch_rule_d<kDnWidth>(r, state_bf16, stream);
-    if (err != hipSuccess) return err;
-    {
-        const StageEvents ev = timing_events(kStageDeltaNorm);
-        LRMOE_LAUNCH(dn_gate_norm, dim3(kDnValueHeads, p.tokens), dim3(kDnWidth), 0, stream, ev.start, ev.stop, w.o, w.z,
-                     p.norm_w, p.eps, w.core);
-        err = hipGetLastError();
-        if (err != hipSuccess) return err;
-    }
-    p.x = w.core;
-    {
-        const StageEvents ev = timing_events(kStageDeltaOut);
-        LRMOE_LAUNCH((dn_project<kProjOut>), dim3(kHidden / (ProjShape<kProjOut>::kRows * ProjShape<kProjOut>::kTiles)),
-                     dim3(ProjShape<kProjOut>::kWaves * 64), 0, stream, ev.start, ev.stop, p);
+    m.p = p;
+    m.state = state;
+    m.state_record = state_record;
+    m.o = w.o;
+    m.core = w.core;
+    m.status = w.status;
+    m.arrive = w.arrive;
+    m.release = w.release;
+    m.heads = w.heads;
+    const StageEvents ev = timing_events(kStageDeltaMixer);
+    if (state_bf16) {
+        LRMOE_LAUNCH(dn_mixer<true>, dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+    } else {
+        LRMOE_LAUNCH(dn_mixer<false>, dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
     }
     return hipGetLastError();
 }

@@ -311,4 +311,47 @@ __device__ __forceinline__ uint32_t block_scan256(uint32_t value, uint32_t* scra
     return tid < kExperts ? before + inclusive - value : 0u;
 }
 
+// ---- agent-scope memory operations (coherent across the XCDs' L2s) -----------
+//
+// Rows that one workgroup writes and a workgroup of the same launch on
+// another XCD reads go through these: agent-scope (sc1) stores and loads.
+
+typedef __attribute__((address_space(1))) uint64_t g_u64;
+typedef __attribute__((address_space(1))) uint32_t g_u32;
+
+__device__ __forceinline__ g_u64* as_g64(const void* p) {
+    return reinterpret_cast<g_u64*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ g_u32* as_g32(const void* p) {
+    return reinterpret_cast<g_u32*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void st_agent64(void* p, uint64_t v) {
+    __hip_atomic_store(as_g64(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent64(const void* p) {
+    return __hip_atomic_load(as_g64(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
+    __hip_atomic_store(as_g32(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent32(const void* p) {
+    return __hip_atomic_load(as_g32(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at base + byte_offset with an agent-scope (sc1) buffer load.
+__device__ __forceinline__ uint4 ld_agent16(const void* base, uint32_t byte_offset) {
+    // Raw buffer over 2 GiB from base; dword 3 = gfx9 untyped 32-bit data format.
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+    constexpr int kSc1 = 16;  // cache policy: sc1 (agent scope)
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(byte_offset), 0, kSc1);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// A wave-uniform copy of a 64-bit value (each half through readfirstlane,
+// whose int result is taken as unsigned before widening).
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
 }  // namespace lrmoe

@@ -277,10 +277,8 @@ enum Stage : int {
     kStageCombine = 8,
     kStageGather = 16,
     kStageLayer = 32,
-    kStageDeltaIn = 64,     // Gated DeltaNet: in_proj + conv
-    kStageDeltaRule = 128,  // Gated DeltaNet: the delta rule
-    kStageDeltaOut = 256,   // Gated DeltaNet: out_proj
-    kStageDeltaNorm = 512,  // Gated DeltaNet: gated RMSNorm
+    kStageDeltaMixer = 64,  // Gated DeltaNet: the mixer step (dn_mixer)
+    kStageDeltaRule = 128,  // Gated DeltaNet: the delta rule (dn_rule)
 };
 struct StageEvents {
     hipEvent_t start = nullptr;
@@ -339,10 +337,9 @@ hipError_t launch_fill_normal(uint16_t* out, int64_t count, uint64_t seed, uint6
 
 // ---- Gated DeltaNet decode (delta.hip) ----
 
-// Arguments of the mixer's two projection kernels (in_proj with the conv /
-// beta / G epilogue, and out_proj).
+// Weights, states and rows of one mixer step.
 struct DnProjectArgs {
-    const uint16_t* x;        // input [T][K]: hidden (in_proj), the gated-norm output (out_proj)
+    const uint16_t* x;        // hidden [T][2048]
     const uint16_t* w_qkv;    // in_proj_qkv [8192][2048]
     const uint16_t* w_z;      // in_proj_z [4096][2048]
     const uint16_t* w_b;      // in_proj_b [32][2048]
@@ -385,6 +382,10 @@ struct DnRuleArgs {
 };
 
 struct DeltaWorkspace {
+    int32_t* status;               // LRMOE_STATUS_TIMEOUT when a wait expired
+    unsigned long long* arrive;    // grid-barrier arrivals (2 x 256 per call, never reset)
+    unsigned long long* release;   // the arrival count the last completed barrier reached
+    unsigned long long* heads;     // [32] rule workgroups done per head (8 per call, never reset)
     uint16_t* act;
     uint16_t* z;
     uint16_t* beta;
@@ -394,11 +395,31 @@ struct DeltaWorkspace {
     size_t bytes;
 };
 
+// Offsets of the mixer workspace's control block (each counter in its own
+// 256-byte block).
+constexpr size_t kDeltaWsStatus = 0;
+constexpr size_t kDeltaWsArrive = 256;
+constexpr size_t kDeltaWsRelease = 512;
+constexpr size_t kDeltaWsHeads = 768;
+constexpr size_t kDeltaWsControl = 1024;
+
+struct DnMixerArgs {
+    DnProjectArgs p;
+    void* state;
+    void* state_record;
+    uint16_t* o;
+    uint16_t* core;
+    int32_t* status;
+    unsigned long long* arrive;
+    unsigned long long* release;
+    unsigned long long* heads;
+};
+
 constexpr int kDeltaMaxTokens = 16;
 DeltaWorkspace carve_delta(void* base, int tokens);
 size_t delta_workspace_bytes(int tokens);
 hipError_t launch_delta_rule(const DnRuleArgs& a, int key_width, bool state_bf16, hipStream_t stream);
-hipError_t launch_delta_mixer(DnProjectArgs p, const void* state, bool state_bf16, void* state_record,
+hipError_t launch_delta_mixer(DnProjectArgs p, void* state, bool state_bf16, void* state_record,
                               const DeltaWorkspace& w, hipStream_t stream);
 
 }  // namespace lrmoe

@@ -11,7 +11,7 @@
 namespace lrmoe {
 namespace {
 
-constexpr int kStages = 10;  // LRMOE_STAGE_* bits 0..9
+constexpr int kStages = 8;  // LRMOE_STAGE_* bits 0..7
 
 struct Timing {
     int mask = 0;

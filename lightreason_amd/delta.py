@@ -6,9 +6,10 @@ before the MoE block in 30 of the 40 decoder layers of the 35B model.
   edge35b/delta_decode.py:38-55 (``_run``): one ``lrmoe_delta_rule`` launch.
 * ``DeltaMixer`` -- a ``Qwen3_5MoeGatedDeltaNet``'s weights ([HF] 385-428)
   bound to ``lrmoe_delta_mixer``: ``step`` runs one cached forward of 1..16
-  tokens ([HF] 430-543 with a previous state) as three kernels (in_proj with
-  conv/beta/g, the delta rule, gated RMSNorm with out_proj), updating the
-  conv and recurrent states in place.
+  tokens ([HF] 430-543 with a previous state) as one persistent launch
+  (in_proj with conv/beta/g, the delta rule, the gated RMSNorm, out_proj),
+  updating the conv and recurrent states in place; ``mixer_status`` reads
+  its timeout bit.
 * ``PrefixStates`` -- the per-token states of the last recorded block of
   every linear-attention layer, and ``commit`` to roll the cache back to an
   accepted speculative prefix (delta_decode.py:58-81).
@@ -94,13 +95,25 @@ _WORKSPACES: dict = {}
 def _workspace(device: torch.device) -> torch.Tensor:
     """Scratch for lrmoe_delta_mixer on the current stream of `device`
     (sized for 16 tokens, so its address never changes; one per stream, as
-    calls sharing a workspace must not overlap)."""
+    calls sharing a workspace must not overlap; zeroed once, as its
+    barrier counters and status word require)."""
     key = (device, _stream(device))
     ws = _WORKSPACES.get(key)
     if ws is None:
         nbytes = int(_native.library().lrmoe_delta_workspace_bytes(MAX_TOKENS))
-        ws = _WORKSPACES[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws = _WORKSPACES[key] = torch.zeros(nbytes, dtype=torch.uint8, device=device)
     return ws
+
+
+def mixer_status(device=None) -> int:
+    """The status word of the current stream's mixer workspace (reads the
+    device): LRMOE_STATUS_TIMEOUT once a call's bounded wait expired (its
+    outputs invalid; a kernel on another stream kept workgroups off the
+    GPU), 0 otherwise."""
+    device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    ws = _workspace(device)
+    off = _native.DELTA_WS_STATUS_OFFSET
+    return int(ws[off:off + 4].view(torch.int32).item())
 
 
 class DeltaMixer:

@@ -185,6 +185,8 @@ def _oracle_chain(oracle, w, x, conv, state):
 @pytest.mark.parametrize("bf16_state", [False, True])
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_delta_mixer_against_oracle(oracle, device, mixer_case, T, bf16_state):
+    from lightreason_amd.delta import mixer_status
+
     w, mixer, conv0, s0 = mixer_case
     what = f"delta_mixer T={T} bf16_state={bf16_state}"
     print(f"[case] {what}", flush=True)
@@ -203,6 +205,7 @@ def test_delta_mixer_against_oracle(oracle, device, mixer_case, T, bf16_state):
     state_rec = torch.empty((T, 32, 128, 128), dtype=state.dtype, device=device)
     out = mixer.step(_dev_bf16(x, device), conv, state, conv_record=conv_rec, state_record=state_rec)
     torch.cuda.synchronize()
+    assert mixer_status(device) == 0
     assert_close_bf16(_bits(out), want_out, what=what)
     _conv_close(_bits(conv), want_convs[-1], what)
     _conv_close(_bits(conv_rec), want_convs, what + " record")
