@@ -28,7 +28,12 @@
  *     them off the GPU.  Every such wait is bounded (50 ms); on expiry the
  *     call still ends, sets LRMOE_STATUS_TIMEOUT in the status word, and
  *     its outputs are invalid.  Callers that share the device with other
- *     streams read the status word after such calls.
+ *     streams read the status word after such calls;
+ *   - the prefill expert stage (tokens > 16) is one launch whose workgroups
+ *     claim work items from counters, down items after the gate/up items
+ *     they read; a claimed gate/up item never waits, so its waits end
+ *     whether or not every workgroup is resident, and they are bounded in
+ *     the same way.
  *
  * Fixed model shape: hidden 2048, 256 routed experts, top-8, expert
  * intermediate 512, one shared expert with intermediate 512.  A routed
@@ -316,8 +321,8 @@ int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t
  * synchronises on those events and returns the summed milliseconds and the
  * launch count, then rewinds. */
 #define LRMOE_STAGE_ROUTE 1
-#define LRMOE_STAGE_GATE_UP 2
-#define LRMOE_STAGE_DOWN 4
+#define LRMOE_STAGE_GATE_UP 2      /* the prefill expert launch (gate/up and down items, tokens > 16) */
+#define LRMOE_STAGE_DOWN 4         /* kept for the mask layout: no launch is timed under it */
 #define LRMOE_STAGE_COMBINE 8
 #define LRMOE_STAGE_GATHER 16
 #define LRMOE_STAGE_LAYER 32       /* lrmoe_moe_layer / lrmoe_moe_chain decode kernel */

@@ -337,10 +337,14 @@ __device__ __forceinline__ void st_agent32(void* p, uint32_t v) {
 __device__ __forceinline__ uint32_t ld_agent32(const void* p) {
     return __hip_atomic_load(as_g32(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16 bytes at base + byte_offset with an agent-scope (sc1) buffer load.
-__device__ __forceinline__ uint4 ld_agent16(const void* base, uint32_t byte_offset) {
-    // Raw buffer over 2 GiB from base; dword 3 = gfx9 untyped 32-bit data format.
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+// 16 bytes at base + byte_offset with an agent-scope (sc1) buffer load from a
+// raw buffer of `bytes` bytes at base: a load at or past the end reads zeros
+// and touches no memory (the buffer's range check), so callers need no
+// branch around it.
+__device__ __forceinline__ uint4 ld_agent16(const void* base, uint32_t byte_offset, uint32_t bytes = 0x7fffffffu) {
+    // dword 3 = gfx9 untyped 32-bit data format
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
     constexpr int kSc1 = 16;  // cache policy: sc1 (agent scope)
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(byte_offset), 0, kSc1);
     return make_uint4(v.x, v.y, v.z, v.w);

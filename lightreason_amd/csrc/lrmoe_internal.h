@@ -74,7 +74,8 @@ struct Control {
     int32_t status;
     int32_t unique;
     int32_t n_units;    // prefill work units of the current plan
-    uint32_t reserved[60];
+    uint32_t claim[8];  // prefill: items claimed from each of the 8 work lists (zeroed by pf_fill)
+    uint32_t reserved[52];
 };
 
 // Route plan: unique experts ascending, per-expert (token, slot) pairs in
@@ -113,6 +114,8 @@ struct Workspace {
     uint32_t* blk_base;   // prefill: [256][nblk_pad] pairs of the expert before the block
     int32_t* bstatus;     // prefill: [nblk] route status per block
     int4* units;          // prefill: work units (expert + 1 or 0 = shared, first pair, pairs, 0)
+    uint32_t* unit_done;  // prefill: gate/up items done per work unit (zeroed by pf_fill)
+    int max_units;
     int nblk_pad;
     size_t bytes;
 };
@@ -163,6 +166,8 @@ inline Workspace carve(void* base, int tokens) {
     ws.bstatus = reinterpret_cast<int32_t*>(take(nblk * 4));
     const size_t units = (T + kPassTok - 1) / kPassTok + 256 + (8 * T + kPassTok - 1) / kPassTok + 8;
     ws.units = reinterpret_cast<int4*>(take(units * sizeof(int4)));
+    ws.unit_done = reinterpret_cast<uint32_t*>(take(units * sizeof(uint32_t)));
+    ws.max_units = static_cast<int>(units);
     ws.plan.unique = &ws.control->unique;
     ws.plan.status = &ws.control->status;
     ws.bytes = offset;

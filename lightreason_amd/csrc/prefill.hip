@@ -11,8 +11,10 @@
 //   pf_fill   expert offsets and ranks, every route placed, and the list of
 //             work units (slot, first pair) of at most kPassTok tokens.
 //
-// Experts (cpu_experts.c:54-69 rounding points; the shared expert is slot 0):
-//   pf_gateup one workgroup per (unit, 128-row tile): 128 gate + 128 up rows
+// Experts (cpu_experts.c:54-69 rounding points; the shared expert is slot 0),
+// one persistent launch (pf_experts) whose workgroups take, from 8 work
+// lists, gate/up items and then down items:
+//   gate/up   one item per (unit, 128-row tile): 128 gate + 128 up rows
 //             of one expert against up to 128 tokens.  Each of the 8 waves
 //             streams its 32 weight rows (16 gate, 16 up) from HBM straight
 //             into MFMA A operands, two K-chunks ahead; the same waves stage
@@ -20,13 +22,16 @@
 //             in registers), shared by all 8 waves, so a weight byte is read
 //             once per 128 tokens and feeds up to 8 16x16x32 MFMAs.  SwiGLU
 //             in the epilogue, act rows out.
-//   pf_down   one workgroup per (unit, 128-row tile): the tile's down rows over
-//             k = 512 stay in registers while the unit's act rows pass through
-//             LDS 64 at a time; y rows out (bf16).
+//   down      one item per (unit, 512 output rows): the unit's act rows are
+//             staged in LDS once, then 4 tiles of 128 down rows over k = 512
+//             pass through registers, each wave loading the next tile's rows
+//             while it multiplies the current one; y rows out (bf16).
 //   The ordered combine is experts.hip's combine_kernel.
 //
-// The 8 (or 16) tiles of a unit run on one XCD (workgroup b runs on XCD
-// b % 8), so the unit's token or act rows are fetched into that XCD's L2 once.
+// A unit's items are on one list, served by the workgroups b with
+// b % 8 = the list (on XCD b % 8), so the unit's token and act rows are
+// fetched into one XCD's L2.  Act rows go out and come back with
+// agent-scope stores and loads, so results do not depend on that placement.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
@@ -43,9 +48,12 @@ constexpr int kXsStride = kGuChunk + 8;    // LDS token row stride (bf16)
 constexpr int kDnThreads = 512;            // down workgroup: 8 waves of 16 output rows
 constexpr int kDnRows = kDnThreads / kWave * 16;  // 128 output rows per down workgroup
 constexpr int kDnTiles = kHidden / kDnRows;       // 16 down tiles per expert
-constexpr int kDnTok = 64;                 // act rows per LDS pass
-constexpr int kDnPieces = kDnTok * (kInner / 8) / kDnThreads;  // 16-byte act pieces per thread per pass
+constexpr int kDnItemTiles = 4;                   // tiles per down item
+constexpr int kDnItems = kDnTiles / kDnItemTiles; // 4 down items per unit
+constexpr int kDnPieces = kPassTok * (kInner / 8) / kDnThreads;  // 16-byte act pieces per thread: a whole unit
 constexpr int kActStride = kInner + 8;     // LDS act row stride (bf16)
+constexpr uint64_t kPfSpinTicks = 5000000; // 50 ms of the 100 MHz wall clock
+constexpr int32_t kStatusTimeoutPf = LRMOE_STATUS_TIMEOUT;
 
 // ---- plan ----------------------------------------------------------------------
 
@@ -135,7 +143,13 @@ __global__ __launch_bounds__(256) void pf_fill(const int64_t* indices, int token
             plan.offset[0] = 0;
             ws.control->n_units = 0;
         }
+        if (blk == 0 && threadIdx.x < 8) ws.control->claim[threadIdx.x] = 0u;
         return;
+    }
+    if (blk == 0) {
+        // pf_experts' claim counters and per-unit gate/up counts, for this call
+        for (int i = threadIdx.x; i < ws.max_units; i += 256) ws.unit_done[i] = 0u;
+        if (threadIdx.x < 8) ws.control->claim[threadIdx.x] = 0u;
     }
     const uint32_t count = ws.counts[e];
     uint32_t pairs = 0, unique = 0;
@@ -199,9 +213,19 @@ struct Unit {
     int count;              // pairs in the unit, 1..kPassTok
 };
 
+// The unit table, the unit count and the expert table are written before
+// the expert launch and only read during it: they are read through the
+// constant address space, so a wave-uniform lookup is a scalar load, counted
+// apart from the vector loads that stream weights and rows.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+    return *reinterpret_cast<const __attribute__((address_space(4))) T*>(reinterpret_cast<uintptr_t>(p));
+}
+
 __device__ __forceinline__ bool load_unit(const ExpertArgs& a, int u, Unit& w) {
-    if (u >= a.ws.control->n_units) return false;
-    const int4 unit = a.ws.units[u];
+    if (u >= ld_const(&a.ws.control->n_units)) return false;
+    const int* rec = reinterpret_cast<const int*>(a.ws.units + u);
+    const int4 unit = make_int4(ld_const(rec), ld_const(rec + 1), ld_const(rec + 2), ld_const(rec + 3));
     w.pair0 = unit.y;
     w.count = unit.z;
     if (unit.x == 0) {
@@ -212,20 +236,12 @@ __device__ __forceinline__ bool load_unit(const ExpertArgs& a, int u, Unit& w) {
         return true;
     }
     const int e = unit.x - 1;
-    const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e]);
+    const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(ld_const(a.expert_ptrs + 2 * e));
     w.gate = gate_up;
     w.up = gate_up + static_cast<size_t>(kInner) * kHidden;
-    w.down = reinterpret_cast<const uint16_t*>(a.expert_ptrs[2 * e + 1]);
+    w.down = reinterpret_cast<const uint16_t*>(ld_const(a.expert_ptrs + 2 * e + 1));
     w.tokens = a.plan.pair_token + unit.y;
     return true;
-}
-
-// XCD-aware placement: the `tiles` workgroups of one unit run on XCD unit % 8.
-__device__ __forceinline__ void unit_tile(int b, int tiles, int& unit, int& tile) {
-    const int group = b / (8 * tiles);
-    const int within = b % (8 * tiles);
-    unit = 8 * group + within % 8;
-    tile = within / 8;
 }
 
 // gate/up workgroup (128 intermediate rows of one work unit): 8 waves, each
@@ -320,107 +336,204 @@ __device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_
                 uint32_t v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = swiglu_bf16(rbf(acc[r][b][i]), rbf(up[i]));
-                *reinterpret_cast<uint2*>((r ? act1 : act0) + static_cast<size_t>(16 * b) * kInner) =
-                    make_uint2(v[0] | (v[1] << 16), v[2] | (v[3] << 16));
+                st_agent64((r ? act1 : act0) + static_cast<size_t>(16 * b) * kInner,
+                           static_cast<uint64_t>(v[0] | (v[1] << 16)) | (static_cast<uint64_t>(v[2] | (v[3] << 16)) << 32));
             }
         }
     }
 }
 
-__global__ __launch_bounds__(kGuThreads, 1) void pf_gateup(ExpertArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [2][kPassTok][kXsStride]
-    int ui, tile;
-    unit_tile(blockIdx.x, kGuTiles, ui, tile);
-    Unit w;
-    if (!load_unit(a, ui, w)) return;
+// The expert stage of a prefill layer in one persistent launch: one
+// workgroup per CU.  Workgroup b serves list b % 8 (units u with
+// u % 8 == b % 8, so a unit's items share an XCD's L2 when workgroup b
+// runs on XCD b % 8): first the 4 gate/up items of each of its units, then
+// the 4 down items of each, claimed from the list's counter one item ahead
+// (a gate/up item claims its successor when it starts, a down item during
+// its third tile).  A down item first waits (bounded) until its unit's 4
+// gate/up items have counted themselves in.  Every gate/up item is claimed
+// before any down item of its list and a claimed gate/up item never waits,
+// so the waits end whether or not all workgroups are resident.  The claim
+// counters and per-unit counts are zeroed by pf_fill.
+__global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    __shared__ int claimed_s;
+    __shared__ int timeout_s;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    // Token pieces of this thread: piece tid % 16 of unit rows tid / 16 + 32 j
-    // (rows past the unit's count repeat its first token).
-    const int piece = tid & 15;
-    const uint16_t* xrow[kGuPieces];
-    int xrow_row[kGuPieces];
-#pragma unroll
-    for (int j = 0; j < kGuPieces; ++j) {
-        const int c = tid / 16 + (kGuThreads / 16) * j;  // token row of the unit, 0..127
-        const int cc = c < w.count ? c : 0;
-        const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
-        xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
-        xrow_row[j] = c;
-    }
-    const int m = lane & 15;
-    const int g = lane >> 4;
-    const int nblk = (w.count + 15) / 16;
-    // MFMA row m < 8 of tile r is gate row 128*tile + 16*wave + 8r + m, m >= 8
-    // the up row with the same index.
-    const uint16_t* rows = m < 8 ? w.gate : w.up;
-    const int row0 = kGuRows * tile + 16 * wave + (m & 7);
-    const uint16_t* arow0 = rows + static_cast<size_t>(row0) * kHidden + 8 * g;
-    const uint16_t* arow1 = rows + static_cast<size_t>(row0 + 8) * kHidden + 8 * g;
-    uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + kGuRows * tile + 16 * wave + 4 * g;
-    uint16_t* act1 = act0 + 8;
-    if (nblk <= 2) {
-        gateup_mfma<2>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
-    } else if (nblk <= 4) {
-        gateup_mfma<4>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
-    } else {
-        gateup_mfma<8>(arow0, arow1, xrow, xrow_row, piece, xs, act0, act1, w.count);
-    }
-}
-
-__global__ __launch_bounds__(kDnThreads, 1) void pf_down(ExpertArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t as[];  // [kDnTok][kActStride]
-    int ui, tile;
-    unit_tile(blockIdx.x, kDnTiles, ui, tile);
-    Unit w;
-    if (!load_unit(a, ui, w)) return;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int m = lane & 15;
-    const int g = lane >> 4;
-    const int h0 = kDnRows * tile + 16 * wave;
-    // The tile's 16 rows x 512 of this wave, kept in registers for every pass.
-    const uint16_t* arow = w.down + static_cast<size_t>(h0 + m) * kInner + 8 * g;
-    uint4 ab[kInner / 32];
-#pragma unroll
-    for (int s = 0; s < kInner / 32; ++s) ab[s] = ldg16(arow + 32 * s);
-    for (int q0 = 0; q0 < w.count; q0 += kDnTok) {
-        const int nt = min(kDnTok, w.count - q0);
-        // Stage act rows q0..q0+kDnTok-1 (1 KiB each, 64 pieces of 16 bytes).
-        uint4 st[kDnPieces];
-#pragma unroll
-        for (int j = 0; j < kDnPieces; ++j) {
-            const int idx = tid + kDnThreads * j;
-            const int r = idx / 64;
-            const int rr = r < nt ? r : 0;
-            st[j] = ldg16(a.ws.act + static_cast<size_t>(w.pair0 + q0 + rr) * kInner + 8 * (idx % 64));
-        }
-        if (q0 > 0) __syncthreads();  // previous pass done with the LDS rows
-#pragma unroll
-        for (int j = 0; j < kDnPieces; ++j) {
-            const int idx = tid + kDnThreads * j;
-            *reinterpret_cast<uint4*>(as + (idx / 64) * kActStride + 8 * (idx % 64)) = st[j];
-        }
+    const int list = blockIdx.x % 8;
+    const int n_units = ld_const(&a.ws.control->n_units);
+    const int units = n_units > list ? (n_units - list + 7) / 8 : 0;
+    const int n_gu = kGuTiles * units;
+    const int n_items = n_gu + kDnItems * units;
+    uint32_t* claim = &a.ws.control->claim[list];
+    auto take = [&]() -> uint32_t { return __builtin_amdgcn_atomic_inc32(claim, 0xffffffffu, __ATOMIC_RELAXED, "agent"); };
+    // The claimed item, broadcast to the workgroup (item indices are
+    // wave-uniform, so the unit lookups are scalar loads).
+    auto publish = [&](uint32_t claimed) -> int {
+        if (tid == 0) claimed_s = static_cast<int>(claimed);
         __syncthreads();
-        const int nb = (nt + 15) / 16;
+        const int item = __builtin_amdgcn_readfirstlane(claimed_s);
+        __syncthreads();  // every thread has read claimed_s before it is written again
+        return item;
+    };
+    if (tid == 0) timeout_s = 0;
+    int cur = publish(tid == 0 ? take() : 0u);
+
+    // ---- gate/up items (every one claimed before any down item) ----
+    while (cur < n_gu) {
+        uint32_t claimed = 0u;
+        if (tid == 0) claimed = take();
+        const int u = list + 8 * (cur / kGuTiles);
+        const int tile = cur % kGuTiles;
+        // The item's code is written out here rather than called as an
+        // inlined function: that form spills registers.
+        Unit w;
+        if (load_unit(a, u, w)) {
+            const int wave = tid >> 6;
+            const int lane = tid & 63;
+            // Token pieces of this thread: piece tid % 16 of unit rows tid / 16 + 32 j
+            // (rows past the unit's count repeat its first token).
+            const int piece = tid & 15;
+            const uint16_t* xrow[kGuPieces];
+            int xrow_row[kGuPieces];
+#pragma unroll
+            for (int j = 0; j < kGuPieces; ++j) {
+                const int c = tid / 16 + (kGuThreads / 16) * j;  // token row of the unit, 0..127
+                const int cc = c < w.count ? c : 0;
+                const int t = w.tokens ? w.tokens[cc] : w.pair0 - kTopK * a.tokens + cc;
+                xrow[j] = a.x + static_cast<size_t>(t) * kHidden + 8 * piece;
+                xrow_row[j] = c;
+            }
+            const int m = lane & 15;
+            const int g = lane >> 4;
+            const int nblk = (w.count + 15) / 16;
+            // MFMA row m < 8 of tile r is gate row 128*tile + 16*wave + 8r + m, m >= 8
+            // the up row with the same index.
+            const uint16_t* rows = m < 8 ? w.gate : w.up;
+            const int row0 = kGuRows * tile + 16 * wave + (m & 7);
+            const uint16_t* arow0 = rows + static_cast<size_t>(row0) * kHidden + 8 * g;
+            const uint16_t* arow1 = rows + static_cast<size_t>(row0 + 8) * kHidden + 8 * g;
+            uint16_t* act0 = a.ws.act + static_cast<size_t>(w.pair0 + m) * kInner + kGuRows * tile + 16 * wave + 4 * g;
+            uint16_t* act1 = act0 + 8;
+            if (nblk <= 2) {
+                gateup_mfma<2>(arow0, arow1, xrow, xrow_row, piece, lds, act0, act1, w.count);
+            } else if (nblk <= 4) {
+                gateup_mfma<4>(arow0, arow1, xrow, xrow_row, piece, lds, act0, act1, w.count);
+            } else {
+                gateup_mfma<8>(arow0, arow1, xrow, xrow_row, piece, lds, act0, act1, w.count);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's act rows are written
+        __syncthreads();
+        if (tid == 0) __hip_atomic_fetch_add(a.ws.unit_done + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        cur = publish(claimed);
+    }
+
+    // ---- down items, one per (unit, quarter of the output rows) ----
+    // The unit's act rows are staged in LDS once, then the item's 4 tiles of
+    // 128 rows run in turn.  Each wave holds its 16 rows of a tile over
+    // k = 512 (16 MFMA A operands per lane) in one of two register sets, and
+    // issues the following tile's rows -- after the third tile, the next
+    // item's first -- once the current tile's have arrived, so a wave
+    // always has one tile's rows in flight while it multiplies.  (The
+    // explicit waits keep the memory counter exact around the stores and
+    // branches: it retires in order.)
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int m = lane & 15;
+    const int g = lane >> 4;
+    struct DnItem {
+        const uint16_t* arow;  // this lane's first weight element of the item's first tile
+        int u, h0, pair0, count;
+    };
+    auto dn_info = [&](int item, DnItem& d) {
+        const int j = item - n_gu;
+        Unit w;
+        d.u = list + 8 * (j / kDnItems);
+        load_unit(a, d.u, w);
+        d.h0 = kDnRows * kDnItemTiles * (j % kDnItems) + 16 * wave;
+        d.arow = w.down + static_cast<size_t>(d.h0 + m) * kInner + 8 * g;
+        d.pair0 = w.pair0;
+        d.count = w.count;
+    };
+    auto tile_rows = [&](const uint16_t* arow, uint4* wt) {
+#pragma unroll
+        for (int s = 0; s < kInner / 32; ++s) wt[s] = ldg16(arow + 32 * s);
+    };
+    auto tile_mfma = [&](const DnItem& d, int t, const uint4* wt) {
+        const int nb = (d.count + 15) / 16;
         for (int b = 0; b < nb; ++b) {
-            const uint16_t* bp = as + (16 * b + m) * kActStride + 8 * g;
+            const uint16_t* bp = lds + (16 * b + m) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < kInner / 32; s += 2) {
-                acc0 = mfma16x16x32(ab[s], *reinterpret_cast<const uint4*>(bp + 32 * s), acc0);
-                acc1 = mfma16x16x32(ab[s + 1], *reinterpret_cast<const uint4*>(bp + 32 * (s + 1)), acc1);
+                acc0 = mfma16x16x32(wt[s], *reinterpret_cast<const uint4*>(bp + 32 * s), acc0);
+                acc1 = mfma16x16x32(wt[s + 1], *reinterpret_cast<const uint4*>(bp + 32 * (s + 1)), acc1);
             }
             const f32x4 y = acc0 + acc1;
             const int col = 16 * b + m;
-            if (col < nt) {
-                uint16_t* dst = a.ws.y + static_cast<size_t>(w.pair0 + q0 + col) * kHidden + h0 + 4 * g;
+            if (col < d.count) {
+                uint16_t* dst = a.ws.y + static_cast<size_t>(d.pair0 + col) * kHidden + d.h0 + kDnRows * t + 4 * g;
                 *reinterpret_cast<uint2*>(dst) = make_uint2(f2bf(y[0]) | (f2bf(y[1]) << 16), f2bf(y[2]) | (f2bf(y[3]) << 16));
             }
         }
+    };
+    constexpr size_t kTileStride = static_cast<size_t>(kDnRows) * kInner;
+    uint4 wa[kInner / 32], wb[kInner / 32];
+    DnItem d;
+    if (cur < n_items) {
+        dn_info(cur, d);
+        tile_rows(d.arow, wa);
     }
+    while (cur < n_items) {
+        // The unit's 4 gate/up items have counted themselves in (bounded wait).
+        if (tid == 0 && ld_agent32(a.ws.unit_done + d.u) < static_cast<uint32_t>(kGuTiles)) {
+            const uint64_t start = wall_clock64();
+            while (ld_agent32(a.ws.unit_done + d.u) < static_cast<uint32_t>(kGuTiles)) {
+                if (wall_clock64() - start > kPfSpinTicks) {
+                    timeout_s = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        __syncthreads();
+        // The unit's act rows (1 KiB each, written by other workgroups of
+        // this launch: agent-scope loads; rows past the unit's count read as
+        // zeros).
+        const uint16_t* act = a.ws.act + static_cast<size_t>(d.pair0) * kInner;
+        const uint32_t act_bytes = static_cast<uint32_t>(d.count) * kInner * 2;
+        uint4 st[kDnPieces];
+#pragma unroll
+        for (int q = 0; q < kDnPieces; ++q) st[q] = ld_agent16(act, static_cast<uint32_t>((tid + kDnThreads * q) * 16), act_bytes);
+#pragma unroll
+        for (int q = 0; q < kDnPieces; ++q) {
+            const int idx = tid + kDnThreads * q;
+            *reinterpret_cast<uint4*>(lds + (idx / 64) * kActStride + 8 * (idx % 64)) = st[q];
+        }
+        __syncthreads();
+        __builtin_amdgcn_s_waitcnt(0);
+        tile_rows(d.arow + kTileStride, wb);
+        tile_mfma(d, 0, wa);
+        __builtin_amdgcn_s_waitcnt(0);
+        uint32_t claimed = 0u;
+        if (tid == 0) claimed = take();
+        tile_rows(d.arow + 2 * kTileStride, wa);
+        tile_mfma(d, 1, wb);
+        __builtin_amdgcn_s_waitcnt(0);
+        tile_rows(d.arow + 3 * kTileStride, wb);
+        tile_mfma(d, 2, wa);
+        const int next = publish(claimed);
+        DnItem dn = d;  // past the list's end: a harmless reload of this item's first tile
+        if (next < n_items) dn_info(next, dn);
+        __builtin_amdgcn_s_waitcnt(0);
+        tile_rows(dn.arow, wa);
+        tile_mfma(d, 3, wb);
+        __syncthreads();  // every wave is done with the act rows in LDS
+        cur = next;
+        d = dn;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the last reload is dropped
+    if (tid == 0 && timeout_s) atomicOr(&a.ws.control->status, kStatusTimeoutPf);
 }
 
 int max_units(int tokens) {
@@ -429,8 +542,11 @@ int max_units(int tokens) {
 
 }  // namespace
 
-size_t prefill_gateup_lds() { return static_cast<size_t>(2) * kPassTok * kXsStride * sizeof(uint16_t); }
-size_t prefill_down_lds() { return static_cast<size_t>(kDnTok) * kActStride * sizeof(uint16_t); }
+size_t prefill_experts_lds() {
+    const size_t gateup = static_cast<size_t>(2) * kPassTok * kXsStride * sizeof(uint16_t);
+    const size_t down = static_cast<size_t>(kPassTok) * kActStride * sizeof(uint16_t);
+    return gateup > down ? gateup : down;
+}
 
 hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in, const uint16_t* weights_in,
                                int64_t* indices, uint16_t* weights, int tokens, int shared_present,
@@ -447,27 +563,25 @@ hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in
 
 hipError_t launch_prefill_experts(const ExpertArgs& a, hipStream_t stream) {
     int device = 0;
-    hipError_t dev_err = hipGetDevice(&device);
-    if (dev_err != hipSuccess) return dev_err;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
     if (device < 0 || device >= 64) return hipErrorInvalidDevice;
-    static bool attrs[64] = {false};  // per device: dynamic LDS limits raised
-    if (!attrs[device]) {
-        hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gateup),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(prefill_gateup_lds()));
+    static int cus[64] = {0};  // per device: CU count, 0 until the LDS limit is raised
+    if (cus[device] == 0) {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_experts), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(prefill_experts_lds()));
         if (err != hipSuccess) return err;
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_down), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(prefill_down_lds()));
+        int n = 0;
+        err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
         if (err != hipSuccess) return err;
-        attrs[device] = true;
+        cus[device] = n;
     }
-    const int units = (max_units(a.tokens) + 7) / 8 * 8;
-    const StageEvents gate_ev = timing_events(kStageGateUp);
-    LRMOE_LAUNCH(pf_gateup, dim3(units * kGuTiles), dim3(kGuThreads), prefill_gateup_lds(), stream, gate_ev.start,
-                 gate_ev.stop, a);
-    const StageEvents down_ev = timing_events(kStageDown);
-    LRMOE_LAUNCH(pf_down, dim3(units * kDnTiles), dim3(kDnThreads), prefill_down_lds(), stream, down_ev.start,
-                 down_ev.stop, a);
+    // one workgroup per CU (all resident: the down items wait for gate/up
+    // items), a multiple of the 8 lists
+    const int grid = cus[device] / 8 * 8;
+    if (grid < 8) return hipErrorNotSupported;
+    const StageEvents ev = timing_events(kStageGateUp);
+    LRMOE_LAUNCH(pf_experts, dim3(grid), dim3(kDnThreads), prefill_experts_lds(), stream, ev.start, ev.stop, a);
     return hipGetLastError();
 }
 
