@@ -28,10 +28,12 @@
 //             while it multiplies the current one; y rows out (bf16).
 //   The ordered combine is experts.hip's combine_kernel.
 //
-// A unit's items are on one list, served by the workgroups b with
-// b % 8 = the list (on XCD b % 8), so the unit's token and act rows are
-// fetched into one XCD's L2.  Act rows go out and come back with
-// agent-scope stores and loads, so results do not depend on that placement.
+// A list is a contiguous eighth of the units, served by the workgroups b
+// with b % 8 = the list (on XCD b % 8): a unit's token and act rows are
+// fetched into one XCD's L2, and an expert's units (consecutive in the
+// plan) run together on one XCD, its weight tiles shared through that L2.
+// Act rows go out and come back with agent-scope stores and loads, so
+// results do not depend on that placement.
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
@@ -344,9 +346,10 @@ __device__ __forceinline__ void gateup_mfma(const uint16_t* arow0, const uint16_
 }
 
 // The expert stage of a prefill layer in one persistent launch: one
-// workgroup per CU.  Workgroup b serves list b % 8 (units u with
-// u % 8 == b % 8, so a unit's items share an XCD's L2 when workgroup b
-// runs on XCD b % 8): first the 4 gate/up items of each of its units, then
+// workgroup per CU.  Workgroup b serves list b % 8 (a contiguous eighth of
+// the units, so a unit's items and an expert's units share an XCD's L2
+// when workgroup b runs on XCD b % 8): first the 4 gate/up items of each of
+// its units, then
 // the 4 down items of each, claimed from the list's counter one item ahead
 // (a gate/up item claims its successor when it starts, a down item during
 // its third tile).  A down item first waits (bounded) until its unit's 4
@@ -361,7 +364,8 @@ __global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
     const int tid = threadIdx.x;
     const int list = blockIdx.x % 8;
     const int n_units = ld_const(&a.ws.control->n_units);
-    const int units = n_units > list ? (n_units - list + 7) / 8 : 0;
+    const int first = n_units * list / 8;  // the list's units: [first, first + units)
+    const int units = n_units * (list + 1) / 8 - first;
     const int n_gu = kGuTiles * units;
     const int n_items = n_gu + kDnItems * units;
     uint32_t* claim = &a.ws.control->claim[list];
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
     while (cur < n_gu) {
         uint32_t claimed = 0u;
         if (tid == 0) claimed = take();
-        const int u = list + 8 * (cur / kGuTiles);
+        const int u = first + cur / kGuTiles;
         const int tile = cur % kGuTiles;
         // The item's code is written out here rather than called as an
         // inlined function: that form spills registers.
@@ -448,7 +452,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
     auto dn_info = [&](int item, DnItem& d) {
         const int j = item - n_gu;
         Unit w;
-        d.u = list + 8 * (j / kDnItems);
+        d.u = first + j / kDnItems;
         load_unit(a, d.u, w);
         d.h0 = kDnRows * kDnItemTiles * (j % kDnItems) + 16 * wave;
         d.arow = w.down + static_cast<size_t>(d.h0 + m) * kInner + 8 * g;
