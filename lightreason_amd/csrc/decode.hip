@@ -577,6 +577,27 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     for (int i = 0; i < 4; ++i) x_lo[i] = ld_row16<kChained>(a.x, xr_lo + 16 * i);
 #pragma unroll
     for (int i = 0; i < 4; ++i) x_hi[i] = ld_row16<kChained>(a.x, xr_hi + 16 * i);
+    // A workgroup whose first item is a shared-expert A tile (routing does
+    // not name it) brings that tile's 1,024 lines of 128 bytes into its L2
+    // now, one 4-byte load per line (two lines per lane), so that the tile
+    // arrives from L2 when it is issued after top-8, ahead of the first
+    // items of the other workgroups.  The others load two words of token
+    // row 0: every path issues the same loads.  Issued after the token rows,
+    // so that no wait for those covers them; consumed just before the first
+    // item's loads, when routing has long ended.
+    const int first_item = (block - (a.router != nullptr ? kRouterWgs : 0) + G) % G;
+    uint32_t warm0, warm1;
+    {
+        const bool warm = a.sh_down != nullptr && first_item < kATiles;
+        const int r = (2 * tid) / 32;   // row of the tile: 16 gate rows, then 16 up rows
+        const int line = (2 * tid) % 32;  // first of the lane's two lines of that row
+        const uint16_t* row = (r < 16 ? a.sh_gate + static_cast<size_t>(16 * first_item + r) * kHidden
+                                      : a.sh_up + static_cast<size_t>(16 * first_item + r - 16) * kHidden);
+        const uint16_t* w0 = warm ? row + 64 * line : a.x;
+        const uint16_t* w1 = warm ? row + 64 * (line + 1) : a.x + 2;
+        warm0 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w0));
+        warm1 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w1));
+    }
     const unsigned long long call = finished / static_cast<unsigned long long>(G) + static_cast<unsigned>(layer);
     const int parity = static_cast<int>(call & 1ull);
     const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
@@ -810,8 +831,9 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                          (c[1].z | c[1].w) != 0u;
         return all ? c : nullptr;
     };
-    const int offset = a.router != nullptr ? kRouterWgs : 0;  // router workgroups take items last
-    int cur = (block - offset + G) % G;
+    // Router workgroups take items last.
+    int cur = first_item;
+    asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
     // The first item (read raw, tile choice 0) is addressed straight from
     // the expert table.
     uint32_t dec = 0u;  // tile choice of the item being run
