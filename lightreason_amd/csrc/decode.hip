@@ -577,19 +577,37 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     for (int i = 0; i < 4; ++i) x_lo[i] = ld_row16<kChained>(a.x, xr_lo + 16 * i);
 #pragma unroll
     for (int i = 0; i < 4; ++i) x_hi[i] = ld_row16<kChained>(a.x, xr_hi + 16 * i);
-    // A workgroup whose first item is a shared-expert A tile (routing does
-    // not name it) brings that tile's 1,024 lines of 128 bytes into its L2
-    // now, one 4-byte load per line (two lines per lane), so that the tile
-    // arrives from L2 when it is issued after top-8, ahead of the first
-    // items of the other workgroups.  The others load two words of token
-    // row 0: every path issues the same loads.  Issued after the token rows,
-    // so that no wait for those covers them; consumed just before the first
-    // item's loads, when routing has long ended.
+    // A workgroup's first item: item (block - 32) mod G with a router (the
+    // router workgroups take items last), else item block.
     const int first_item = (block - (a.router != nullptr ? kRouterWgs : 0) + G) % G;
-    uint32_t warm0, warm1;
-    {
+    // With a router and a shared expert (raw weights), the workgroups whose
+    // first item is a shared-expert A tile (not named by routing) run it
+    // while the router works, right after the token rows are staged; their
+    // fixed items are then first_item + G and 2G + first_item, and claims
+    // number items from 2G + kATiles on.  With every routed A item of a T=1
+    // layer then in the first round, no down item waits for a second one.
+    const bool early_path =  // launch-uniform; the early workgroups are not router workgroups
+        !kCodec && a.router != nullptr && a.sh_down != nullptr && G >= kRouterWgs + kATiles;
+    const bool early = early_path && first_item < kATiles;
+    uint4 b0[kLoads], b1[kLoads];
+    // Otherwise, a workgroup whose first item is a shared-expert A tile
+    // brings that tile's 1,024 lines of 128 bytes into its L2 during
+    // routing, one 4-byte load per line (two lines per lane), so that the
+    // tile arrives from L2 when it is issued after top-8, ahead of the first
+    // items of the other workgroups; the others load two words of token row
+    // 0.  Issued after the token rows, so that no wait for those covers
+    // them; consumed just before the first item's loads.
+    uint32_t warm0 = 0u, warm1 = 0u;
+    if (early) {
+        const int m = lane & 15;
+        const int row = 16 * first_item + 8 * (wave >> 2) + (m & 7);
+        const uint16_t* p =
+            (m < 8 ? a.sh_gate : a.sh_up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * i);
+    } else {
         const bool warm = a.sh_down != nullptr && first_item < kATiles;
-        const int r = (2 * tid) / 32;   // row of the tile: 16 gate rows, then 16 up rows
+        const int r = (2 * tid) / 32;     // row of the tile: 16 gate rows, then 16 up rows
         const int line = (2 * tid) % 32;  // first of the lane's two lines of that row
         const uint16_t* row = (r < 16 ? a.sh_gate + static_cast<size_t>(16 * first_item + r) * kHidden
                                       : a.sh_up + static_cast<size_t>(16 * first_item + r - 16) * kHidden);
@@ -651,6 +669,38 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     if (a.router != nullptr) {
         stage_rows();
         __syncthreads();
+        if (early) {
+            // The shared-expert A tile first_item, exactly as the item loop
+            // runs an A item of slot 0 (columns = tokens 0..T-1, pairs from
+            // kTopK * T).
+            const int m = lane & 15;
+            const int g = lane >> 4;
+            const uint16_t* bp = x_lds + (m < T ? m : 0) * kXStride + kInner * (wave & 3) + 8 * g;
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < kLoads; q += 2) {
+                acc0 = mfma16x16x32(b0[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                acc1 = mfma16x16x32(b0[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+            }
+            part[wave * kWave + lane] = acc0 + acc1;
+            __syncthreads();
+            if ((wave & 3) == 0) {
+                const f32x4* pp = part + wave * kWave + lane;
+                const f32x4 sum = ((pp[0] + pp[kWave]) + pp[2 * kWave]) + pp[3 * kWave];
+                f32x4 up;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(sum[i], 32, kWave);
+                if (g < 2 && m < T) {
+                    uint32_t act[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) act[i] = swiglu_bf16(rbf(sum[i]), rbf(up[i]));
+                    uint64_t* dst = a.act + static_cast<size_t>(kTopK * T + m) * (kInner / 2) +
+                                    (16 * first_item + 8 * (wave >> 2) + 4 * g) / 2;
+                    st_agent64(dst, tag_bits | (act[0] | (act[1] << 16)));
+                    st_agent64(dst + 1, tag_bits | (act[2] | (act[3] << 16)));
+                }
+            }
+        }
         if (router_wg) {
             for (int t = 0; t < T; ++t) {
                 const float s = wave_butterfly_sum(lane_dot32(w_router, x_lds + t * kXStride, lane));
@@ -751,7 +801,6 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // first_slot + k / 32 with k < G <= 256 -- names slot 0 (the shared
     // expert) or one of token 0's experts, and streams in while the rest of
     // the plan is built.
-    uint4 b0[kLoads], b1[kLoads];
     // Prefetch target of an item without weights (C items): 1 KiB of token
     // row 0, in cache after the first read.
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
@@ -831,8 +880,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                          (c[1].z | c[1].w) != 0u;
         return all ? c : nullptr;
     };
-    // Router workgroups take items last.
-    int cur = first_item;
+    int cur = early ? first_item + G : first_item;
     asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
     // The first item (read raw, tile choice 0) is addressed straight from
     // the expert table.
@@ -1045,7 +1093,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         __builtin_amdgcn_sched_barrier(0);
         TL(tl_at + 1, 0);
         bases = next_bases;
-        if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + (kCodec ? 3 : 2) * G;
+        if (tid == 0) P.claim[cpar] = static_cast<int32_t>(claimed) + (kCodec ? 3 * G : 2 * G + (early_path ? kATiles : 0));
         const int m = lane & 15;
         const int g = lane >> 4;
         if (it.kind == 1) {
@@ -1160,8 +1208,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // The first three items of a workgroup are fixed (the first one's
     // weights are already in flight); the rest are claimed.
     if (cur < end) {
-        int nxt = cur + G;
-        int nxt2 = cur + 2 * G;
+        int nxt = early ? 2 * G + first_item : cur + G;
+        int nxt2 = cur + 2 * G;  // (codec: no early items)
         if (a.router == nullptr) {
             // Token rows staged while the first weights stream in.
             stage_rows();
