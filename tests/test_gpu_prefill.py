@@ -2,12 +2,14 @@
 at the sizes where every branch of the grouped kernels runs (needs an
 MI355X).
 
-The prefill grid cuts each expert's token list into work units of at most
-128 tokens (the shared expert's units are tokens 128u .. 128u+127).  A unit
-of more than 64 tokens runs the 8-column-block gate/up MFMA loop and a
-second 64-token pass of the down kernel; an expert with more than 128
-tokens is split over several units.  These tests route so that all three
-happen, assert that they did, and compare against the oracle:
+The prefill plan cuts each expert's token list into work units of at most
+128 tokens (the shared expert's units are tokens 128u .. 128u+127); the
+expert launch gives each of 8 work lists a contiguous range of units.  A
+unit of more than 64 tokens runs the 8-column-block gate/up MFMA loop and
+stages more than 64 act rows per down item; an expert with more than 128
+tokens is split over several units, which then share a list.  These tests
+route so that all of this happens, assert that it did, and compare against
+the oracle:
 
   - routes (indices and weights) bit-exact for every token;
   - outputs, for a token sample that covers every unit boundary of the
@@ -153,3 +155,26 @@ def _bf16_bits(values: np.ndarray) -> np.ndarray:
     f32 = np.ascontiguousarray(values, dtype=np.float32)
     bits = f32.view(np.uint32).astype(np.uint64)
     return (((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("tokens", [20, 260])
+def test_prefill_concentrated_routes(model, oracle, host_experts, tokens):
+    """Every token routed to the same 8 experts (distinct weights per token):
+    at T=260 each of them has 3 work units (128, 128, 4 tokens) and the
+    shared expert 3, at T=20 one each -- 27 and 9 units over the 8 lists.
+    Every token checked."""
+    hot = np.array([3, 40, 77, 100, 150, 201, 230, 255])
+    rng = np.random.default_rng(tokens + 11)
+    base = rng.normal(0.0, 1.0, size=(tokens, 256))
+    base[:, hot] += 12.0 + rng.normal(0.0, 1.0, size=(tokens, 8))
+    x = model.hidden(tokens, step=4100 + tokens)
+    logits = torch.from_numpy(base.astype(np.float32)).to(torch.bfloat16).to(x.device)
+    print(f"[prefill] concentrated T={tokens}", flush=True)
+    layer, out, idx, wts = _run(model, x, logits, norm=False)
+    o_idx, o_w = oracle.route_logits(to_u16(logits))
+    np.testing.assert_array_equal(idx, o_idx)
+    np.testing.assert_array_equal(wts, o_w)
+    assert set(np.unique(idx).tolist()) == set(hot.tolist())
+    xb = to_u16(x)
+    want, _, _ = oracle_layer_rows(oracle, layer, xb, host_experts, logits_bits=to_u16(logits))
+    assert_layer_close(to_u16(out), want, None, what=f"concentrated T={tokens}")
