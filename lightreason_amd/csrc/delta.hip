@@ -16,6 +16,28 @@
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
+// Timeline build (-DLRMOE_TIMELINE, liblrmoe_timeline.so; the product
+// library has none of it): thread 0 of every dn_mixer workgroup stamps the
+// 100 MHz wall clock at its phases into the buffer given by
+// lrmoe_mixer_timeline_set (16 words per workgroup): 0 entry, 1 unit 0
+// multiplied, 2 unit 0's epilogue done, 3 unit 1 and beta/G done, 4 phase A
+// end, 5 first barrier passed, 6 rule done, 7 z unit done and counted in,
+// 8 gated norm done (word 12: 1 on the head's last workgroup), 9 second
+// barrier passed, 10 out_proj done.
+#ifdef LRMOE_TIMELINE
+__device__ unsigned long long* g_mixer_timeline;
+extern "C" int lrmoe_mixer_timeline_set(void* p) {
+    return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(g_mixer_timeline), &p, sizeof(p)));
+}
+#define MX_WORD(k, v)                                                                        \
+    do {                                                                                     \
+        if (threadIdx.x == 0 && g_mixer_timeline != nullptr) g_mixer_timeline[blockIdx.x * 16 + (k)] = (v); \
+    } while (0)
+#else
+#define MX_WORD(k, v)
+#endif
+#define MX_TL(k) MX_WORD(k, wall_clock64())
+
 namespace lrmoe {
 namespace {
 
@@ -238,33 +260,38 @@ hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
 // ---- the mixer step in one persistent launch (dn_mixer) ---------------------
 //
 // 256 workgroups of 8 waves, one per CU, all resident (the grid barriers
-// rely on it).  Everything that comes from HBM is requested at the start
-// or streamed in phase A, so the later phases touch only rows the launch
-// wrote itself:
+// rely on it).  The first barrier waits only for what the rule needs (q, k,
+// v, beta, G); the rest of the workgroup's HBM stream (in_proj's z unit and
+// out_proj's rows) is requested behind the rule's inputs and lands while the
+// rule runs:
 //
-//   start    the rule's state slab (waves 0-3), A_log and dt_bias;
-//   phase A  in_proj's qkv and z rows in 768 units of 16 rows, units
-//            b, b + 256, b + 512 requested at once (192 KiB per CU), each
-//            load instruction reading 1 KiB of one row (5.4 TB/s for the
-//            48 MiB on this part, against 3.9 TB/s when an instruction
-//            gathers the MFMA layout's 64 bytes from each of 16 rows); a
-//            unit passes through LDS into the MFMA layout, wave w
-//            multiplying k in [256 w, 256 w + 256); per unit the causal conv
-//            + SiLU, the conv-state update and z, written with agent-scope
-//            stores; into the registers of consumed units, head b / 8's
+//   start    A_log and dt_bias, the barrier counter, the rule's state slab,
+//            the token rows, then in_proj units b and b + 256 (q, k and v
+//            rows: 768 units of 16 rows in all, 128 KiB per CU), every load
+//            unconditional (clamped dummy addresses where a lane needs
+//            none) so that the compiler's in-order waits cover only what
+//            is consumed; each load instruction reads 1 KiB of one row
+//            (5.4 TB/s on this part, against 3.9 TB/s when an instruction
+//            gathers the MFMA layout's 64 bytes from each of 16 rows);
+//   phase A  a unit passes through LDS into the MFMA layout, wave w
+//            multiplying k in [256 w, 256 w + 256); per unit the causal
+//            conv + SiLU and the conv-state update, written with
+//            agent-scope stores; into unit 0's registers, head b / 8's
 //            in_proj_b and in_proj_a rows (its beta and G go to LDS: no
-//            other workgroup needs them) and out_proj rows 8b .. 8b + 7 (A
-//            operands of phase D);
+//            other workgroup needs them);
 //   barrier
-//   phase B  the rule for (head b / 8, columns 16 (b % 8) .. +15): q and k
-//            staged and l2norm'd by the workgroup, waves 0-3 four columns
-//            each (dn_rule's arithmetic); outputs through LDS to agent-scope
-//            rows; the last of a head's 8 workgroups to count itself in
-//            (a monotonic counter, 8 per call) forms the head's gated
-//            RMSNorm (phase C);
+//   phase B  the rule's inputs, then unit b + 512 (z) and out_proj rows
+//            8b .. 8b + 7 (A operands of phase D) requested; the rule for
+//            (head b / 8, columns 16 (b % 8) .. +15): q and k staged and
+//            l2norm'd by the workgroup, waves 0-3 four columns each
+//            (dn_rule's arithmetic); outputs through LDS to agent-scope
+//            rows; then the z unit; the last of a head's 8 workgroups to
+//            count itself in (a monotonic counter, 8 per call) forms the
+//            head's gated RMSNorm (phase C: o, z and the norm weights in
+//            one round trip);
 //   barrier
-//   phase D  out_proj rows 8b .. 8b + 7 from the registers loaded at the
-//            start and the normed rows.
+//   phase D  out_proj rows 8b .. 8b + 7 from the registers and the normed
+//            rows.
 //
 // Barriers: one arrival counter (2 x 256 per call, never reset) and a
 // release word set by the arrival that completes a barrier, as moe_chain's.
@@ -328,13 +355,16 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     const int T = a.tokens;
     const int b = blockIdx.x;
     const bool live = t < kMixRows;  // this lane's MFMA row holds a weight row
+    MX_TL(0);
 
-    // conv weights and cached inputs of a unit's rows (threads 0-31)
+    // conv weights and cached inputs of a unit's rows (threads 0-31 of a
+    // unit below the z rows keep them; every other thread loads conv row
+    // tid % 16 and drops it, so that no branch makes the compiler wait for
+    // the load before the units behind it are issued)
     auto load_conv = [&](int v) -> uint2 {
         const int n0 = kMixInRows * v;
-        if (tid < 2 * kMixInRows && n0 < kDnZRow)
-            return *reinterpret_cast<const uint2*>((tid < kMixInRows ? a.conv_w : a.conv_state) + (n0 + (tid & 15)) * kDnTaps);
-        return make_uint2(0u, 0u);
+        const bool kept = tid < 2 * kMixInRows && n0 < kDnZRow;
+        return *reinterpret_cast<const uint2*>(((tid & 16) ? a.conv_state : a.conv_w) + ((kept ? n0 : 0) + (tid & 15)) * kDnTaps);
     };
     // A unit's rows as the memory system streams them best: each load
     // instruction of a wave reads 1 KiB of one row (wave w: rows 2w, 2w + 1;
@@ -345,48 +375,61 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         for (int i = 0; i < 8; ++i) w[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
         cv = load_conv(v);
     };
-    // the three in_proj units first: nothing else is in the memory queue ahead of them
-    uint4 w0[8], w1[8], w2[8];
-    uint2 c0, c1, c2;
-    const int v0 = b, v1 = b + kMixGrid, v2 = b + 2 * kMixGrid;
-    load_unit(w0, c0, v0);
-    load_unit(w1, c1, v1);
-    load_unit(w2, c2, v2);
-
-    if (tid == 0) {
-        base_s = ld_agent64(m.arrive) / kMixGrid * kMixGrid;
-        timeout_s = 0;
-    }
-    if (tid < 2 * kDnValueHeads) gate_lds[tid >> 5][tid & 31] = bf2f(ldg_u16((tid < 32 ? a.A_log : a.dt_bias) + (tid & 31)));
-
-    // the rule's state: head rh, column rc, rows 8 rg .. 8 rg + 7 (waves 0-3)
+    // The small inputs first -- A_log and dt_bias, the barrier counter, the
+    // rule's state slab, the token rows -- then in_proj units 0 (q, k) and 1
+    // (v).  The memory counter retires in order: waiting for a small input
+    // then never waits for a unit, and unit 0 is multiplied as soon as it
+    // arrives.  (Every thread issues every one of these loads, with valid
+    // dummy addresses where it needs none, so that no branch blurs the
+    // waits.)  Unit 2 (z, needed only by the gated norm) is requested behind
+    // the rule's inputs, after the first barrier, which would otherwise wait
+    // for it.
+    const uint16_t gate_raw = static_cast<uint16_t>(ldg_u16(((tid >> 5) & 1 ? a.dt_bias : a.A_log) + (tid & 31)));
+    const unsigned long long arrived = ld_agent64(m.arrive);
+    // the rule's state: head rh, column rc, rows 8 rg .. 8 rg + 7 (waves 0-3;
+    // waves 4-7 load the same words as waves 0-3 and drop them)
     const int rg = lane & 15;
     const int cq = lane >> 4;
     const int rh = b / kMixHeadGroups;
     const int rc0 = 16 * (b % kMixHeadGroups);
-    const int rc = rc0 + 4 * wave + cq;
+    const int rc = rc0 + 4 * (wave % kMixRuleWaves) + cq;
     const int64_t slab = static_cast<int64_t>(rh) * kDnWidth * kDnWidth;
     float S[8];
-    if (wave < kMixRuleWaves) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) S[i] = state_at<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc);
-    }
-
-    // ---- phase A: in_proj (wave w multiplies k in [256 w, 256 w + 256)) ----
+    for (int i = 0; i < 8; ++i) S[i] = state_at<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc);
+    // token rows (columns t >= T load token 0: their results are dropped)
     uint4 xb[8];
     {
-        const uint16_t* xrow = a.x + static_cast<int64_t>(t) * kHidden + 256 * wave + 8 * g;
+        const uint16_t* xrow = a.x + static_cast<int64_t>(t < T ? t : 0) * kHidden + 256 * wave + 8 * g;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xb[4 * s + j] = t < T ? ldg16(xrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
+            for (int j = 0; j < 4; ++j) xb[4 * s + j] = ldg16(xrow + 128 * s + 32 * j);
     }
-    auto load_rows = [&](uint4 (&w)[8], const uint16_t* row0, bool have) {
+    uint4 w0[8], w1[8], w2[8];
+    uint2 c0, c1;
+    const int v0 = b, v1 = b + kMixGrid, v2 = b + 2 * kMixGrid;
+    load_unit(w0, c0, v0);
+    load_unit(w1, c1, v1);
+    if (tid == 0) {
+        base_s = arrived / kMixGrid * kMixGrid;
+        timeout_s = 0;
+    }
+    if (tid < 2 * kDnValueHeads) gate_lds[tid >> 5][tid & 31] = bf2f(gate_raw);
+    // Take the state slab here, behind only the gate rows: its first use is
+    // in the rule's token loop, where the compiler would otherwise wait for
+    // every load in flight (the z unit and the out_proj rows) before the loop.
+    asm volatile("" ::"v"(S[0]), "v"(S[1]), "v"(S[2]), "v"(S[3]), "v"(S[4]), "v"(S[5]), "v"(S[6]), "v"(S[7]));
+
+    // ---- phase A: in_proj (wave w multiplies k in [256 w, 256 w + 256)) ----
+    // MFMA A rows from row0 (every lane loads: an output row depends on its
+    // own A row only, so rows the caller drops may hold anything)
+    auto load_rows = [&](uint4 (&w)[8], const uint16_t* row0) {
         const uint16_t* wrow = row0 + 256 * wave + 8 * g;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[4 * s + j] = have ? ldg16(wrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
+            for (int j = 0; j < 4; ++j) w[4 * s + j] = ldg16(wrow + 128 * s + 32 * j);
     };
     // The unit's rows through LDS into the MFMA layout, its partial tile
     // into red (rows 4 g + i, token t).  The caller's next barrier (the
@@ -463,22 +506,15 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     uint4 wo[16];  // out_proj rows 8b + t (t < 8), k in [512 wave, 512 wave + 512): phase D's A operands
     {
         unit_mfma(w0, c0, v0, 0);
-        // head rh's b row (MFMA row 0) and a row (row 1), into w0's registers
-        load_rows(w0, (t == 0 ? a.w_b : a.w_a) + static_cast<int64_t>(rh) * kHidden, t < 2);
+        // head rh's b row (MFMA row 0) and a row (rows 1-15; only rows 0 and
+        // 1 are kept), into w0's registers
+        load_rows(w0, (t == 0 ? a.w_b : a.w_a) + static_cast<int64_t>(rh) * kHidden);
+        MX_TL(1);
         unit_epilogue(v0, 0);
+        MX_TL(2);
         unit_mfma(w1, c1, v1, 1);
         unit_epilogue(v1, 1);
-        unit_mfma(w2, c2, v2, 0);
-        // every in_proj load is issued and w1, w2 are consumed: out_proj's
-        // rows stream from here on
-        {
-            const uint16_t* wrow = a.w_out + static_cast<int64_t>(kMixRows * b + (live ? t : 0)) * kDnValue + 512 * wave + 8 * g;
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wo[4 * s + j] = live ? ldg16(wrow + 128 * s + 32 * j) : make_uint4(0u, 0u, 0u, 0u);
-        }
-        unit_epilogue(v2, 0);
+        MX_TL(3);
         {
             // beta and G of head rh for every token, from its b and a rows
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -521,24 +557,53 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         __syncthreads();
     };
     const unsigned long long base = base_s;
+    // q, k and v (units 0 and 1 of every workgroup) are complete; z (unit 2)
+    // is not needed before the gated norm.
+    MX_TL(4);
     grid_sync(base + kMixGrid);
+    MX_TL(5);
 
     // ---- phase B: the rule for head rh, columns rc0 .. rc0 + 15 ----
     {
         const int kh = rh >> 1;  // value head h reads key head h / 2
-        if (tid < 16 * T) {
-            const int tt = tid >> 4;
-            const int ch = tid & 15;
-            const uint32_t qoff = static_cast<uint32_t>((tt * kDnConv + kh * kDnWidth + ch * 8) * 2);
-            unpack8(ld_agent16(a.act, qoff), &qs[tt][ch * 8]);
-            unpack8(ld_agent16(a.act, qoff + kDnKey * 2), &ks[tt][ch * 8]);
-        } else if (tid >= 256 && tid < 256 + kMixRuleWaves * T) {
-            const int i = tid - 256;
-            const int w = i & 3;
-            const int tt = i >> 2;
-            const uint64_t v4 = ld_agent64(a.act + static_cast<int64_t>(tt) * kDnConv + 2 * kDnKey + rh * kDnWidth + rc0 + 4 * w);
+        // The rule's inputs, loaded by every thread (clamped to token 0: no
+        // branch around loads, so that the waits below cover only them).
+        const bool is_qk = tid < 16 * T;
+        const int tq = is_qk ? tid >> 4 : 0;
+        const int ch = tid & 15;
+        const uint32_t qoff = static_cast<uint32_t>((tq * kDnConv + kh * kDnWidth + ch * 8) * 2);
+        const uint4 qraw = ld_agent16(a.act, qoff);
+        const uint4 kraw = ld_agent16(a.act, qoff + kDnKey * 2);
+        const int vi = tid - 256;
+        const bool is_v = vi >= 0 && vi < kMixRuleWaves * T;
+        const int vw = is_v ? vi & 3 : 0;
+        const int vt = is_v ? vi >> 2 : 0;
+        const uint64_t v4 = ld_agent64(a.act + static_cast<int64_t>(vt) * kDnConv + 2 * kDnKey + rh * kDnWidth + rc0 + 4 * vw);
+        // behind them: in_proj unit 2 (z rows 16 b .. 16 b + 15) and out_proj
+        // rows 8 b .. 8 b + 7 (phase D's A operands)
+        {
+            const uint16_t* row0 = mix_row_ptr(a, kMixInRows * v2 + 2 * wave) + 8 * lane;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w2[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
+            // (lanes t >= 8 load row 8 b too: MFMA output rows 8-15, which
+            // they feed, are dropped)
+            const uint16_t* wrow = a.w_out + static_cast<int64_t>(kMixRows * b + (live ? t : 0)) * kDnValue + 512 * wave + 8 * g;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wo[4 * s2 + j] = ldg16(wrow + 128 * s2 + 32 * j);
+        }
+        // (taken on every path: a wait inside only one branch would leave
+        // the registers pending at the merge, and the compiler then waits
+        // for every load in flight before the token loop)
+        asm volatile("" ::"v"(qraw.x), "v"(kraw.x), "v"(v4));
+        if (is_qk) {
+            unpack8(qraw, &qs[tq][ch * 8]);
+            unpack8(kraw, &ks[tq][ch * 8]);
+        }
+        if (is_v) {
             const uint32_t lo = static_cast<uint32_t>(v4), hi = static_cast<uint32_t>(v4 >> 32);
-            vs[w][tt][0] = lo_bf(lo); vs[w][tt][1] = hi_bf(lo); vs[w][tt][2] = lo_bf(hi); vs[w][tt][3] = hi_bf(hi);
+            vs[vw][vt][0] = lo_bf(lo); vs[vw][vt][1] = hi_bf(lo); vs[vw][vt][2] = lo_bf(hi); vs[vw][vt][3] = hi_bf(hi);
         }
         __syncthreads();
         {
@@ -612,6 +677,12 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
                                 (static_cast<uint64_t>(os[tt][4 * q4 + 3]) << 48);
             st_agent64(m.o + static_cast<int64_t>(tt) * kDnValue + rh * kDnWidth + rc0 + 4 * q4, w4);
         }
+        // z rows 16 b .. 16 b + 15 (head rh's: its 8 workgroups write all of
+        // its z rows), while the rule's stores drain; counted in below with
+        // the rule's outputs.
+        MX_TL(6);
+        unit_mfma(w2, make_uint2(0u, 0u), v2, 0);
+        unit_epilogue(v2, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) {
@@ -620,18 +691,20 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             last_s = (before + 1) % kMixHeadGroups == 0;
         }
         __syncthreads();
+        MX_TL(7);
         // ---- phase C (the head's last workgroup): gated RMSNorm of head rh ----
         if (last_s) {
             const int tt = tid >> 5;
             const int q4 = tid & 31;
             const bool act_t = tt < T;
-            const int64_t at = static_cast<int64_t>(tt) * kDnValue + rh * kDnWidth + 4 * q4;
-            float ov[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (act_t) {
-                const uint64_t o4 = ld_agent64(m.o + at);
-                ov[0] = lo_bf(static_cast<uint32_t>(o4)); ov[1] = hi_bf(static_cast<uint32_t>(o4));
-                ov[2] = lo_bf(static_cast<uint32_t>(o4 >> 32)); ov[3] = hi_bf(static_cast<uint32_t>(o4 >> 32));
-            }
+            // o, z and the norm weights in one round trip (rows t >= T read
+            // token 0's and store nothing)
+            const int64_t at = static_cast<int64_t>(act_t ? tt : 0) * kDnValue + rh * kDnWidth + 4 * q4;
+            const uint64_t o4 = ld_agent64(m.o + at);
+            const uint64_t z4 = ld_agent64(a.z + at);
+            const uint2 w4 = *reinterpret_cast<const uint2*>(a.norm_w + 4 * q4);
+            const float ov[4] = {lo_bf(static_cast<uint32_t>(o4)), hi_bf(static_cast<uint32_t>(o4)),
+                                 lo_bf(static_cast<uint32_t>(o4 >> 32)), hi_bf(static_cast<uint32_t>(o4 >> 32))};
             float sq = ov[0] * ov[0] + ov[1] * ov[1] + ov[2] * ov[2] + ov[3] * ov[3];
             sq = sq + __int_as_float(lane_xor<1>(__float_as_int(sq)));
             sq = sq + __int_as_float(lane_xor<2>(__float_as_int(sq)));
@@ -640,8 +713,6 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             sq = sq + __int_as_float(lane_xor<16>(__float_as_int(sq)));
             if (act_t) {
                 const float r = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kDnWidth) + a.eps);
-                const uint64_t z4 = ld_agent64(a.z + at);
-                const uint2 w4 = *reinterpret_cast<const uint2*>(a.norm_w + 4 * q4);
                 const float zv[4] = {lo_bf(static_cast<uint32_t>(z4)), hi_bf(static_cast<uint32_t>(z4)),
                                      lo_bf(static_cast<uint32_t>(z4 >> 32)), hi_bf(static_cast<uint32_t>(z4 >> 32))};
                 const float wv[4] = {lo_bf(w4.x), hi_bf(w4.x), lo_bf(w4.y), hi_bf(w4.y)};
@@ -653,17 +724,21 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             }
         }
     }
+    MX_TL(8);
+    MX_WORD(12, static_cast<unsigned long long>(last_s));
     grid_sync(base + 2 * kMixGrid);
+    MX_TL(9);
 
     // ---- phase D: out_proj rows 8b .. 8b + 7 ----
     {
+        // columns t >= T read token 0's row: their output columns are dropped
         uint4 cb[16];
+        const int tc = t < T ? t : 0;
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                cb[4 * s + j] = t < T ? ld_agent16(m.core, static_cast<uint32_t>((t * kDnValue + 512 * wave + 128 * s + 32 * j + 8 * g) * 2))
-                                      : make_uint4(0u, 0u, 0u, 0u);
+                cb[4 * s + j] = ld_agent16(m.core, static_cast<uint32_t>((tc * kDnValue + 512 * wave + 128 * s + 32 * j + 8 * g) * 2));
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc = mfma16x16x32(wo[i], cb[i], acc);
@@ -681,6 +756,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             if (tt < T) a.out[static_cast<int64_t>(tt) * kHidden + kMixRows * b + row] = static_cast<uint16_t>(f2bf(p));
         }
     }
+    MX_TL(10);
     if (tid == 0 && timeout_s) atomicOr(m.status, LRMOE_STATUS_TIMEOUT);
 }
 

@@ -1,7 +1,8 @@
 """Per-workgroup timeline of one decode layer (lrmoe_moe_layer, T <= 16),
-from the timeline build of the library (`python -m lightreason_amd.build
---timeline`: liblrmoe_timeline.so, whose decode kernel stamps the wall clock
-at its phases).
+or with --mixer of one Gated DeltaNet mixer step (lrmoe_delta_mixer), from
+the timeline build of the library (`python -m lightreason_amd.build
+--timeline`: liblrmoe_timeline.so, whose decode and mixer kernels stamp the
+wall clock at their phases).
 
 Runs the workload the benchmark times -- 40 resident seeded layers (seed
 2026), T tokens, with Zipf(1.1) Gumbel logits (T > 1) or the router (T = 1)
@@ -11,7 +12,11 @@ call, the median and maximum over workgroups of each phase (microseconds
 from the first workgroup's entry) and per item step the median start, wait
 for the step's weights, wait for its inputs, and end.
 
-Usage: python -m lightreason_amd.timeline [--tokens T] [--layers L]
+The mixer run steps 30 resident seeded mixers of the 35B shape (seed 7)
+three times over, stamps every call of the last two passes, and prints per
+phase the median over calls of the per-workgroup median and maximum.
+
+Usage: python -m lightreason_amd.timeline [--tokens T] [--layers L] [--mixer]
 """
 
 from __future__ import annotations
@@ -30,11 +35,57 @@ PHASES = (("entry", 0), ("top8", 1), ("first_issued_w0", 2), ("first_issued_w7",
           ("rows_staged", 6), ("end", 4))
 
 
+MIXER_PHASES = (("unit 0 multiplied", 1), ("unit 0 epilogue", 2), ("unit 1 + beta/G", 3), ("phase A end", 4),
+                ("barrier 1", 5), ("rule done", 6), ("z done, counted in", 7), ("gated norm done", 8),
+                ("barrier 2", 9), ("out_proj done", 10))
+
+
+def mixer_timeline(lib, tokens: int, layers: int, seed: int) -> int:
+    from .delta import mixer_status
+    from .synthetic import SyntheticMixers
+
+    lib.lrmoe_mixer_timeline_set.argtypes = [C.c_void_p]
+    lib.lrmoe_mixer_timeline_set.restype = C.c_int
+    device = torch.device("cuda:0")
+    mix = SyntheticMixers(layers, device, seed)
+    stamps = torch.zeros(256 * 16, dtype=torch.int64, device=device)
+    if lib.lrmoe_mixer_timeline_set(C.c_void_p(stamps.data_ptr())) != 0:
+        raise RuntimeError("lrmoe_mixer_timeline_set failed")
+    x = mix.hidden(tokens, 1)
+    outs = [torch.empty(tokens, x.shape[1], dtype=torch.bfloat16, device=device) for _ in range(layers)]
+    calls = []
+    for rep in range(3):
+        for l in range(layers):
+            stamps.zero_()
+            mix.mixers[l].step(x, mix.conv[l], mix.state[l], out=outs[l])
+            torch.cuda.synchronize()
+            if rep > 0:
+                calls.append(stamps.view(256, 16).cpu().numpy().astype(np.int64))
+    if mixer_status(device) != 0:
+        raise RuntimeError(f"mixer status {mixer_status(device)}")
+    st = np.stack(calls)
+    rel = (st[:, :, :11] - st[:, :, 0].min(1)[:, None, None]) / 100.0
+    last = st[:, :, 12] == 1
+    print(f"Gated DeltaNet mixer step T={tokens}, {len(calls)} calls over {layers} layers, 256 workgroups; "
+          "us from the first workgroup's entry, median over calls of the per-workgroup median / max")
+    print(f"  {'entry':20s} {np.median(np.median(rel[:, :, 0], 1)):6.2f} / {np.median(rel[:, :, 0].max(1)):6.2f}")
+    for name, i in MIXER_PHASES:
+        v = rel[:, :, i]
+        if i == 8:  # the gated norm runs on each head's last workgroup only
+            med = np.median([np.median(v[c][last[c]]) for c in range(len(calls))])
+            mx = np.median([v[c][last[c]].max() for c in range(len(calls))])
+        else:
+            med, mx = np.median(np.median(v, 1)), np.median(v.max(1))
+        print(f"  {name:20s} {med:6.2f} / {mx:6.2f}")
+    return 0
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--tokens", type=int, default=8)
-    parser.add_argument("--layers", type=int, default=40)
-    parser.add_argument("--seed", type=int, default=2026)
+    parser.add_argument("--layers", type=int, default=None, help="40 decode layers, 30 mixers")
+    parser.add_argument("--seed", type=int, default=None, help="2026 decode, 7 mixers")
+    parser.add_argument("--mixer", action="store_true", help="time the Gated DeltaNet mixer step instead")
     args = parser.parse_args(argv)
     from .build import TIMELINE_LIBRARY
     if not TIMELINE_LIBRARY.exists():
@@ -42,6 +93,10 @@ def main(argv=None) -> int:
         return 2
     _native.LIBRARY = TIMELINE_LIBRARY
     lib = _native.library()
+    if args.mixer:
+        return mixer_timeline(lib, args.tokens, args.layers or 30, 7 if args.seed is None else args.seed)
+    args.layers = args.layers or 40
+    args.seed = 2026 if args.seed is None else args.seed
     lib.lrmoe_timeline_set.argtypes = [C.c_void_p]
     lib.lrmoe_timeline_set.restype = C.c_int
 
