@@ -21,9 +21,10 @@
 // 100 MHz wall clock at its phases into the buffer given by
 // lrmoe_mixer_timeline_set (16 words per workgroup): 0 entry, 1 unit 0
 // multiplied, 2 unit 0's epilogue done, 3 unit 1 and beta/G done, 4 phase A
-// end, 5 first barrier passed, 6 rule done, 7 z unit done and counted in,
-// 8 gated norm done (word 12: 1 on the head's last workgroup), 9 second
-// barrier passed, 10 out_proj done.
+// end, 5 first barrier passed, 11 the rule's inputs staged, 13 q and k
+// l2norm'd, 14 wave 0's token loop done, 6 rule done, 7 z unit done and
+// counted in, 8 gated norm done (word 12: 1 on the head's last workgroup),
+// 9 second barrier passed, 10 out_proj done.
 #ifdef LRMOE_TIMELINE
 __device__ unsigned long long* g_mixer_timeline;
 extern "C" int lrmoe_mixer_timeline_set(void* p) {
@@ -606,6 +607,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             vs[vw][vt][0] = lo_bf(lo); vs[vw][vt][1] = hi_bf(lo); vs[vw][vt][2] = lo_bf(hi); vs[vw][vt][3] = hi_bf(hi);
         }
         __syncthreads();
+        MX_TL(11);
         {
             const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kDnWidth));
             const int tt = tid >> 4;  // one DPP row per token
@@ -630,6 +632,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             }
         }
         __syncthreads();
+        MX_TL(13);
         if (wave < kMixRuleWaves) {
             for (int tt = 0; tt < T; ++tt) {
                 float q[8], k[8];
@@ -668,6 +671,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) state_put<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc, S[i]);
         }
+        MX_TL(14);
         __syncthreads();
         if (tid < 4 * T) {
             const int tt = tid >> 2;
@@ -739,6 +743,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 cb[4 * s + j] = ld_agent16(m.core, static_cast<uint32_t>((tc * kDnValue + 512 * wave + 128 * s + 32 * j + 8 * g) * 2));
+        __builtin_amdgcn_sched_barrier(0);  // all 16 loads in flight before the first MFMA
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc = mfma16x16x32(wo[i], cb[i], acc);

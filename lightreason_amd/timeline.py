@@ -36,7 +36,7 @@ PHASES = (("entry", 0), ("top8", 1), ("first_issued_w0", 2), ("first_issued_w7",
 
 
 MIXER_PHASES = (("unit 0 multiplied", 1), ("unit 0 epilogue", 2), ("unit 1 + beta/G", 3), ("phase A end", 4),
-                ("barrier 1", 5), ("rule done", 6), ("z done, counted in", 7), ("gated norm done", 8),
+                ("barrier 1", 5), ("rule inputs staged", 11), ("q, k l2norm'd", 13), ("token loop done", 14), ("rule done", 6), ("z done, counted in", 7), ("gated norm done", 8),
                 ("barrier 2", 9), ("out_proj done", 10))
 
 
@@ -64,7 +64,7 @@ def mixer_timeline(lib, tokens: int, layers: int, seed: int) -> int:
     if mixer_status(device) != 0:
         raise RuntimeError(f"mixer status {mixer_status(device)}")
     st = np.stack(calls)
-    rel = (st[:, :, :11] - st[:, :, 0].min(1)[:, None, None]) / 100.0
+    rel = (st[:, :, :15] - st[:, :, 0].min(1)[:, None, None]) / 100.0
     last = st[:, :, 12] == 1
     print(f"Gated DeltaNet mixer step T={tokens}, {len(calls)} calls over {layers} layers, 256 workgroups; "
           "us from the first workgroup's entry, median over calls of the per-workgroup median / max")
