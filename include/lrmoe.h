@@ -328,6 +328,7 @@ int lrmoe_fill_normal_bf16(uint16_t *out, int64_t count, uint64_t seed, uint64_t
 #define LRMOE_STAGE_LAYER 32       /* lrmoe_moe_layer / lrmoe_moe_chain decode kernel */
 #define LRMOE_STAGE_DELTA_MIXER 64 /* lrmoe_delta_mixer (one launch) */
 #define LRMOE_STAGE_DELTA_RULE 128 /* lrmoe_delta_rule */
+#define LRMOE_STAGE_ATTENTION 256  /* lrmoe_attn_decode (first to last of its launches) */
 int lrmoe_timing_enable(int mask, int launches);
 int lrmoe_timing_collect(int stage, double *total_ms, int *launches);
 
@@ -398,6 +399,40 @@ int lrmoe_delta_mixer(const uint16_t *hidden, int tokens, const uint16_t *in_pro
                       const uint16_t *out_proj, uint16_t *conv_state, void *state, int state_bf16,
                       uint16_t *conv_record, void *state_record, uint16_t *out, void *workspace,
                       size_t workspace_bytes, void *stream);
+
+/* ---- full-attention decode (the attention before each of the 10
+ * full-attention layers' MoE) ----------------------------------------------- */
+
+/* Bytes of workspace lrmoe_attn_decode needs for `tokens` tokens (1..16; 0
+ * outside that range).  No reference counterpart. */
+#define LRMOE_ATTN_MAX_TOKENS 16
+size_t lrmoe_attn_workspace_bytes(int tokens);
+
+/* One cached step of a full-attention layer of the 35B model (hidden 2048,
+ * 16 query heads over 2 key/value heads of width 256, rotary width 64) for
+ * 1..16 tokens after `length` cached positions: [HF]
+ * Qwen3_5MoeAttention.forward with a key/value cache, which the reference
+ * runs stock (edge35b/benchmark.py:141-146 and dflash_probe.py:122 decode
+ * and verify through the Transformers model; edge35b/delta_decode.py:84-126
+ * replaces only the linear-attention layers).  Weights as the module holds
+ * them, bf16: q_proj [8192][2048] (per head 256 query rows, then 256 gate
+ * rows), k_proj and v_proj [512][2048], o_proj [2048][4096], q_norm and
+ * k_norm [256] (applied as 1 + w).  cos, sin [tokens][64] bf16: the
+ * model's position embeddings for the new positions.  k_cache, v_cache
+ * [2][capacity][256] bf16 hold the normed, rotated keys and the values of
+ * positions 0 .. length - 1 and receive positions length .. length +
+ * tokens - 1 (capacity >= length + tokens, at most 2^22).  Token t attends
+ * to positions 0 .. length + t (causal within the block).  out
+ * [tokens][2048] bf16 (the module's output, before the residual).
+ * Workspace of lrmoe_attn_workspace_bytes(tokens), 256-byte aligned, used by
+ * one stream at a time.  Rounding points: those of the Transformers forward
+ * in bf16 (eager attention); the softmax runs in fp32 over chunks of
+ * positions whose partial results are merged at the end. */
+int lrmoe_attn_decode(const uint16_t *hidden, int tokens, const uint16_t *q_proj, const uint16_t *k_proj,
+                      const uint16_t *v_proj, const uint16_t *o_proj, const uint16_t *q_norm, const uint16_t *k_norm,
+                      float eps, const uint16_t *cos, const uint16_t *sin, uint16_t *k_cache, uint16_t *v_cache,
+                      int capacity, int length, uint16_t *out, void *workspace, size_t workspace_bytes,
+                      void *stream);
 
 #ifdef __cplusplus
 }

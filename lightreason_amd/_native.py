@@ -58,6 +58,9 @@ _SIGNATURES = {
     "lrmoe_delta_rule": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "lrmoe_delta_mixer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _I, _P, _P, _P, _P,
                            C.c_size_t, _P], _I),
+    "lrmoe_attn_workspace_bytes": ([_I], C.c_size_t),
+    "lrmoe_attn_decode": ([_P, _I, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _I, _I, _P, _P, C.c_size_t,
+                           _P], _I),
 }
 
 STAGE_ROUTE = 1
@@ -70,6 +73,8 @@ STAGE_DELTA_MIXER = 64
 STAGE_DELTA_RULE = 128
 DELTA_WS_STATUS_OFFSET = 0  # int32 status word of a mixer workspace
 DELTA_MAX_TOKENS = 16    # tokens per lrmoe_delta_mixer call
+STAGE_ATTENTION = 256
+ATTN_MAX_TOKENS = 16     # tokens per lrmoe_attn_decode call
 
 
 class NativeError(RuntimeError):

@@ -539,4 +539,49 @@ int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_pro
     return status_of(lrmoe::launch_delta_mixer(p, state, state_bf16 != 0, state_record, w, as_stream(stream)));
 }
 
+size_t lrmoe_attn_workspace_bytes(int tokens) {
+    if (tokens < 1 || tokens > lrmoe::kAttnMaxTokens) return 0;
+    return lrmoe::attn_workspace_bytes(tokens);
+}
+
+int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
+                      const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm,
+                      float eps, const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
+                      int capacity, int length, uint16_t* out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    if (tokens < 0 || tokens > lrmoe::kAttnMaxTokens || length < 0 || capacity < 1 || capacity > (1 << 22) ||
+        length > capacity - tokens)
+        return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (!hidden || !q_proj || !k_proj || !v_proj || !o_proj || !q_norm || !k_norm || !cos || !sin || !k_cache ||
+        !v_cache || !out || !workspace)
+        return LRMOE_E_ARG;
+    if (misaligned(hidden, 16) || misaligned(q_proj, 16) || misaligned(k_proj, 16) || misaligned(v_proj, 16) ||
+        misaligned(o_proj, 16) || misaligned(q_norm, 8) || misaligned(k_norm, 8) || misaligned(cos, 8) ||
+        misaligned(sin, 8) || misaligned(k_cache, 16) || misaligned(v_cache, 16) || misaligned(out, 2) ||
+        misaligned(workspace, 256))
+        return LRMOE_E_ARG;
+    if (workspace_bytes < lrmoe::attn_workspace_bytes(tokens)) return LRMOE_E_WORKSPACE;
+    if (int d = check_device()) return d;
+    const lrmoe::AttnWorkspace w = lrmoe::carve_attn(workspace, tokens);
+    lrmoe::AttnArgs a{};
+    a.proj = w.proj;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.eps = eps;
+    a.cos = cos;
+    a.sin = sin;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.capacity = capacity;
+    a.length = length;
+    a.tokens = tokens;
+    a.chunk = lrmoe::attn_chunk(tokens, length + tokens);
+    a.chunks = (length + tokens + a.chunk - 1) / a.chunk;
+    a.part_o = w.part_o;
+    a.part_ml = w.part_ml;
+    a.att = w.att;
+    return status_of(lrmoe::launch_attn_decode(a, hidden, q_proj, k_proj, v_proj, o_proj, out, as_stream(stream)));
+}
+
 }  // extern "C"

@@ -1,0 +1,404 @@
+// Full-attention decode step of the 35B model (10 of its 40 decoder layers):
+// [HF] Qwen3_5MoeAttention.forward for 1..16 tokens that follow `length`
+// cached positions -- q_proj (query and output gate per head), k_proj,
+// v_proj, per-head RMSNorm of query and key, the rotary embedding of the
+// first 64 of each head's 256 dims, the key/value cache append, causal
+// attention of 16 query heads over 2 key/value heads, the sigmoid output
+// gate and o_proj.  The reference runs this module stock
+// (Transformers SDPA); edge35b/delta_decode.py replaces only the
+// linear-attention layers.
+//
+// Four launches on the caller's stream:
+//
+//   at_project<16, 2048>  q/gate, k and v rows of x (9216 rows in 576
+//        workgroups of 16 rows): each wave streams 1 KiB of one row per load
+//        instruction, the rows pass through LDS into the MFMA layout, the
+//        T <= 16 tokens are the MFMA's 16 columns; bf16 out (proj).
+//   at_attend  one workgroup per (key/value head g, chunk of P positions):
+//        the query rows of heads 8g..8g+7 normalised and rotated into LDS,
+//        the chunk's new positions (those >= length) normalised, rotated
+//        and appended to the caches, then per 32-position sub-block: key
+//        rows into LDS, value rows transposed into LDS, scores by MFMA
+//        (bf16-rounded, / 16), an online softmax per query row, P.V by MFMA
+//        into per-wave accumulators; the chunk's (max, sum, unnormalised
+//        rows) go to the partial buffers.
+//   at_combine  per (token, head): the chunks' partials merged, the sigmoid
+//        gate applied (att, bf16).
+//   at_project<8, 4096>  o_proj rows of att (2048 rows in 256 workgroups).
+//
+// Rounding points follow the Transformers forward in bf16: projections,
+// normed and rotated q/k, scores (then / 16, exact) and the attention
+// output are bf16; the softmax is fp32 (its probabilities enter P.V as
+// bf16 values relative to the chunk's running maximum).
+#include "lrmoe_device.h"
+#include "lrmoe_internal.h"
+
+namespace lrmoe {
+namespace {
+
+constexpr int kAtHeads = 16;                       // query heads
+constexpr int kAtKv = 2;                           // key/value heads
+constexpr int kAtGroup = kAtHeads / kAtKv;         // query heads per key/value head
+constexpr int kAtD = 256;                          // head width
+constexpr int kAtRot = 64;                         // rotary width
+constexpr int kAtQg = kAtHeads * 2 * kAtD;         // 8192 q_proj rows (256 query, 256 gate per head)
+constexpr int kAtKRow = kAtQg;                     // first k_proj row of proj
+constexpr int kAtVRow = kAtQg + kAtKv * kAtD;      // first v_proj row of proj
+constexpr int kAtProj = kAtQg + 2 * kAtKv * kAtD;  // 9216 projected rows
+constexpr int kAtO = kAtHeads * kAtD;              // 4096 o_proj inputs
+constexpr int kAtThreads = 512;
+constexpr int kAtWaves = kAtThreads / 64;
+constexpr int kAtMaxRows = kAtGroup * kAttnMaxTokens;  // query rows of one key/value head: 8 T <= 128
+constexpr int kAtSub = 32;                          // positions per sub-block
+constexpr int kAtQStride = kAtD + 8;                // LDS row strides (bf16 / fp32 elements)
+constexpr int kAtVStride = kAtSub + 8;
+constexpr int kAtSStride = kAtSub + 1;
+constexpr float kAtScale = 0.0625f;                 // 256^-0.5, exact
+
+// ---- projections: y[t][row] = bf16(sum_k W[row][k] x[t][k]) ---------------
+
+template <int kRows, int kK>
+__global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+                                                         int tokens, uint16_t* __restrict__ y, int y_stride) {
+    constexpr int kRowsPerWave = kRows / kAtWaves;        // 2 or 1
+    constexpr int kLoadsPerRow = 8 / kRowsPerWave;        // 4 or 8 loads of 1 KiB per wave and row
+    static_assert(kK == 512 * kLoadsPerRow, "a wave streams its rows in 8 loads of 1 KiB");
+    constexpr int kKw = kK / kAtWaves;                    // k range of a wave in the MFMA
+    constexpr int kSteps = kKw / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kRows][kK + 8];
+    __shared__ float red[kAtWaves][16][17];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int t = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * kRows;
+    // the rows first (every lane loads: the tile is always full)
+    uint4 wv[8];
+    const uint16_t* wrow = w + static_cast<int64_t>(row0 + kRowsPerWave * wave) * kK + 8 * lane;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wv[i] = ldg16(wrow + (i / kLoadsPerRow) * kK + 512 * (i % kLoadsPerRow));
+    // token rows (columns t >= T read token 0: their outputs are dropped)
+    uint4 xb[kSteps];
+    const uint16_t* xrow = x + static_cast<int64_t>(t < tokens ? t : 0) * kK + kKw * wave + 8 * g;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) xb[s] = ldg16(xrow + 32 * s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<uint4*>(&tile[kRowsPerWave * wave + i / kLoadsPerRow][512 * (i % kLoadsPerRow) + 8 * lane]) = wv[i];
+    __syncthreads();
+    // MFMA row m (rows m >= kRows repeat row m - kRows; their outputs are dropped)
+    const int m = t % kRows;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+        acc = mfma16x16x32(*reinterpret_cast<const uint4*>(&tile[m][kKw * wave + 32 * s + 8 * g]), xb[s], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][4 * g + i][t] = acc[i];
+    __syncthreads();
+    if (tid < kRows * 16) {
+        const int r = tid >> 4;
+        const int tt = tid & 15;
+        float p = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kAtWaves; ++ww) p += red[ww][r][tt];
+        if (tt < tokens) y[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(f2bf(p));
+    }
+}
+
+// ---- attention partials ------------------------------------------------------
+
+// One head row (256 dims, 4 per lane: dims 4 lane .. 4 lane + 3) normalised
+// ((x rsqrt(mean x^2 + eps)) (1 + w), fp32, then bf16) and rotated on dims
+// 0..63 (bf16(bf16(x cos) + bf16(rot(x) sin)), rot = [-x[32..63], x[0..31]]:
+// lane l < 16 pairs with lane l ^ 8).  Every lane of the wave calls it.
+__device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float eps, const uint16_t* cos_r,
+                                          const uint16_t* sin_r, int lane) {
+    const float x[4] = {lo_bf(raw.x), hi_bf(raw.x), lo_bf(raw.y), hi_bf(raw.y)};
+    const float ss = wave_butterfly_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kAtD) + eps);
+    const uint2 wr = *reinterpret_cast<const uint2*>(w + 4 * lane);
+    const float wf[4] = {lo_bf(wr.x), hi_bf(wr.x), lo_bf(wr.y), hi_bf(wr.y)};
+    float n[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n[i] = rbf((x[i] * r) * (1.0f + wf[i]));
+    // rotary (lanes 0..15 hold dims 0..63); the shuffles run on every lane
+    const int d0 = 4 * (lane & 15);
+    const uint2 cr = *reinterpret_cast<const uint2*>(cos_r + d0);
+    const uint2 sr = *reinterpret_cast<const uint2*>(sin_r + d0);
+    const float cf[4] = {lo_bf(cr.x), hi_bf(cr.x), lo_bf(cr.y), hi_bf(cr.y)};
+    const float sf[4] = {lo_bf(sr.x), hi_bf(sr.x), lo_bf(sr.y), hi_bf(sr.y)};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float partner = __shfl_xor(n[i], 8, 64);
+        const float rot = (lane & 8) ? partner : -partner;
+        const float v = rbf(rbf(n[i] * cf[i]) + rbf(rot * sf[i]));
+        o[i] = f2bf(lane < 16 ? v : n[i]);
+    }
+    return make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+}
+
+__global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t qs[kAtMaxRows][kAtQStride];  // normed, rotated query rows
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kAtSub][kAtQStride];      // a sub-block's key rows
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kAtD][kAtVStride];        // its value rows, transposed
+    __shared__ float sc[kAtMaxRows][kAtSStride];                                  // its scores
+    __shared__ __attribute__((aligned(16))) uint16_t es[kAtMaxRows][kAtVStride];  // its exp(score - max), bf16
+    __shared__ float mrow[kAtMaxRows], lrow[kAtMaxRows], frow[kAtMaxRows];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int m = lane & 15;
+    const int gq = lane >> 4;
+    const int T = a.tokens;
+    const int R = kAtGroup * T;  // query rows r = 8 t + local head
+    const int RT = (R + 15) / 16;
+    const int g = blockIdx.x / a.chunks;
+    const int c = blockIdx.x % a.chunks;
+    const int L = a.length;
+    const int total = L + T;
+    const int p0 = c * a.chunk;
+    const int p1 = min(p0 + a.chunk, total);
+    uint16_t* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
+    uint16_t* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
+
+    // query rows of heads 8g .. 8g + 7 (wave w: rows w, w + 8, ...)
+    for (int r = wave; r < R; r += kAtWaves) {
+        const int t = r >> 3;
+        const int h = kAtGroup * g + (r & 7);
+        const uint2 raw = *reinterpret_cast<const uint2*>(a.proj + static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + 4 * lane);
+        const uint2 q = norm_rope(raw, a.q_norm, a.eps, a.cos + t * kAtRot, a.sin + t * kAtRot, lane);
+        *reinterpret_cast<uint2*>(&qs[r][4 * lane]) = q;
+    }
+    // new positions of this chunk: keys normed and rotated, values as
+    // projected, appended to the caches (agent-scope stores, complete before
+    // this workgroup's agent-scope loads below read them)
+    for (int p = max(p0, L) + wave; p < p1; p += kAtWaves) {
+        const int t = p - L;
+        const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
+        const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
+        const uint2 vraw = *reinterpret_cast<const uint2*>(pr + kAtVRow + g * kAtD + 4 * lane);
+        const uint2 k = norm_rope(kraw, a.k_norm, a.eps, a.cos + t * kAtRot, a.sin + t * kAtRot, lane);
+        st_agent64(kc + static_cast<int64_t>(p) * kAtD + 4 * lane, static_cast<uint64_t>(k.x) | (static_cast<uint64_t>(k.y) << 32));
+        st_agent64(vc + static_cast<int64_t>(p) * kAtD + 4 * lane, static_cast<uint64_t>(vraw.x) | (static_cast<uint64_t>(vraw.y) << 32));
+    }
+    if (tid < kAtMaxRows) {
+        mrow[tid] = -__builtin_inff();
+        lrow[tid] = 0.0f;
+        frow[tid] = 1.0f;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // P.V accumulators: wave w owns dim tiles 2w, 2w + 1 of every row tile
+    f32x4 acc[8][2];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[rt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // rows past the chunk read zeros (the buffer range ends at p1)
+    const uint32_t range = static_cast<uint32_t>(p1) * kAtD * 2;
+    for (int q0 = p0; q0 < p1; q0 += kAtSub) {
+        // (a) key rows into ks, value rows transposed into vt
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int j = tid + kAtThreads * i;  // 16-byte piece: row j / 32, dims 8 (j % 32) ..
+            const int row = j >> 5;
+            const int col = 8 * (j & 31);
+            const uint32_t off = static_cast<uint32_t>(((q0 + row) * kAtD + col) * 2);
+            const uint4 kv = ld_agent16(kc, off, range);
+            const uint4 vv = ld_agent16(vc, off, range);
+            *reinterpret_cast<uint4*>(&ks[row][col]) = kv;
+            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[col + 2 * e][row] = static_cast<uint16_t>(w4[e] & 0xffffu);
+                vt[col + 2 * e + 1][row] = static_cast<uint16_t>(w4[e] >> 16);
+            }
+        }
+        __syncthreads();
+        // (b) scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
+        {
+            const int ct = wave & 1;
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const int rt = (wave >> 1) + 4 * k2;
+                if (rt < RT) {
+                    f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int s = 0; s < kAtD / 32; ++s)
+                        s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
+                                          *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
+                    const int pos = q0 + 16 * ct + m;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 16 * rt + 4 * gq + i;
+                        const bool ok = r < R && pos < p1 && pos <= L + (r >> 3);
+                        sc[r][16 * ct + m] = ok ? rbf(s4[i]) * kAtScale : -__builtin_inff();
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // (c) online softmax: four threads per row, eight positions each
+        {
+            const int r = tid >> 2;
+            const int q = tid & 3;
+            if (r < R) {  // (R is a multiple of 8: whole quads take part)
+                float s8[8];
+                float mx = -__builtin_inff();
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s8[j] = sc[r][8 * q + j];
+                    mx = fmaxf(mx, s8[j]);
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+                const float m_old = mrow[r];
+                const float m_new = fmaxf(m_old, mx);
+                const bool none = m_new == -__builtin_inff();
+                float sum = 0.0f;
+                uint32_t e2[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const uint32_t lo = none ? 0u : f2bf(lr_exp(s8[j] - m_new));
+                    const uint32_t hi = none ? 0u : f2bf(lr_exp(s8[j + 1] - m_new));
+                    sum += bf2f(lo) + bf2f(hi);
+                    e2[j / 2] = lo | (hi << 16);
+                }
+                *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
+                sum += __shfl_xor(sum, 1, 64);
+                sum += __shfl_xor(sum, 2, 64);
+                const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : lr_exp(m_old - m_new));
+                if (q == 0) {
+                    mrow[r] = m_new;
+                    lrow[r] = lrow[r] * f + sum;
+                    frow[r] = f;
+                }
+            }
+        }
+        __syncthreads();
+        // (d) P.V: rescale, then one k-step of 32 positions per tile
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) {
+            if (rt < RT) {
+                const uint4 ea = *reinterpret_cast<const uint4*>(&es[16 * rt + m][8 * gq]);
+                float f[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) f[i] = frow[16 * rt + 4 * gq + i];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int dt = 2 * wave + j;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[rt][j][i] *= f[i];
+                    acc[rt][j] = mfma16x16x32(ea, *reinterpret_cast<const uint4*>(&vt[16 * dt + m][8 * gq]), acc[rt][j]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // the chunk's partials: unnormalised rows, running max and sum per row
+    float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks + c) * kAtMaxRows * kAtD;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+        if (rt < RT) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * rt + 4 * gq + i;
+                    if (r < R) po[r * kAtD + 16 * (2 * wave + j) + m] = acc[rt][j][i];
+                }
+            }
+        }
+    }
+    if (tid < R) {
+        float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * kAtMaxRows + tid) * 2;
+        pm[0] = mrow[tid];
+        pm[1] = lrow[tid];
+    }
+}
+
+// ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
+
+__global__ __launch_bounds__(kAtD) void at_combine(AttnArgs a) {
+    const int t = blockIdx.x / kAtHeads;
+    const int h = blockIdx.x % kAtHeads;
+    const int d = threadIdx.x;
+    const int g = h / kAtGroup;
+    const int r = kAtGroup * t + (h % kAtGroup);
+    const float* pm = a.part_ml + (static_cast<int64_t>(g) * a.chunks * kAtMaxRows + r) * 2;
+    const float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks * kAtMaxRows + r) * kAtD + d;
+    float M = -__builtin_inff();
+    for (int c = 0; c < a.chunks; ++c) M = fmaxf(M, pm[static_cast<int64_t>(c) * kAtMaxRows * 2]);
+    float num = 0.0f, den = 0.0f;
+    for (int c = 0; c < a.chunks; ++c) {
+        const float mc = pm[static_cast<int64_t>(c) * kAtMaxRows * 2];
+        if (mc == -__builtin_inff()) continue;  // a chunk this token sees nothing of
+        const float wgt = lr_exp(mc - M);
+        den += pm[static_cast<int64_t>(c) * kAtMaxRows * 2 + 1] * wgt;
+        num += po[static_cast<int64_t>(c) * kAtMaxRows * kAtD] * wgt;
+    }
+    const float o = rbf(num / den);
+    const float gate = bf2f(a.proj[static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + d]);
+    const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
+    a.att[static_cast<int64_t>(t) * kAtO + h * kAtD + d] = static_cast<uint16_t>(f2bf(o * sg));
+}
+
+}  // namespace
+
+int attn_chunk(int tokens, int total) {
+    // at least 64 positions per chunk per 4 tokens (the partials stay below
+    // the key/value bytes), at most kAttnMaxChunks chunks per key/value head
+    const int floor_p = kAtSub * 2 * ((tokens + 3) / 4);
+    const int need = (total + kAttnMaxChunks - 1) / kAttnMaxChunks;
+    const int p = ((need + kAtSub - 1) / kAtSub) * kAtSub;
+    return p > floor_p ? p : floor_p;
+}
+
+size_t attn_workspace_bytes(int tokens) {
+    return carve_attn(nullptr, tokens).bytes;
+}
+
+AttnWorkspace carve_attn(void* base, int tokens) {
+    AttnWorkspace w{};
+    uint8_t* p = static_cast<uint8_t*>(base);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) & ~static_cast<size_t>(255);
+        return p + at;
+    };
+    const size_t T = static_cast<size_t>(tokens);
+    w.proj = reinterpret_cast<uint16_t*>(take(T * kAtProj * 2));
+    w.att = reinterpret_cast<uint16_t*>(take(T * kAtO * 2));
+    w.part_o = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * kAtMaxRows * kAtD * 4));
+    w.part_ml = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * kAtMaxRows * 2 * 4));
+    w.bytes = off;
+    return w;
+}
+
+hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q, const uint16_t* w_k,
+                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, hipStream_t stream) {
+    static_assert(kAtProj % 16 == 0 && kHidden % 8 == 0, "projection grids");
+    const int T = a.tokens;
+    const StageEvents ev = timing_events(kStageAttention);
+    // q/gate, k, v rows: three weight matrices, one launch each over its rows
+    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtQg / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr, w_q, x, T,
+                 a.proj, kAtProj);
+    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtKv * kAtD / 16), dim3(kAtThreads), 0, stream, nullptr, nullptr, w_k,
+                 x, T, a.proj + kAtKRow, kAtProj);
+    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtKv * kAtD / 16), dim3(kAtThreads), 0, stream, nullptr, nullptr, w_v,
+                 x, T, a.proj + kAtVRow, kAtProj);
+    LRMOE_LAUNCH(at_attend, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
+    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads), dim3(kAtD), 0, stream, nullptr, nullptr, a);
+    LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, a.att, T,
+                 out, kHidden);
+    return hipGetLastError();
+}
+
+}  // namespace lrmoe

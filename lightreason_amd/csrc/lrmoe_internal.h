@@ -284,6 +284,7 @@ enum Stage : int {
     kStageLayer = 32,
     kStageDeltaMixer = 64,  // Gated DeltaNet: the mixer step (dn_mixer)
     kStageDeltaRule = 128,  // Gated DeltaNet: the delta rule (dn_rule)
+    kStageAttention = 256,  // full-attention decode step (first to last of its launches)
 };
 struct StageEvents {
     hipEvent_t start = nullptr;
@@ -421,6 +422,40 @@ struct DnMixerArgs {
 };
 
 constexpr int kDeltaMaxTokens = 16;
+
+// ---- full-attention decode step (attention.hip) ----
+constexpr int kAttnMaxTokens = 16;
+constexpr int kAttnMaxChunks = 128;  // position chunks per key/value head
+struct AttnArgs {
+    uint16_t* proj;         // [T][9216]: per token q/gate (8192), k (512), v (512) rows, bf16
+    const uint16_t* q_norm; // [256]
+    const uint16_t* k_norm; // [256]
+    float eps;
+    const uint16_t* cos;    // [T][64] bf16
+    const uint16_t* sin;    // [T][64] bf16
+    uint16_t* k_cache;      // [2][capacity][256] bf16 (normed, rotated keys)
+    uint16_t* v_cache;      // [2][capacity][256] bf16
+    int capacity;
+    int length;             // cached positions before the call
+    int tokens;
+    int chunk;              // positions per chunk (a multiple of 32)
+    int chunks;             // chunks per key/value head (<= kAttnMaxChunks)
+    float* part_o;          // [2][chunks][128][256] unnormalised rows
+    float* part_ml;         // [2][chunks][128][2] running max and sum
+    uint16_t* att;          // [T][4096] gated attention rows, bf16
+};
+struct AttnWorkspace {
+    uint16_t* proj;
+    uint16_t* att;
+    float* part_o;
+    float* part_ml;
+    size_t bytes;
+};
+AttnWorkspace carve_attn(void* base, int tokens);
+size_t attn_workspace_bytes(int tokens);
+int attn_chunk(int tokens, int total);
+hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q, const uint16_t* w_k,
+                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, hipStream_t stream);
 DeltaWorkspace carve_delta(void* base, int tokens);
 size_t delta_workspace_bytes(int tokens);
 hipError_t launch_delta_rule(const DnRuleArgs& a, int key_width, bool state_bf16, hipStream_t stream);

@@ -11,7 +11,7 @@
 namespace lrmoe {
 namespace {
 
-constexpr int kStages = 8;  // LRMOE_STAGE_* bits 0..7
+constexpr int kStages = 9;  // LRMOE_STAGE_* bits 0..8
 
 struct Timing {
     int mask = 0;

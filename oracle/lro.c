@@ -21,7 +21,11 @@
  *       Transformers Qwen3_5Moe classes the reference patches
  *       (modeling_qwen3_5_moe.py: TopKRouter.forward, MLP.forward,
  *       SparseMoeBlock.forward, RMSNorm.forward), called from
- *       edge35b/expert_stream.py:383-454.
+ *       edge35b/expert_stream.py:383-454;
+ *   - the Gated DeltaNet decode step (edge35b/delta_decode.py and the
+ *       Transformers Qwen3_5MoeGatedDeltaNet it patches) and the
+ *       full-attention decode step (Transformers Qwen3_5MoeAttention with
+ *       eager_attention_forward, which the reference runs stock).
  *
  * The router GEMV, the softmax denominator and the RMSNorm sum of squares use
  * one fixed fp32 reduction order (64 lane partials over contiguous chunks,
@@ -761,4 +765,128 @@ void lro_delta_mixer(const uint16_t *x, int T, const uint16_t *w_qkv, const uint
     free(bb);
     free(z);
     free(mixed);
+}
+
+/* ---- full-attention decode step ([HF] Qwen3_5MoeAttention) -------------- */
+
+#define LRO_AT_HEADS 16   /* query heads */
+#define LRO_AT_KV 2       /* key/value heads */
+#define LRO_AT_D 256      /* head width */
+#define LRO_AT_ROT 64     /* rotary width (partial_rotary_factor 0.25) */
+#define LRO_AT_QG (LRO_AT_HEADS * 2 * LRO_AT_D)   /* 8192 q_proj rows: per head 256 query, 256 gate */
+#define LRO_AT_O (LRO_AT_HEADS * LRO_AT_D)        /* 4096 o_proj inputs */
+
+/* Qwen3_5MoeRMSNorm over one head (fp32: x rsqrt(mean x^2 + eps), times
+ * (1 + w), then bf16), then the rotary embedding of dims 0..63
+ * (apply_rotary_pos_emb with cos, sin bf16 as given: every product and the
+ * sum rounded to bf16, rotate_half = [-x[32..63], x[0..31]]). */
+static void attn_norm_rope(const uint16_t *raw, const uint16_t *w, float eps, const uint16_t *cos_r,
+                           const uint16_t *sin_r, uint16_t *out) {
+    float var = 0.0f;
+    for (int d = 0; d < LRO_AT_D; ++d) var += lro_bf16_value(raw[d]) * lro_bf16_value(raw[d]);
+    var = var / (float)LRO_AT_D;
+    const float r = 1.0f / sqrtf(var + eps);
+    float n[LRO_AT_D];
+    for (int d = 0; d < LRO_AT_D; ++d) n[d] = rbf((lro_bf16_value(raw[d]) * r) * (1.0f + lro_bf16_value(w[d])));
+    for (int d = 0; d < LRO_AT_D; ++d) {
+        if (d < LRO_AT_ROT) {
+            const float rot = d < LRO_AT_ROT / 2 ? -n[d + LRO_AT_ROT / 2] : n[d - LRO_AT_ROT / 2];
+            const float a = rbf(n[d] * lro_bf16_value(cos_r[d]));
+            const float b = rbf(rot * lro_bf16_value(sin_r[d]));
+            out[d] = lro_bf16_round(a + b);
+        } else {
+            out[d] = lro_bf16_round(n[d]);
+        }
+    }
+}
+
+/* One cached full-attention forward of T tokens after `length` cached
+ * positions ([HF] Qwen3_5MoeAttention.forward with eager_attention_forward;
+ * 35B dims: hidden 2048, 16 query heads over 2 key/value heads, width 256,
+ * rotary width 64):
+ *   qg = bf16(x Wq^T) viewed [T][16][512]: query = [..., :256], gate = [..., 256:];
+ *   k = bf16(x Wk^T), v = bf16(x Wv^T) viewed [T][2][256];
+ *   query and k: per-head RMSNorm with (1 + w), then the rotary embedding
+ *   (attn_norm_rope) with cos, sin [T][64];
+ *   k_cache, v_cache [2][capacity][256] receive positions length .. length + T - 1;
+ *   head h reads key/value head h / 8 (repeat_kv); for token t the scores
+ *   over positions p <= length + t (the causal mask) are
+ *   s = bf16(q . k_p) / 16 (exact), p = bf16(softmax_fp32(s)),
+ *   o = bf16(sum_p p v_p) (fp32, positions ascending);
+ *   a = bf16(o bf16(sigmoid(gate))); out = bf16(a Wo^T) [T][2048].
+ * Projections and q.k use lro_canon_dot's fixed fp32 order. */
+void lro_attn_decode(const uint16_t *x, int T, const uint16_t *w_q, const uint16_t *w_k, const uint16_t *w_v,
+                     const uint16_t *w_o, const uint16_t *q_norm, const uint16_t *k_norm, float eps,
+                     const uint16_t *cos_t, const uint16_t *sin_t, uint16_t *k_cache, uint16_t *v_cache,
+                     int capacity, int length, uint16_t *out) {
+    const size_t H = LRO_HIDDEN;
+    const size_t KVW = (size_t)LRO_AT_KV * LRO_AT_D;
+    uint16_t *qg = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_AT_QG);
+    uint16_t *kr = (uint16_t *)malloc(sizeof(uint16_t) * T * KVW);
+    uint16_t *vr = (uint16_t *)malloc(sizeof(uint16_t) * T * KVW);
+    uint16_t *q = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_AT_O);
+    uint16_t *att = (uint16_t *)malloc(sizeof(uint16_t) * T * LRO_AT_O);
+    float *xf = (float *)malloc(sizeof(float) * LRO_AT_O);
+    const int total = length + T;
+    float *s = (float *)malloc(sizeof(float) * total);
+    for (int t = 0; t < T; ++t) {
+        to_floats(x + t * H, xf, (int)H);
+        for (int r = 0; r < LRO_AT_QG; ++r) qg[(size_t)t * LRO_AT_QG + r] = lro_bf16_round(lro_canon_dot(w_q + r * H, xf, (int)H));
+        for (size_t r = 0; r < KVW; ++r) kr[t * KVW + r] = lro_bf16_round(lro_canon_dot(w_k + r * H, xf, (int)H));
+        for (size_t r = 0; r < KVW; ++r) vr[t * KVW + r] = lro_bf16_round(lro_canon_dot(w_v + r * H, xf, (int)H));
+    }
+    for (int t = 0; t < T; ++t) {
+        const uint16_t *cr = cos_t + t * LRO_AT_ROT;
+        const uint16_t *sr = sin_t + t * LRO_AT_ROT;
+        for (int h = 0; h < LRO_AT_HEADS; ++h)
+            attn_norm_rope(qg + (size_t)t * LRO_AT_QG + h * 2 * LRO_AT_D, q_norm, eps, cr, sr,
+                           q + (size_t)t * LRO_AT_O + h * LRO_AT_D);
+        for (int g = 0; g < LRO_AT_KV; ++g) {
+            const size_t at = ((size_t)g * capacity + length + t) * LRO_AT_D;
+            attn_norm_rope(kr + t * KVW + g * LRO_AT_D, k_norm, eps, cr, sr, k_cache + at);
+            memcpy(v_cache + at, vr + t * KVW + g * LRO_AT_D, sizeof(uint16_t) * LRO_AT_D);
+        }
+    }
+    float qf[LRO_AT_D];
+    float o[LRO_AT_D];
+    for (int t = 0; t < T; ++t) {
+        const int seen = length + t + 1;
+        for (int h = 0; h < LRO_AT_HEADS; ++h) {
+            const int g = h / (LRO_AT_HEADS / LRO_AT_KV);
+            const uint16_t *kc = k_cache + (size_t)g * capacity * LRO_AT_D;
+            const uint16_t *vc = v_cache + (size_t)g * capacity * LRO_AT_D;
+            to_floats(q + (size_t)t * LRO_AT_O + h * LRO_AT_D, qf, LRO_AT_D);
+            float m = -INFINITY;
+            for (int p = 0; p < seen; ++p) {
+                s[p] = rbf(lro_canon_dot(kc + (size_t)p * LRO_AT_D, qf, LRO_AT_D)) * 0.0625f;
+                if (s[p] > m) m = s[p];
+            }
+            float sum = 0.0f;
+            for (int p = 0; p < seen; ++p) {
+                s[p] = lro_exp(s[p] - m);
+                sum += s[p];
+            }
+            for (int d = 0; d < LRO_AT_D; ++d) o[d] = 0.0f;
+            for (int p = 0; p < seen; ++p) {
+                const float pr = rbf(s[p] / sum);
+                for (int d = 0; d < LRO_AT_D; ++d) o[d] = fmaf(pr, lro_bf16_value(vc[(size_t)p * LRO_AT_D + d]), o[d]);
+            }
+            const uint16_t *gate = qg + (size_t)t * LRO_AT_QG + h * 2 * LRO_AT_D + LRO_AT_D;
+            for (int d = 0; d < LRO_AT_D; ++d) {
+                const float sg = rbf(1.0f / (1.0f + lro_exp(-lro_bf16_value(gate[d]))));
+                att[(size_t)t * LRO_AT_O + h * LRO_AT_D + d] = lro_bf16_round(rbf(o[d]) * sg);
+            }
+        }
+    }
+    for (int t = 0; t < T; ++t) {
+        to_floats(att + (size_t)t * LRO_AT_O, xf, LRO_AT_O);
+        for (size_t r = 0; r < H; ++r) out[t * H + r] = lro_bf16_round(lro_canon_dot(w_o + r * LRO_AT_O, xf, LRO_AT_O));
+    }
+    free(s);
+    free(xf);
+    free(att);
+    free(q);
+    free(vr);
+    free(kr);
+    free(qg);
 }

@@ -79,6 +79,8 @@ def lib() -> C.CDLL:
     so.lro_delta_rule.restype = None
     so.lro_delta_mixer.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, C.c_int, _P, _P]
     so.lro_delta_mixer.restype = None
+    so.lro_attn_decode.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, C.c_int, C.c_int, _P]
+    so.lro_attn_decode.restype = None
     so.lro_codec_pack.argtypes = [_P, C.c_int64, C.c_int, _P, _P]
     so.lro_codec_pack.restype = C.c_int64
     so.lro_codec_unpack.argtypes = [_P, _P, C.c_int64, C.c_int, _P]
@@ -326,6 +328,36 @@ def delta_mixer(x, weights: dict, conv_state, state, eps: float = 1e-6, record: 
                           _ptr(w["norm"]), float(eps), _ptr(w["out_proj"]), _ptr(conv), _ptr(st), int(bf16_state),
                           _ptr(rec), _ptr(out))
     return out, conv, st, rec
+
+
+AT_HEADS, AT_KV, AT_D, AT_ROT = 16, 2, 256, 64
+
+
+def attn_decode(x, weights: dict, cos, sin, k_cache, v_cache, length: int, eps: float = 1e-6):
+    """The full-attention decode step for x [T, 2048] after `length` cached
+    positions (lro_attn_decode).  weights: q_proj [8192, 2048], k_proj and
+    v_proj [512, 2048], o_proj [2048, 4096], q_norm and k_norm [256], all
+    bf16 bits; cos, sin [T, 64] bf16 bits; k_cache, v_cache [2, capacity,
+    256] bf16 bits are copied.  Returns (out [T, 2048], new k_cache, new
+    v_cache)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    T = x.shape[0]
+    w = {name: np.ascontiguousarray(weights[name], dtype=np.uint16)
+         for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")}
+    cos = np.ascontiguousarray(cos, dtype=np.uint16)
+    sin = np.ascontiguousarray(sin, dtype=np.uint16)
+    kc = np.array(k_cache, dtype=np.uint16, copy=True, order="C")
+    vc = np.array(v_cache, dtype=np.uint16, copy=True, order="C")
+    capacity = kc.shape[1]
+    if kc.shape != (AT_KV, capacity, AT_D) or vc.shape != kc.shape or length + T > capacity:
+        raise ValueError(f"caches must be [{AT_KV}, capacity >= {length + T}, {AT_D}], got {kc.shape}, {vc.shape}")
+    if cos.shape != (T, AT_ROT) or sin.shape != (T, AT_ROT):
+        raise ValueError(f"cos and sin must be [{T}, {AT_ROT}]")
+    out = np.empty((T, HIDDEN), dtype=np.uint16)
+    lib().lro_attn_decode(_ptr(x), T, _ptr(w["q_proj"]), _ptr(w["k_proj"]), _ptr(w["v_proj"]), _ptr(w["o_proj"]),
+                          _ptr(w["q_norm"]), _ptr(w["k_norm"]), float(eps), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc),
+                          capacity, int(length), _ptr(out))
+    return out, kc, vc
 
 
 CODEC_TILE = 256
