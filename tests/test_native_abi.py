@@ -96,6 +96,19 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_moe_chain(dummy, 1, 0, table, C.c_float(1e-6), dummy, null, null, dummy, 8, null) == 0
     # zero tokens is a successful no-op
     assert lib.lrmoe_moe_experts(dummy, 0, dummy, dummy, dummy, dummy, dummy, 0, null) == 0
+    # attention decode: more than 16 tokens, a cache too short for the new
+    # positions, missing pointers, a short workspace; zero tokens is a no-op
+    w8 = dummy
+    aligned = C.c_void_p(256)  # the workspace must be 256-byte aligned
+    args = lambda tokens, cap, length, ws: (w8, tokens, w8, w8, w8, w8, w8, w8, C.c_float(1e-6), w8, w8, w8, w8,
+                                            cap, length, w8, aligned, ws, null)
+    assert lib.lrmoe_attn_workspace_bytes(17) == 0 and lib.lrmoe_attn_workspace_bytes(16) > 0
+    assert lib.lrmoe_attn_decode(*args(17, 100, 0, big)) == -1
+    assert lib.lrmoe_attn_decode(*args(4, 100, 97, big)) == -1
+    assert lib.lrmoe_attn_decode(*args(4, (1 << 22) + 1, 0, big)) == -1
+    assert lib.lrmoe_attn_decode(null, 1, *args(1, 100, 0, big)[2:]) == -1
+    assert lib.lrmoe_attn_decode(*args(1, 100, 0, 8)) == -2
+    assert lib.lrmoe_attn_decode(*args(0, 100, 0, 0)) == 0
     from lightreason_amd import _native
 
     with pytest.raises(ValueError):
