@@ -11,9 +11,12 @@ Also reported under "configs": T=1 decode layer with the router (latency and
 GB/s), the raw expert gather at T in {1,4,8,16}, the 40-layer decode chain
 with RMSNorm + residual at T=1 and T=16 (one persistent launch, and for
 comparison one launch per layer in a graph), the T=2048 prefill (TFLOPS),
-and (C7) the Gated DeltaNet mixer step of the 30 linear-attention layers at
+(C7) the Gated DeltaNet mixer step of the 30 linear-attention layers at
 T=1 and T=16 (µs and GB/s on its weight and state bytes, per-kernel times,
-a torch gate, and the oracle's C step timed on one core beside it).
+a torch gate, and the oracle's C step timed on one core beside it), and (C8)
+the full-attention decode step of the 10 full-attention layers at a
+4096-position context, T=1 and T=16 (the same figures on its weight and
+key/value bytes).
 
 `roofline` is for moe_decode, the one kernel of the headline step, timed
 with HIP events stamped by its own dispatches, against the 8 TB/s spec and,
@@ -684,6 +687,130 @@ def mixer_cpu_leg(mix, budget_s: float = 3.0) -> dict:
             "sample": f"{calls} calls of the oracle's C mixer step on one layer"}
 
 
+ATTN_LAYERS = 10     # full-attention layers of the 35B model
+ATTN_CONTEXT = 4096  # cached positions before each C8 step
+ATTN_WEIGHT_BYTES = ((8192 + 512 + 512) * HIDDEN + HIDDEN * 4096) * 2
+
+
+def attn_bytes(tokens: int, length: int) -> int:
+    """Algorithmic HBM bytes of one full-attention step: the weights once,
+    the key and value rows of every position read (2 heads x 256 x 2 B
+    each), the new rows written, per token the hidden row in and out."""
+    return ATTN_WEIGHT_BYTES + (length + tokens) * 2 * 2 * 256 * 2 + tokens * 2 * 2 * 256 * 2 + tokens * 2 * HIDDEN * 2
+
+
+def torch_attn_step(a, x, cos, sin, k_cache, v_cache, length):
+    """The full-attention step in torch on the GPU, fp32 arithmetic with the
+    Transformers eager forward's bf16 rounding points ([HF]
+    Qwen3_5MoeAttention.forward, Qwen3_5MoeRMSNorm, apply_rotary_pos_emb,
+    eager_attention_forward): the bench's gate for C8.  Caches are read, not
+    modified.  Returns out [T, 2048] fp32."""
+    r = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    T = x.shape[0]
+    xf = x.float()
+    qg = r(xf @ a.q_proj.float().T).view(T, 16, 512)
+    q, gate = qg[..., :256], qg[..., 256:]
+    k = r(xf @ a.k_proj.float().T).view(T, 2, 256)
+    v = r(xf @ a.v_proj.float().T).view(T, 2, 256)
+
+    def norm_rope(h, w):
+        n = r((h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + a.eps)) * (1.0 + w.float()))
+        c, s_ = cos.float()[:, None, :], sin.float()[:, None, :]
+        rot = torch.cat([-n[..., 32:64], n[..., :32]], dim=-1)
+        return torch.cat([r(r(n[..., :64] * c) + r(rot * s_)), n[..., 64:]], dim=-1)
+
+    q, k = norm_rope(q, a.q_norm), norm_rope(k, a.k_norm)
+    keys = torch.cat([k_cache[:, :length].float(), k.transpose(0, 1)], dim=1)     # [2, L + T, 256]
+    vals = torch.cat([v_cache[:, :length].float(), v.transpose(0, 1)], dim=1)
+    kk, vv = keys.repeat_interleave(8, 0), vals.repeat_interleave(8, 0)          # [16, L + T, 256]
+    s = r(torch.einsum("thd,hpd->htp", q, kk)) * 0.0625
+    mask = torch.arange(length + T, device=x.device)[None, :] > (length + torch.arange(T, device=x.device))[:, None]
+    s = s.masked_fill(mask[None], float("-inf"))
+    p = r(torch.softmax(s, dim=-1))
+    o = r(torch.einsum("htp,hpd->thd", p, vv))
+    att = r(o * r(torch.sigmoid(gate))).reshape(T, 4096)
+    return r(att @ a.o_proj.float().T)
+
+
+def bench_attention(device, seed: int, passes: int, skip_cpu: bool) -> dict:
+    """C8: one cached full-attention decode step (lrmoe_attn_decode) at T = 1
+    (decode) and T = 16 (a verify block) after 4096 cached positions,
+    rotating over 10 resident layers (0.55 GB of weights: no step finds its
+    weights in the Infinity Cache), as graph replays; the step's kernel time
+    from the event pair stamped by its first and last dispatches; a torch
+    gate on layer 0 before timing.  Random weights ~N(0, 0.02), norms
+    ~N(0, 0.1), cached rows ~N(0, 1)."""
+    from lightreason_amd.attention import AttentionDecode
+
+    g = torch.Generator(device=device).manual_seed(seed + 8)
+    rnd = lambda *shape, s=0.02: (torch.randn(*shape, generator=g, device=device) * s).to(torch.bfloat16)  # noqa: E731
+    layers = [AttentionDecode(q_proj=rnd(8192, HIDDEN), k_proj=rnd(512, HIDDEN), v_proj=rnd(512, HIDDEN),
+                              o_proj=rnd(HIDDEN, 4096), q_norm=rnd(256, s=0.1), k_norm=rnd(256, s=0.1))
+              for _ in range(ATTN_LAYERS)]
+    L = ATTN_CONTEXT
+    caches = [(rnd(2, L + 16, 256, s=1.0), rnd(2, L + 16, 256, s=1.0)) for _ in range(ATTN_LAYERS)]
+    pos = torch.arange(L, L + 16, device=device, dtype=torch.float32)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, device=device, dtype=torch.float32) / 64))
+    ang = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], dim=1)
+    cos_all, sin_all = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    out = {}
+    for T in (1, 16):
+        xs = [(torch.randn(T, HIDDEN, generator=g, device=device)).to(torch.bfloat16) for _ in range(ATTN_LAYERS)]
+        outs = [torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=device) for _ in range(ATTN_LAYERS)]
+        cos, sin = cos_all[:T].contiguous(), sin_all[:T].contiguous()
+        a0, (k0, v0) = layers[0], caches[0]
+        want = torch_attn_step(a0, xs[0], cos, sin, k0, v0, L)
+        got = a0.step(xs[0], cos, sin, k0, v0, L).float()
+        tensor_rel = float((got - want).abs().max() / want.abs().max().clamp_min(1e-30))
+        row_l2 = float(((got - want).norm(dim=1) / want.norm(dim=1).clamp_min(1e-30)).max())
+        gate = {"tokens_checked": T, "max_rel": round(tensor_rel, 5), "worst_row_l2_rel": round(row_l2, 5),
+                "tolerance": 1e-2, "ok": bool(tensor_rel <= 1e-2 and row_l2 <= 1e-2 and torch.isfinite(got).all())}
+
+        def run(n, T=T, xs=xs, outs=outs, cos=cos, sin=sin):
+            for i in range(n):
+                l = i % ATTN_LAYERS
+                layers[l].step(xs[l], cos, sin, caches[l][0], caches[l][1], L, out=outs[l])
+
+        steps = ATTN_LAYERS * passes * 3
+        graph = capture(lambda: run(steps))
+        graph.replay()
+        ms = timed_replays(graph, 1) / steps
+        del graph
+        torch.cuda.synchronize()
+        _native.timing_enable(_native.STAGE_ATTENTION, 2 * ATTN_LAYERS + 8)
+        run(2 * ATTN_LAYERS)
+        total, n = _native.timing_collect(_native.STAGE_ATTENTION)
+        _native.timing_enable(0)
+        kernel_us = total / max(n, 1) * 1e3
+        nbytes = attn_bytes(T, L)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"t{T}"] = dict(us_per_layer=round(ms * 1e3, 2), context=L, algorithmic_bytes=nbytes, gbs=round(gbs, 1),
+                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), kernels_us=round(kernel_us, 2),
+                            kernels_gbs=round(nbytes / (kernel_us * 1e-6) / 1e9, 1), parity=gate)
+    if not skip_cpu:
+        out["cpu_reference"] = attn_cpu_leg(layers[0], caches[0], cos_all[:1], sin_all[:1], L)
+    return out
+
+
+def attn_cpu_leg(a, cache, cos, sin, length, budget_s: float = 3.0) -> dict:
+    """The oracle's C attention step (oracle/lro.c lro_attn_decode, one
+    thread: the reference runs this step in Transformers) at T = 1 after
+    `length` cached positions, as many calls as fit in `budget_s`."""
+    from oracle import oracle as O
+
+    w = {name: bits(getattr(a, name)) for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")}
+    x = bits(torch.randn(1, HIDDEN, device=cos.device).to(torch.bfloat16))
+    kc, vc = bits(cache[0]), bits(cache[1])
+    c, s_ = bits(cos), bits(sin)
+    calls, t0 = 0, time.perf_counter()
+    while calls < 2 or time.perf_counter() - t0 < budget_s:
+        O.attn_decode(x, w, c, s_, kc, vc, length, eps=a.eps)
+        calls += 1
+    sec = (time.perf_counter() - t0) / calls
+    return {"value": round(sec * 1e6, 1), "unit": "us per T=1 attention step", "cores": 1, "kind": "port",
+            "sample": f"{calls} calls of the oracle's C attention step on one layer, {length} cached positions"}
+
+
 def bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
@@ -698,7 +825,7 @@ def main() -> int:
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=1.0, help="scale of the CPU legs' time budgets")
-    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6,c7 to run besides the headline "
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6,c7,c8 to run besides the headline "
                                                    "(default all)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
@@ -720,7 +847,7 @@ def main() -> int:
         f"in {time.perf_counter() - t0:.1f}s")
     L = args.layers
     aux = max(2, min(10, args.steps // L))  # graph replays of the secondary configs
-    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6", "c7"}
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6", "c7", "c8"}
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
@@ -975,6 +1102,10 @@ def main() -> int:
     if "c7" in only:
         configs["c7_delta_mixer"] = bench_mixers(device, args.seed, aux, args.skip_cpu)
         log(f"[bench] C7 mixer: {configs['c7_delta_mixer']}")
+    # ---- C8: full-attention decode step (the 10 full-attention layers) ----
+    if "c8" in only:
+        configs["c8_attention"] = bench_attention(device, args.seed, aux, args.skip_cpu)
+        log(f"[bench] C8 attention: {configs['c8_attention']}")
 
     cpu = {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference", "sample": "skipped"}
     if not args.skip_cpu:

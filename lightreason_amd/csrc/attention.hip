@@ -18,7 +18,7 @@
 //        the query rows of heads 8g..8g+7 normalised and rotated into LDS,
 //        the chunk's new positions (those >= length) normalised, rotated
 //        and appended to the caches, then per 32-position sub-block: key
-//        rows into LDS, value rows transposed into LDS, scores by MFMA
+//        and value rows into LDS, scores by MFMA
 //        (bf16-rounded, / 16), an online softmax per query row, P.V by MFMA
 //        into per-wave accumulators; the chunk's (max, sum, unnormalised
 //        rows) go to the partial buffers.
@@ -57,9 +57,13 @@ constexpr float kAtScale = 0.0625f;                 // 256^-0.5, exact
 
 // ---- projections: y[t][row] = bf16(sum_k W[row][k] x[t][k]) ---------------
 
+// Rows [0, split1) come from w0, [split1, split2) from w1 (row - split1),
+// the rest from w2 (row - split2): the q/gate, k and v matrices in one grid.
 template <int kRows, int kK>
-__global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
-                                                         int tokens, uint16_t* __restrict__ y, int y_stride) {
+__global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restrict__ w0, const uint16_t* __restrict__ w1,
+                                                         const uint16_t* __restrict__ w2, int split1, int split2,
+                                                         const uint16_t* __restrict__ x, int tokens,
+                                                         uint16_t* __restrict__ y, int y_stride) {
     constexpr int kRowsPerWave = kRows / kAtWaves;        // 2 or 1
     constexpr int kLoadsPerRow = 8 / kRowsPerWave;        // 4 or 8 loads of 1 KiB per wave and row
     static_assert(kK == 512 * kLoadsPerRow, "a wave streams its rows in 8 loads of 1 KiB");
@@ -73,9 +77,11 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
     const int t = lane & 15;
     const int g = lane >> 4;
     const int row0 = blockIdx.x * kRows;
+    const uint16_t* w = row0 < split1 ? w0 : (row0 < split2 ? w1 : w2);
+    const int wrow0 = row0 < split1 ? row0 : (row0 < split2 ? row0 - split1 : row0 - split2);
     // the rows first (every lane loads: the tile is always full)
     uint4 wv[8];
-    const uint16_t* wrow = w + static_cast<int64_t>(row0 + kRowsPerWave * wave) * kK + 8 * lane;
+    const uint16_t* wrow = w + static_cast<int64_t>(wrow0 + kRowsPerWave * wave) * kK + 8 * lane;
 #pragma unroll
     for (int i = 0; i < 8; ++i) wv[i] = ldg16(wrow + (i / kLoadsPerRow) * kK + 512 * (i % kLoadsPerRow));
     // token rows (columns t >= T read token 0: their outputs are dropped)
@@ -139,13 +145,22 @@ __device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float e
     return make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
-__global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t qs[kAtMaxRows][kAtQStride];  // normed, rotated query rows
+// kRows: the query rows the launch supports (8 T for T <= kRows / 8): 32
+// (about 63 KB of LDS, two workgroups per CU) or 128.
+template <int kRows>
+__global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(AttnArgs a) {
+    constexpr int kMaxT = kRows / kAtGroup;
+    constexpr int kRowTiles = kRows / 16;
+    __shared__ __attribute__((aligned(16))) uint16_t qs[kRows][kAtQStride];  // normed, rotated query rows
     __shared__ __attribute__((aligned(16))) uint16_t ks[kAtSub][kAtQStride];      // a sub-block's key rows
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kAtD][kAtVStride];        // its value rows, transposed
-    __shared__ float sc[kAtMaxRows][kAtSStride];                                  // its scores
-    __shared__ __attribute__((aligned(16))) uint16_t es[kAtMaxRows][kAtVStride];  // its exp(score - max), bf16
-    __shared__ float mrow[kAtMaxRows], lrow[kAtMaxRows], frow[kAtMaxRows];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kAtSub][kAtQStride];      // its value rows
+    __shared__ float sc[kRows][kAtSStride];                                  // its scores
+    __shared__ __attribute__((aligned(16))) uint16_t es[kRows][kAtVStride];  // its exp(score - max), bf16
+    __shared__ float mrow[kRows], lrow[kRows], frow[kRows];
+    __shared__ __attribute__((aligned(16))) uint16_t nw[2][kAtD];           // q_norm, k_norm
+    __shared__ __attribute__((aligned(16))) uint16_t cs[2][kMaxT][kAtRot];  // cos, sin
+    __shared__ __attribute__((aligned(16))) uint16_t fk[kMaxT][kAtD];       // the new positions' key rows
+    __shared__ __attribute__((aligned(16))) uint16_t fv[kMaxT][kAtD];       // and value rows
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -164,67 +179,121 @@ __global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
     uint16_t* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
     uint16_t* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
 
-    // query rows of heads 8g .. 8g + 7 (wave w: rows w, w + 8, ...)
-    for (int r = wave; r < R; r += kAtWaves) {
-        const int t = r >> 3;
-        const int h = kAtGroup * g + (r & 7);
-        const uint2 raw = *reinterpret_cast<const uint2*>(a.proj + static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + 4 * lane);
-        const uint2 q = norm_rope(raw, a.q_norm, a.eps, a.cos + t * kAtRot, a.sin + t * kAtRot, lane);
-        *reinterpret_cast<uint2*>(&qs[r][4 * lane]) = q;
+    // Every load below is issued by every lane (dummy addresses where a lane
+    // needs none), in the order of need, so that the compiler's in-order
+    // waits for one cover only what is older.
+    // (1) wave w's query rows: head 8g + w, tokens 0 .. T - 1 (rows w + 8 t)
+    uint2 raw[kMaxT];
+    const uint16_t* qsrc = a.proj + (kAtGroup * g + wave) * 2 * kAtD + 4 * lane;
+#pragma unroll
+    for (int j = 0; j < kMaxT; ++j)
+        raw[j] = *reinterpret_cast<const uint2*>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
+    // (2) norm weights, cos, sin: 8-byte pieces; piece i < 128 a norm
+    // weight's, then T x 16 pieces of cos and of sin
+    const int pieces = 128 + 32 * T;
+    uint2 pc[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = tid + kAtThreads * k < pieces ? tid + kAtThreads * k : 0;
+        const uint16_t* src = i < 64 ? a.q_norm + 4 * i
+                            : i < 128 ? a.k_norm + 4 * (i - 64)
+                            : ((i - 128) < 16 * T ? a.cos : a.sin) + 4 * ((i - 128) % (16 * T));
+        pc[k] = *reinterpret_cast<const uint2*>(src);
     }
-    // new positions of this chunk: keys normed and rotated, values as
-    // projected, appended to the caches (agent-scope stores, complete before
-    // this workgroup's agent-scope loads below read them)
+    // (3) key and value rows of sub-blocks 0 and 1 (16-byte piece j of a
+    // sub-block: row j / 32, dims 8 (j % 32) ..; rows past the chunk read
+    // zeros: the buffer range ends at p1).  Rows of new positions read
+    // whatever the cache held; the staging below takes them from fk / fv.
+    const uint32_t range = static_cast<uint32_t>(p1) * kAtD * 2;
+    uint4 kb[2][2], vb[2][2];  // [sub-block parity][piece]
+    auto issue = [&](int parity, int q0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int j = tid + kAtThreads * i;
+            const uint32_t off = static_cast<uint32_t>(((q0 + (j >> 5)) * kAtD + 8 * (j & 31)) * 2);
+            kb[parity][i] = ld_agent16(kc, off, range);
+            vb[parity][i] = ld_agent16(vc, off, range);
+        }
+    };
+    issue(0, p0);
+    issue(1, p0 + kAtSub);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = tid + kAtThreads * k;
+        if (i < pieces) {
+            uint16_t* dst = i < 128 ? &nw[i >> 6][4 * (i & 63)]
+                                    : &cs[(i - 128) / (16 * T)][((i - 128) % (16 * T)) >> 4][4 * ((i - 128) & 15)];
+            *reinterpret_cast<uint2*>(dst) = pc[k];
+        }
+    }
+    if (tid < kRows) {
+        mrow[tid] = -__builtin_inff();
+        lrow[tid] = 0.0f;
+        frow[tid] = 1.0f;
+    }
+    __syncthreads();
+    // (4) the query rows normed and rotated into qs
+#pragma unroll
+    for (int j = 0; j < kMaxT; ++j) {
+        if (j < T) {
+            const uint2 q = norm_rope(raw[j], nw[0], a.eps, cs[0][j], cs[1][j], lane);
+            *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * j][4 * lane]) = q;
+        }
+    }
+    // (5) new positions of this chunk: keys normed and rotated, values as
+    // projected, into fk / fv for this call and appended to the caches for
+    // later ones (no other workgroup reads them in this call)
     for (int p = max(p0, L) + wave; p < p1; p += kAtWaves) {
         const int t = p - L;
         const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
         const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
         const uint2 vraw = *reinterpret_cast<const uint2*>(pr + kAtVRow + g * kAtD + 4 * lane);
-        const uint2 k = norm_rope(kraw, a.k_norm, a.eps, a.cos + t * kAtRot, a.sin + t * kAtRot, lane);
-        st_agent64(kc + static_cast<int64_t>(p) * kAtD + 4 * lane, static_cast<uint64_t>(k.x) | (static_cast<uint64_t>(k.y) << 32));
-        st_agent64(vc + static_cast<int64_t>(p) * kAtD + 4 * lane, static_cast<uint64_t>(vraw.x) | (static_cast<uint64_t>(vraw.y) << 32));
+        const uint2 k = norm_rope(kraw, nw[1], a.eps, cs[0][t], cs[1][t], lane);
+        *reinterpret_cast<uint2*>(&fk[t][4 * lane]) = k;
+        *reinterpret_cast<uint2*>(&fv[t][4 * lane]) = vraw;
+        st_agent64(kc + static_cast<int64_t>(p) * kAtD + 4 * lane,
+                   static_cast<uint64_t>(k.x) | (static_cast<uint64_t>(k.y) << 32));
+        st_agent64(vc + static_cast<int64_t>(p) * kAtD + 4 * lane,
+                   static_cast<uint64_t>(vraw.x) | (static_cast<uint64_t>(vraw.y) << 32));
     }
-    if (tid < kAtMaxRows) {
-        mrow[tid] = -__builtin_inff();
-        lrow[tid] = 0.0f;
-        frow[tid] = 1.0f;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     // P.V accumulators: wave w owns dim tiles 2w, 2w + 1 of every row tile
-    f32x4 acc[8][2];
+    f32x4 acc[kRowTiles][2];
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+    for (int rt = 0; rt < kRowTiles; ++rt)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[rt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // rows past the chunk read zeros (the buffer range ends at p1)
-    const uint32_t range = static_cast<uint32_t>(p1) * kAtD * 2;
-    for (int q0 = p0; q0 < p1; q0 += kAtSub) {
-        // (a) key rows into ks, value rows transposed into vt
+    // One sub-block: its rows from registers into ks / vs (16-byte stores
+    // along a row), the registers refilled with the sub-block two ahead,
+    // then scores, softmax, P.V.
+    auto sub_block = [&](int parity, int q0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int j = tid + kAtThreads * i;  // 16-byte piece: row j / 32, dims 8 (j % 32) ..
+            const int j = tid + kAtThreads * i;
             const int row = j >> 5;
             const int col = 8 * (j & 31);
-            const uint32_t off = static_cast<uint32_t>(((q0 + row) * kAtD + col) * 2);
-            const uint4 kv = ld_agent16(kc, off, range);
-            const uint4 vv = ld_agent16(vc, off, range);
-            *reinterpret_cast<uint4*>(&ks[row][col]) = kv;
-            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt[col + 2 * e][row] = static_cast<uint16_t>(w4[e] & 0xffffu);
-                vt[col + 2 * e + 1][row] = static_cast<uint16_t>(w4[e] >> 16);
-            }
+            const int t = q0 + row - L;  // a new position: its rows from fk / fv
+            const bool fresh = t >= 0 && q0 + row < p1;
+            // (both read, then selected: a select of addresses would put the
+            // register rows in memory)
+            const uint4 nk = *reinterpret_cast<const uint4*>(&fk[fresh ? t : 0][col]);
+            const uint4 nv = *reinterpret_cast<const uint4*>(&fv[fresh ? t : 0][col]);
+            const uint4 ok = kb[parity][i];
+            const uint4 ov = vb[parity][i];
+            *reinterpret_cast<uint4*>(&ks[row][col]) =
+                make_uint4(fresh ? nk.x : ok.x, fresh ? nk.y : ok.y, fresh ? nk.z : ok.z, fresh ? nk.w : ok.w);
+            *reinterpret_cast<uint4*>(&vs[row][col]) =
+                make_uint4(fresh ? nv.x : ov.x, fresh ? nv.y : ov.y, fresh ? nv.z : ov.z, fresh ? nv.w : ov.w);
         }
+        issue(parity, q0 + 2 * kAtSub);
         __syncthreads();
-        // (b) scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
+        // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
         {
             const int ct = wave & 1;
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
+            for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
                 const int rt = (wave >> 1) + 4 * k2;
                 if (rt < RT) {
                     f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -243,7 +312,7 @@ __global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
             }
         }
         __syncthreads();
-        // (c) online softmax: four threads per row, eight positions each
+        // online softmax: four threads per row, eight positions each
         {
             const int r = tid >> 2;
             const int q = tid & 3;
@@ -281,9 +350,21 @@ __global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
             }
         }
         __syncthreads();
-        // (d) P.V: rescale, then one k-step of 32 positions per tile
+        // P.V: rescale, then one k-step of 32 positions per tile; the B
+        // operand (positions 8 gq .. 8 gq + 7 of dim 16 dt + m) gathered
+        // from vs, once per dim tile
+        uint4 vop[2];
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt) {
+        for (int j = 0; j < 2; ++j) {
+            const int d = 16 * (2 * wave + j) + m;
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = static_cast<uint32_t>(vs[8 * gq + 2 * e][d]) | (static_cast<uint32_t>(vs[8 * gq + 2 * e + 1][d]) << 16);
+            vop[j] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) {
             if (rt < RT) {
                 const uint4 ea = *reinterpret_cast<const uint4*>(&es[16 * rt + m][8 * gq]);
                 float f[4];
@@ -291,20 +372,23 @@ __global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
                 for (int i = 0; i < 4; ++i) f[i] = frow[16 * rt + 4 * gq + i];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int dt = 2 * wave + j;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[rt][j][i] *= f[i];
-                    acc[rt][j] = mfma16x16x32(ea, *reinterpret_cast<const uint4*>(&vt[16 * dt + m][8 * gq]), acc[rt][j]);
+                    acc[rt][j] = mfma16x16x32(ea, vop[j], acc[rt][j]);
                 }
             }
         }
         __syncthreads();
+    };
+    for (int q0 = p0; q0 < p1; q0 += 2 * kAtSub) {
+        sub_block(0, q0);
+        if (q0 + kAtSub < p1) sub_block(1, q0 + kAtSub);
     }
 
     // the chunk's partials: unnormalised rows, running max and sum per row
-    float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks + c) * kAtMaxRows * kAtD;
+    float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks + c) * R * kAtD;
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
+    for (int rt = 0; rt < kRowTiles; ++rt) {
         if (rt < RT) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -317,34 +401,102 @@ __global__ __launch_bounds__(kAtThreads, 1) void at_attend(AttnArgs a) {
         }
     }
     if (tid < R) {
-        float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * kAtMaxRows + tid) * 2;
+        float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * R + tid) * 2;
         pm[0] = mrow[tid];
         pm[1] = lrow[tid];
     }
 }
 
 // ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
+// One workgroup of 1024 threads per (token, head): the chunks' (max, sum)
+// pairs into LDS, the weights exp(m_c - M); thread group q (64 threads, four
+// dims each) sums chunks q, q + 16, ... (one batch of loads in flight for up
+// to 128 chunks); the 16 partial rows meet in LDS in group order.
+constexpr int kAtCombineThreads = 1024;
+constexpr int kAtCombineGroups = kAtCombineThreads / 64;
 
-__global__ __launch_bounds__(kAtD) void at_combine(AttnArgs a) {
+__global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
+    __shared__ float wc[kAttnMaxChunks];
+    __shared__ float lc[kAttnMaxChunks];
+    __shared__ __attribute__((aligned(16))) float part[kAtCombineGroups][kAtD];
+    __shared__ float den_s;
     const int t = blockIdx.x / kAtHeads;
     const int h = blockIdx.x % kAtHeads;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x;
     const int g = h / kAtGroup;
+    const int R = kAtGroup * a.tokens;
     const int r = kAtGroup * t + (h % kAtGroup);
-    const float* pm = a.part_ml + (static_cast<int64_t>(g) * a.chunks * kAtMaxRows + r) * 2;
-    const float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks * kAtMaxRows + r) * kAtD + d;
-    float M = -__builtin_inff();
-    for (int c = 0; c < a.chunks; ++c) M = fmaxf(M, pm[static_cast<int64_t>(c) * kAtMaxRows * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int c = 0; c < a.chunks; ++c) {
-        const float mc = pm[static_cast<int64_t>(c) * kAtMaxRows * 2];
-        if (mc == -__builtin_inff()) continue;  // a chunk this token sees nothing of
-        const float wgt = lr_exp(mc - M);
-        den += pm[static_cast<int64_t>(c) * kAtMaxRows * 2 + 1] * wgt;
-        num += po[static_cast<int64_t>(c) * kAtMaxRows * kAtD] * wgt;
+    const int C = a.chunks;
+    const int64_t chunk_rows = static_cast<int64_t>(g) * C;  // first chunk of head g
+    // every load at once: the gate (threads < 256), the chunks' (max, sum)
+    // pairs, the first batch of partial rows (dummy rows where none)
+    const int q = tid >> 6;
+    const int d0 = 4 * (tid & 63);
+    const float* po = a.part_o + (chunk_rows * R + r) * kAtD + d0;
+    const int64_t cstride = static_cast<int64_t>(R) * kAtD;
+    const uint32_t graw = ldg_u16(a.proj + static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + (tid & (kAtD - 1)));
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2);
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int c = q + kAtCombineGroups * k;
+        v[k] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c < C ? c : 0) * cstride);
     }
-    const float o = rbf(num / den);
-    const float gate = bf2f(a.proj[static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + d]);
+    if (tid < C) {
+        wc[tid] = ml.x;
+        lc[tid] = ml.y;
+    }
+    __syncthreads();
+    if (tid < 64) {  // wave 0: the maximum, the weights, the denominator
+        float M = -__builtin_inff();
+        for (int c = tid; c < C; c += 64) M = fmaxf(M, wc[c]);
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        float den = 0.0f;
+        float wv[kAttnMaxChunks / 64];
+#pragma unroll
+        for (int k = 0; k < kAttnMaxChunks / 64; ++k) {
+            const int c = tid + 64 * k;
+            const float mc = c < C ? wc[c] : -__builtin_inff();
+            wv[k] = mc == -__builtin_inff() ? 0.0f : lr_exp(mc - M);  // a chunk this token sees nothing of: 0
+            if (c < C) den += lc[c] * wv[k];
+        }
+        den = wave_butterfly_sum(den);
+#pragma unroll
+        for (int k = 0; k < kAttnMaxChunks / 64; ++k) {
+            const int c = tid + 64 * k;
+            if (c < C) wc[c] = wv[k];
+        }
+        if (tid == 0) den_s = den;
+    }
+    __syncthreads();
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = q; c0 < C; c0 += kAtCombineGroups * 8) {
+        if (c0 != q) {  // chunks past the first batch (more than 128)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = c0 + kAtCombineGroups * k;
+                v[k] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c < C ? c : 0) * cstride);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int c = c0 + kAtCombineGroups * k;
+            const float wk = c < C ? wc[c] : 0.0f;
+            acc.x += v[k].x * wk;
+            acc.y += v[k].y * wk;
+            acc.z += v[k].z * wk;
+            acc.w += v[k].w * wk;
+        }
+    }
+    *reinterpret_cast<float4*>(&part[q][d0]) = acc;
+    __syncthreads();
+    if (tid >= kAtD) return;
+    const int d = tid;
+    float num = part[0][d];
+#pragma unroll
+    for (int k = 1; k < kAtCombineGroups; ++k) num += part[k][d];
+    const float o = rbf(num / den_s);
+    const float gate = bf2f(graw);
     const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
     a.att[static_cast<int64_t>(t) * kAtO + h * kAtD + d] = static_cast<uint16_t>(f2bf(o * sg));
 }
@@ -352,12 +504,14 @@ __global__ __launch_bounds__(kAtD) void at_combine(AttnArgs a) {
 }  // namespace
 
 int attn_chunk(int tokens, int total) {
-    // at least 64 positions per chunk per 4 tokens (the partials stay below
-    // the key/value bytes), at most kAttnMaxChunks chunks per key/value head
-    const int floor_p = kAtSub * 2 * ((tokens + 3) / 4);
-    const int need = (total + kAttnMaxChunks - 1) / kAttnMaxChunks;
-    const int p = ((need + kAtSub - 1) / kAtSub) * kAtSub;
-    return p > floor_p ? p : floor_p;
+    // one sub-block per chunk up to 4 tokens, two above (the partials of
+    // 8 T rows per chunk stay near the key/value bytes), and few enough
+    // chunks for both heads' workgroups to be resident at once: 256 per head
+    // up to 4 tokens (two workgroups per CU), 128 above (one)
+    const int floor_p = tokens <= 4 ? kAtSub : 2 * kAtSub;
+    const int cap = tokens <= 4 ? kAttnMaxChunks : kAttnMaxChunks / 2;
+    const int need = (total + cap - 1) / cap;
+    return need > floor_p ? need : floor_p;
 }
 
 size_t attn_workspace_bytes(int tokens) {
@@ -376,8 +530,9 @@ AttnWorkspace carve_attn(void* base, int tokens) {
     const size_t T = static_cast<size_t>(tokens);
     w.proj = reinterpret_cast<uint16_t*>(take(T * kAtProj * 2));
     w.att = reinterpret_cast<uint16_t*>(take(T * kAtO * 2));
-    w.part_o = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * kAtMaxRows * kAtD * 4));
-    w.part_ml = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * kAtMaxRows * 2 * 4));
+    const size_t rows = static_cast<size_t>(kAtGroup) * T;
+    w.part_o = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * rows * kAtD * 4));
+    w.part_ml = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * rows * 2 * 4));
     w.bytes = off;
     return w;
 }
@@ -387,17 +542,17 @@ hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q
     static_assert(kAtProj % 16 == 0 && kHidden % 8 == 0, "projection grids");
     const int T = a.tokens;
     const StageEvents ev = timing_events(kStageAttention);
-    // q/gate, k, v rows: three weight matrices, one launch each over its rows
-    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtQg / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr, w_q, x, T,
-                 a.proj, kAtProj);
-    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtKv * kAtD / 16), dim3(kAtThreads), 0, stream, nullptr, nullptr, w_k,
-                 x, T, a.proj + kAtKRow, kAtProj);
-    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtKv * kAtD / 16), dim3(kAtThreads), 0, stream, nullptr, nullptr, w_v,
-                 x, T, a.proj + kAtVRow, kAtProj);
-    LRMOE_LAUNCH(at_attend, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
-    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads), dim3(kAtD), 0, stream, nullptr, nullptr, a);
-    LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, a.att, T,
-                 out, kHidden);
+    // q/gate, k and v rows: the three weight matrices in one grid
+    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr, w_q, w_k,
+                 w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj);
+    if (T <= 4) {
+        LRMOE_LAUNCH(at_attend<32>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
+    } else {
+        LRMOE_LAUNCH(at_attend<kAtMaxRows>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
+    }
+    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);
+    LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, w_o, w_o,
+                 kHidden, kHidden, a.att, T, out, kHidden);
     return hipGetLastError();
 }
 

@@ -425,7 +425,7 @@ constexpr int kDeltaMaxTokens = 16;
 
 // ---- full-attention decode step (attention.hip) ----
 constexpr int kAttnMaxTokens = 16;
-constexpr int kAttnMaxChunks = 128;  // position chunks per key/value head
+constexpr int kAttnMaxChunks = 256;  // position chunks per key/value head (up to 4 tokens; 128 above)
 struct AttnArgs {
     uint16_t* proj;         // [T][9216]: per token q/gate (8192), k (512), v (512) rows, bf16
     const uint16_t* q_norm; // [256]
@@ -438,10 +438,10 @@ struct AttnArgs {
     int capacity;
     int length;             // cached positions before the call
     int tokens;
-    int chunk;              // positions per chunk (a multiple of 32)
+    int chunk;              // positions per chunk
     int chunks;             // chunks per key/value head (<= kAttnMaxChunks)
-    float* part_o;          // [2][chunks][128][256] unnormalised rows
-    float* part_ml;         // [2][chunks][128][2] running max and sum
+    float* part_o;          // [2][chunks][8 T][256] unnormalised rows
+    float* part_ml;         // [2][chunks][8 T][2] running max and sum
     uint16_t* att;          // [T][4096] gated attention rows, bf16
 };
 struct AttnWorkspace {
