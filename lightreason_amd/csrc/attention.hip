@@ -145,22 +145,74 @@ __device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float e
     return make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
-// kRows: the query rows the launch supports (8 T for T <= kRows / 8): 32
-// (about 63 KB of LDS, two workgroups per CU) or 128.
 template <int kRows>
-__global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(AttnArgs a) {
+struct AttendLds {
+    static constexpr int kMaxT = kRows / kAtGroup;
+    __attribute__((aligned(16))) uint16_t qs[kRows][kAtQStride];  // normed, rotated query rows
+    __attribute__((aligned(16))) uint16_t ks[kAtSub][kAtQStride];  // a sub-block's key rows
+    __attribute__((aligned(16))) uint16_t vs[kAtSub][kAtQStride];  // its value rows
+    float sc[kRows][kAtSStride];                                   // its scores
+    __attribute__((aligned(16))) uint16_t es[kRows][kAtVStride];   // its exp(score - max), bf16
+    float mrow[kRows], lrow[kRows], frow[kRows];
+    __attribute__((aligned(16))) uint16_t nw[2][kAtD];             // q_norm, k_norm
+    __attribute__((aligned(16))) uint16_t cs[2][kMaxT][kAtRot];    // cos, sin
+    __attribute__((aligned(16))) uint16_t fk[kMaxT][kAtD];         // the new positions' key rows
+    __attribute__((aligned(16))) uint16_t fv[kMaxT][kAtD];         // and value rows
+};
+
+// Key and value rows of the sub-block at q0 into kb[parity] / vb[parity]
+// (16-byte piece j = tid + 512 i: row j / 32, dims 8 (j % 32) ..; rows at or
+// past p1 read zeros: the buffer range ends there).
+__device__ __forceinline__ void attend_issue(uint4 (&kb)[2][2], uint4 (&vb)[2][2], int parity, const uint16_t* kc,
+                                             const uint16_t* vc, int q0, uint32_t range, int tid) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int j = tid + kAtThreads * i;
+        const uint32_t off = static_cast<uint32_t>(((q0 + (j >> 5)) * kAtD + 8 * (j & 31)) * 2);
+        kb[parity][i] = ld_agent16(kc, off, range);
+        vb[parity][i] = ld_agent16(vc, off, range);
+    }
+}
+
+__device__ __forceinline__ uint32_t attend_range(const AttnArgs& a, int c) {
+    return static_cast<uint32_t>(min((c + 1) * a.chunk, a.length + a.tokens)) * kAtD * 2;
+}
+
+// proj rows are read with agent-scope loads (kShared) when this launch's
+// other workgroups wrote them, else with plain ones; so are the partials
+// written.
+template <bool kShared>
+__device__ __forceinline__ uint2 ld_pair(const uint16_t* p) {
+    if constexpr (kShared) {
+        const uint64_t v = ld_agent64(p);
+        return make_uint2(static_cast<uint32_t>(v), static_cast<uint32_t>(v >> 32));
+    } else {
+        return *reinterpret_cast<const uint2*>(p);
+    }
+}
+
+// The attention partials of chunk c of key/value head g, for 8 T <= kRows
+// query rows (512 threads): the query rows normed and rotated, the chunk's
+// new positions appended, then per 32-position sub-block scores, online
+// softmax and P.V; (max, sum, unnormalised rows) to the partial buffers.
+// kb / vb hold sub-blocks 0 and 1 if `issued`, else are requested here.
+template <int kRows, bool kShared>
+__device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>& S, int g, int c, uint4 (&kb)[2][2],
+                                             uint4 (&vb)[2][2], bool issued) {
     constexpr int kMaxT = kRows / kAtGroup;
     constexpr int kRowTiles = kRows / 16;
-    __shared__ __attribute__((aligned(16))) uint16_t qs[kRows][kAtQStride];  // normed, rotated query rows
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kAtSub][kAtQStride];      // a sub-block's key rows
-    __shared__ __attribute__((aligned(16))) uint16_t vs[kAtSub][kAtQStride];      // its value rows
-    __shared__ float sc[kRows][kAtSStride];                                  // its scores
-    __shared__ __attribute__((aligned(16))) uint16_t es[kRows][kAtVStride];  // its exp(score - max), bf16
-    __shared__ float mrow[kRows], lrow[kRows], frow[kRows];
-    __shared__ __attribute__((aligned(16))) uint16_t nw[2][kAtD];           // q_norm, k_norm
-    __shared__ __attribute__((aligned(16))) uint16_t cs[2][kMaxT][kAtRot];  // cos, sin
-    __shared__ __attribute__((aligned(16))) uint16_t fk[kMaxT][kAtD];       // the new positions' key rows
-    __shared__ __attribute__((aligned(16))) uint16_t fv[kMaxT][kAtD];       // and value rows
+    auto& qs = S.qs;
+    auto& ks = S.ks;
+    auto& vs = S.vs;
+    auto& sc = S.sc;
+    auto& es = S.es;
+    auto& mrow = S.mrow;
+    auto& lrow = S.lrow;
+    auto& frow = S.frow;
+    auto& nw = S.nw;
+    auto& cs = S.cs;
+    auto& fk = S.fk;
+    auto& fv = S.fv;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -170,8 +222,6 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
     const int T = a.tokens;
     const int R = kAtGroup * T;  // query rows r = 8 t + local head
     const int RT = (R + 15) / 16;
-    const int g = blockIdx.x / a.chunks;
-    const int c = blockIdx.x % a.chunks;
     const int L = a.length;
     const int total = L + T;
     const int p0 = c * a.chunk;
@@ -187,7 +237,7 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
     const uint16_t* qsrc = a.proj + (kAtGroup * g + wave) * 2 * kAtD + 4 * lane;
 #pragma unroll
     for (int j = 0; j < kMaxT; ++j)
-        raw[j] = *reinterpret_cast<const uint2*>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
+        raw[j] = ld_pair<kShared>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
     // (2) norm weights, cos, sin: 8-byte pieces; piece i < 128 a norm
     // weight's, then T x 16 pieces of cos and of sin
     const int pieces = 128 + 32 * T;
@@ -205,18 +255,10 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
     // zeros: the buffer range ends at p1).  Rows of new positions read
     // whatever the cache held; the staging below takes them from fk / fv.
     const uint32_t range = static_cast<uint32_t>(p1) * kAtD * 2;
-    uint4 kb[2][2], vb[2][2];  // [sub-block parity][piece]
-    auto issue = [&](int parity, int q0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int j = tid + kAtThreads * i;
-            const uint32_t off = static_cast<uint32_t>(((q0 + (j >> 5)) * kAtD + 8 * (j & 31)) * 2);
-            kb[parity][i] = ld_agent16(kc, off, range);
-            vb[parity][i] = ld_agent16(vc, off, range);
-        }
-    };
-    issue(0, p0);
-    issue(1, p0 + kAtSub);
+    if (!issued) {
+        attend_issue(kb, vb, 0, kc, vc, p0, range, tid);
+        attend_issue(kb, vb, 1, kc, vc, p0 + kAtSub, range, tid);
+    }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = tid + kAtThreads * k;
@@ -246,8 +288,8 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
     for (int p = max(p0, L) + wave; p < p1; p += kAtWaves) {
         const int t = p - L;
         const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
-        const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
-        const uint2 vraw = *reinterpret_cast<const uint2*>(pr + kAtVRow + g * kAtD + 4 * lane);
+        const uint2 kraw = ld_pair<kShared>(pr + kAtKRow + g * kAtD + 4 * lane);
+        const uint2 vraw = ld_pair<kShared>(pr + kAtVRow + g * kAtD + 4 * lane);
         const uint2 k = norm_rope(kraw, nw[1], a.eps, cs[0][t], cs[1][t], lane);
         *reinterpret_cast<uint2*>(&fk[t][4 * lane]) = k;
         *reinterpret_cast<uint2*>(&fv[t][4 * lane]) = vraw;
@@ -287,7 +329,7 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
             *reinterpret_cast<uint4*>(&vs[row][col]) =
                 make_uint4(fresh ? nv.x : ov.x, fresh ? nv.y : ov.y, fresh ? nv.z : ov.z, fresh ? nv.w : ov.w);
         }
-        issue(parity, q0 + 2 * kAtSub);
+        attend_issue(kb, vb, parity, kc, vc, q0 + 2 * kAtSub, range, tid);
         __syncthreads();
         // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
         {
@@ -395,33 +437,58 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 16 * rt + 4 * gq + i;
-                    if (r < R) po[r * kAtD + 16 * (2 * wave + j) + m] = acc[rt][j][i];
+                    if (r < R) {
+                        float* dst = po + r * kAtD + 16 * (2 * wave + j) + m;
+                        if constexpr (kShared) st_agent32(dst, __float_as_uint(acc[rt][j][i]));
+                        else *dst = acc[rt][j][i];
+                    }
                 }
             }
         }
     }
     if (tid < R) {
         float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * R + tid) * 2;
-        pm[0] = mrow[tid];
-        pm[1] = lrow[tid];
+        if constexpr (kShared) {
+            st_agent64(pm, static_cast<uint64_t>(__float_as_uint(mrow[tid])) |
+                               (static_cast<uint64_t>(__float_as_uint(lrow[tid])) << 32));
+        } else {
+            pm[0] = mrow[tid];
+            pm[1] = lrow[tid];
+        }
     }
 }
 
-// ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
-// One workgroup of 1024 threads per (token, head): the chunks' (max, sum)
-// pairs into LDS, the weights exp(m_c - M); thread group q (64 threads, four
-// dims each) sums chunks q, q + 16, ... (one batch of loads in flight for up
-// to 128 chunks); the 16 partial rows meet in LDS in group order.
-constexpr int kAtCombineThreads = 1024;
-constexpr int kAtCombineGroups = kAtCombineThreads / 64;
+// kRows: the query rows the launch supports (8 T for T <= kRows / 8): 32
+// (about 63 KB of LDS, two workgroups per CU) or 128.
+template <int kRows>
+__global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(AttnArgs a) {
+    __shared__ AttendLds<kRows> S;
+    uint4 kb[2][2], vb[2][2];  // [sub-block parity][piece]
+    attend_chunk<kRows, false>(a, S, blockIdx.x / a.chunks, blockIdx.x % a.chunks, kb, vb, false);
+}
 
-__global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
-    __shared__ float wc[kAttnMaxChunks];
-    __shared__ float lc[kAttnMaxChunks];
-    __shared__ __attribute__((aligned(16))) float part[kAtCombineGroups][kAtD];
-    __shared__ float den_s;
-    const int t = blockIdx.x / kAtHeads;
-    const int h = blockIdx.x % kAtHeads;
+// ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
+// One workgroup per (token, head): the chunks' (max, sum) pairs into LDS, the
+// weights exp(m_c - M); thread group q (64 threads, four dims each) sums
+// chunks q, q + kGroups, ... (every load issued at once: the gate, the pairs
+// and 8 partial rows per thread); the groups' rows meet in LDS in group
+// order.
+template <int kGroups>
+struct CombineLds {
+    float wc[kAttnMaxChunks];
+    float lc[kAttnMaxChunks];
+    __attribute__((aligned(16))) float part[kGroups][kAtD];
+    __attribute__((aligned(16))) uint16_t out[kAtD];
+    float den;
+};
+
+template <int kThreads, bool kShared>
+__device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThreads / 64>& S, int t, int h) {
+    constexpr int kAtCombineGroups = kThreads / 64;
+    auto& wc = S.wc;
+    auto& lc = S.lc;
+    auto& part = S.part;
+    float& den_s = S.den;
     const int tid = threadIdx.x;
     const int g = h / kAtGroup;
     const int R = kAtGroup * a.tokens;
@@ -434,13 +501,31 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
     const int d0 = 4 * (tid & 63);
     const float* po = a.part_o + (chunk_rows * R + r) * kAtD + d0;
     const int64_t cstride = static_cast<int64_t>(R) * kAtD;
-    const uint32_t graw = ldg_u16(a.proj + static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + (tid & (kAtD - 1)));
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2);
+    // (the gate as the 4-byte word holding it)
+    const int64_t gi = static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + (tid & (kAtD - 1));
+    const uint32_t gword = kShared ? ld_agent32(a.proj + (gi & ~1ll)) : *reinterpret_cast<const uint32_t*>(a.proj + (gi & ~1ll));
+    const float* pml = a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2;
+    float2 ml;
+    if constexpr (kShared) {
+        const uint64_t w = ld_agent64(pml);
+        ml = make_float2(__uint_as_float(static_cast<uint32_t>(w)), __uint_as_float(static_cast<uint32_t>(w >> 32)));
+    } else {
+        ml = *reinterpret_cast<const float2*>(pml);
+    }
+    auto load_row = [&](int c) -> float4 {
+        const float* src = po + static_cast<int64_t>(c) * cstride;
+        if constexpr (kShared) {
+            const uint4 u = ld_agent16(a.part_o, static_cast<uint32_t>((src - a.part_o) * 4));
+            return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+        } else {
+            return *reinterpret_cast<const float4*>(src);
+        }
+    };
     float4 v[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int c = q + kAtCombineGroups * k;
-        v[k] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c < C ? c : 0) * cstride);
+        v[k] = load_row(c < C ? c : 0);
     }
     if (tid < C) {
         wc[tid] = ml.x;
@@ -475,7 +560,7 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int c = c0 + kAtCombineGroups * k;
-                v[k] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c < C ? c : 0) * cstride);
+                v[k] = load_row(c < C ? c : 0);
             }
         }
 #pragma unroll
@@ -490,15 +575,31 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
     }
     *reinterpret_cast<float4*>(&part[q][d0]) = acc;
     __syncthreads();
-    if (tid >= kAtD) return;
-    const int d = tid;
-    float num = part[0][d];
+    if (tid < kAtD) {
+        const int d = tid;
+        float num = part[0][d];
 #pragma unroll
-    for (int k = 1; k < kAtCombineGroups; ++k) num += part[k][d];
-    const float o = rbf(num / den_s);
-    const float gate = bf2f(graw);
-    const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
-    a.att[static_cast<int64_t>(t) * kAtO + h * kAtD + d] = static_cast<uint16_t>(f2bf(o * sg));
+        for (int k = 1; k < kAtCombineGroups; ++k) num += part[k][d];
+        const float o = rbf(num / den_s);
+        const float gate = bf2f((gi & 1) ? gword >> 16 : gword & 0xffffu);
+        const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
+        S.out[d] = static_cast<uint16_t>(f2bf(o * sg));
+    }
+    __syncthreads();
+    // the row as 4-byte words
+    if (tid < kAtD / 2) {
+        const uint32_t w = static_cast<uint32_t>(S.out[2 * tid]) | (static_cast<uint32_t>(S.out[2 * tid + 1]) << 16);
+        uint16_t* dst = a.att + static_cast<int64_t>(t) * kAtO + h * kAtD + 2 * tid;
+        if constexpr (kShared) st_agent32(dst, w);
+        else *reinterpret_cast<uint32_t*>(dst) = w;
+    }
+}
+
+constexpr int kAtCombineThreads = 1024;
+
+__global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
+    __shared__ CombineLds<kAtCombineThreads / 64> S;
+    combine_row<kAtCombineThreads, false>(a, S, blockIdx.x / kAtHeads, blockIdx.x % kAtHeads);
 }
 
 }  // namespace
