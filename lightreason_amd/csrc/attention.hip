@@ -114,35 +114,73 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
 
 // ---- attention partials ------------------------------------------------------
 
+// exp(x) for the softmax with the hardware base-2 exponential (x <= 0 here;
+// exp(-inf) = 0).  The attention parity is a float tolerance, not bits.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+// A lane's value moved by DPP control kCtrl (rows outside kRowMask get
+// `old`): a VALU cross-lane move, no LDS round trip.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp_f(float v, float old = 0.0f) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), kCtrl, kRowMask, 0xf, false));
+}
+
+// Sum and maximum over the 64 lanes, returned to every lane: quads (quad_perm
+// [1,0,3,2], [2,3,0,1]), the other quad of each 8 (row_half_mirror), the
+// other 8 of each row (row_mirror), then rows 0+1 and 2+3 (row_bcast15 into
+// rows 1, 3) and all four (row_bcast31 into rows 2, 3): lane 63 holds the
+// result.  The attention's sums need float accuracy, not a fixed order.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    v += dpp_f<0x142, 0xa>(v);
+    v += dpp_f<0x143, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v, v));  // (rows the broadcast skips keep their own)
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // One head row (256 dims, 4 per lane: dims 4 lane .. 4 lane + 3) normalised
 // ((x rsqrt(mean x^2 + eps)) (1 + w), fp32, then bf16) and rotated on dims
 // 0..63 (bf16(bf16(x cos) + bf16(rot(x) sin)), rot = [-x[32..63], x[0..31]]:
-// lane l < 16 pairs with lane l ^ 8).  Every lane of the wave calls it.
+// lane l < 16 pairs with lane l ^ 8, the row rotation by 8).  Every lane of
+// the wave calls it.
 __device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float eps, const uint16_t* cos_r,
                                           const uint16_t* sin_r, int lane) {
     const float x[4] = {lo_bf(raw.x), hi_bf(raw.x), lo_bf(raw.y), hi_bf(raw.y)};
-    const float ss = wave_butterfly_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float ss = wave_sum_dpp(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
     const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kAtD) + eps);
     const uint2 wr = *reinterpret_cast<const uint2*>(w + 4 * lane);
     const float wf[4] = {lo_bf(wr.x), hi_bf(wr.x), lo_bf(wr.y), hi_bf(wr.y)};
     float n[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) n[i] = rbf((x[i] * r) * (1.0f + wf[i]));
-    // rotary (lanes 0..15 hold dims 0..63); the shuffles run on every lane
+    // rotary (lanes 0..15 hold dims 0..63); the moves run on every lane
     const int d0 = 4 * (lane & 15);
     const uint2 cr = *reinterpret_cast<const uint2*>(cos_r + d0);
     const uint2 sr = *reinterpret_cast<const uint2*>(sin_r + d0);
     const float cf[4] = {lo_bf(cr.x), hi_bf(cr.x), lo_bf(cr.y), hi_bf(cr.y)};
     const float sf[4] = {lo_bf(sr.x), hi_bf(sr.x), lo_bf(sr.y), hi_bf(sr.y)};
-    uint32_t o[4];
+    float o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float partner = __shfl_xor(n[i], 8, 64);
+        const float partner = dpp_f<0x128>(n[i]);  // row_ror:8
         const float rot = (lane & 8) ? partner : -partner;
         const float v = rbf(rbf(n[i] * cf[i]) + rbf(rot * sf[i]));
-        o[i] = f2bf(lane < 16 ? v : n[i]);
+        o[i] = lane < 16 ? v : n[i];
     }
-    return make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    return make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
 }
 
 template <int kRows>
@@ -153,7 +191,9 @@ struct AttendLds {
     __attribute__((aligned(16))) uint16_t vs[kAtSub][kAtQStride];  // its value rows
     float sc[kRows][kAtSStride];                                   // its scores
     __attribute__((aligned(16))) uint16_t es[kRows][kAtVStride];   // its exp(score - max), bf16
-    float mrow[kRows], lrow[kRows], frow[kRows];
+    __attribute__((aligned(16))) float mrow[kRows];
+    __attribute__((aligned(16))) float lrow[kRows];
+    __attribute__((aligned(16))) float frow[kRows];
     __attribute__((aligned(16))) uint16_t nw[2][kAtD];             // q_norm, k_norm
     __attribute__((aligned(16))) uint16_t cs[2][kMaxT][kAtRot];    // cos, sin
     __attribute__((aligned(16))) uint16_t fk[kMaxT][kAtD];         // the new positions' key rows
@@ -274,12 +314,26 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         frow[tid] = 1.0f;
     }
     __syncthreads();
-    // (4) the query rows normed and rotated into qs
+    // (4) the query rows normed and rotated into qs: one row when T = 1,
+    // else up to 8 rows of the wave per pass (rows past T repeat token 0 and
+    // are not stored), so that their independent reductions interleave
+    constexpr int kPass = kMaxT < 8 ? kMaxT : 8;
+    if (T == 1) {
+        *reinterpret_cast<uint2*>(&qs[wave][4 * lane]) = norm_rope(raw[0], nw[0], a.eps, cs[0][0], cs[1][0], lane);
+    } else {
 #pragma unroll
-    for (int j = 0; j < kMaxT; ++j) {
-        if (j < T) {
-            const uint2 q = norm_rope(raw[j], nw[0], a.eps, cs[0][j], cs[1][j], lane);
-            *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * j][4 * lane]) = q;
+        for (int j0 = 0; j0 < kMaxT; j0 += kPass) {
+            if (j0 < T) {
+                uint2 q[kPass];
+#pragma unroll
+                for (int j = 0; j < kPass; ++j) {
+                    const int tj = j0 + j < T ? j0 + j : 0;
+                    q[j] = norm_rope(raw[j0 + j], nw[0], a.eps, cs[0][tj], cs[1][tj], lane);
+                }
+#pragma unroll
+                for (int j = 0; j < kPass; ++j)
+                    if (j0 + j < T) *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * (j0 + j)][4 * lane]) = q[j];
+            }
         }
     }
     // (5) new positions of this chunk: keys normed and rotated, values as
@@ -366,8 +420,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
                     s8[j] = sc[r][8 * q + j];
                     mx = fmaxf(mx, s8[j]);
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+                mx = fmaxf(mx, dpp_f<0xB1>(mx));
+                mx = fmaxf(mx, dpp_f<0x4E>(mx));
                 const float m_old = mrow[r];
                 const float m_new = fmaxf(m_old, mx);
                 const bool none = m_new == -__builtin_inff();
@@ -375,15 +429,15 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
                 uint32_t e2[4];
 #pragma unroll
                 for (int j = 0; j < 8; j += 2) {
-                    const uint32_t lo = none ? 0u : f2bf(lr_exp(s8[j] - m_new));
-                    const uint32_t hi = none ? 0u : f2bf(lr_exp(s8[j + 1] - m_new));
-                    sum += bf2f(lo) + bf2f(hi);
-                    e2[j / 2] = lo | (hi << 16);
+                    const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(s8[j] - m_new),
+                                                none ? 0.0f : fast_exp(s8[j + 1] - m_new));
+                    sum += lo_bf(e) + hi_bf(e);
+                    e2[j / 2] = e;
                 }
                 *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
-                sum += __shfl_xor(sum, 1, 64);
-                sum += __shfl_xor(sum, 2, 64);
-                const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : lr_exp(m_old - m_new));
+                sum += dpp_f<0xB1>(sum);
+                sum += dpp_f<0x4E>(sum);
+                const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : fast_exp(m_old - m_new));
                 if (q == 0) {
                     mrow[r] = m_new;
                     lrow[r] = lrow[r] * f + sum;
@@ -409,9 +463,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         for (int rt = 0; rt < kRowTiles; ++rt) {
             if (rt < RT) {
                 const uint4 ea = *reinterpret_cast<const uint4*>(&es[16 * rt + m][8 * gq]);
-                float f[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) f[i] = frow[16 * rt + 4 * gq + i];
+                const float4 f4 = *reinterpret_cast<const float4*>(&frow[16 * rt + 4 * gq]);
+                const float f[4] = {f4.x, f4.y, f4.z, f4.w};
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -535,7 +588,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThrea
     if (tid < 64) {  // wave 0: the maximum, the weights, the denominator
         float M = -__builtin_inff();
         for (int c = tid; c < C; c += 64) M = fmaxf(M, wc[c]);
-        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        M = wave_max_dpp(M);
         float den = 0.0f;
         float wv[kAttnMaxChunks / 64];
 #pragma unroll
@@ -545,7 +598,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThrea
             wv[k] = mc == -__builtin_inff() ? 0.0f : lr_exp(mc - M);  // a chunk this token sees nothing of: 0
             if (c < C) den += lc[c] * wv[k];
         }
-        den = wave_butterfly_sum(den);
+        den = wave_sum_dpp(den);
 #pragma unroll
         for (int k = 0; k < kAttnMaxChunks / 64; ++k) {
             const int c = tid + 64 * k;

@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void project_kernel(const int64_t* pointers, c
     }
     // D holds rows c0 + 4g + i (output columns) of route column n.
     uint16_t* dst = Y + static_cast<size_t>(e * 16 + n) * out + c0 + 4 * g;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(f2bf(acc[0]) | (f2bf(acc[1]) << 16), f2bf(acc[2]) | (f2bf(acc[3]) << 16));
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(acc[0], acc[1]), pack_bf2(acc[2], acc[3]));
 }
 
 // SwiGLU over [rows][1024] gate|up halves -> [rows][512] (the torch

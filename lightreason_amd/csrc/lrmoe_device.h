@@ -23,9 +23,18 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
+// bf16 bits of a float rounded to nearest even (gfx950's v_cvt_pk_bf16_f32;
+// for every non-NaN input the same bits as adding 0x7fff + the kept lsb and
+// truncating).
 __device__ __forceinline__ uint32_t f2bf(float value) {
-    const uint32_t bits = __float_as_uint(value);
-    return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
+}
+
+// Two floats as one word of bf16 bits, lo in the low half (one conversion).
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ float rbf(float value) { return bf2f(f2bf(value)); }

@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
             const int col = 16 * b + m;
             if (col < d.count) {
                 uint16_t* dst = a.ws.y + static_cast<size_t>(d.pair0 + col) * kHidden + d.h0 + kDnRows * t + 4 * g;
-                *reinterpret_cast<uint2*>(dst) = make_uint2(f2bf(y[0]) | (f2bf(y[1]) << 16), f2bf(y[2]) | (f2bf(y[3]) << 16));
+                *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]));
             }
         }
     };
