@@ -151,22 +151,41 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// One head row (256 dims, 4 per lane: dims 4 lane .. 4 lane + 3) normalised
-// ((x rsqrt(mean x^2 + eps)) (1 + w), fp32, then bf16) and rotated on dims
-// 0..63 (bf16(bf16(x cos) + bf16(rot(x) sin)), rot = [-x[32..63], x[0..31]]:
-// lane l < 16 pairs with lane l ^ 8, the row rotation by 8).  Every lane of
-// the wave calls it.
-__device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float eps, const uint16_t* cos_r,
-                                          const uint16_t* sin_r, int lane) {
-    const float x[4] = {lo_bf(raw.x), hi_bf(raw.x), lo_bf(raw.y), hi_bf(raw.y)};
-    const float ss = wave_sum_dpp(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
-    const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kAtD) + eps);
+// The norm factors 1 + w of a lane's 4 dims (dims 4 lane .. 4 lane + 3).
+__device__ __forceinline__ void norm_scale(const uint16_t* w, int lane, float (&w1)[4]) {
     const uint2 wr = *reinterpret_cast<const uint2*>(w + 4 * lane);
     const float wf[4] = {lo_bf(wr.x), hi_bf(wr.x), lo_bf(wr.y), hi_bf(wr.y)};
-    float n[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) n[i] = rbf((x[i] * r) * (1.0f + wf[i]));
-    // rotary (lanes 0..15 hold dims 0..63); the moves run on every lane
+    for (int i = 0; i < 4; ++i) w1[i] = 1.0f + wf[i];
+}
+
+// One head row (256 dims, 4 per lane) normalised: x rsqrt(mean x^2 + eps)
+// (1 + w) in fp32, not yet rounded (v_rsq_f32: the attention's bar is a
+// float tolerance).  Every lane of the wave calls it.
+__device__ __forceinline__ void rms_norm_row(uint2 raw, const float (&w1)[4], float eps, float (&n)[4]) {
+    const float x[4] = {lo_bf(raw.x), hi_bf(raw.x), lo_bf(raw.y), hi_bf(raw.y)};
+    const float ss = wave_sum_dpp(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(kAtD) + eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n[i] = (x[i] * r) * w1[i];
+}
+
+// The rotary embedding of one element: bf16(bf16(x cos) + bf16(rot sin)),
+// rot = -x[d + 32] for d < 32, x[d - 32] for 32 <= d < 64.
+__device__ __forceinline__ float rope1(float x, float rot, float c, float s) {
+    return rbf(rbf(x * c) + rbf(rot * s));
+}
+
+// A head row normalised and rotated on dims 0..63 (lanes 0..15 hold them;
+// lane l pairs with lane l ^ 8, the row rotation by 8), as packed bf16.
+// Every lane of the wave calls it.
+__device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float eps, const uint16_t* cos_r,
+                                          const uint16_t* sin_r, int lane) {
+    float w1[4], n[4];
+    norm_scale(w, lane, w1);
+    rms_norm_row(raw, w1, eps, n);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n[i] = rbf(n[i]);
     const int d0 = 4 * (lane & 15);
     const uint2 cr = *reinterpret_cast<const uint2*>(cos_r + d0);
     const uint2 sr = *reinterpret_cast<const uint2*>(sin_r + d0);
@@ -176,8 +195,7 @@ __device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float e
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float partner = dpp_f<0x128>(n[i]);  // row_ror:8
-        const float rot = (lane & 8) ? partner : -partner;
-        const float v = rbf(rbf(n[i] * cf[i]) + rbf(rot * sf[i]));
+        const float v = rope1(n[i], (lane & 8) ? partner : -partner, cf[i], sf[i]);
         o[i] = lane < 16 ? v : n[i];
     }
     return make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
@@ -314,26 +332,65 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         frow[tid] = 1.0f;
     }
     __syncthreads();
-    // (4) the query rows normed and rotated into qs: one row when T = 1,
-    // else up to 8 rows of the wave per pass (rows past T repeat token 0 and
-    // are not stored), so that their independent reductions interleave
-    constexpr int kPass = kMaxT < 8 ? kMaxT : 8;
+    // (4) the query rows normed and rotated into qs: one row when T = 1;
+    // else (a) every row of the wave normalised, up to 8 rows per pass (rows
+    // past T repeat token 0 and are not stored) so that their independent
+    // reductions interleave, then (b) the rotary dims of the wave's rows
+    // rotated in place, lane l taking row l / 4, dims 16 (l % 4) .. + 15
     if (T == 1) {
         *reinterpret_cast<uint2*>(&qs[wave][4 * lane]) = norm_rope(raw[0], nw[0], a.eps, cs[0][0], cs[1][0], lane);
     } else {
+        constexpr int kPass = kMaxT < 8 ? kMaxT : 8;
+        float w1[4];
+        norm_scale(nw[0], lane, w1);
 #pragma unroll
         for (int j0 = 0; j0 < kMaxT; j0 += kPass) {
             if (j0 < T) {
-                uint2 q[kPass];
+                float n[kPass][4];
 #pragma unroll
-                for (int j = 0; j < kPass; ++j) {
-                    const int tj = j0 + j < T ? j0 + j : 0;
-                    q[j] = norm_rope(raw[j0 + j], nw[0], a.eps, cs[0][tj], cs[1][tj], lane);
-                }
+                for (int j = 0; j < kPass; ++j) rms_norm_row(raw[j0 + j], w1, a.eps, n[j]);
 #pragma unroll
                 for (int j = 0; j < kPass; ++j)
-                    if (j0 + j < T) *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * (j0 + j)][4 * lane]) = q[j];
+                    if (j0 + j < T)
+                        *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * (j0 + j)][4 * lane]) =
+                            make_uint2(pack_bf2(n[j][0], n[j][1]), pack_bf2(n[j][2], n[j][3]));
             }
+        }
+        // (the wave's LDS stores above are complete before its loads below)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int j = lane >> 2;
+        const int qd = lane & 3;
+        if (j < T) {
+            uint16_t* row = &qs[wave + kAtGroup * j][0];
+            const uint4* own = reinterpret_cast<const uint4*>(row + 16 * qd);
+            const uint4* mate = reinterpret_cast<const uint4*>(row + 16 * (qd ^ 2));
+            const uint4* cp = reinterpret_cast<const uint4*>(&cs[0][j][16 * qd]);
+            const uint4* sp = reinterpret_cast<const uint4*>(&cs[1][j][16 * qd]);
+            const uint4 xv[2] = {own[0], own[1]};
+            const uint4 pv[2] = {mate[0], mate[1]};
+            const uint4 cv[2] = {cp[0], cp[1]};
+            const uint4 sv[2] = {sp[0], sp[1]};
+            const float sign = qd < 2 ? -1.0f : 1.0f;
+            uint4 out[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t xw[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
+                const uint32_t pw[4] = {pv[h].x, pv[h].y, pv[h].z, pv[h].w};
+                const uint32_t cw[4] = {cv[h].x, cv[h].y, cv[h].z, cv[h].w};
+                const uint32_t sw[4] = {sv[h].x, sv[h].y, sv[h].z, sv[h].w};
+                uint32_t ow[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ow[e] = pack_bf2(rope1(lo_bf(xw[e]), sign * lo_bf(pw[e]), lo_bf(cw[e]), lo_bf(sw[e])),
+                                     rope1(hi_bf(xw[e]), sign * hi_bf(pw[e]), hi_bf(cw[e]), hi_bf(sw[e])));
+                out[h] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            }
+            // (a lane's own dims are read by it and by its mate, lane l ^ 2;
+            // the stores use every value loaded, so they follow both reads)
+            reinterpret_cast<uint4*>(row + 16 * qd)[0] = out[0];
+            reinterpret_cast<uint4*>(row + 16 * qd)[1] = out[1];
         }
     }
     // (5) new positions of this chunk: keys normed and rotated, values as
