@@ -22,8 +22,8 @@
 //        (bf16-rounded, / 16), an online softmax per query row, P.V by MFMA
 //        into per-wave accumulators; the chunk's (max, sum, unnormalised
 //        rows) go to the partial buffers.
-//   at_combine  per (token, head): the chunks' partials merged, the sigmoid
-//        gate applied (att, bf16).
+//   at_combine  per (token, head, quarter of the dims): the chunks'
+//        partials merged, the sigmoid gate applied (att, bf16).
 //   at_project<8, 4096>  o_proj rows of att (2048 rows in 256 workgroups).
 //
 // Rounding points follow the Transformers forward in bf16: projections,
@@ -578,23 +578,31 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
 }
 
 // ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
-// One workgroup per (token, head): the chunks' (max, sum) pairs into LDS, the
-// weights exp(m_c - M); thread group q (64 threads, four dims each) sums
-// chunks q, q + kGroups, ... (every load issued at once: the gate, the pairs
-// and 8 partial rows per thread); the groups' rows meet in LDS in group
-// order.
-template <int kGroups>
+// kSplit workgroups per (token, head), each merging 256 / kSplit dims: the
+// chunks' (max, sum) pairs into LDS, the weights exp(m_c - M) (every
+// workgroup of the row computes them); thread group q (four dims per
+// thread) sums chunks q, q + kGroups, ... (every load issued at once: the
+// gate, the pairs and 8 partial rows per thread); the groups' rows meet in
+// LDS in group order.
+template <int kGroups, int kDims>
 struct CombineLds {
     float wc[kAttnMaxChunks];
     float lc[kAttnMaxChunks];
-    __attribute__((aligned(16))) float part[kGroups][kAtD];
-    __attribute__((aligned(16))) uint16_t out[kAtD];
+    __attribute__((aligned(16))) float part[kGroups][kDims];
+    __attribute__((aligned(16))) uint16_t out[kDims];
     float den;
 };
 
-template <int kThreads, bool kShared>
-__device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThreads / 64>& S, int t, int h) {
-    constexpr int kAtCombineGroups = kThreads / 64;
+template <int kThreads, int kSplit>
+using CombineLdsOf = CombineLds<kThreads * kSplit / 64, kAtD / kSplit>;
+
+template <int kThreads, int kSplit, bool kShared>
+__device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThreads, kSplit>& S, int t, int h,
+                                            int piece) {
+    constexpr int kDims = kAtD / kSplit;             // dims of this workgroup
+    constexpr int kRowThreads = kDims / 4;           // threads per partial row
+    constexpr int kAtCombineGroups = kThreads / kRowThreads;
+    static_assert(kThreads >= kAttnMaxChunks && kThreads >= 2 * kDims, "pairs and stores one per thread");
     auto& wc = S.wc;
     auto& lc = S.lc;
     auto& part = S.part;
@@ -607,12 +615,13 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThrea
     const int64_t chunk_rows = static_cast<int64_t>(g) * C;  // first chunk of head g
     // every load at once: the gate (threads < 256), the chunks' (max, sum)
     // pairs, the first batch of partial rows (dummy rows where none)
-    const int q = tid >> 6;
-    const int d0 = 4 * (tid & 63);
-    const float* po = a.part_o + (chunk_rows * R + r) * kAtD + d0;
+    const int q = tid / kRowThreads;
+    const int dbase = kDims * piece;
+    const int d0 = 4 * (tid % kRowThreads);
+    const float* po = a.part_o + (chunk_rows * R + r) * kAtD + dbase + d0;
     const int64_t cstride = static_cast<int64_t>(R) * kAtD;
     // (the gate as the 4-byte word holding it)
-    const int64_t gi = static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + (tid & (kAtD - 1));
+    const int64_t gi = static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + dbase + (tid % kDims);
     const uint32_t gword = kShared ? ld_agent32(a.proj + (gi & ~1ll)) : *reinterpret_cast<const uint32_t*>(a.proj + (gi & ~1ll));
     const float* pml = a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2;
     float2 ml;
@@ -685,7 +694,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThrea
     }
     *reinterpret_cast<float4*>(&part[q][d0]) = acc;
     __syncthreads();
-    if (tid < kAtD) {
+    if (tid < kDims) {
         const int d = tid;
         float num = part[0][d];
 #pragma unroll
@@ -697,19 +706,22 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLds<kThrea
     }
     __syncthreads();
     // the row as 4-byte words
-    if (tid < kAtD / 2) {
+    if (tid < kDims / 2) {
         const uint32_t w = static_cast<uint32_t>(S.out[2 * tid]) | (static_cast<uint32_t>(S.out[2 * tid + 1]) << 16);
-        uint16_t* dst = a.att + static_cast<int64_t>(t) * kAtO + h * kAtD + 2 * tid;
+        uint16_t* dst = a.att + static_cast<int64_t>(t) * kAtO + h * kAtD + dbase + 2 * tid;
         if constexpr (kShared) st_agent32(dst, w);
         else *reinterpret_cast<uint32_t*>(dst) = w;
     }
 }
 
-constexpr int kAtCombineThreads = 1024;
+constexpr int kAtCombineThreads = 256;
+constexpr int kAtCombineSplit = 4;
 
 __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
-    __shared__ CombineLds<kAtCombineThreads / 64> S;
-    combine_row<kAtCombineThreads, false>(a, S, blockIdx.x / kAtHeads, blockIdx.x % kAtHeads);
+    __shared__ CombineLdsOf<kAtCombineThreads, kAtCombineSplit> S;
+    const int row = blockIdx.x / kAtCombineSplit;
+    combine_row<kAtCombineThreads, kAtCombineSplit, false>(a, S, row / kAtHeads, row % kAtHeads,
+                                                           blockIdx.x % kAtCombineSplit);
 }
 
 }  // namespace
@@ -761,7 +773,8 @@ hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q
     } else {
         LRMOE_LAUNCH(at_attend<kAtMaxRows>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
     }
-    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);
+    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads * kAtCombineSplit), dim3(kAtCombineThreads), 0, stream, nullptr,
+                 nullptr, a);
     LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, w_o, w_o,
                  kHidden, kHidden, a.att, T, out, kHidden);
     return hipGetLastError();
