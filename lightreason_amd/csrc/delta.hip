@@ -712,8 +712,8 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             float sq = ov[0] * ov[0] + ov[1] * ov[1] + ov[2] * ov[2] + ov[3] * ov[3];
             sq = sq + __int_as_float(lane_xor<1>(__float_as_int(sq)));
             sq = sq + __int_as_float(lane_xor<2>(__float_as_int(sq)));
-            sq = sq + __int_as_float(lane_xor<4>(__float_as_int(sq)));
-            sq = sq + __int_as_float(lane_xor<8>(__float_as_int(sq)));
+            sq = butterfly_step4(sq);
+            sq = butterfly_step8(sq);
             sq = sq + __int_as_float(lane_xor<16>(__float_as_int(sq)));
             if (act_t) {
                 const float r = 1.0f / __builtin_sqrtf(sq / static_cast<float>(kDnWidth) + a.eps);

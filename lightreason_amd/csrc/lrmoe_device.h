@@ -98,14 +98,26 @@ __device__ __forceinline__ int lane_xor(int x) {
     }
 }
 
+// Steps 4 and 8 of an xor butterfly, on values already equal across each
+// group of 4 (resp. 8) lanes: lane i and lane 7 - i (resp. 15 - i) then hold
+// the same bits as lane i ^ 4 (resp. i ^ 8), so DPP row_half_mirror and
+// row_mirror bring the partner's value without an LDS round trip.
+__device__ __forceinline__ float butterfly_step4(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float butterfly_step8(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+}
+
 // xor butterfly over the 64 lanes with offsets 1,2,4,...,32: the fixed
 // reduction order shared with the oracle for router and norm sums (every lane
-// ends with the same total).
+// ends with the same total; each partial sum is a+b on one lane and b+a on
+// its partner, the same bits).
 __device__ __forceinline__ float wave_butterfly_sum(float value) {
     value = value + __int_as_float(lane_xor<1>(__float_as_int(value)));
     value = value + __int_as_float(lane_xor<2>(__float_as_int(value)));
-    value = value + __int_as_float(lane_xor<4>(__float_as_int(value)));
-    value = value + __int_as_float(lane_xor<8>(__float_as_int(value)));
+    value = butterfly_step4(value);
+    value = butterfly_step8(value);
     value = value + __int_as_float(lane_xor<16>(__float_as_int(value)));
     value = value + __int_as_float(lane_xor<32>(__float_as_int(value)));
     return value;
