@@ -554,12 +554,13 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
 #pragma unroll
         for (int i = 0; i < 5; ++i) ec[i] = ldg16(a.codec + kCodecTableColumns * tid + 2 * i);
     }
-    const uint32_t xr_lo = static_cast<uint32_t>(((has_lo ? t_lo : 0) * kHidden + 32 * lane) * 2);
-    const uint32_t xr_hi = static_cast<uint32_t>(((has_hi ? t_hi : 0) * kHidden + 32 * lane) * 2);
-    const uint16_t* nr = (a.norm != nullptr ? a.norm : a.x) + 32 * lane;
-    const uint16_t* gr = (a.shared_expert_gate != nullptr ? a.shared_expert_gate : a.x) + 32 * lane;
-    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * block + wave) * kHidden + 32 * lane
-                                   : a.x + 32 * lane;
+    // (a dummy load reads the first 64 bytes of x on every lane: the same
+    // lines for the whole workgroup, not a row per wave)
+    const uint32_t xr_lo = has_lo ? static_cast<uint32_t>((t_lo * kHidden + 32 * lane) * 2) : 0u;
+    const uint32_t xr_hi = has_hi ? static_cast<uint32_t>((t_hi * kHidden + 32 * lane) * 2) : 0u;
+    const uint16_t* nr = a.norm != nullptr ? a.norm + 32 * lane : a.x;
+    const uint16_t* gr = a.shared_expert_gate != nullptr ? a.shared_expert_gate + 32 * lane : a.x;
+    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * block + wave) * kHidden + 32 * lane : a.x;
     uint4 x_lo[4], x_hi[4], w_norm[4], w_sg[4], w_router[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) w_norm[i] = ldg16(nr + 8 * i);
@@ -616,7 +617,14 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         warm0 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w0));
         warm1 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w1));
     }
-    const unsigned long long call = finished / static_cast<unsigned long long>(G) + static_cast<unsigned>(layer);
+    // (a single layer's count stays in VGPRs until here, so that its load is
+    // waited for here, after every entry load is issued, and not at entry; a
+    // chain's comes from LDS)
+    uint32_t fin_lo = static_cast<uint32_t>(finished), fin_hi = static_cast<uint32_t>(finished >> 32);
+    if constexpr (!kChained) asm volatile("" : "+v"(fin_lo), "+v"(fin_hi));
+    const unsigned long long call = ((static_cast<unsigned long long>(fin_hi) << 32) | fin_lo) /
+                                        static_cast<unsigned long long>(G) +
+                                    static_cast<unsigned>(layer);
     const int parity = static_cast<int>(call & 1ull);
     const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
     DecodeCounters* const cnt = &sync->set[parity];
