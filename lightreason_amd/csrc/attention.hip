@@ -236,27 +236,14 @@ __device__ __forceinline__ uint32_t attend_range(const AttnArgs& a, int c) {
     return static_cast<uint32_t>(min((c + 1) * a.chunk, a.length + a.tokens)) * kAtD * 2;
 }
 
-// proj rows are read with agent-scope loads (kShared) when this launch's
-// other workgroups wrote them, else with plain ones; so are the partials
-// written.
-template <bool kShared>
-__device__ __forceinline__ uint2 ld_pair(const uint16_t* p) {
-    if constexpr (kShared) {
-        const uint64_t v = ld_agent64(p);
-        return make_uint2(static_cast<uint32_t>(v), static_cast<uint32_t>(v >> 32));
-    } else {
-        return *reinterpret_cast<const uint2*>(p);
-    }
-}
-
 // The attention partials of chunk c of key/value head g, for 8 T <= kRows
 // query rows (512 threads): the query rows normed and rotated, the chunk's
 // new positions appended, then per 32-position sub-block scores, online
 // softmax and P.V; (max, sum, unnormalised rows) to the partial buffers.
-// kb / vb hold sub-blocks 0 and 1 if `issued`, else are requested here.
-template <int kRows, bool kShared>
+// kb / vb carry the key and value rows of two sub-blocks in flight.
+template <int kRows>
 __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>& S, int g, int c, uint4 (&kb)[2][2],
-                                             uint4 (&vb)[2][2], bool issued) {
+                                             uint4 (&vb)[2][2]) {
     constexpr int kMaxT = kRows / kAtGroup;
     constexpr int kRowTiles = kRows / 16;
     auto& qs = S.qs;
@@ -295,7 +282,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     const uint16_t* qsrc = a.proj + (kAtGroup * g + wave) * 2 * kAtD + 4 * lane;
 #pragma unroll
     for (int j = 0; j < kMaxT; ++j)
-        raw[j] = ld_pair<kShared>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
+        raw[j] = *reinterpret_cast<const uint2*>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
     // (2) norm weights, cos, sin: 8-byte pieces; piece i < 128 a norm
     // weight's, then T x 16 pieces of cos and of sin
     const int pieces = 128 + 32 * T;
@@ -313,10 +300,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     // zeros: the buffer range ends at p1).  Rows of new positions read
     // whatever the cache held; the staging below takes them from fk / fv.
     const uint32_t range = static_cast<uint32_t>(p1) * kAtD * 2;
-    if (!issued) {
-        attend_issue(kb, vb, 0, kc, vc, p0, range, tid);
-        attend_issue(kb, vb, 1, kc, vc, p0 + kAtSub, range, tid);
-    }
+    attend_issue(kb, vb, 0, kc, vc, p0, range, tid);
+    attend_issue(kb, vb, 1, kc, vc, p0 + kAtSub, range, tid);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = tid + kAtThreads * k;
@@ -399,8 +384,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     for (int p = max(p0, L) + wave; p < p1; p += kAtWaves) {
         const int t = p - L;
         const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
-        const uint2 kraw = ld_pair<kShared>(pr + kAtKRow + g * kAtD + 4 * lane);
-        const uint2 vraw = ld_pair<kShared>(pr + kAtVRow + g * kAtD + 4 * lane);
+        const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
+        const uint2 vraw = *reinterpret_cast<const uint2*>(pr + kAtVRow + g * kAtD + 4 * lane);
         const uint2 k = norm_rope(kraw, nw[1], a.eps, cs[0][t], cs[1][t], lane);
         *reinterpret_cast<uint2*>(&fk[t][4 * lane]) = k;
         *reinterpret_cast<uint2*>(&fv[t][4 * lane]) = vraw;
@@ -549,8 +534,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
                     const int r = 16 * rt + 4 * gq + i;
                     if (r < R) {
                         float* dst = po + r * kAtD + 16 * (2 * wave + j) + m;
-                        if constexpr (kShared) st_agent32(dst, __float_as_uint(acc[rt][j][i]));
-                        else *dst = acc[rt][j][i];
+                        *dst = acc[rt][j][i];
                     }
                 }
             }
@@ -558,13 +542,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     }
     if (tid < R) {
         float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * R + tid) * 2;
-        if constexpr (kShared) {
-            st_agent64(pm, static_cast<uint64_t>(__float_as_uint(mrow[tid])) |
-                               (static_cast<uint64_t>(__float_as_uint(lrow[tid])) << 32));
-        } else {
-            pm[0] = mrow[tid];
-            pm[1] = lrow[tid];
-        }
+        pm[0] = mrow[tid];
+        pm[1] = lrow[tid];
     }
 }
 
@@ -574,7 +553,7 @@ template <int kRows>
 __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(AttnArgs a) {
     __shared__ AttendLds<kRows> S;
     uint4 kb[2][2], vb[2][2];  // [sub-block parity][piece]
-    attend_chunk<kRows, false>(a, S, blockIdx.x / a.chunks, blockIdx.x % a.chunks, kb, vb, false);
+    attend_chunk<kRows>(a, S, blockIdx.x / a.chunks, blockIdx.x % a.chunks, kb, vb);
 }
 
 // ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
@@ -596,7 +575,7 @@ struct CombineLds {
 template <int kThreads, int kSplit>
 using CombineLdsOf = CombineLds<kThreads * kSplit / 64, kAtD / kSplit>;
 
-template <int kThreads, int kSplit, bool kShared>
+template <int kThreads, int kSplit>
 __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThreads, kSplit>& S, int t, int h,
                                             int piece) {
     constexpr int kDims = kAtD / kSplit;             // dims of this workgroup
@@ -622,23 +601,11 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
     const int64_t cstride = static_cast<int64_t>(R) * kAtD;
     // (the gate as the 4-byte word holding it)
     const int64_t gi = static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + dbase + (tid % kDims);
-    const uint32_t gword = kShared ? ld_agent32(a.proj + (gi & ~1ll)) : *reinterpret_cast<const uint32_t*>(a.proj + (gi & ~1ll));
+    const uint32_t gword = *reinterpret_cast<const uint32_t*>(a.proj + (gi & ~1ll));
     const float* pml = a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2;
-    float2 ml;
-    if constexpr (kShared) {
-        const uint64_t w = ld_agent64(pml);
-        ml = make_float2(__uint_as_float(static_cast<uint32_t>(w)), __uint_as_float(static_cast<uint32_t>(w >> 32)));
-    } else {
-        ml = *reinterpret_cast<const float2*>(pml);
-    }
+    const float2 ml = *reinterpret_cast<const float2*>(pml);
     auto load_row = [&](int c) -> float4 {
-        const float* src = po + static_cast<int64_t>(c) * cstride;
-        if constexpr (kShared) {
-            const uint4 u = ld_agent16(a.part_o, static_cast<uint32_t>((src - a.part_o) * 4));
-            return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
-        } else {
-            return *reinterpret_cast<const float4*>(src);
-        }
+        return *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c) * cstride);
     };
     float4 v[8];
 #pragma unroll
@@ -709,8 +676,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
     if (tid < kDims / 2) {
         const uint32_t w = static_cast<uint32_t>(S.out[2 * tid]) | (static_cast<uint32_t>(S.out[2 * tid + 1]) << 16);
         uint16_t* dst = a.att + static_cast<int64_t>(t) * kAtO + h * kAtD + dbase + 2 * tid;
-        if constexpr (kShared) st_agent32(dst, w);
-        else *reinterpret_cast<uint32_t*>(dst) = w;
+        *reinterpret_cast<uint32_t*>(dst) = w;
     }
 }
 
@@ -720,8 +686,7 @@ constexpr int kAtCombineSplit = 4;
 __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
     __shared__ CombineLdsOf<kAtCombineThreads, kAtCombineSplit> S;
     const int row = blockIdx.x / kAtCombineSplit;
-    combine_row<kAtCombineThreads, kAtCombineSplit, false>(a, S, row / kAtHeads, row % kAtHeads,
-                                                           blockIdx.x % kAtCombineSplit);
+    combine_row<kAtCombineThreads, kAtCombineSplit>(a, S, row / kAtHeads, row % kAtHeads, blockIdx.x % kAtCombineSplit);
 }
 
 }  // namespace
