@@ -141,6 +141,22 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum and maximum over each 16-lane row of the wave (the MFMA output lanes
+// of one row group), returned to every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));
@@ -403,6 +419,24 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[rt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // The 128-row variant: wave w owns row tile w, its query operands held in
+    // registers for the chunk and its rows' running max and sum too (lanes
+    // of 16-lane row gq hold rows 16 w + 4 gq + i, i < 4); the 32-row one
+    // keeps them in LDS.
+    constexpr bool kOwn = kRows == kAtMaxRows;
+    uint4 qreg[kOwn ? kAtD / 32 : 1];
+    float mrun[4], lrun[4];
+    if constexpr (kOwn) {
+        const int rq = wave < RT ? 16 * wave + m : 0;
+#pragma unroll
+        for (int s = 0; s < kAtD / 32; ++s) qreg[s] = *reinterpret_cast<const uint4*>(&qs[rq][32 * s + 8 * gq]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mrun[i] = -__builtin_inff();
+            lrun[i] = 0.0f;
+        }
+    }
+
     // One sub-block: its rows from registers into ks / vs (16-byte stores
     // along a row), the registers refilled with the sub-block two ahead,
     // then scores, softmax, P.V.
@@ -427,63 +461,99 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         }
         attend_issue(kb, vb, parity, kc, vc, q0 + 2 * kAtSub, range, tid);
         __syncthreads();
-        // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
-        {
-            const int ct = wave & 1;
+        if constexpr (kOwn) {
+            // scores of both column tiles of the wave's row tile, then the
+            // online softmax on the MFMA outputs (row reductions in 16 lanes)
+            if (wave < RT) {
+                f32x4 s4[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-            for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
-                const int rt = (wave >> 1) + 4 * k2;
-                if (rt < RT) {
-                    f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int s = 0; s < kAtD / 32; ++s)
 #pragma unroll
-                    for (int s = 0; s < kAtD / 32; ++s)
-                        s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
-                                          *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
-                    const int pos = q0 + 16 * ct + m;
+                    for (int ct = 0; ct < 2; ++ct)
+                        s4[ct] = mfma16x16x32(qreg[s], *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]),
+                                              s4[ct]);
+                float f[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = 16 * rt + 4 * gq + i;
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * wave + 4 * gq + i;
+                    float sv[2];
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) {
+                        const int pos = q0 + 16 * ct + m;
                         const bool ok = r < R && pos < p1 && pos <= L + (r >> 3);
-                        sc[r][16 * ct + m] = ok ? rbf(s4[i]) * kAtScale : -__builtin_inff();
+                        sv[ct] = ok ? rbf(s4[ct][i]) * kAtScale : -__builtin_inff();
+                    }
+                    const float m_new = fmaxf(mrun[i], row16_max(fmaxf(sv[0], sv[1])));
+                    const bool none = m_new == -__builtin_inff();
+                    const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(sv[0] - m_new), none ? 0.0f : fast_exp(sv[1] - m_new));
+                    es[r][m] = static_cast<uint16_t>(e);
+                    es[r][16 + m] = static_cast<uint16_t>(e >> 16);
+                    const float sum = row16_sum(lo_bf(e) + hi_bf(e));
+                    f[i] = none ? 1.0f : (mrun[i] == -__builtin_inff() ? 0.0f : fast_exp(mrun[i] - m_new));
+                    lrun[i] = lrun[i] * f[i] + sum;
+                    mrun[i] = m_new;
+                }
+                if (m == 0) *reinterpret_cast<float4*>(&frow[16 * wave + 4 * gq]) = make_float4(f[0], f[1], f[2], f[3]);
+            }
+        } else {
+            // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
+            {
+                const int ct = wave & 1;
+#pragma unroll
+                for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
+                    const int rt = (wave >> 1) + 4 * k2;
+                    if (rt < RT) {
+                        f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int s = 0; s < kAtD / 32; ++s)
+                            s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
+                                              *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
+                        const int pos = q0 + 16 * ct + m;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = 16 * rt + 4 * gq + i;
+                            const bool ok = r < R && pos < p1 && pos <= L + (r >> 3);
+                            sc[r][16 * ct + m] = ok ? rbf(s4[i]) * kAtScale : -__builtin_inff();
+                        }
                     }
                 }
             }
-        }
-        __syncthreads();
-        // online softmax: four threads per row, eight positions each
-        {
-            const int r = tid >> 2;
-            const int q = tid & 3;
-            if (r < R) {  // (R is a multiple of 8: whole quads take part)
-                float s8[8];
-                float mx = -__builtin_inff();
+            __syncthreads();
+            // online softmax: four threads per row, eight positions each
+            {
+                const int r = tid >> 2;
+                const int q = tid & 3;
+                if (r < R) {  // (R is a multiple of 8: whole quads take part)
+                    float s8[8];
+                    float mx = -__builtin_inff();
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    s8[j] = sc[r][8 * q + j];
-                    mx = fmaxf(mx, s8[j]);
-                }
-                mx = fmaxf(mx, dpp_f<0xB1>(mx));
-                mx = fmaxf(mx, dpp_f<0x4E>(mx));
-                const float m_old = mrow[r];
-                const float m_new = fmaxf(m_old, mx);
-                const bool none = m_new == -__builtin_inff();
-                float sum = 0.0f;
-                uint32_t e2[4];
+                    for (int j = 0; j < 8; ++j) {
+                        s8[j] = sc[r][8 * q + j];
+                        mx = fmaxf(mx, s8[j]);
+                    }
+                    mx = fmaxf(mx, dpp_f<0xB1>(mx));
+                    mx = fmaxf(mx, dpp_f<0x4E>(mx));
+                    const float m_old = mrow[r];
+                    const float m_new = fmaxf(m_old, mx);
+                    const bool none = m_new == -__builtin_inff();
+                    float sum = 0.0f;
+                    uint32_t e2[4];
 #pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(s8[j] - m_new),
-                                                none ? 0.0f : fast_exp(s8[j + 1] - m_new));
-                    sum += lo_bf(e) + hi_bf(e);
-                    e2[j / 2] = e;
-                }
-                *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
-                sum += dpp_f<0xB1>(sum);
-                sum += dpp_f<0x4E>(sum);
-                const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : fast_exp(m_old - m_new));
-                if (q == 0) {
-                    mrow[r] = m_new;
-                    lrow[r] = lrow[r] * f + sum;
-                    frow[r] = f;
+                    for (int j = 0; j < 8; j += 2) {
+                        const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(s8[j] - m_new),
+                                                    none ? 0.0f : fast_exp(s8[j + 1] - m_new));
+                        sum += lo_bf(e) + hi_bf(e);
+                        e2[j / 2] = e;
+                    }
+                    *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
+                    sum += dpp_f<0xB1>(sum);
+                    sum += dpp_f<0x4E>(sum);
+                    const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : fast_exp(m_old - m_new));
+                    if (q == 0) {
+                        mrow[r] = m_new;
+                        lrow[r] = lrow[r] * f + sum;
+                        frow[r] = f;
+                    }
                 }
             }
         }
@@ -520,6 +590,13 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     for (int q0 = p0; q0 < p1; q0 += 2 * kAtSub) {
         sub_block(0, q0);
         if (q0 + kAtSub < p1) sub_block(1, q0 + kAtSub);
+    }
+    if constexpr (kOwn) {
+        if (wave < RT && m == 0) {
+            *reinterpret_cast<float4*>(&mrow[16 * wave + 4 * gq]) = make_float4(mrun[0], mrun[1], mrun[2], mrun[3]);
+            *reinterpret_cast<float4*>(&lrow[16 * wave + 4 * gq]) = make_float4(lrun[0], lrun[1], lrun[2], lrun[3]);
+        }
+        __syncthreads();
     }
 
     // the chunk's partials: unnormalised rows, running max and sum per row
