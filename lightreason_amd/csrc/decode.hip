@@ -911,6 +911,13 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
 
     TL(2, 0);
     TL(5, 7 * kWave);
+    // With caller logits, each wave stages its token rows right after
+    // issuing its share of the first item, while later waves are still
+    // issuing theirs; the plan's barriers below publish the rows.
+    if (a.router == nullptr) {
+        stage_rows();
+        TL(6, 0);
+    }
     if (block == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
@@ -1218,12 +1225,6 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     if (cur < end) {
         int nxt = early ? 2 * G + first_item : cur + G;
         int nxt2 = cur + 2 * G;  // (codec: no early items)
-        if (a.router == nullptr) {
-            // Token rows staged while the first weights stream in.
-            stage_rows();
-            __syncthreads();
-            TL(6, 0);
-        }
         // Everything but the first item's 16 loads is complete by now; the
         // wait tells the compiler so, which keeps it from draining the
         // first item's loads where the loop reuses the prologue's
