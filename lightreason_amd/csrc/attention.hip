@@ -22,8 +22,8 @@
 //        (bf16-rounded, / 16), an online softmax per query row, P.V by MFMA
 //        into per-wave accumulators; the chunk's (max, sum, unnormalised
 //        rows) go to the partial buffers.
-//   at_combine  per (token, head, quarter of the dims): the chunks'
-//        partials merged, the sigmoid gate applied (att, bf16).
+//   at_combine  per (token, head, eighth or quarter of the dims): the
+//        chunks' partials merged, the sigmoid gate applied (att, bf16).
 //   at_project<8, 4096>  o_proj rows of att (2048 rows in 256 workgroups).
 //
 // Rounding points follow the Transformers forward in bf16: projections,
@@ -758,12 +758,13 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
 }
 
 constexpr int kAtCombineThreads = 256;
-constexpr int kAtCombineSplit = 4;
 
+// kSplit workgroups per (token, head): 8 up to 4 tokens, 4 above.
+template <int kSplit>
 __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
-    __shared__ CombineLdsOf<kAtCombineThreads, kAtCombineSplit> S;
-    const int row = blockIdx.x / kAtCombineSplit;
-    combine_row<kAtCombineThreads, kAtCombineSplit>(a, S, row / kAtHeads, row % kAtHeads, blockIdx.x % kAtCombineSplit);
+    __shared__ CombineLdsOf<kAtCombineThreads, kSplit> S;
+    const int row = blockIdx.x / kSplit;
+    combine_row<kAtCombineThreads, kSplit>(a, S, row / kAtHeads, row % kAtHeads, blockIdx.x % kSplit);
 }
 
 }  // namespace
@@ -815,8 +816,11 @@ hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q
     } else {
         LRMOE_LAUNCH(at_attend<kAtMaxRows>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
     }
-    LRMOE_LAUNCH(at_combine, dim3(T * kAtHeads * kAtCombineSplit), dim3(kAtCombineThreads), 0, stream, nullptr,
-                 nullptr, a);
+    if (T <= 4) {
+        LRMOE_LAUNCH(at_combine<8>, dim3(T * kAtHeads * 8), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);
+    } else {
+        LRMOE_LAUNCH(at_combine<4>, dim3(T * kAtHeads * 4), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);
+    }
     LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, w_o, w_o,
                  kHidden, kHidden, a.att, T, out, kHidden);
     return hipGetLastError();
