@@ -163,8 +163,10 @@ int lrmoe_moe_layer(const uint16_t *hidden, int tokens, const uint16_t *router_w
  * LRMOE_STATUS_* bits of that call) goes to *status_out when status_out (a
  * device int32) is given.  Its scratch (3 MiB: counters and tagged rows) is
  * a static device array of the library, one per GPU, held until the process
- * ends; the first call on a GPU looks up its address and zeroes it with a
- * kernel on that call's stream.  Every call on a GPU shares that GPU's
+ * ends, zero-filled when the library's code object is loaded; the first
+ * call on a GPU looks up its address and, unless that call's stream is
+ * capturing a graph, zeroes it again with a kernel on that stream (a first
+ * call under capture records no clear).  Every call on a GPU shares that GPU's
  * array: calls that overlap on one GPU (two streams, or two host threads)
  * race, as calls sharing one workspace do.  Calls nothing that allocates.
  * Returns LRMOE_E_ARG for tokens > LRMOE_STATIC_MAX_TOKENS. */

@@ -47,8 +47,12 @@ bool misaligned(const void* p, size_t bytes) { return (reinterpret_cast<uintptr_
 constexpr size_t kStaticScratchBytes = 3u << 20;  // >= lrmoe::workspace_bytes(16)
 __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
-// Zeroes the scratch on its first use on a device (a fill kernel, not a
-// memset node, so that a caller capturing its first call records a kernel).
+// Zeroes the scratch on its first uncaptured use on a device.  The array has
+// static storage and no initialiser, so the code-object loader hands it out
+// zero-filled; the clear only restates that for a first call made outside a
+// graph capture.  A first call made under capture does not record it (a
+// recorded clear would rerun on every replay and reset the counters and
+// tagged rows that later calls rely on).
 __global__ __launch_bounds__(256) void clear_scratch(uint4* p, size_t n16) {
     for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n16; i += static_cast<size_t>(gridDim.x) * 256)
         p[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -82,10 +86,15 @@ int static_scratch(void** out, hipStream_t stream) {
         s.ptr[device] = p;
     }
     if (!s.cleared[device]) {
-        hipLaunchKernelGGL(clear_scratch, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(s.ptr[device]),
-                           kStaticScratchBytes / 16);
-        err = hipGetLastError();
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        err = hipStreamIsCapturing(stream, &capture);
         if (err != hipSuccess) return static_cast<int>(err);
+        if (capture == hipStreamCaptureStatusNone) {
+            hipLaunchKernelGGL(clear_scratch, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(s.ptr[device]),
+                               kStaticScratchBytes / 16);
+            err = hipGetLastError();
+            if (err != hipSuccess) return static_cast<int>(err);
+        }
         s.cleared[device] = true;
     }
     *out = s.ptr[device];

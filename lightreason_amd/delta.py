@@ -105,6 +105,31 @@ def _workspace(device: torch.device) -> torch.Tensor:
     return ws
 
 
+def check_mixer_status(device=None, what: str = "lrmoe_delta_mixer") -> int:
+    """Raise RuntimeError when a mixer call on `device` (through any
+    stream's workspace) had a bounded wait expire since the last check: the
+    conv and recurrent states that call updated in place are invalid.  The
+    timeout bit is sticky (every call ORs into the word), so it is cleared
+    before raising and later calls report afresh.  Reads the device
+    (synchronises); returns the OR of the status words otherwise."""
+    device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    off = _native.DELTA_WS_STATUS_OFFSET
+    status = 0
+    for (dev, _stream_id), ws in list(_WORKSPACES.items()):
+        if dev != device:
+            continue
+        word = ws[off:off + 4].view(torch.int32)
+        value = int(word.item())
+        if value & _native.STATUS_TIMEOUT:
+            word.zero_()
+        status |= value
+    if status & _native.STATUS_TIMEOUT:
+        raise RuntimeError(f"{what}: a cross-workgroup wait timed out, so the conv and recurrent states it updated "
+                           "are invalid (the mixer kernel needs every workgroup resident: is another kernel "
+                           "running on the device?)")
+    return status
+
+
 def mixer_status(device=None) -> int:
     """The status word of the current stream's mixer workspace (reads the
     device): LRMOE_STATUS_TIMEOUT once a call's bounded wait expired (its
@@ -206,6 +231,7 @@ class PrefixStates:
         self.conv = {}
         self.recurrent = {}
         self.cache = None
+        self.devices = set()  # devices whose mixer steps ran natively (status checked by commit)
 
     @contextmanager
     def record(self, cache):
@@ -221,7 +247,11 @@ class PrefixStates:
         """Keep the first `accepted` of the `width` positions verified after
         `prefix` cached tokens: attention layers are cut to prefix +
         accepted, linear-attention layers take the states recorded after
-        position accepted - 1.  Nothing to do when all were accepted."""
+        position accepted - 1.  Nothing to do when all were accepted.
+        First raises RuntimeError (check_mixer_status) when a native mixer
+        step since the last check timed out: its states are invalid."""
+        for device in self.devices:
+            check_mixer_status(device, "fused_delta")
         if accepted == width:
             return
         if not 1 <= accepted < width or self.conv.keys() != self.recurrent.keys() or not self.conv:
@@ -244,7 +274,9 @@ def fused_delta(model):
     """Run every linear-attention layer's cached forward of 1..16 tokens
     (batch 1) through ``lrmoe_delta_mixer`` on the live cache for the
     duration of the block; yields the ``PrefixStates`` that blocks of
-    2..16 tokens inside ``histories.record(cache)`` fill."""
+    2..16 tokens inside ``histories.record(cache)`` fill.  The mixer's
+    status word is checked by every ``histories.commit`` and when the block
+    ends without an exception: RuntimeError if a step timed out."""
     histories = PrefixStates()
     restore = []
 
@@ -268,7 +300,10 @@ def fused_delta(model):
                 histories.recurrent[index] = state_rec
             # batch 1: the padding mask leaves the states untouched ([HF] apply_mask_to_padding_states)
             out = bound.step(hidden_states[0].contiguous(), conv, state, conv_record=conv_rec, state_record=state_rec)
+            histories.devices.add(conv.device)
             return out.unsqueeze(0)
+
+        forward.lrmoe_native = True
         return forward
 
     try:
@@ -279,6 +314,8 @@ def fused_delta(model):
             restore.append((mixer, mixer.__dict__.get("forward")))
             mixer.forward = native_forward(mixer, mixer.forward, index)
         yield histories
+        for device in histories.devices:
+            check_mixer_status(device, "fused_delta")
     finally:
         for mixer, previous in restore:
             if previous is None:

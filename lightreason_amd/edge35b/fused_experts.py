@@ -69,8 +69,8 @@ def fused_forward(layer, hidden, indices, weights, *, torch_projections=False, v
     word after the launches.  ``validate=False`` makes the call free of host
     synchronisation (graph-capturable); bad routes then only set the
     workspace status bits and yield zeros.  ``torch_projections=True`` is the
-    reference's ``batched`` ablation: the projections run as torch linears
-    (host-side schedule, as there), the combine on liblrmoe."""
+    reference's ``batched`` ablation: the projections run as torch batched
+    products (scheduled on the device), the combine on liblrmoe."""
     _check_single_token(layer, hidden, indices, weights)
     if indices.dtype != torch.int64:
         raise ValueError("Fused expert decode requires int64 routes")
@@ -84,17 +84,25 @@ def fused_forward(layer, hidden, indices, weights, *, torch_projections=False, v
 
 
 def _torch_projection_forward(layer, hidden, indices, weights):
-    schedule = sorted(enumerate(indices[0].tolist()), key=lambda pair: pair[1])
-    if len({e for _, e in schedule}) != 8 or not all(0 <= e < moe.EXPERTS for _, e in schedule):
+    """The ``batched`` ablation: the expert projections as torch products
+    instead of the decode kernel (the reference runs one torch linear per
+    expert from a host-side schedule).  Here the schedule stays on the
+    device: the eight routes are sorted there and checked with one device
+    read (the same ValueError), the selected experts' weights are gathered
+    with ``index_select`` into one batched product for gate/up and one for
+    down, SwiGLU is the module's ``act_fn`` on bf16 tensors, and the ordered
+    combine is the ``_ordered_sum`` shim over a device-built table."""
+    experts, slots = torch.sort(indices.reshape(moe.TOPK), stable=True)
+    valid = (experts[0] >= 0) & (experts[-1] < moe.EXPERTS) & (experts[1:] != experts[:-1]).all()
+    if not bool(valid):
         raise ValueError(_ROUTE_ERROR)
-    experts = [layer.pool._expert(layer, e, cached=True) for _, e in schedule]
-    table = torch.tensor([(g.data_ptr(), d.data_ptr(), slot) for (slot, _), (g, d) in zip(schedule, experts)],
-                         dtype=torch.int64, device=hidden.device)
-    linear = torch.nn.functional.linear
-    gate_up = torch.cat([linear(hidden, g) for g, _ in experts], dim=0)
-    gate, up = gate_up.chunk(2, dim=-1)
-    activated = layer.act_fn(gate) * up
-    projected = torch.cat([linear(activated[i:i + 1], d) for i, (_, d) in enumerate(experts)], dim=0).contiguous()
+    column = hidden.reshape(1, moe.HIDDEN, 1).expand(moe.TOPK, moe.HIDDEN, 1).contiguous()
+    products = torch.bmm(layer.gate_up.index_select(0, experts).contiguous(), column).squeeze(2)
+    gate, up = products.split(moe.INNER, dim=1)
+    act = (layer.act_fn(gate) * up).unsqueeze(2).contiguous()
+    projected = torch.bmm(layer.down.index_select(0, experts).contiguous(), act).squeeze(2).contiguous()
+    addresses = expert_table(layer).index_select(0, experts)
+    table = torch.cat((addresses, slots.unsqueeze(1)), dim=1).contiguous()
     result = torch.empty_like(hidden)
     _ordered_sum[(8,)](table, projected, weights, result, 2048, 256, enable_fp_fusion=False)
     return result

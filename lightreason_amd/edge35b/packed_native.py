@@ -14,19 +14,24 @@ reduce to:
 
 The captured graphs read the routes and weights from fixed device buffers
 (the device table is rebuilt in place before each replay), so a call never
-reads the routes on the host.  The reference's ``mixer_graphs`` (82-149), a
-replay of the eager single-token mixer, is replaced by the native Gated
-DeltaNet step in ``lightreason_amd.delta`` (``native_mixers``), which updates
-the live cache in place and needs no captured copy of it.
+reads the routes on the host.
+
+``mixer_graphs(model, pool)`` keeps the reference's name and report
+attribute (packed_native.py:96-149, read by native_bench.py:143-155,198).
+The reference captures the eager single-token mixer into one graph per
+layer and copies the live states in and out around each replay; here the
+single-token step is the native Gated DeltaNet launch of
+``lightreason_amd.delta.fused_delta``, which works on the live cache states
+in place, so there is nothing to capture or copy.
 """
 
 from __future__ import annotations
 
-from contextlib import contextmanager
+from contextlib import ExitStack, contextmanager
 
 import torch
 
-from .. import _native, moe
+from .. import _native, delta, moe
 from . import packed_hybrid
 from ._grid import stream_of
 from .fused_experts import _matvec
@@ -123,3 +128,47 @@ def configure(pool, mode):
         yield
     finally:
         packed_hybrid.packed_forward = original
+
+
+def _counting(inner, index, served):
+    """A mixer forward that notes layer `index` in `served` when it gets a
+    single-token cached step (the reference's capture condition,
+    packed_native.py:107-109), then runs `inner`."""
+
+    def forward(hidden_states, cache_params=None, attention_mask=None, **kwargs):
+        if (hidden_states.shape[:2] == (1, 1) and cache_params is not None and attention_mask is None
+                and cache_params.has_previous_state(index)):
+            served.setdefault(index, "native")
+        return inner(hidden_states, cache_params=cache_params, attention_mask=attention_mask, **kwargs)
+
+    forward.lrmoe_native = True
+    return forward
+
+
+@contextmanager
+def mixer_graphs(model, pool):
+    """Single-token Gated DeltaNet steps on the native mixer for the
+    duration of the block.  Enters ``delta.fused_delta(model)`` unless every
+    linear-attention mixer already runs natively (an enclosing
+    ``fused_delta``, as native_bench.py:138 sets up).  ``pool.mixer_graphs``
+    maps each layer index whose single-token cached step ran to "native",
+    the keys the reference's report counts (native_bench.py:198)."""
+    served = getattr(pool, "mixer_graphs", None)
+    if served is None:
+        served = pool.mixer_graphs = {}
+    mixers = [(i, layer.linear_attn) for i, layer in enumerate(model.model.layers) if hasattr(layer, "linear_attn")]
+    restore = []
+    with ExitStack() as stack:
+        if not all(getattr(m.__dict__.get("forward"), "lrmoe_native", False) for _, m in mixers):
+            stack.enter_context(delta.fused_delta(model))
+        try:
+            for index, mixer in mixers:
+                restore.append((mixer, mixer.__dict__.get("forward")))
+                mixer.forward = _counting(mixer.forward, index, served)
+            yield
+        finally:
+            for mixer, previous in reversed(restore):
+                if previous is None:
+                    del mixer.forward
+                else:
+                    mixer.forward = previous

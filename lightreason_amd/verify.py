@@ -93,7 +93,12 @@ class VerifyGraphs:
                       weights=static["weights"], workspace=self.workspace)
         return run
 
-    def verify(self, hidden: torch.Tensor) -> torch.Tensor:
+    def verify(self, hidden: torch.Tensor, *, check: bool = True) -> torch.Tensor:
+        """Replay the block's width graph.  ``check`` (default) reads the
+        workspace status word afterwards (a host synchronisation) and raises
+        RuntimeError when a bounded wait of the chain kernel expired (its
+        outputs are invalid: another kernel kept workgroups off the GPU);
+        ``check=False`` leaves the status to ``status()``."""
         width = hidden.shape[0]
         entry = self.graphs.get(width)
         if entry is None:
@@ -103,6 +108,8 @@ class VerifyGraphs:
         graph, static = entry
         static["hidden"].copy_(hidden)
         graph.replay()
+        if check:
+            self.workspace.check("VerifyGraphs.verify")
         return static["out"]
 
     def routes(self, width: int):

@@ -185,3 +185,99 @@ def test_header_declares_the_timeout_bit():
 
     header = (Path(__file__).resolve().parents[1] / "include" / "lrmoe.h").read_text()
     assert "#define LRMOE_STATUS_TIMEOUT 8" in header
+
+
+def test_reference_driver_imports_mixer_graphs():
+    """native_bench.py:143,151 import these names from edge35b.packed_native."""
+    import lightreason_amd.edge35b as pkg
+
+    pkg.install_as_edge35b()
+    from edge35b.packed_native import configure, mixer_graphs  # noqa: F401 -- the reference's import line
+
+    assert mixer_graphs is packed_native.mixer_graphs
+
+
+def _fake_model(native: bool):
+    """A model shell with two linear-attention layers (indices 0 and 2) and
+    one attention layer, whose mixer forwards echo their input; marked as
+    already native (an enclosing fused_delta) when ``native``."""
+    calls = []
+
+    def make_forward(index):
+        def forward(hidden_states, cache_params=None, attention_mask=None, **kwargs):
+            calls.append(index)
+            return hidden_states
+        forward.lrmoe_native = native
+        return forward
+
+    layers = []
+    for index in range(3):
+        layer = types.SimpleNamespace()
+        if index != 1:
+            mixer = types.SimpleNamespace()
+            mixer.forward = make_forward(index)
+            layer.linear_attn = mixer
+        layers.append(layer)
+    return types.SimpleNamespace(model=types.SimpleNamespace(layers=layers)), calls
+
+
+class _Cache:
+    def has_previous_state(self, index):
+        return True
+
+
+def test_mixer_graphs_records_single_token_steps_and_restores():
+    """Inside mixer_graphs (with the mixers already native) a single-token
+    cached step of layer i is noted in pool.mixer_graphs[i]; longer blocks
+    and uncached calls are not; the forwards are restored on exit."""
+    model, calls = _fake_model(native=True)
+    originals = [l.linear_attn.forward for l in model.model.layers if hasattr(l, "linear_attn")]
+    pool = types.SimpleNamespace()
+    x1 = torch.zeros((1, 1, 8))
+    with packed_native.mixer_graphs(model, pool):
+        assert pool.mixer_graphs == {}
+        mixer0 = model.model.layers[0].linear_attn
+        mixer2 = model.model.layers[2].linear_attn
+        assert mixer0.forward(x1, cache_params=_Cache()) is x1
+        mixer2.forward(torch.zeros((1, 4, 8)), cache_params=_Cache())   # a verify block
+        mixer2.forward(x1)                                              # no cache
+        assert pool.mixer_graphs == {0: "native"}
+        mixer2.forward(x1, cache_params=_Cache())
+    assert pool.mixer_graphs == {0: "native", 2: "native"}
+    assert calls == [0, 2, 2, 2]
+    assert [l.linear_attn.forward for l in model.model.layers if hasattr(l, "linear_attn")] == originals
+
+
+def test_mixer_status_timeout_raises_and_clears(monkeypatch):
+    """A mixer workspace whose sticky timeout bit is set (a bounded wait of a
+    step expired) makes check_mixer_status, PrefixStates.commit and the end
+    of fused_delta's block raise RuntimeError; the bit is cleared by the
+    raise, so the next check passes."""
+    from lightreason_amd import _native, delta
+
+    cpu = torch.device("cpu")
+    ws = torch.zeros(64, dtype=torch.uint8)
+    off = _native.DELTA_WS_STATUS_OFFSET
+    monkeypatch.setitem(delta._WORKSPACES, (cpu, 0), ws)
+
+    def set_timeout():
+        ws[off:off + 4].view(torch.int32)[0] = _native.STATUS_TIMEOUT
+
+    assert delta.check_mixer_status(cpu) == 0
+    set_timeout()
+    with pytest.raises(RuntimeError, match="timed out"):
+        delta.check_mixer_status(cpu)
+    assert delta.check_mixer_status(cpu) == 0
+    histories = delta.PrefixStates()
+    histories.devices.add(cpu)
+    set_timeout()
+    with pytest.raises(RuntimeError, match="timed out"):
+        histories.commit(None, 10, 4, 4)          # even a fully accepted block is checked
+    histories.commit(None, 10, 4, 4)
+
+    shell = types.SimpleNamespace(model=types.SimpleNamespace(layers=[types.SimpleNamespace()]))
+    set_timeout()
+    with pytest.raises(RuntimeError, match="timed out"):
+        with delta.fused_delta(shell) as h:
+            h.devices.add(cpu)
+    assert delta.check_mixer_status(cpu) == 0

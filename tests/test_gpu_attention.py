@@ -3,7 +3,7 @@
 oracle's lro_attn_decode (pinned against the Transformers module itself in
 test_attn_oracle.py), through the C ABI.
 
-Cases cover one chunk of positions and many (up to 126 per key/value head),
+Cases cover one chunk of positions and many (up to 128 per key/value head),
 a first token with an empty cache, blocks of 3, 5, 8 and 16 tokens (causal
 within the block), chunk and 32-position sub-block boundaries, and a cache
 filled to its capacity.  Bars: the appended key and value rows equal the
@@ -79,8 +79,13 @@ def _close_rows(got, want, what):
     assert same >= 0.98 and excess <= 1.0, what
 
 
+# Blocks of more than 4 tokens run the 128-row attention variant; beyond 8192
+# cached positions its chunks are longer than 64 and not a multiple of 32
+# (partial sub-blocks, chunk boundaries inside a sub-block, up to 128 chunks
+# to merge): (9000, 8), (16383, 5) and (20000, 16).
 CASES = [(0, 1), (1, 1), (37, 1), (63, 1), (300, 1), (2000, 1), (5000, 1), (20000, 1),
-         (40, 3), (31, 5), (3000, 8), (130, 16), (600, 16), (4100, 16)]
+         (40, 3), (31, 5), (3000, 8), (130, 16), (600, 16), (4100, 16),
+         (9000, 8), (16383, 5), (20000, 16)]
 
 
 @pytest.mark.parametrize("L,T", CASES)

@@ -82,6 +82,11 @@ def test_fused_attention_decode_and_verify_match_stock(model, device):
     stock, sk, sv, _ = run(False)
     native, nk, nv, layer = run(True)
     assert nk.shape == sk.shape == (1, 2, PREFIX + 8, 256)
+    # lrmoe_attn_decode ran: the native path keeps the layer's rows as views
+    # of a buffer with room to grow
+    row_bytes = (PREFIX + 8) * 2 * 256 * 2
+    assert layer.keys.untyped_storage().nbytes() > row_bytes
+    assert layer.values.untyped_storage().nbytes() > row_bytes
     assert layer.get_seq_length() == PREFIX + 8
     for i in range(stock.shape[0]):
         r = _rel(native[i], stock[i])

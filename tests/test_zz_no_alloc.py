@@ -78,3 +78,20 @@ def test_static_layer_rejects_oversize_and_reports_bad_routes(model):
     assert _static(lib, x, layer, out, None, None, status, logits) == 0
     torch.cuda.synchronize()
     assert int(status.item()) == 0   # equal logits: experts 0..7, valid routes
+
+
+def test_first_static_call_under_capture(model):
+    """A process whose first lrmoe_moe_layer_static call is captured into a
+    graph (tests/static_capture_child.py): the graph holds only the decode
+    kernel (no scratch clear recorded), and its replays, interleaved with
+    eager static and workspace calls, are bit-identical to lrmoe_moe_layer.
+    Run in a child process so that its static call is that process's first."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    child = Path(__file__).resolve().parent / "static_capture_child.py"
+    print("[no-alloc] child process: first static call under capture", flush=True)
+    result = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True, timeout=300)
+    print(result.stdout[-4000:], result.stderr[-4000:], flush=True)
+    assert result.returncode == 0 and "static capture ok" in result.stdout
