@@ -16,7 +16,10 @@ T=1 and T=16 (µs and GB/s on its weight and state bytes, per-kernel times,
 a torch gate, and the oracle's C step timed on one core beside it), and (C8)
 the full-attention decode step of the 10 full-attention layers at a
 4096-position context, T=1 and T=16 (the same figures on its weight and
-key/value bytes).
+key/value bytes), and (C9) the whole 40-layer decoder step -- input RMSNorm,
+Gated DeltaNet mixer or full attention, residual add, MoE block -- as one
+captured graph per verify width 1/4/8/16 (ms per verify pass, and GB/s on
+every weight, state and cached byte the pass touches).
 
 `roofline` is for moe_decode, the one kernel of the headline step, timed
 with HIP events stamped by its own dispatches, against the 8 TB/s spec and,
@@ -792,6 +795,53 @@ def bench_attention(device, seed: int, passes: int, skip_cpu: bool) -> dict:
     return out
 
 
+DECODER_WIDTHS = (1, 4, 8, 16)
+
+
+def bench_decoder(model, device, seed: int, reps: int) -> dict:
+    """C9: the whole 35B decoder step (per layer the input RMSNorm, the Gated
+    DeltaNet mixer or the full attention, the residual add, the MoE block;
+    30 + 10 layers over the resident MoE blocks of `model`) as one captured
+    graph per verify width (lightreason_amd.decoder.VerifyPass) after 4096
+    cached positions, fp32 mixer states; ms per verify pass, and HBM bytes
+    touched per pass: every layer's unique routed experts, shared expert,
+    router and norm rows; every mixer's weights and state read and written;
+    every attention layer's weights and cached rows."""
+    from lightreason_amd.decoder import VerifyPass, is_full_attention
+    from lightreason_amd.synthetic import SyntheticDecoder
+
+    L = len(model.layers)
+    t0 = time.perf_counter()
+    dec = SyntheticDecoder(L, device, seed, context=ATTN_CONTEXT, moe=model)
+    vp = VerifyPass(dec.stack, DECODER_WIDTHS, ATTN_CONTEXT)
+    torch.cuda.synchronize()
+    log(f"[bench] C9 decoder stack ({sum(not is_full_attention(l) for l in range(L))} Gated DeltaNet + "
+        f"{sum(is_full_attention(l) for l in range(L))} attention layers) captured in {time.perf_counter() - t0:.1f}s")
+    out = {}
+    for W in DECODER_WIDTHS:
+        x = dec.hidden(W, step=900 + W)
+        cos, sin = dec.rope(W, ATTN_CONTEXT)
+        vp.verify(x, cos, sin)  # warm, and the status words checked
+        graph, static = vp.graphs[W]
+        ms = timed_replays(graph, reps) / reps
+        dec.stack.check_status()
+        uniques = [len(set(i.ravel().tolist())) for i in static["buffers"].indices.cpu().numpy()]
+        nbytes = 0
+        for l in range(L):
+            nbytes += uniques[l] * EXPERT_BYTES + ROUTER_BYTES + SHARED_BYTES + 4 * HIDDEN  # norm rows in, h out
+            nbytes += attn_bytes(W, ATTN_CONTEXT) if is_full_attention(l) else mixer_bytes(W)
+            nbytes += HIDDEN * 2  # the input RMSNorm weight
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"t{W}"] = dict(ms_per_pass=round(ms, 4), positions_per_s=round(W / (ms * 1e-3), 1),
+                            bytes_per_pass=nbytes, gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
+                            mean_unique=round(float(np.mean(uniques)), 1))
+    del vp, dec
+    torch.cuda.empty_cache()
+    out["note"] = ("one replay = one verify pass of the 40-layer decoder (embedding and lm_head omitted) after "
+                   f"{ATTN_CONTEXT} cached positions, router-driven routes; status words checked after timing")
+    return out
+
+
 def attn_cpu_leg(a, cache, cos, sin, length, budget_s: float = 3.0) -> dict:
     """The oracle's C attention step (oracle/lro.c lro_attn_decode, one
     thread: the reference runs this step in Transformers) at T = 1 after
@@ -825,7 +875,7 @@ def main() -> int:
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-prefill", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=1.0, help="scale of the CPU legs' time budgets")
-    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6,c7,c8 to run besides the headline "
+    parser.add_argument("--only", default="", help="comma list of c0,c1,c3,c4,c5,c6,c7,c8,c9 to run besides the headline "
                                                    "(default all)")
     parser.add_argument("--calibrate-copy", action="store_true",
                         help="also run a plain 256 MiB device copy (untimed) so that HBM byte counters "
@@ -847,7 +897,7 @@ def main() -> int:
         f"in {time.perf_counter() - t0:.1f}s")
     L = args.layers
     aux = max(2, min(10, args.steps // L))  # graph replays of the secondary configs
-    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6", "c7", "c8"}
+    only = set(filter(None, args.only.split(","))) or {"c0", "c1", "c3", "c4", "c5", "c6", "c7", "c8", "c9"}
     if args.skip_prefill:
         only.discard("c4")
     configs = {}
@@ -1102,6 +1152,11 @@ def main() -> int:
     if "c7" in only:
         configs["c7_delta_mixer"] = bench_mixers(device, args.seed, aux, args.skip_cpu)
         log(f"[bench] C7 mixer: {configs['c7_delta_mixer']}")
+    # ---- C9: the whole decoder step per verify width ----
+    if "c9" in only:
+        configs["c9_decoder_verify"] = bench_decoder(model, device, args.seed, max(5, 2 * aux))
+        log(f"[bench] C9 decoder verify pass: {configs['c9_decoder_verify']}")
+
     # ---- C8: full-attention decode step (the 10 full-attention layers) ----
     if "c8" in only:
         configs["c8_attention"] = bench_attention(device, args.seed, aux, args.skip_cpu)

@@ -301,6 +301,21 @@ int lrmoe_project(const int64_t *pointers, const int32_t *routes, const uint16_t
  * _project launches (edge35b/block_experts.py:131-132, fused_experts.py:61-62). */
 int lrmoe_swiglu_rows(const uint16_t *gates, uint16_t *active, int rows, void *stream);
 
+/* The decoder layer's glue around its mixer, per token row of x
+ * [tokens][2048] bf16: s = bf16(x + add) elementwise when add is given (the
+ * residual add after the mixer, [HF] Qwen3_5MoeDecoderLayer.forward 866:
+ * hidden = residual + mixer output), else s = x; sum_out (requires add)
+ * receives s; with norm_weight [2048], norm_out receives RMSNorm(s) =
+ * bf16(s rsqrt(mean(s^2) + eps) (1 + w)) (the input_layernorm before the
+ * mixer, Qwen3_5MoeRMSNorm [HF] 801-818, in the canonical summation order of
+ * the router and decode kernels, so the rows equal lrmoe_route_topk's
+ * normed_out bit for bit).  norm_weight and norm_out come together; at least
+ * one of sum_out, norm_out is given.  Every pointer 16-byte aligned.  No
+ * reference counterpart as a kernel: the reference runs these as torch ops
+ * inside the stock decoder layer. */
+int lrmoe_add_rmsnorm(const uint16_t *x, const uint16_t *add, int tokens, const uint16_t *norm_weight, float eps,
+                      uint16_t *sum_out, uint16_t *norm_out, void *stream);
+
 /* Per-token ordered combine through inverse [tokens][8][3] = (expert, row,
  * slot): out[t][h] = bf16 running sum of bf16(v * router[t*8 + slot]),
  * v = X[(expert*16 + row)][h], or cold[row][h] when hybrid and expert < 0.

@@ -49,6 +49,7 @@ _SIGNATURES = {
     "lrmoe_gate_silu": ([_P, _P, _P, _I, _I, _P], _I),
     "lrmoe_project": ([_P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
     "lrmoe_swiglu_rows": ([_P, _P, _I, _P], _I),
+    "lrmoe_add_rmsnorm": ([_P, _P, _I, _P, C.c_float, _P, _P, _P], _I),
     "lrmoe_block_combine": ([_P, _P, _P, _P, _P, _I, _I, _P], _I),
     "lrmoe_fill_normal_bf16": ([_P, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_int64, _P], _I),
     "lrmoe_timing_enable": ([_I, _I], _I),

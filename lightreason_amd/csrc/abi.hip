@@ -451,6 +451,20 @@ int lrmoe_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows, void* s
     return status_of(lrmoe::launch_swiglu_rows(gates, active, rows, as_stream(stream)));
 }
 
+int lrmoe_add_rmsnorm(const uint16_t* x, const uint16_t* add, int tokens, const uint16_t* norm_weight, float eps,
+                      uint16_t* sum_out, uint16_t* norm_out, void* stream) {
+    if (bad_tokens(tokens)) return LRMOE_E_ARG;
+    if (tokens > 0 && (!x || (!sum_out && !norm_out) || (norm_weight && !norm_out) || (!norm_weight && norm_out) ||
+                       (sum_out && !add)))
+        return LRMOE_E_ARG;
+    if (misaligned(x, 16) || misaligned(add, 16) || misaligned(norm_weight, 16) || misaligned(sum_out, 16) ||
+        misaligned(norm_out, 16))
+        return LRMOE_E_ARG;
+    if (tokens == 0) return LRMOE_OK;
+    if (int d = check_device()) return d;
+    return status_of(lrmoe::launch_add_rmsnorm(x, add, tokens, norm_weight, eps, sum_out, norm_out, as_stream(stream)));
+}
+
 int lrmoe_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
                         uint16_t* out, int tokens, int hybrid, void* stream) {
     if (!inverse || !X || !router || !out || bad_tokens(tokens) || (hybrid && !cold)) return LRMOE_E_ARG;

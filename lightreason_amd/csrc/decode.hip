@@ -54,9 +54,11 @@
 // stamps to the buffer given by lrmoe_timeline_set (kTimelineWords per
 // workgroup).  Word 0 launch entry, 1 top-8 in the plan, 2 first item's
 // loads issued (wave 0), 3 plan done, 4 items done, 5 first item's loads
-// issued (wave 7), 6 token rows staged; 8 + 5n the n-th item step: start,
-// its weights in, its inputs in, end, and item code (kind + 1) * 1e6 +
-// slot * 1e3 + tile.
+// issued (wave 7), 6 token rows staged, 7 call counters read; 8 + 5n the
+// n-th item step (n < 22): start, its weights in, its inputs in, end, and
+// item code (kind + 1) * 1e6 + slot * 1e3 + tile; 118 wave 0's top-8
+// extracted, 119 expert masks built, 120 slots numbered, 121 token rows
+// staged (wave 7).
 #ifdef LRMOE_TIMELINE
 __device__ unsigned long long* g_timeline;
 extern "C" int lrmoe_timeline_set(void* p) {
@@ -102,6 +104,17 @@ constexpr int kRouterWgs = kExperts / kWaves; // 32 workgroups x 8 router rows
 constexpr int kXStride = kHidden + 8;         // LDS token row stride (bf16)
 constexpr int kActStride = kInner + 8;        // LDS act row stride (bf16)
 constexpr int kLoads = 16;                    // 16-byte weight loads per lane per item
+// Raw items load their weights as 4 rows x 256 B per instruction (16-byte
+// non-temporal loads; load i: MFMA row 4 (i % 4) + lane / 16 of the wave's
+// 16, bytes 256 (i / 4) + 16 (lane % 16) of the row's slice) and pass them
+// through a per-wave LDS stage of 16 rows x 256 B (+16 B pad: conflict-free
+// in both directions) into the MFMA layout (lane (m, g) of step q: row m,
+// elements 32 q + 8 g ..).  An instruction then covers four rows' whole
+// 128-byte lines instead of sixteen rows' half lines: the HBM stream of a
+// C2 layer runs about 7% faster.  Every MFMA sees the operands, in the
+// order, of loads made directly in the MFMA layout.
+constexpr int kStageRow = 256 + 16;           // bytes per staged row
+constexpr int kStageBytes = 16 * kStageRow;   // per wave
 constexpr int kCombineItems = kBTiles;        // C items, one per 128-row output tile
 constexpr uint64_t kSpinTicks = 5000000;      // 50 ms of the 100 MHz wall clock
 // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14.
@@ -211,16 +224,18 @@ struct SlotCodec {
     int32_t pad;
 };
 
+// kCodec: the codec kernel's plan (the other one carries no codec tables).
+template <bool kCodec>
 struct Plan {
     SlotInfo slot[kDecodeSlots];
-    SlotCodec scodec[kDecodeSlots];   // codec calls
+    SlotCodec scodec[kCodec ? kDecodeSlots : 1];   // codec calls
     int16_t comb_pair[kMaxT][kTopK];  // per token: pair of the k-th smallest expert
     float comb_w[kMaxT][kTopK];       // its routing weight
     float sg[kMaxT];                  // shared-expert gate per token
     int32_t ids[kMaxT][kTopK];        // routed experts, rank order
     uint16_t wts[kMaxT][kTopK];       // routing weights (bf16), rank order
     uint4 eptr[kExperts];             // (gate_up, down) address of every expert
-    uint4 ecodec[kExperts + 1][5];    // codec table rows of every expert and the shared one (codec calls):
+    uint4 ecodec[kCodec ? kExperts + 1 : 1][5];  // codec table rows of every expert and the shared one (codec calls):
                                       // 4 addresses, then 48 bytes of per-(item, wave) raw flags
     uint32_t tokmask[kExperts];
     uint32_t poff[kExperts];
@@ -240,7 +255,8 @@ struct Plan {
 // the row.  (__syncthreads_or reads the workgroup size from the dispatch
 // packet with vector loads; the wait for those also waits for every older
 // load in flight, such as the next item's prefetch.)
-__device__ __forceinline__ bool block_or(bool pred, Plan& P, int& row, int wave, int lane) {
+template <typename PlanT>
+__device__ __forceinline__ bool block_or(bool pred, PlanT& P, int& row, int wave, int lane) {
     const uint64_t ballot = __ballot(pred);
     if (lane == 0) P.vote[row][wave] = ballot != 0ull ? 1u : 0u;
     __syncthreads();
@@ -333,6 +349,62 @@ __device__ __forceinline__ const uint16_t* item_base(const SlotInfo& s, const It
     const uint16_t* rows = m < 8 ? s.gate : s.up;
     const int row = 16 * it.tile + 8 * (wave >> 2) + (m & 7);
     return rows + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * g;
+}
+
+// The four row pointers of a lane's staged loads of an item (row
+// 4 a + lane / 16 of the wave's 16 MFMA rows, at element 8 (lane % 16) of
+// the wave's k slice); load 4 j + a reads 16 bytes at rows[a] + 128 j.
+__device__ __forceinline__ void item_rows(const SlotInfo& s, const Item& it, int wave, int lane,
+                                          const uint16_t* (&rows)[4]) {
+    const int r = lane >> 4;
+    const int e = 8 * (lane & 15);
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        if (it.kind == 1) {
+            rows[a] = s.down + static_cast<size_t>(kBRows * it.tile + 16 * wave + 4 * a + r) * kInner + e;
+        } else {
+            // MFMA rows 0..7 are gate rows, 8..15 up rows
+            const int row = 16 * it.tile + 8 * (wave >> 2) + 4 * (a & 1) + r;
+            rows[a] = (a < 2 ? s.gate : s.up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + e;
+        }
+    }
+}
+
+__device__ __forceinline__ void issue_rows(const uint16_t* const (&rows)[4], uint4* buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) buf[i] = ldg16_nt(rows[i & 3] + 128 * (i >> 2));
+}
+
+// The MFMAs of a raw item whose staged loads are in buf, B operand rows at
+// bp (32 elements per step): per 128-element span j, the wave's four loads
+// 4 j .. 4 j + 3 into its LDS stage, then steps 4 j .. 4 j + 3 read back in
+// the MFMA layout (even steps into acc0, odd ones into acc1, in order).
+__device__ __forceinline__ void staged_mfmas(const uint4* buf, uint8_t* stage, const uint16_t* bp, int lane,
+                                             f32x4& acc0, f32x4& acc1) {
+    const int m = lane & 15;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < kLoads / 4; ++j) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<uint4*>(stage + (4 * a + (lane >> 4)) * kStageRow + 16 * (lane & 15)) = buf[4 * j + a];
+        // (the stage is the wave's own: in-order LDS access within the wave,
+        // and no reordering by the compiler across these fences)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        uint4 op[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) op[q] = *reinterpret_cast<const uint4*>(stage + m * kStageRow + 16 * (4 * q + g));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+            acc0 = mfma16x16x32(op[q], *reinterpret_cast<const uint4*>(bp + 32 * (4 * j + q)), acc0);
+            acc1 = mfma16x16x32(op[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (4 * j + q + 1)), acc1);
+        }
+    }
 }
 
 // Tile-codec rows of a lane in an item of a codec slot (format in
@@ -430,8 +502,8 @@ __device__ __forceinline__ int column_token(const SlotInfo& s, int n) {
 // threads: token tid/32, rows 4*(tid%32)..+3), then the shared-expert and
 // residual adds.  The tile's y words are reloaded (bounded) until each
 // carries this call's tag.
-template <bool kChained>
-__device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int tid, int tile, int T, bool shared,
+template <bool kChained, typename PlanT>
+__device__ __forceinline__ void combine_tile(const DecodeArgs& a, PlanT& P, int tid, int tile, int T, bool shared,
                                              uint32_t tag, int& vote_row) {
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -509,7 +581,7 @@ __device__ __forceinline__ void combine_tile(const DecodeArgs& a, Plan& P, int t
 // all of the workgroup's memory operations complete; returns kStatusTimeout
 // when one of its bounded waits expired.
 template <bool kChained, bool kCodec, typename WaitInput>
-__device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, uint8_t* dyn,
+__device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec>& P, uint8_t* dyn,
                                                 unsigned long long finished, int layer, WaitInput wait_input) {
     const int T = a.tokens;
     // Thread and workgroup indices as opaque values: what is derived from
@@ -525,6 +597,8 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     uint16_t* x_lds = reinterpret_cast<uint16_t*>(dyn);                       // [T][kXStride]
     uint16_t* act_lds = x_lds + T * kXStride;                                  // [16][kActStride]
     f32x4* part = reinterpret_cast<f32x4*>(act_lds + kMaxT * kActStride);      // [2][8][64]
+    // the wave's weight stage (raw kernel only)
+    uint8_t* const stage = reinterpret_cast<uint8_t*>(part + 2 * kWaves * kWave) + (kCodec ? 0 : wave * kStageBytes);
     DecodeSync* sync = a.sync;
     TL_DECLARE;
     TL_CLEAR;
@@ -550,7 +624,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     uint4 ec[5];
 #pragma unroll
     for (int i = 0; i < 5; ++i) ec[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (a.codec != nullptr && tid <= kExperts) {
+    if (kCodec && a.codec != nullptr && tid <= kExperts) {
 #pragma unroll
         for (int i = 0; i < 5; ++i) ec[i] = ldg16(a.codec + kCodecTableColumns * tid + 2 * i);
     }
@@ -600,12 +674,12 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // them; consumed just before the first item's loads.
     uint32_t warm0 = 0u, warm1 = 0u;
     if (early) {
-        const int m = lane & 15;
-        const int row = 16 * first_item + 8 * (wave >> 2) + (m & 7);
-        const uint16_t* p =
-            (m < 8 ? a.sh_gate : a.sh_up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4);
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * i);
+        SlotInfo sh;
+        sh.gate = a.sh_gate;
+        sh.up = a.sh_up;
+        const uint16_t* rows[4];
+        item_rows(sh, Item{0, 0, first_item}, wave, lane, rows);
+        issue_rows(rows, b0);
     } else {
         const bool warm = a.sh_down != nullptr && first_item < kATiles;
         const int r = (2 * tid) / 32;     // row of the tile: 16 gate rows, then 16 up rows
@@ -617,24 +691,34 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         warm0 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w0));
         warm1 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w1));
     }
-    // (a single layer's count stays in VGPRs until here, so that its load is
-    // waited for here, after every entry load is issued, and not at entry; a
-    // chain's comes from LDS)
+    // This call's number, tag and counter set, resolved where they are first
+    // needed: before the router's logits are published, or (with caller
+    // logits) once the first item's weights are issued.  A single layer's
+    // count comes from an agent-scope load issued at launch, whose ~2 us
+    // latency would otherwise hold up routing; it stays in VGPRs until then,
+    // so that its wait is placed there (a chain's count comes from LDS).
     uint32_t fin_lo = static_cast<uint32_t>(finished), fin_hi = static_cast<uint32_t>(finished >> 32);
-    if constexpr (!kChained) asm volatile("" : "+v"(fin_lo), "+v"(fin_hi));
-    const unsigned long long call = ((static_cast<unsigned long long>(fin_hi) << 32) | fin_lo) /
-                                        static_cast<unsigned long long>(G) +
-                                    static_cast<unsigned>(layer);
-    const int parity = static_cast<int>(call & 1ull);
-    const uint32_t tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
-    DecodeCounters* const cnt = &sync->set[parity];
-    const uint64_t tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
+    int parity = 0;
+    uint32_t tag = 0u;
+    DecodeCounters* cnt = nullptr;
+    uint64_t tag_bits = 0ull;
+    auto resolve_call = [&]() __attribute__((always_inline)) {
+        if constexpr (!kChained) asm volatile("" : "+v"(fin_lo), "+v"(fin_hi));
+        const unsigned long long call = ((static_cast<unsigned long long>(fin_hi) << 32) | fin_lo) /
+                                            static_cast<unsigned long long>(G) +
+                                        static_cast<unsigned>(layer);
+        parity = static_cast<int>(call & 1ull);
+        tag = static_cast<uint32_t>(call % 0xffffffffull) + 1u;
+        cnt = &sync->set[parity];
+        tag_bits = static_cast<uint64_t>(tag) << kDecodeTagShift;
+        if (block == 0 && tid == kThreads - 1) {
+            // The next call's counter (this call never touches it).
+            st_agent32(&sync->set[parity ^ 1].claim, 0u);
+        }
+    };
     int vote_row = 0;  // block_or row
-    if (block == 0 && tid == kThreads - 1) {
-        // The next call's counter (this call never touches it).
-        st_agent32(&sync->set[parity ^ 1].claim, 0u);
-    }
     __syncthreads();
+    TL(7, 0);
 
     // Token rows (normalised when the layer norms) into LDS, and the
     // shared-expert gate of each token.
@@ -677,6 +761,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     if (a.router != nullptr) {
         stage_rows();
         __syncthreads();
+        resolve_call();
         if (early) {
             // The shared-expert A tile first_item, exactly as the item loop
             // runs an A item of slot 0 (columns = tokens 0..T-1, pairs from
@@ -685,11 +770,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const int g = lane >> 4;
             const uint16_t* bp = x_lds + (m < T ? m : 0) * kXStride + kInner * (wave & 3) + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int q = 0; q < kLoads; q += 2) {
-                acc0 = mfma16x16x32(b0[q], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
-                acc1 = mfma16x16x32(b0[q + 1], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
-            }
+            staged_mfmas(b0, stage, bp, lane, acc0, acc1);  // (the early path runs the raw kernel only)
             part[wave * kWave + lane] = acc0 + acc1;
             __syncthreads();
             if ((wave & 3) == 0) {
@@ -780,6 +861,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             }
         } else if (has_lo) {
             topk8_wave(lg_lo, e_lo, w_lo, lane);
+            TL(118, 0);
             if (lane < kTopK) {
                 P.ids[t_lo][lane] = e_lo;
                 P.wts[t_lo][lane] = static_cast<uint16_t>(w_lo);
@@ -796,19 +878,15 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         if (bad) atomicOr(&P.status, bad);
     }
     if (tid < kExperts) P.eptr[tid] = eptr;
-    if (a.codec != nullptr && tid <= kExperts) {
+    if constexpr (kCodec) {
+        if (a.codec != nullptr && tid <= kExperts) {
 #pragma unroll
-        for (int i = 0; i < 5; ++i) P.ecodec[tid][i] = ec[i];
+            for (int i = 0; i < 5; ++i) P.ecodec[tid][i] = ec[i];
+        }
     }
     __syncthreads();
 
     TL(1, 0);
-    // ---- the first item's weights, before the rest of the plan ----
-    // Slots are numbered in discovery order (token 0's routes first, in rank
-    // order), so a workgroup's first item -- A tile k % 32 of slot
-    // first_slot + k / 32 with k < G <= 256 -- names slot 0 (the shared
-    // expert) or one of token 0's experts, and streams in while the rest of
-    // the plan is built.
     // Prefetch target of an item without weights (C items): 1 KiB of token
     // row 0, in cache after the first read.
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
@@ -849,10 +927,14 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // k-step kRawStep[j] of the tile.
     auto issue_item = [&](const Item& it, uint4* buf, uint32_t dec) __attribute__((always_inline)) {
         if constexpr (!kCodec) {
-            const uint16_t* p = (it.kind == 0 || it.kind == 1) ? item_base(P.slot[it.slot], it, wave, lane)
-                                                                : idle_rows;
+            // (row pointers selected, not loads branched: a join after the
+            // loads would make the compiler wait for them)
+            const uint16_t* rows[4];
+            item_rows(P.slot[it.slot], it, wave, lane, rows);
+            const bool weights = it.kind == 0 || it.kind == 1;
 #pragma unroll
-            for (int i = 0; i < kLoads; ++i) buf[i] = ldg16(p + 32 * i);
+            for (int r = 0; r < 4; ++r) rows[r] = weights ? rows[r] : idle_rows + 8 * (lane & 15) - 8 * (lane >> 4);
+            issue_rows(rows, buf);
             return;
         }
         const uint8_t* raw = reinterpret_cast<const uint8_t*>(idle_rows);
@@ -882,42 +964,12 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     // null when the call has no codec table or the expert's row does not
     // give all four addresses (then it is read raw).
     auto codec_of = [&](int row) -> const uint4* {
-        if (a.codec == nullptr) return nullptr;
+        if (!kCodec || a.codec == nullptr) return nullptr;
         const uint4* c = P.ecodec[row];
         const bool all = (c[0].x | c[0].y) != 0u && (c[0].z | c[0].w) != 0u && (c[1].x | c[1].y) != 0u &&
                          (c[1].z | c[1].w) != 0u;
         return all ? c : nullptr;
     };
-    int cur = early ? first_item + G : first_item;
-    asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
-    // The first item (read raw, tile choice 0) is addressed straight from
-    // the expert table.
-    uint32_t dec = 0u;  // tile choice of the item being run
-    {
-        // item_base's A geometry for tile cur % 32 of slot s0.
-        const int s0 = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
-        const uint4 ptrs = P.eptr[P.ids[0][s0 > 0 ? s0 - 1 : 0]];
-        const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(ptrs.x) |
-                                                                    (static_cast<uintptr_t>(ptrs.y) << 32));
-        const uint16_t* gate = s0 == 0 ? a.sh_gate : gate_up;
-        const uint16_t* up = s0 == 0 ? a.sh_up : gate_up + static_cast<size_t>(kInner) * kHidden;
-        const int m = lane & 15;
-        const int row = 16 * (cur % kATiles) + 8 * (wave >> 2) + (m & 7);
-        const uint16_t* p =
-            (m < 8 ? gate : up) + static_cast<size_t>(row) * kHidden + kInner * (wave & 3) + 8 * (lane >> 4);
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) b0[i] = ldg16(p + 32 * (kCodec ? (i & 8) + kRawStep[i & 7] : i));
-    }
-
-    TL(2, 0);
-    TL(5, 7 * kWave);
-    // With caller logits, each wave stages its token rows right after
-    // issuing its share of the first item, while later waves are still
-    // issuing theirs; the plan's barriers below publish the rows.
-    if (a.router == nullptr) {
-        stage_rows();
-        TL(6, 0);
-    }
     if (block == 0 && tid < T * kTopK) {
         if (a.indices_out != nullptr) a.indices_out[tid] = P.ids[tid / kTopK][tid % kTopK];
         if (a.weights_out != nullptr) a.weights_out[tid] = P.wts[tid / kTopK][tid % kTopK];
@@ -925,24 +977,54 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
     const bool routes_ok = (P.status & ~kStatusTimeout) == 0;
     if (routes_ok && tid < T * kTopK) atomicOr(&P.tokmask[P.ids[tid / kTopK][tid % kTopK]], 1u << (tid / kTopK));
     __syncthreads();
+    TL(119, 0);
     {
         // Route i = tid (token i / 8, rank i % 8) opens a slot when its token
-        // is the first routed to the expert; one scan over the routes gives
-        // each new expert its slot and its first pair.
-        int e = 0;
-        uint32_t mask = 0u;
-        uint32_t opens = 0u;
-        if (routes_ok && tid < T * kTopK) {
-            const int t = tid / kTopK;
-            e = P.ids[t][tid % kTopK];
-            mask = P.tokmask[e];
-            if ((mask & ((1u << t) - 1u)) == 0u) opens = (1u << 16) | static_cast<uint32_t>(__popc(mask));
+        // is the first routed to the expert.  A new expert's slot is the
+        // number of routes before it that open one, its first pair the sum
+        // of their token counts: ballots over the (at most 128) routes, the
+        // counts bit-sliced, so that no block scan is needed.  Waves 0 and 1
+        // (the routes' threads) both evaluate all routes.
+        auto route_opens = [&](int i, int& e_out, uint32_t& mask_out) -> uint32_t {
+            e_out = 0;
+            mask_out = 0u;
+            if (!routes_ok || i >= T * kTopK) return 0u;
+            const int t = i / kTopK;
+            e_out = P.ids[t][i % kTopK];
+            mask_out = P.tokmask[e_out];
+            return (mask_out & ((1u << t) - 1u)) == 0u ? static_cast<uint32_t>(__popc(mask_out)) : 0u;
+        };
+        const bool route_thread = tid < 2 * kWave;
+        const int own = route_thread ? tid : 0;
+        int e = 0, e_other = 0;
+        uint32_t mask = 0u, mask_other = 0u;
+        const uint32_t count = route_opens(own, e, mask);                              // 0 or 1..16
+        const uint32_t count_other = route_opens(own ^ kWave, e_other, mask_other);   // the other wave's route
+        const uint32_t opens = route_thread && count != 0u ? (1u << 16) | count : 0u;
+        // lanes of this route's wave below it, and the routes of wave 0 when
+        // this is wave 1
+        const uint64_t below = (1ull << lane) - 1ull;
+        const bool second = own >= kWave;
+        uint32_t rank = 0u, pair0 = 0u, unique = 0u;
+        {
+            const uint64_t o_own = __ballot(count != 0u);
+            const uint64_t o_oth = __ballot(count_other != 0u);
+            const uint64_t o_first = second ? o_oth : o_own;
+            rank = static_cast<uint32_t>(__popcll(o_own & below)) + (second ? static_cast<uint32_t>(__popcll(o_first)) : 0u);
+            unique = static_cast<uint32_t>(__popcll(o_own) + __popcll(o_oth));
+#pragma unroll
+            for (int b = 0; b < 5; ++b) {
+                const uint64_t c_own = __ballot(((count >> b) & 1u) != 0u);
+                const uint64_t c_oth = __ballot(((count_other >> b) & 1u) != 0u);
+                const uint64_t c_first = second ? c_oth : c_own;
+                pair0 += (static_cast<uint32_t>(__popcll(c_own & below)) +
+                          (second ? static_cast<uint32_t>(__popcll(c_first)) : 0u)) << b;
+            }
         }
-        uint32_t packed_total = 0;
-        const uint32_t packed = block_scan256(opens, P.scan, &packed_total, tid);
-        const uint32_t pair0 = packed & 0xffffu;
-        const uint32_t rank = packed >> 16;
-        const uint32_t unique = packed_total >> 16;
+        // (thread 0, which numbers the shared expert's slot below, is in wave
+        // 0, whose ballots cover every route)
+        (void)e_other;
+        (void)mask_other;
         if (opens) {
             P.poff[e] = pair0;
             SlotInfo& s = P.slot[1 + rank];
@@ -994,6 +1076,41 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         }
     }
     __syncthreads();
+    TL(120, 0);
+    // The route status of a launch's first layer replaces the previous
+    // launch's; later layers add theirs (timeouts are OR-ed in at the end).
+    if (block == 0 && tid == 0) {
+        const int32_t route_status = P.status & ~kStatusTimeout;
+        if (layer == 0) {
+            st_agent32(a.status, static_cast<uint32_t>(route_status));
+        } else if (route_status != 0) {
+            atomicOr(a.status, route_status);
+        }
+    }
+    TL(3, 0);
+    const int n_slots = P.n_slots;
+    const int first_slot = P.first_slot;
+    const int total = (kATiles + kBTiles) * n_slots;          // A and B items
+    const int end = n_slots > 0 ? total + kCombineItems : 0;  // and the C items
+
+    if (a.router == nullptr) resolve_call();
+
+    // ---- the first item's weights ----
+    // Issued as soon as the slots are numbered; the first step then issues
+    // the second item's at once, so that two items are in flight from the
+    // start.  The token rows (with caller logits) and the combine order are
+    // worked out while they stream.
+    int cur = early ? first_item + G : first_item;
+    asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
+    uint32_t dec = 0u;  // tile choice of the item being run (the first is read raw)
+    issue_item(item_at(cur, total, n_slots, first_slot), b0, 0u);
+    TL(2, 0);
+    TL(5, 7 * kWave);
+    if (a.router == nullptr) {
+        stage_rows();
+        TL(6, 0);
+        TL(121, 7 * kWave);
+    }
     if (routes_ok && tid < T * kTopK) {
         const int t = tid / kTopK;
         const int k = tid % kTopK;
@@ -1005,23 +1122,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         P.comb_pair[t][order] = static_cast<int16_t>(p);
         P.comb_w[t][order] = bf2f(P.wts[t][k]);
     }
-    // The route status of a launch's first layer replaces the previous
-    // launch's; later layers add theirs (timeouts are OR-ed in at the end).
-    if (block == 0 && tid == 0) {
-        const int32_t route_status = P.status & ~kStatusTimeout;
-        if (layer == 0) {
-            st_agent32(a.status, static_cast<uint32_t>(route_status));
-        } else if (route_status != 0) {
-            atomicOr(a.status, route_status);
-        }
-    }
     __syncthreads();
-
-    TL(3, 0);
-    const int n_slots = P.n_slots;
-    const int first_slot = P.first_slot;
-    const int total = (kATiles + kBTiles) * n_slots;          // A and B items
-    const int end = n_slots > 0 ? total + kCombineItems : 0;  // and the C items
 
     // Bad routes: the output is the residual (or zeros); no expert runs.
     if (!routes_ok) {
@@ -1064,6 +1165,23 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
                                 *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
             acc1 = mfma16x16x32(pick(pk, packed_operand(buf, q + 1, base), buf[raw_reg(q + 1)]),
                                 *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+        }
+    };
+    // The MFMAs of an A or B item whose weights are in buf (B operand rows
+    // at bp): raw items of the raw kernel through the wave's stage; codec
+    // kernel items per tile packed or raw (raw loads in kRawStep order).
+    auto item_mfmas = [&](const Item& it, const uint4* buf, const uint16_t* bp, uint32_t dec, f32x4& acc0,
+                          f32x4& acc1) __attribute__((always_inline)) {
+        if constexpr (!kCodec) {
+            staged_mfmas(buf, stage, bp, lane, acc0, acc1);
+        } else if (P.scodec[it.slot].pk_gu != nullptr) {
+            codec_mfmas(buf, bp, dec, packed_lane(P.scodec[it.slot], it, wave, lane).base_byte, acc0, acc1);
+        } else {
+#pragma unroll
+            for (int q = 0; q < kLoads; q += 2) {
+                acc0 = mfma16x16x32(buf[raw_reg(q)], *reinterpret_cast<const uint4*>(bp + 32 * q), acc0);
+                acc1 = mfma16x16x32(buf[raw_reg(q + 1)], *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
+            }
         }
     };
     // Runs item kk, whose weights are in buf (tile choice `dec`), prefetches
@@ -1150,17 +1268,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
             const int tok = column_token(s, m < s.count ? m : 0);
             const uint16_t* bp = x_lds + tok * kXStride + kInner * (wave & 3) + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (kCodec && P.scodec[it.slot].pk_gu != nullptr) {
-                codec_mfmas(buf, bp, dec, packed_lane(P.scodec[it.slot], it, wave, lane).base_byte, acc0, acc1);
-            } else {
-#pragma unroll
-                for (int q = 0; q < kLoads; q += 2) {
-                    acc0 = mfma16x16x32(buf[kCodec ? raw_reg(q) : q], *reinterpret_cast<const uint4*>(bp + 32 * q),
-                                        acc0);
-                    acc1 = mfma16x16x32(buf[kCodec ? raw_reg(q + 1) : q + 1],
-                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
-                }
-            }
+            item_mfmas(it, buf, bp, dec, acc0, acc1);
             part[(par * kWaves + wave) * kWave + lane] = acc0 + acc1;
             __syncthreads();
             if ((wave & 3) == 0) {
@@ -1183,17 +1291,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan& P, ui
         } else if (it.kind == 1) {
             const uint16_t* bp = act_lds + (m < s.count ? m : 0) * kActStride + 8 * g;
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (kCodec && P.scodec[it.slot].pk_gu != nullptr) {
-                codec_mfmas(buf, bp, dec, packed_lane(P.scodec[it.slot], it, wave, lane).base_byte, acc0, acc1);
-            } else {
-#pragma unroll
-                for (int q = 0; q < kLoads; q += 2) {
-                    acc0 = mfma16x16x32(buf[kCodec ? raw_reg(q) : q], *reinterpret_cast<const uint4*>(bp + 32 * q),
-                                        acc0);
-                    acc1 = mfma16x16x32(buf[kCodec ? raw_reg(q + 1) : q + 1],
-                                        *reinterpret_cast<const uint4*>(bp + 32 * (q + 1)), acc1);
-                }
-            }
+            item_mfmas(it, buf, bp, dec, acc0, acc1);
             const f32x4 y = acc0 + acc1;
             if (m < s.count) {
                 uint32_t o[4];
@@ -1287,7 +1385,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode(DecodeArgs args) {
     // the kernel-argument block into private memory.
     const DecodeArgs a = args;
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
-    __shared__ Plan P;
+    __shared__ Plan<kCodec> P;
     // This call's number, from the count of finished workgroups (DecodeSync).
     const unsigned long long finished = ld_agent64(&a.sync->finished);
     const int32_t timeout = decode_layer<false, kCodec>(a, P, dyn, finished, 0, [] {});
@@ -1311,7 +1409,7 @@ struct ChainState {
 template <bool kCodec>
 __global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
-    __shared__ Plan P;
+    __shared__ Plan<kCodec> P;
     __shared__ ChainState S;
     const unsigned long long G = gridDim.x;
     if (threadIdx.x == 0) {
@@ -1402,9 +1500,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_chain(ChainArgs args) {
 
 }  // namespace
 
-size_t decode_lds_bytes(int tokens) {
+size_t decode_lds_bytes(int tokens, bool codec) {
     return static_cast<size_t>(tokens) * kXStride * 2 + static_cast<size_t>(kMaxT) * kActStride * 2 +
-           2 * kWaves * kWave * sizeof(f32x4);
+           2 * kWaves * kWave * sizeof(f32x4) + (codec ? 0 : static_cast<size_t>(kWaves) * kStageBytes);
 }
 
 namespace {
@@ -1425,7 +1523,7 @@ struct LaunchSetup {
 // workgroup per CU, all resident at once, which the cross-workgroup waits
 // rely on).
 template <typename Kernel>
-hipError_t persistent_grid(Kernel kernel, LaunchSetup (&setup)[64], int* grid) {
+hipError_t persistent_grid(Kernel kernel, bool codec, LaunchSetup (&setup)[64], int* grid) {
     int device = 0;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return err;
@@ -1437,10 +1535,10 @@ hipError_t persistent_grid(Kernel kernel, LaunchSetup (&setup)[64], int* grid) {
     }
     if (!d.ready) {
         err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(decode_lds_bytes(kMaxT)));
+                                  static_cast<int>(decode_lds_bytes(kMaxT, codec)));
         if (err != hipSuccess) return err;
         int blocks = 0;
-        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, decode_lds_bytes(kMaxT));
+        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, decode_lds_bytes(kMaxT, codec));
         if (err != hipSuccess) return err;
         if (blocks < 1) return hipErrorLaunchOutOfResources;
         d.ready = true;
@@ -1463,15 +1561,15 @@ hipError_t launch_moe_decode(const DecodeArgs& a, hipStream_t stream) {
     static LaunchSetup setup[2][64];
     const bool codec = a.codec != nullptr && a.tokens >= kCodecMinTokens;
     int grid = 0;
-    const hipError_t err = codec ? persistent_grid(moe_decode<true>, setup[1], &grid)
-                                 : persistent_grid(moe_decode<false>, setup[0], &grid);
+    const hipError_t err = codec ? persistent_grid(moe_decode<true>, true, setup[1], &grid)
+                                 : persistent_grid(moe_decode<false>, false, setup[0], &grid);
     if (err != hipSuccess) return err;
     const StageEvents ev = timing_events(kStageLayer);
     if (codec) {
-        LRMOE_LAUNCH(moe_decode<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start,
+        LRMOE_LAUNCH(moe_decode<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens, codec), stream, ev.start,
                      ev.stop, a);
     } else {
-        LRMOE_LAUNCH(moe_decode<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens), stream, ev.start,
+        LRMOE_LAUNCH(moe_decode<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.tokens, codec), stream, ev.start,
                      ev.stop, a);
     }
     return hipGetLastError();
@@ -1485,15 +1583,15 @@ hipError_t launch_moe_chain(const ChainArgs& a, hipStream_t stream) {
     for (int l = 0; l < a.layers; ++l) codec |= a.layer[l].codec != nullptr;
     codec = codec && a.base.tokens >= kCodecMinTokens;  // as in launch_moe_decode
     int grid = 0;
-    const hipError_t err = codec ? persistent_grid(moe_chain<true>, setup[1], &grid)
-                                 : persistent_grid(moe_chain<false>, setup[0], &grid);
+    const hipError_t err = codec ? persistent_grid(moe_chain<true>, true, setup[1], &grid)
+                                 : persistent_grid(moe_chain<false>, false, setup[0], &grid);
     if (err != hipSuccess) return err;
     const StageEvents ev = timing_events(kStageLayer);
     if (codec) {
-        LRMOE_LAUNCH(moe_chain<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start,
+        LRMOE_LAUNCH(moe_chain<true>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens, codec), stream, ev.start,
                      ev.stop, a);
     } else {
-        LRMOE_LAUNCH(moe_chain<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens), stream, ev.start,
+        LRMOE_LAUNCH(moe_chain<false>, dim3(grid), dim3(kThreads), decode_lds_bytes(a.base.tokens, codec), stream, ev.start,
                      ev.stop, a);
     }
     return hipGetLastError();

@@ -109,6 +109,22 @@ __device__ __forceinline__ float butterfly_step8(float v) {
     return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
 }
 
+// Steps 16 and 32 of an xor butterfly with gfx950's lane-half swaps (VALU,
+// no LDS round trip): v_permlane16_swap on two copies of v leaves, in every
+// lane, its own value in one output and the value of lane l ^ 16 in the
+// other (v_permlane32_swap: lane l ^ 32); their sum is own + partner, or
+// partner + own, the same bits.
+__device__ __forceinline__ float butterfly_step16(float v) {
+    const int x = __float_as_int(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float butterfly_step32(float v) {
+    const int x = __float_as_int(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 // xor butterfly over the 64 lanes with offsets 1,2,4,...,32: the fixed
 // reduction order shared with the oracle for router and norm sums (every lane
 // ends with the same total; each partial sum is a+b on one lane and b+a on
@@ -118,8 +134,8 @@ __device__ __forceinline__ float wave_butterfly_sum(float value) {
     value = value + __int_as_float(lane_xor<2>(__float_as_int(value)));
     value = butterfly_step4(value);
     value = butterfly_step8(value);
-    value = value + __int_as_float(lane_xor<16>(__float_as_int(value)));
-    value = value + __int_as_float(lane_xor<32>(__float_as_int(value)));
+    value = butterfly_step16(value);
+    value = butterfly_step32(value);
     return value;
 }
 
@@ -197,6 +213,13 @@ __device__ __forceinline__ uint32_t ldg_u16(const void* p) {
 
 __device__ __forceinline__ uint4 ldg16(const void* p) {
     const u32x4 v = *reinterpret_cast<global_u32x4*>(reinterpret_cast<uintptr_t>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16-byte non-temporal load (global_load_dwordx4 ... nt): for weight rows
+// read once per call, streamed past the caches.
+__device__ __forceinline__ uint4 ldg16_nt(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<global_u32x4*>(reinterpret_cast<uintptr_t>(p)));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

@@ -322,6 +322,8 @@ hipError_t launch_gate_silu(const int64_t* table, const uint16_t* hidden, uint16
 hipError_t launch_project(const int64_t* pointers, const int32_t* routes, const uint16_t* X, uint16_t* Y, int in,
                           int out, int down, int experts, hipStream_t stream);
 hipError_t launch_swiglu_rows(const uint16_t* gates, uint16_t* active, int rows, hipStream_t stream);
+hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* add, int tokens, const uint16_t* norm, float eps,
+                              uint16_t* sum_out, uint16_t* norm_out, hipStream_t stream);
 hipError_t launch_block_combine(const int32_t* inverse, const uint16_t* X, const uint16_t* cold, const uint16_t* router,
                                 uint16_t* out, int tokens, int hybrid, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& args, hipStream_t stream);
@@ -333,7 +335,7 @@ hipError_t launch_prefill_plan(const uint16_t* logits, const int64_t* indices_in
                                int64_t* indices, uint16_t* weights, int tokens, int shared_present,
                                const Workspace& ws, const Plan& plan, hipStream_t stream);
 hipError_t launch_prefill_experts(const ExpertArgs& args, hipStream_t stream);
-size_t decode_lds_bytes(int tokens);
+size_t decode_lds_bytes(int tokens, bool codec);
 hipError_t launch_codec_pack(const uint16_t* w, int64_t rows, int cols, uint8_t* packed, uint8_t* bases,
                              unsigned long long* misfit, hipStream_t stream);
 hipError_t launch_codec_unpack(const uint8_t* packed, const uint8_t* bases, int64_t rows, int cols, uint16_t* w,

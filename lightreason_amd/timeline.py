@@ -31,8 +31,10 @@ import torch
 from . import _native
 
 WORDS = 128  # stamps per workgroup (kTimelineWords)
-PHASES = (("entry", 0), ("top8", 1), ("first_issued_w0", 2), ("first_issued_w7", 5), ("plan", 3),
-          ("rows_staged", 6), ("end", 4))
+PHASES = (("entry", 0), ("counters", 7), ("top8_w0", 118), ("top8", 1), ("first_issued_w0", 2),
+          ("first_issued_w7", 5), ("rows_staged", 6), ("rows_staged_w7", 121), ("masks", 119), ("slots", 120),
+          ("plan", 3), ("end", 4))
+STEPS = 22  # item steps stamped (words 8 + 5 n .. 8 + 5 n + 4; words 118 and up hold phases)
 
 
 MIXER_PHASES = (("unit 0 multiplied", 1), ("unit 0 epilogue", 2), ("unit 1 + beta/G", 3), ("phase A end", 4),
@@ -146,10 +148,8 @@ def main(argv=None) -> int:
             v = f(t[:, i])
             cells.append(f"{name} {np.nanmedian(v):.2f}/{np.nanmax(v):.2f}" if (~np.isnan(v)).any() else f"{name} -")
         print("  " + " | ".join(cells) + "   (median/max)")
-        for n in range(24):
+        for n in range(STEPS):
             b = 8 + 5 * n
-            if b + 4 >= WORDS:
-                break
             s0, s1, s2, s3 = (f(t[:, b + i]) for i in range(4))
             ok = ~np.isnan(s0)
             if not ok.any():

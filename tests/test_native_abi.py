@@ -109,6 +109,16 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_attn_decode(null, 1, *args(1, 100, 0, big)[2:]) == -1
     assert lib.lrmoe_attn_decode(*args(1, 100, 0, 8)) == -2
     assert lib.lrmoe_attn_decode(*args(0, 100, 0, 0)) == 0
+    # decoder glue: nothing to write, a sum without an addend, a norm weight
+    # without its output (or the reverse), a misaligned row, a negative count
+    eps = C.c_float(1e-6)
+    assert lib.lrmoe_add_rmsnorm(aligned, null, 1, null, eps, null, null, null) == -1
+    assert lib.lrmoe_add_rmsnorm(aligned, null, 1, null, eps, aligned, null, null) == -1
+    assert lib.lrmoe_add_rmsnorm(aligned, null, 1, aligned, eps, null, null, null) == -1
+    assert lib.lrmoe_add_rmsnorm(aligned, null, 1, null, eps, null, aligned, null) == -1
+    assert lib.lrmoe_add_rmsnorm(C.c_void_p(8), null, 1, aligned, eps, null, aligned, null) == -1
+    assert lib.lrmoe_add_rmsnorm(aligned, null, -1, aligned, eps, null, aligned, null) == -1
+    assert lib.lrmoe_add_rmsnorm(aligned, null, 0, aligned, eps, null, aligned, null) == 0
     from lightreason_amd import _native
 
     with pytest.raises(ValueError):
