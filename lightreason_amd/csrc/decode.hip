@@ -58,7 +58,8 @@
 // n-th item step (n < 22): start, its weights in, its inputs in, end, and
 // item code (kind + 1) * 1e6 + slot * 1e3 + tile; 118 wave 0's top-8
 // extracted, 119 expert masks built, 120 slots numbered, 121 token rows
-// staged (wave 7).
+// staged (wave 7), 122 token rows staged before the router, 123 router
+// logits published (router workgroups), 124 every logit's tag seen.
 #ifdef LRMOE_TIMELINE
 __device__ unsigned long long* g_timeline;
 extern "C" int lrmoe_timeline_set(void* p) {
@@ -761,6 +762,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     if (a.router != nullptr) {
         stage_rows();
         __syncthreads();
+        TL(122, 0);
         resolve_call();
         if (early) {
             // The shared-expert A tile first_item, exactly as the item loop
@@ -804,6 +806,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
                 const uint32_t pair = static_cast<uint32_t>(P.lg[t][2 * q]) | (static_cast<uint32_t>(P.lg[t][2 * q + 1]) << 16);
                 st_agent64(a.logits + static_cast<size_t>(t) * (kExperts / 2) + (kWaves / 2) * block + q, tag_bits | pair);
             }
+            TL(123, 0);
         }
     }
 
@@ -833,6 +836,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
                 if (!block_or(fetch(), P, vote_row, wave, lane)) break;
             }
         }
+        TL(124, 0);
         lg_lo = (lw[0] & 0xffffffffull) | (lw[1] << 32);
         lg_hi = (lw[2] & 0xffffffffull) | (lw[3] << 32);
     }
