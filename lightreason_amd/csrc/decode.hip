@@ -609,8 +609,7 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     // In order of need: the caller's logits rows of this wave's tokens
     // (tokens wave and wave + 8), the 256-entry expert address table, the
     // token rows, the RMSNorm and shared-gate rows and a router workgroup's
-    // router row.  Absent rows load a valid dummy row instead, so that every
-    // path issues the same loads (exact wait counts).
+    // router row.
     const int t_lo = wave;
     const int t_hi = wave + kWaves;
     const bool has_lo = t_lo < T;
@@ -618,9 +617,11 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     const bool router_wg = a.router != nullptr && block < kRouterWgs;
     const bool logits_given = a.logits_in != nullptr;
     const uint16_t* lg_src = logits_given ? a.logits_in : a.x;
-    uint64_t lg_lo = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_lo ? t_lo : 0) * kExperts * logits_given + 4 * lane);
-    uint64_t lg_hi = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(has_hi ? t_hi : 0) * kExperts * logits_given + 4 * lane);
-    const uint4 eptr = ldg16(a.expert_ptrs + 2 * (tid & (kExperts - 1)));
+    uint64_t lg_lo = 0ull, lg_hi = 0ull;
+    if (logits_given && has_lo) lg_lo = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(t_lo) * kExperts + 4 * lane);
+    if (logits_given && has_hi) lg_hi = *reinterpret_cast<const uint64_t*>(lg_src + static_cast<size_t>(t_hi) * kExperts + 4 * lane);
+    uint4 eptr = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < kExperts) eptr = ldg16(a.expert_ptrs + 2 * tid);
     // Codec table row of expert tid (tid 256: the shared expert).
     uint4 ec[5];
 #pragma unroll
@@ -629,30 +630,46 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
 #pragma unroll
         for (int i = 0; i < 5; ++i) ec[i] = ldg16(a.codec + kCodecTableColumns * tid + 2 * i);
     }
-    // (a dummy load reads the first 64 bytes of x on every lane: the same
-    // lines for the whole workgroup, not a row per wave)
-    const uint32_t xr_lo = has_lo ? static_cast<uint32_t>((t_lo * kHidden + 32 * lane) * 2) : 0u;
-    const uint32_t xr_hi = has_hi ? static_cast<uint32_t>((t_hi * kHidden + 32 * lane) * 2) : 0u;
-    const uint16_t* nr = a.norm != nullptr ? a.norm + 32 * lane : a.x;
-    const uint16_t* gr = a.shared_expert_gate != nullptr ? a.shared_expert_gate + 32 * lane : a.x;
-    const uint16_t* rr = router_wg ? a.router + static_cast<size_t>(kWaves * block + wave) * kHidden + 32 * lane : a.x;
+    // Rows are loaded only by the waves that use them (wave-uniform
+    // branches): the norm and shared-gate rows by waves with a token, a
+    // router row by the router workgroups.  Every load instruction costs
+    // the CU's load path 1 KiB however few distinct bytes it reads, and the
+    // prologue's loads are all issued before the first result is needed.
+    const bool token_wave = has_lo || has_hi;
+    const uint32_t xr_lo = static_cast<uint32_t>((t_lo * kHidden + 32 * lane) * 2);
+    const uint32_t xr_hi = static_cast<uint32_t>((t_hi * kHidden + 32 * lane) * 2);
     uint4 x_lo[4], x_hi[4], w_norm[4], w_sg[4], w_router[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w_norm[i] = ldg16(nr + 8 * i);
+    for (int i = 0; i < 4; ++i) {
+        x_lo[i] = x_hi[i] = w_norm[i] = w_sg[i] = w_router[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (token_wave && a.norm != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w_sg[i] = ldg16(gr + 8 * i);
+        for (int i = 0; i < 4; ++i) w_norm[i] = ldg16(a.norm + 32 * lane + 8 * i);
+    }
+    if (token_wave && a.shared_expert_gate != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
+        for (int i = 0; i < 4; ++i) w_sg[i] = ldg16(a.shared_expert_gate + 32 * lane + 8 * i);
+    }
+    if (router_wg) {
+        const uint16_t* rr = a.router + static_cast<size_t>(kWaves * block + wave) * kHidden + 32 * lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w_router[i] = ldg16(rr + 8 * i);
+    }
     if (tid < kExperts) P.tokmask[tid] = 0u;
     if (tid == 0) P.status = 0;
     // The layer input and the counters are touched only once the input is
     // complete (a chain waits for the previous layer here; the loads above
     // are already in flight).
     wait_input();
+    if (has_lo) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x_lo[i] = ld_row16<kChained>(a.x, xr_lo + 16 * i);
+        for (int i = 0; i < 4; ++i) x_lo[i] = ld_row16<kChained>(a.x, xr_lo + 16 * i);
+    }
+    if (has_hi) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x_hi[i] = ld_row16<kChained>(a.x, xr_hi + 16 * i);
+        for (int i = 0; i < 4; ++i) x_hi[i] = ld_row16<kChained>(a.x, xr_hi + 16 * i);
+    }
     // A workgroup's first item: item (block - 32) mod G with a router (the
     // router workgroups take items last), else item block.
     const int first_item = (block - (a.router != nullptr ? kRouterWgs : 0) + G) % G;
@@ -670,10 +687,26 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     // brings that tile's 1,024 lines of 128 bytes into its L2 during
     // routing, one 4-byte load per line (two lines per lane), so that the
     // tile arrives from L2 when it is issued after top-8, ahead of the first
-    // items of the other workgroups; the others load two words of token row
-    // 0.  Issued after the token rows, so that no wait for those covers
-    // them; consumed just before the first item's loads.
+    // items of the other workgroups; the others load two words of the expert
+    // table (read-only, cached).  Issued after the token rows, so that no
+    // wait for those covers them, and after a chain's input wait, whose
+    // poll would otherwise wait for them; consumed just before the first
+    // item's loads.  (The warming loads are issued on every path, so that
+    // the early tile's loads never reuse their registers: that reuse made
+    // the compiler wait for every entry load before issuing the tile.)
     uint32_t warm0 = 0u, warm1 = 0u;
+    {
+        const bool warm = !early && a.sh_down != nullptr && first_item < kATiles;
+        const int r = (2 * tid) / 32;     // row of the tile: 16 gate rows, then 16 up rows
+        const int line = (2 * tid) % 32;  // first of the lane's two lines of that row
+        const uint16_t* row = (r < 16 ? a.sh_gate + static_cast<size_t>(16 * first_item + r) * kHidden
+                                      : a.sh_up + static_cast<size_t>(16 * first_item + r - 16) * kHidden);
+        const uint16_t* table = reinterpret_cast<const uint16_t*>(a.expert_ptrs);
+        const uint16_t* w0 = warm ? row + 64 * line : table;
+        const uint16_t* w1 = warm ? row + 64 * (line + 1) : table + 2;
+        warm0 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w0));
+        warm1 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w1));
+    }
     if (early) {
         SlotInfo sh;
         sh.gate = a.sh_gate;
@@ -681,16 +714,6 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
         const uint16_t* rows[4];
         item_rows(sh, Item{0, 0, first_item}, wave, lane, rows);
         issue_rows(rows, b0);
-    } else {
-        const bool warm = a.sh_down != nullptr && first_item < kATiles;
-        const int r = (2 * tid) / 32;     // row of the tile: 16 gate rows, then 16 up rows
-        const int line = (2 * tid) % 32;  // first of the lane's two lines of that row
-        const uint16_t* row = (r < 16 ? a.sh_gate + static_cast<size_t>(16 * first_item + r) * kHidden
-                                      : a.sh_up + static_cast<size_t>(16 * first_item + r - 16) * kHidden);
-        const uint16_t* w0 = warm ? row + 64 * line : a.x;
-        const uint16_t* w1 = warm ? row + 64 * (line + 1) : a.x + 2;
-        warm0 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w0));
-        warm1 = *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(reinterpret_cast<uintptr_t>(w1));
     }
     // This call's number, tag and counter set, resolved where they are first
     // needed: before the router's logits are published, or (with caller
