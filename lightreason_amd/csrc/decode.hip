@@ -59,7 +59,8 @@
 // item code (kind + 1) * 1e6 + slot * 1e3 + tile; 118 wave 0's top-8
 // extracted, 119 expert masks built, 120 slots numbered, 121 token rows
 // staged (wave 7), 122 token rows staged before the router, 123 router
-// logits published (router workgroups), 124 every logit's tag seen.
+// logits published (router workgroups), 124 every logit's tag seen, 125 the
+// first half of the first item's loads issued (wave 0).
 #ifdef LRMOE_TIMELINE
 __device__ unsigned long long* g_timeline;
 extern "C" int lrmoe_timeline_set(void* p) {
@@ -914,6 +915,34 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     __syncthreads();
 
     TL(1, 0);
+    // ---- the first item's weights, first half (raw kernel) ----
+    // A workgroup's first item is an A tile of slot s < 9: the shared
+    // expert (slot 0) or token 0's route of rank s - 1 (slots are numbered
+    // in discovery order), known once top-8 is done.  Half of its loads
+    // are issued here, before the rest of the plan (64 KiB per CU, which the
+    // load path accepts without stalling the waves); the other half after
+    // it.  With bad routes no item runs and these loads are only reads of
+    // expert 0's rows.
+    int cur = early ? first_item + G : first_item;
+    const uint16_t* first_rows[4] = {a.x, a.x, a.x, a.x};
+    if constexpr (!kCodec) {
+        const int slot = (a.sh_down != nullptr ? 0 : 1) + cur / kATiles;
+        SlotInfo s0;
+        s0.gate = a.sh_gate;
+        s0.up = a.sh_up;
+        if (slot > 0) {
+            const uint4 pe = P.eptr[P.ids[0][slot - 1]];
+            const uint16_t* gate_up = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(pe.x) |
+                                                                        (static_cast<uintptr_t>(pe.y) << 32));
+            s0.gate = gate_up;
+            s0.up = gate_up + static_cast<size_t>(kInner) * kHidden;
+        }
+        item_rows(s0, Item{0, slot, cur % kATiles}, wave, lane, first_rows);
+        asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
+#pragma unroll
+        for (int i = 0; i < kLoads / 2; ++i) b0[i] = ldg16_nt(first_rows[i & 3] + 128 * (i >> 2));
+        TL(125, 0);
+    }
     // Prefetch target of an item without weights (C items): 1 KiB of token
     // row 0, in cache after the first read.
     const uint16_t* const idle_rows = a.x + 8 * (lane >> 4);
@@ -1122,15 +1151,19 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
 
     if (a.router == nullptr) resolve_call();
 
-    // ---- the first item's weights ----
+    // ---- the first item's weights (the codec kernel), or their second half ----
     // Issued as soon as the slots are numbered; the first step then issues
     // the second item's at once, so that two items are in flight from the
     // start.  The token rows (with caller logits) and the combine order are
     // worked out while they stream.
-    int cur = early ? first_item + G : first_item;
-    asm volatile("" ::"v"(warm0), "v"(warm1));  // the warming loads are complete
     uint32_t dec = 0u;  // tile choice of the item being run (the first is read raw)
-    issue_item(item_at(cur, total, n_slots, first_slot), b0, 0u);
+    if constexpr (!kCodec) {
+        // the same rows as the plan's slot gives
+#pragma unroll
+        for (int i = kLoads / 2; i < kLoads; ++i) b0[i] = ldg16_nt(first_rows[i & 3] + 128 * (i >> 2));
+    } else {
+        issue_item(item_at(cur, total, n_slots, first_slot), b0, 0u);
+    }
     TL(2, 0);
     TL(5, 7 * kWave);
     if (a.router == nullptr) {

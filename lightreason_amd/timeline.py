@@ -33,7 +33,7 @@ from . import _native
 WORDS = 128  # stamps per workgroup (kTimelineWords)
 PHASES = (("entry", 0), ("counters", 7), ("top8_w0", 118), ("top8", 1), ("first_issued_w0", 2),
           ("first_issued_w7", 5), ("rows_staged", 6), ("rows_staged_w7", 121), ("masks", 119), ("slots", 120),
-          ("plan", 3), ("router_rows", 122), ("published", 123), ("logits_seen", 124), ("end", 4))
+          ("plan", 3), ("router_rows", 122), ("published", 123), ("logits_seen", 124), ("half1_w0", 125), ("end", 4))
 STEPS = 22  # item steps stamped (words 8 + 5 n .. 8 + 5 n + 4; words 118 and up hold phases)
 
 
