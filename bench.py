@@ -787,9 +787,11 @@ def bench_attention(device, seed: int, passes: int, skip_cpu: bool) -> dict:
         kernel_us = total / max(n, 1) * 1e3
         nbytes = attn_bytes(T, L)
         gbs = nbytes / (ms * 1e-3) / 1e9
+        # (the event pair spans an eager step: from the first kernel's start
+        # to the last one's end, host launch gaps between them included)
         out[f"t{T}"] = dict(us_per_layer=round(ms * 1e3, 2), context=L, algorithmic_bytes=nbytes, gbs=round(gbs, 1),
-                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), kernels_us=round(kernel_us, 2),
-                            kernels_gbs=round(nbytes / (kernel_us * 1e-6) / 1e9, 1), parity=gate)
+                            frac_hbm=round(gbs / HBM_PEAK_GBS, 4), eager_step_span_us=round(kernel_us, 2),
+                            parity=gate)
     if not skip_cpu:
         out["cpu_reference"] = attn_cpu_leg(layers[0], caches[0], cos_all[:1], sin_all[:1], L)
     return out
@@ -1139,8 +1141,16 @@ def main() -> int:
         hit = float(np.mean([(c > 0).sum() for c in idx_counts]))
         skew = float(np.mean([c.max() / c.mean() for c in idx_counts]))
         tflops = flops / (ms4 * 1e-3) / 1e12
+        # The roofline of this shape: every hit expert's weights and the
+        # shared expert's read once, the token rows in and out once; the
+        # ceiling is min(dense bf16 MFMA peak, HBM peak x FLOP per byte).
+        c4_bytes = (hit + 1) * EXPERT_BYTES + 2 * T * HIDDEN * 2
+        intensity = flops / c4_bytes
+        ceiling = min(BF16_PEAK_TFLOPS, HBM_PEAK_GBS * 1e9 * intensity / 1e12)
         configs["c4_prefill_t2048"] = dict(ms_per_layer=round(ms4, 3), tflops=round(tflops, 2) if gate4["ok"] else None,
                                            frac_mfma=round(tflops / BF16_PEAK_TFLOPS, 4) if gate4["ok"] else None,
+                                           flop_per_byte=round(intensity, 1), ceiling_tflops=round(ceiling, 1),
+                                           frac_of_ceiling=round(tflops / ceiling, 4) if gate4["ok"] else None,
                                            experts_hit=hit, max_over_mean=round(skew, 2), bias_sigma=sigma_bias,
                                            flop_per_layer=flops, parity=gate4, status=statuses["c4"],
                                            note="router GEMV excluded (logits given)")
