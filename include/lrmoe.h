@@ -451,6 +451,20 @@ int lrmoe_attn_decode(const uint16_t *hidden, int tokens, const uint16_t *q_proj
                       int capacity, int length, uint16_t *out, void *workspace, size_t workspace_bytes,
                       void *stream);
 
+/* lrmoe_attn_decode with the cached length read on the device from
+ * *length (int32) when the launches run, so that one captured graph serves
+ * a cache that grows between replays (a verify loop: the reference's
+ * dflash_probe.py:111-148 advances the cache after every accepted block).
+ * The positions are split into chunks sized for `capacity`; chunks past
+ * *length + tokens do no work.  *length must lie in [0, capacity - tokens]:
+ * a value outside it is clamped for every cache access and the call's out
+ * rows are NaN.  Host-side argument checks as lrmoe_attn_decode's. */
+int lrmoe_attn_decode_at(const uint16_t *hidden, int tokens, const uint16_t *q_proj, const uint16_t *k_proj,
+                         const uint16_t *v_proj, const uint16_t *o_proj, const uint16_t *q_norm,
+                         const uint16_t *k_norm, float eps, const uint16_t *cos, const uint16_t *sin,
+                         uint16_t *k_cache, uint16_t *v_cache, int capacity, const int32_t *length, uint16_t *out,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

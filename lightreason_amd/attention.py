@@ -98,13 +98,19 @@ class AttentionDecode:
                    eps=attn.q_norm.eps)
 
     def step(self, hidden: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
-             v_cache: torch.Tensor, length: int, *, out: torch.Tensor | None = None) -> torch.Tensor:
+             v_cache: torch.Tensor, length, *, out: torch.Tensor | None = None) -> torch.Tensor:
         """One cached forward of T = hidden.shape[0] (1..16) tokens after
         `length` cached positions: hidden [T, 2048] bf16; cos, sin [T, 64]
         bf16 (the model's position embeddings of the new positions);
         k_cache, v_cache [2, capacity, 256] bf16 (normed, rotated keys and
         values), into which positions length .. length + T - 1 are written.
-        Returns out [T, 2048] bf16."""
+        Returns out [T, 2048] bf16.
+
+        ``length`` is an int, or a one-element int32 tensor on the device
+        that the kernels read when they run (``lrmoe_attn_decode_at``): a
+        captured call then serves a cache that grows between replays.  The
+        caller keeps its value in [0, capacity - T]; outside that range the
+        output rows are NaN."""
         dev = self.device
         T = hidden.shape[0] if hidden.dim() == 2 else -1
         if not 1 <= T <= MAX_TOKENS:
@@ -115,16 +121,23 @@ class AttentionDecode:
         capacity = k_cache.shape[1] if k_cache.dim() == 3 else -1
         _require(k_cache, "k_cache", (torch.bfloat16,), (KV_HEADS, capacity, HEAD_DIM), dev)
         _require(v_cache, "v_cache", (torch.bfloat16,), (KV_HEADS, capacity, HEAD_DIM), dev)
-        if not 0 <= length <= capacity - T:
+        on_device = isinstance(length, torch.Tensor)
+        if on_device:
+            _require(length, "length", (torch.int32,), (1,), dev)
+            if capacity < T:
+                raise ValueError(f"{T} tokens exceed the cache capacity {capacity}")
+        elif not 0 <= length <= capacity - T:
             raise ValueError(f"length {length} + {T} tokens exceeds the cache capacity {capacity}")
         if out is None:
             out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev)
         _require(out, "out", (torch.bfloat16,), (T, HIDDEN), dev)
         ws = _workspace(dev)
-        _native.call("lrmoe_attn_decode", hidden.data_ptr(), T, self.q_proj.data_ptr(), self.k_proj.data_ptr(),
-                     self.v_proj.data_ptr(), self.o_proj.data_ptr(), self.q_norm.data_ptr(), self.k_norm.data_ptr(),
-                     self.eps, cos.data_ptr(), sin.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity,
-                     int(length), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+        _native.call("lrmoe_attn_decode_at" if on_device else "lrmoe_attn_decode", hidden.data_ptr(), T,
+                     self.q_proj.data_ptr(), self.k_proj.data_ptr(), self.v_proj.data_ptr(), self.o_proj.data_ptr(),
+                     self.q_norm.data_ptr(), self.k_norm.data_ptr(), self.eps, cos.data_ptr(), sin.data_ptr(),
+                     k_cache.data_ptr(), v_cache.data_ptr(), capacity,
+                     length.data_ptr() if on_device else int(length), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                     _stream(dev))
         return out
 
 

@@ -567,15 +567,19 @@ size_t lrmoe_attn_workspace_bytes(int tokens) {
     return lrmoe::attn_workspace_bytes(tokens);
 }
 
-int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
-                      const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm,
-                      float eps, const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
-                      int capacity, int length, uint16_t* out, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+// Both attention entry points: `length_dev` null runs the call at `length`
+// (checked here); otherwise the kernels read the length from length_dev and
+// the chunks cover `capacity`.
+static int attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
+                const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm,
+                float eps, const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
+                int capacity, int length, const int32_t* length_dev, uint16_t* out, void* workspace,
+                size_t workspace_bytes, void* stream) {
     if (tokens < 0 || tokens > lrmoe::kAttnMaxTokens || length < 0 || capacity < 1 || capacity > (1 << 22) ||
         length > capacity - tokens)
         return LRMOE_E_ARG;
     if (tokens == 0) return LRMOE_OK;
+    if (length_dev != nullptr && misaligned(length_dev, 4)) return LRMOE_E_ARG;
     if (!hidden || !q_proj || !k_proj || !v_proj || !o_proj || !q_norm || !k_norm || !cos || !sin || !k_cache ||
         !v_cache || !out || !workspace)
         return LRMOE_E_ARG;
@@ -598,13 +602,34 @@ int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj
     a.v_cache = v_cache;
     a.capacity = capacity;
     a.length = length;
+    a.length_dev = length_dev;
     a.tokens = tokens;
-    a.chunk = lrmoe::attn_chunk(tokens, length + tokens);
-    a.chunks = (length + tokens + a.chunk - 1) / a.chunk;
+    const int span = length_dev != nullptr ? capacity : length + tokens;  // positions the chunks cover
+    a.chunk = lrmoe::attn_chunk(tokens, span);
+    a.chunks = (span + a.chunk - 1) / a.chunk;
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.att = w.att;
     return status_of(lrmoe::launch_attn_decode(a, hidden, q_proj, k_proj, v_proj, o_proj, out, as_stream(stream)));
+}
+
+int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
+                      const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm,
+                      float eps, const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
+                      int capacity, int length, uint16_t* out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    return attn_decode(hidden, tokens, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, eps, cos, sin, k_cache,
+                       v_cache, capacity, length, nullptr, out, workspace, workspace_bytes, stream);
+}
+
+int lrmoe_attn_decode_at(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
+                         const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm,
+                         const uint16_t* k_norm, float eps, const uint16_t* cos, const uint16_t* sin,
+                         uint16_t* k_cache, uint16_t* v_cache, int capacity, const int32_t* length, uint16_t* out,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    if (length == nullptr) return LRMOE_E_ARG;
+    return attn_decode(hidden, tokens, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, eps, cos, sin, k_cache,
+                       v_cache, capacity, 0, length, out, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

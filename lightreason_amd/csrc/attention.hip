@@ -248,8 +248,20 @@ __device__ __forceinline__ void attend_issue(uint4 (&kb)[2][2], uint4 (&vb)[2][2
     }
 }
 
-__device__ __forceinline__ uint32_t attend_range(const AttnArgs& a, int c) {
-    return static_cast<uint32_t>(min((c + 1) * a.chunk, a.length + a.tokens)) * kAtD * 2;
+// Cached positions before the call: the host's value or, for a call whose
+// launches are replayed as the cache grows, the value at length_dev (read
+// at kernel start), clamped to [0, capacity - tokens] so that no read leaves
+// the caches; for a value outside that range at_attend writes no cache row
+// and at_combine writes NaN rows.
+__device__ __forceinline__ int attn_length(const AttnArgs& a) {
+    if (a.length_dev == nullptr) return a.length;
+    const int v = *a.length_dev;
+    return v < 0 ? 0 : (v > a.capacity - a.tokens ? a.capacity - a.tokens : v);
+}
+__device__ __forceinline__ bool attn_length_bad(const AttnArgs& a) {
+    if (a.length_dev == nullptr) return false;
+    const int v = *a.length_dev;
+    return v < 0 || v > a.capacity - a.tokens;
 }
 
 // The attention partials of chunk c of key/value head g, for 8 T <= kRows
@@ -283,7 +295,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     const int T = a.tokens;
     const int R = kAtGroup * T;  // query rows r = 8 t + local head
     const int RT = (R + 15) / 16;
-    const int L = a.length;
+    const int L = attn_length(a);  // (chunks past L + T read and write nothing: empty partials)
     const int total = L + T;
     const int p0 = c * a.chunk;
     const int p1 = min(p0 + a.chunk, total);
@@ -397,7 +409,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     // (5) new positions of this chunk: keys normed and rotated, values as
     // projected, into fk / fv for this call and appended to the caches for
     // later ones (no other workgroup reads them in this call)
-    for (int p = max(p0, L) + wave; p < p1; p += kAtWaves) {
+    const int p_new = attn_length_bad(a) ? p1 : max(p0, L);  // (no cache row written for a bad length)
+    for (int p = p_new + wave; p < p1; p += kAtWaves) {
         const int t = p - L;
         const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
         const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
@@ -746,7 +759,7 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
         const float o = rbf(num / den_s);
         const float gate = bf2f((gi & 1) ? gword >> 16 : gword & 0xffffu);
         const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
-        S.out[d] = static_cast<uint16_t>(f2bf(o * sg));
+        S.out[d] = attn_length_bad(a) ? static_cast<uint16_t>(0x7fc0u) : static_cast<uint16_t>(f2bf(o * sg));
     }
     __syncthreads();
     // the row as 4-byte words

@@ -439,6 +439,7 @@ struct AttnArgs {
     uint16_t* v_cache;      // [2][capacity][256] bf16
     int capacity;
     int length;             // cached positions before the call
+    const int32_t* length_dev;  // or, when set, read on the device (a graph replayed as the cache grows)
     int tokens;
     int chunk;              // positions per chunk
     int chunks;             // chunks per key/value head (<= kAttnMaxChunks)

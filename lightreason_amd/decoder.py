@@ -20,9 +20,11 @@ HIP graph.
 hold ``length`` positions before it, the mixers' states are advanced in
 place).  ``VerifyPass(stack, widths, length)`` captures one graph per width
 over static buffers: a replay reads the block from ``hidden``, the rotary
-rows from ``cos``/``sin``, appends at positions ``length ..`` of every
-attention cache and advances every mixer state, so it is bound to the cache
-length it was captured at (the attention launch's grid depends on it).
+rows from ``cos``/``sin`` and the cache length from a device word
+(``lrmoe_attn_decode_at``), appends at positions ``length ..`` of every
+attention cache and advances every mixer state.  ``verify(..., length=n)``
+sets that word before the replay, so the same graphs serve a cache that
+grows between verify blocks.
 
 There is no CPU path: the calls raise when liblrmoe.so is missing.
 """
@@ -141,13 +143,15 @@ class DecoderStack:
         self.device = torch.device(device) if device is not None else self.layers[0].input_norm.device
         self.workspace = Workspace(self.device, DECODE_MAX_TOKENS)
 
-    def step(self, hidden: torch.Tensor, length: int, cos: torch.Tensor | None = None,
+    def step(self, hidden: torch.Tensor, length, cos: torch.Tensor | None = None,
              sin: torch.Tensor | None = None, *, buffers: StepBuffers | None = None,
              out: torch.Tensor | None = None) -> torch.Tensor:
         """One cached forward of T = hidden.shape[0] (1..16) positions after
-        ``length`` cached positions; cos, sin [T, 64] bf16 (the rotary rows of
-        the new positions) are needed when the stack has attention layers.
-        Returns the last layer's output [T, 2048] bf16 (``out`` if given)."""
+        ``length`` cached positions (an int, or a one-element int32 device
+        tensor read by the attention kernels when they run); cos, sin [T, 64]
+        bf16 (the rotary rows of the new positions) are needed when the stack
+        has attention layers.  Returns the last layer's output [T, 2048] bf16
+        (``out`` if given)."""
         T = hidden.shape[0]
         if not 1 <= T <= DECODE_MAX_TOKENS or hidden.shape != (T, HIDDEN) or hidden.dtype != torch.bfloat16:
             raise ValueError(f"hidden must be bf16 [T, {HIDDEN}] with 1 <= T <= {DECODE_MAX_TOKENS}")
@@ -184,19 +188,26 @@ class DecoderStack:
 class VerifyPass:
     """The whole decoder step captured once per width in ``widths`` (1..16)
     as one HIP graph, for verify blocks after ``length`` cached positions.
-    ``verify(hidden, cos, sin)`` copies the block in, replays the width's
+    ``verify(hidden, cos, sin, length=n)`` copies the block in, sets the
+    cache length (when given; else the last one stays), replays the width's
     graph and returns its static output (valid until the next verify of that
     width); ``buffers(width)`` gives that width's StepBuffers (per layer when
     ``trace``).  Every replay advances the mixers' states and rewrites
-    positions ``length .. length + width - 1`` of the attention caches."""
+    positions ``length .. length + width - 1`` of the attention caches.  The
+    attention steps read the length from a device word, and their positions
+    are split into chunks sized for the caches' capacity."""
 
     def __init__(self, stack: DecoderStack, widths, length: int, *, trace: bool = False):
         self.stack = stack
-        self.length = int(length)
         self.widths = sorted(set(int(w) for w in widths))
         if not self.widths or self.widths[0] < 1 or self.widths[-1] > DECODE_MAX_TOKENS:
             raise ValueError(f"verify widths must lie in 1..{DECODE_MAX_TOKENS}")
         device = stack.device
+        caps = [layer.k_cache.shape[1] for layer in stack.layers if layer.attention is not None]
+        self.capacity = min(caps) if caps else None
+        self.length_dev = torch.zeros(1, dtype=torch.int32, device=device)
+        self.length = 0
+        self.set_length(length, self.widths[-1])
         self.pool = torch.cuda.graph_pool_handle()
         self.graphs = {}
         L = len(stack.layers)
@@ -211,7 +222,7 @@ class VerifyPass:
                               buffers=StepBuffers(L, w, device, trace))
 
                 def run(static=static):
-                    stack.step(static["hidden"], self.length, static["cos"], static["sin"],
+                    stack.step(static["hidden"], self.length_dev, static["cos"], static["sin"],
                                buffers=static["buffers"], out=static["out"])
 
                 run()  # eager once: any one-time set-up happens outside the capture
@@ -221,12 +232,26 @@ class VerifyPass:
                 self.graphs[w] = (graph, static)
         torch.cuda.current_stream(device).wait_stream(capture_stream)
 
+    def set_length(self, length: int, width: int | None = None) -> None:
+        """The cache length the next replays read (checked against the
+        caches' capacity for ``width`` new positions, default the widest)."""
+        length = int(length)
+        width = self.widths[-1] if width is None else int(width)
+        if length < 0 or (self.capacity is not None and length + width > self.capacity):
+            raise ValueError(f"length {length} + {width} positions exceeds the cache capacity {self.capacity}")
+        self.length_dev.fill_(length)
+        self.length = length
+
     def verify(self, hidden: torch.Tensor, cos: torch.Tensor | None = None, sin: torch.Tensor | None = None, *,
-               check: bool = True) -> torch.Tensor:
+               length: int | None = None, check: bool = True) -> torch.Tensor:
         width = hidden.shape[0]
         entry = self.graphs.get(width)
         if entry is None:
             raise ValueError(f"no verify graph of width {width} (captured: {self.widths})")
+        if length is not None:
+            self.set_length(length, width)
+        elif self.capacity is not None and self.length + width > self.capacity:
+            raise ValueError(f"length {self.length} + {width} positions exceeds the cache capacity {self.capacity}")
         graph, static = entry
         static["hidden"].copy_(hidden)
         if cos is not None:

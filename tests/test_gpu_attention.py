@@ -151,6 +151,60 @@ def test_attn_decode_fills_the_cache_to_capacity(oracle, device, attn_case):
         bound.step(_dev(x, device), _dev(cos, device), _dev(sin, device), k_dev, v_dev, L + 1)
 
 
+@pytest.mark.parametrize("L,T", [(0, 1), (37, 3), (700, 8), (2050, 16), (5993, 1), (5984, 16)])
+def test_attn_decode_at_reads_the_length_on_the_device(oracle, device, attn_case, L, T):
+    """lrmoe_attn_decode_at (the length in device memory, chunks sized for
+    the capacity, 6000 positions): the oracle's bars at lengths from an
+    empty cache to a full one, rows past length + T untouched."""
+    w, bound = attn_case
+    what = f"attn_decode_at L={L} T={T}"
+    print(f"[case] {what}", flush=True)
+    cap = 6000
+    rng = np.random.default_rng(3000 * T + L)
+    kc = np.full((KV, cap, D), SENTINEL, dtype=np.uint16)
+    vc = np.full((KV, cap, D), SENTINEL, dtype=np.uint16)
+    kc[:, :L] = _bf(rng.normal(0, 1.0, (KV, L, D)))
+    vc[:, :L] = _bf(rng.normal(0, 1.0, (KV, L, D)))
+    x = _bf(rng.normal(0, 1.0, (T, 2048)))
+    cos, sin = _rope(T, L)
+    want, want_k, want_v = oracle.attn_decode(x, w, cos, sin, kc, vc, L)
+    k_dev, v_dev = _dev(kc, device), _dev(vc, device)
+    length = torch.tensor([L], dtype=torch.int32, device=device)
+    out = bound.step(_dev(x, device), _dev(cos, device), _dev(sin, device), k_dev, v_dev, length)
+    torch.cuda.synchronize()
+    got_k, got_v, got = _host(k_dev), _host(v_dev), _host(out)
+    np.testing.assert_array_equal(got_k[:, :L], kc[:, :L])
+    np.testing.assert_array_equal(got_v[:, :L], vc[:, :L])
+    assert np.all(got_k[:, L + T:] == SENTINEL) and np.all(got_v[:, L + T:] == SENTINEL)
+    _close_rows(got_k[:, L:L + T], want_k[:, L:L + T], f"{what} keys")
+    _close_rows(got_v[:, L:L + T], want_v[:, L:L + T], f"{what} values")
+    g, wv = _f(got).astype(np.float64), _f(want).astype(np.float64)
+    err = np.abs(g - wv).max() / np.abs(wv).max()
+    l2 = np.linalg.norm(g - wv) / np.linalg.norm(wv)
+    print(f"{what}: output max rel {err:.2e}, L2 rel {l2:.2e}", flush=True)
+    assert err <= 1e-2 and l2 <= 1e-2
+
+
+def test_attn_decode_at_bad_length_writes_nothing(device, attn_case):
+    """A device length past capacity - tokens: the output rows are NaN and
+    no cache row is written."""
+    w, bound = attn_case
+    cap, T = 300, 4
+    rng = np.random.default_rng(11)
+    kc = _bf(rng.normal(0, 1.0, (KV, cap, D)))
+    vc = _bf(rng.normal(0, 1.0, (KV, cap, D)))
+    x = _bf(rng.normal(0, 1.0, (T, 2048)))
+    cos, sin = _rope(T, cap)
+    k_dev, v_dev = _dev(kc, device), _dev(vc, device)
+    for bad in (cap - T + 1, -5):
+        length = torch.tensor([bad], dtype=torch.int32, device=device)
+        out = bound.step(_dev(x, device), _dev(cos, device), _dev(sin, device), k_dev, v_dev, length)
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all(), bad
+        np.testing.assert_array_equal(_host(k_dev), kc)
+        np.testing.assert_array_equal(_host(v_dev), vc)
+
+
 def test_attn_decode_one_block_equals_token_steps(device, attn_case):
     """A block of 8 tokens against the same tokens one at a time (causal
     masking inside the block): the caches agree exactly (same kernels, same

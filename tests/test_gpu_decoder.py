@@ -5,7 +5,9 @@ composition on an MI355X.
 
 Workload: a 4-layer stack in the 35B pattern (layers 0-2 Gated DeltaNet,
 layer 3 full attention; seeded weights, fp32 recurrent states, 300 cached
-positions), widths 1, 5 and 16, each replayed twice with a new block.
+positions in caches of 364), widths 1, 5 and 16, each replayed twice with a
+new block, then at two longer cache lengths from the same graphs (the
+attention reads the length from a device word).
 
 Bar, per replay and layer l, the oracle given the layer's own device input:
   - the normed rows equal oracle.rmsnorm bit for bit;
@@ -19,7 +21,10 @@ Bar, per replay and layer l, the oracle given the layer's own device input:
   - the MoE block's routes equal the oracle's bit for bit and its output is
     within helpers.assert_layer_close;
 and the replay's output, routes and final states equal an eager
-DecoderStack.step from the same states bit for bit."""
+DecoderStack.step from the same states bit for bit (the graphs' attention
+chunks are sized for the capacity and the eager step's for the length: the
+chunk size is the same here, and the graphs' extra chunks are empty, which
+adds exact zeros to the merge)."""
 
 from __future__ import annotations
 
@@ -33,6 +38,7 @@ pytestmark = pytest.mark.gpu
 
 LAYERS = 4
 CONTEXT = 300
+CAPACITY = CONTEXT + 64
 WIDTHS = (1, 5, 16)
 MIXER_FIELDS = ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "conv1d", "A_log", "dt_bias", "norm", "out_proj")
 ATTN_FIELDS = ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
@@ -43,7 +49,7 @@ def decoder(device):
     from lightreason_amd.decoder import VerifyPass
     from lightreason_amd.synthetic import SyntheticDecoder
 
-    model = SyntheticDecoder(LAYERS, device, seed=4321, context=CONTEXT)
+    model = SyntheticDecoder(LAYERS, device, seed=4321, context=CONTEXT, capacity=CAPACITY)
     vp = VerifyPass(model.stack, WIDTHS, CONTEXT, trace=True)
     torch.cuda.synchronize()
     host = [HostExperts(model.moe.bank, l) for l in range(LAYERS)]
@@ -164,7 +170,49 @@ def test_verify_pass_against_oracle(decoder, oracle, device, width):
         np.testing.assert_array_equal(to_u16(out), h_in)
 
 
+@pytest.mark.parametrize("width", WIDTHS)
+def test_verify_pass_follows_the_cache_length(decoder, oracle, width):
+    """The graphs captured at CONTEXT replayed at two longer cache lengths
+    (a verify loop's cache grows between blocks): output and states equal
+    the eager step at that length bit for bit, and the attention layer's
+    output and appended rows meet the oracle at that length."""
+    model, vp, _, weights = decoder
+    eps = model.layers[0].eps
+    for length in (CONTEXT + width + 3, CAPACITY - 24):
+        what = f"decoder width {width} at length {length}"
+        print(f"[case] {what}", flush=True)
+        x = model.hidden(width, step=8000 + 10 * width + length)
+        cos, sin = model.rope(width, length)
+        before = _snapshot(model)
+        out = vp.verify(x, cos, sin, length=length).clone()
+        buf = vp.buffers(width)
+        after = _snapshot(model)
+        _restore(model, before)
+        eager = model.stack.step(x, length, cos, sin)
+        torch.cuda.synchronize()
+        assert torch.equal(eager.view(torch.int16), out.view(torch.int16)), f"{what}: graph != eager"
+        for (a, b), (c, d) in zip(_snapshot(model), after):
+            assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                               c.view(torch.int16) if c.dtype == torch.bfloat16 else c)
+            assert torch.equal(b.view(torch.int16) if b.dtype == torch.bfloat16 else b,
+                               d.view(torch.int16) if d.dtype == torch.bfloat16 else d)
+        _restore(model, after)
+        l = LAYERS - 1  # the attention layer
+        kc0, vc0 = before[l]
+        n = to_u16(buf.n[l])
+        want, want_k, want_v = oracle.attn_decode(n, weights[l], to_u16(cos), to_u16(sin), to_u16(kc0),
+                                                  to_u16(vc0), length, eps=eps)
+        assert_close_bf16(to_u16(buf.mix[l]), want, what=what + " attention")
+        kc1, vc1 = after[l]
+        new = slice(length, length + width)
+        _rows_close(to_u16(kc1)[:, new], want_k[:, new], what + " appended keys")
+        _rows_close(to_u16(vc1)[:, new], want_v[:, new], what + " appended values")
+    vp.set_length(CONTEXT)
+
+
 def test_verify_pass_rejects_unknown_width(decoder):
     model, vp, _, _ = decoder
     with pytest.raises(ValueError, match="no verify graph"):
         vp.verify(model.hidden(3, step=1))
+    with pytest.raises(ValueError, match="capacity"):
+        vp.verify(model.hidden(16, step=1), length=CAPACITY - 15)

@@ -109,6 +109,12 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_attn_decode(null, 1, *args(1, 100, 0, big)[2:]) == -1
     assert lib.lrmoe_attn_decode(*args(1, 100, 0, 8)) == -2
     assert lib.lrmoe_attn_decode(*args(0, 100, 0, 0)) == 0
+    # the device-length variant: no length pointer, or one not 4-byte aligned
+    args_at = lambda tokens, cap, length: (w8, tokens, w8, w8, w8, w8, w8, w8, C.c_float(1e-6), w8, w8, w8, w8,
+                                           cap, length, w8, aligned, big, null)
+    assert lib.lrmoe_attn_decode_at(*args_at(4, 100, null)) == -1
+    assert lib.lrmoe_attn_decode_at(*args_at(4, 100, C.c_void_p(258))) == -1
+    assert lib.lrmoe_attn_decode_at(*args_at(17, 100, aligned)) == -1
     # decoder glue: nothing to write, a sum without an addend, a norm weight
     # without its output (or the reverse), a misaligned row, a negative count
     eps = C.c_float(1e-6)
