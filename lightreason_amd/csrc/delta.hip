@@ -580,23 +580,9 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         const int vw = is_v ? vi & 3 : 0;
         const int vt = is_v ? vi >> 2 : 0;
         const uint64_t v4 = ld_agent64(a.act + static_cast<int64_t>(vt) * kDnConv + 2 * kDnKey + rh * kDnWidth + rc0 + 4 * vw);
-        // behind them: in_proj unit 2 (z rows 16 b .. 16 b + 15) and out_proj
-        // rows 8 b .. 8 b + 7 (phase D's A operands)
-        {
-            const uint16_t* row0 = mix_row_ptr(a, kMixInRows * v2 + 2 * wave) + 8 * lane;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) w2[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
-            // (lanes t >= 8 load row 8 b too: MFMA output rows 8-15, which
-            // they feed, are dropped)
-            const uint16_t* wrow = a.w_out + static_cast<int64_t>(kMixRows * b + (live ? t : 0)) * kDnValue + 512 * wave + 8 * g;
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wo[4 * s2 + j] = ldg16(wrow + 128 * s2 + 32 * j);
-        }
         // (taken on every path: a wait inside only one branch would leave
         // the registers pending at the merge, and the compiler then waits
-        // for every load in flight before the token loop)
+        // for every load in flight)
         asm volatile("" ::"v"(qraw.x), "v"(kraw.x), "v"(v4));
         if (is_qk) {
             unpack8(qraw, &qs[tq][ch * 8]);
@@ -670,6 +656,24 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) state_put<BF16>(m.state, slab + static_cast<int64_t>(8 * rg + i) * kDnWidth + rc, S[i]);
+        }
+        // Then in_proj unit 2 (z rows 16 b .. 16 b + 15) and out_proj rows
+        // 8 b .. 8 b + 7 (phase D's A operands): waves 4-7 reach this point
+        // as soon as the inputs are normed and stream their rows during the
+        // token loop, the rule waves after it.  (Issued before the rule, the
+        // 32 MiB of rows every CU requests held up the rule's own input loads
+        // behind them for ~6 us.)
+        {
+            const uint16_t* row0 = mix_row_ptr(a, kMixInRows * v2 + 2 * wave) + 8 * lane;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w2[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
+            // (lanes t >= 8 load row 8 b too: MFMA output rows 8-15, which
+            // they feed, are dropped)
+            const uint16_t* wrow = a.w_out + static_cast<int64_t>(kMixRows * b + (live ? t : 0)) * kDnValue + 512 * wave + 8 * g;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wo[4 * s2 + j] = ldg16(wrow + 128 * s2 + 32 * j);
         }
         MX_TL(14);
         __syncthreads();
