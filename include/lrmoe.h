@@ -401,7 +401,7 @@ size_t lrmoe_delta_workspace_bytes(int tokens);
  * [tokens][2048] bf16.  Workspace of lrmoe_delta_workspace_bytes(tokens),
  * 256-byte aligned, zeroed once after allocation (its counters never need
  * a reset), used by one stream at a time.  One persistent launch of 256
- * workgroups, one per CU, which wait for each other at two grid barriers:
+ * workgroups, one per CU, which wait for flags that other workgroups set:
  * all must be resident (a device with fewer than 256 CUs gets
  * hipErrorNotSupported; a kernel running on another stream can keep some
  * off the GPU).  Waits are bounded (50 ms); on expiry the call still ends,

@@ -260,13 +260,13 @@ hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
 
 // ---- the mixer step in one persistent launch (dn_mixer) ---------------------
 //
-// 256 workgroups of 8 waves, one per CU, all resident (the grid barriers
-// rely on it).  The first barrier waits only for what the rule needs (q, k,
-// v, beta, G); the rest of the workgroup's HBM stream (in_proj's z unit and
-// out_proj's rows) is requested behind the rule's inputs and lands while the
+// 256 workgroups of 8 waves, one per CU, all resident (the workgroups wait
+// for each other's flags).  The rule waits only for the rows it reads (q, k
+// and v); the rest of the workgroup's HBM stream (in_proj's z unit and
+// out_proj's rows) is requested after the rule's inputs and lands while the
 // rule runs:
 //
-//   start    A_log and dt_bias, the barrier counter, the rule's state slab,
+//   start    A_log and dt_bias, the head's counter, the rule's state slab,
 //            the token rows, then in_proj units b and b + 256 (q, k and v
 //            rows: 768 units of 16 rows in all, 128 KiB per CU), every load
 //            unconditional (clamped dummy addresses where a lane needs
@@ -279,23 +279,30 @@ hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
 //            conv + SiLU and the conv-state update, written with
 //            agent-scope stores; into unit 0's registers, head b / 8's
 //            in_proj_b and in_proj_a rows (its beta and G go to LDS: no
-//            other workgroup needs them);
-//   barrier
-//   phase B  the rule's inputs, then unit b + 512 (z) and out_proj rows
-//            8b .. 8b + 7 (A operands of phase D) requested; the rule for
-//            (head b / 8, columns 16 (b % 8) .. +15): q and k staged and
-//            l2norm'd by the workgroup, waves 0-3 four columns each
-//            (dn_rule's arithmetic); outputs through LDS to agent-scope
-//            rows; then the z unit; the last of a head's 8 workgroups to
-//            count itself in (a monotonic counter, 8 per call) forms the
-//            head's gated RMSNorm (phase C: o, z and the norm weights in
-//            one round trip);
-//   barrier
+//            other workgroup needs them); then the workgroup's "staged"
+//            flag;
+//   wait     for the staged flags of the 16 workgroups whose unit 0 holds
+//            key head (b / 16)'s q and k rows (its own unit 1 holds its v
+//            rows);
+//   phase B  the rule's inputs; the rule for (head b / 8, columns
+//            16 (b % 8) .. +15): q and k staged and l2norm'd by the
+//            workgroup, waves 0-3 four columns each (dn_rule's
+//            arithmetic); outputs through LDS to agent-scope rows; then
+//            unit b + 512 (z) and out_proj rows 8b .. 8b + 7 (A operands of
+//            phase D) requested, and the z unit; the last of a head's 8
+//            workgroups to count itself in (a monotonic counter, 8 per
+//            call) forms the head's gated RMSNorm (phase C: o, z and the
+//            norm weights in one round trip) and sets the head's "normed"
+//            flag;
+//   wait     for all 32 normed flags;
 //   phase D  out_proj rows 8b .. 8b + 7 from the registers and the normed
 //            rows.
 //
-// Barriers: one arrival counter (2 x 256 per call, never reset) and a
-// release word set by the arrival that completes a barrier, as moe_chain's.
+// Flags hold the number of the last call that set them (the head counter at
+// the start, divided by 8, plus 1), so nothing is ever reset; each sits in a
+// 128-byte line of its own and takes plain agent-scope stores, no atomics.
+// (A grid barrier on one counter serialises 256 atomics: ~4 us back to
+// back; the flags let a workgroup wait only for its producers.)
 // Waits are bounded (50 ms); on expiry the launch still ends and sets
 // LRMOE_STATUS_TIMEOUT in the status word.
 
@@ -376,7 +383,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         for (int i = 0; i < 8; ++i) w[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
         cv = load_conv(v);
     };
-    // The small inputs first -- A_log and dt_bias, the barrier counter, the
+    // The small inputs first -- A_log and dt_bias, the barrier release word, the
     // rule's state slab, the token rows -- then in_proj units 0 (q, k) and 1
     // (v).  The memory counter retires in order: waiting for a small input
     // then never waits for a unit, and unit 0 is multiplied as soon as it
@@ -386,7 +393,9 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     // the rule's inputs, after the first barrier, which would otherwise wait
     // for it.
     const uint16_t gate_raw = static_cast<uint16_t>(ldg_u16(((tid >> 5) & 1 ? a.dt_bias : a.A_log) + (tid & 31)));
-    const unsigned long long arrived = ld_agent64(m.arrive);
+    // (this call's number: each call counts 8 workgroups in on every head's
+    // counter, and none of this head's can count in 8 before this one has)
+    const unsigned long long counted = ld_agent64(m.heads + kDeltaWsStride * (b / kMixHeadGroups));
     // the rule's state: head rh, column rc, rows 8 rg .. 8 rg + 7 (waves 0-3;
     // waves 4-7 load the same words as waves 0-3 and drop them)
     const int rg = lane & 15;
@@ -413,7 +422,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     load_unit(w0, c0, v0);
     load_unit(w1, c1, v1);
     if (tid == 0) {
-        base_s = arrived / kMixGrid * kMixGrid;
+        base_s = counted / kMixHeadGroups + 1;
         timeout_s = 0;
     }
     if (tid < 2 * kDnValueHeads) gate_lds[tid >> 5][tid & 31] = bf2f(gate_raw);
@@ -539,15 +548,18 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         }
     }
 
-    auto grid_sync = [&](unsigned long long target) {
+    // Publish this workgroup's flag (when `flag` is not null) once its
+    // agent-scope stores are complete, then wait until the `count` flags
+    // named by `flag_of(i)` hold this call's number.
+    const unsigned long long call = base_s;
+    auto publish_wait = [&](unsigned long long* flag, int count, auto flag_of) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's agent-scope stores are complete
         __syncthreads();
-        if (tid == 0) {
-            const unsigned long long before =
-                __hip_atomic_fetch_add(m.arrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (before + 1 == target) st_agent64(m.release, target);
+        if (tid == 0 && flag != nullptr) st_agent64(flag, call);
+        if (tid < count) {
+            const unsigned long long* f = flag_of(tid);
             const uint64_t start = wall_clock64();
-            while (ld_agent64(m.release) < target) {
+            while (ld_agent64(f) < call) {
                 if (wall_clock64() - start > kMixSpinTicks) {
                     timeout_s = 1;
                     break;
@@ -557,16 +569,19 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         }
         __syncthreads();
     };
-    const unsigned long long base = base_s;
-    // q, k and v (units 0 and 1 of every workgroup) are complete; z (unit 2)
-    // is not needed before the gated norm.
+    const int kh = rh >> 1;  // value head h reads key head h / 2
+    // The rule's inputs: its own v rows (unit 1) and key head kh's q and k
+    // rows, units 8 kh .. 8 kh + 7 and 128 + 8 kh .. 128 + 8 kh + 7, which
+    // are workgroups' unit 0 of the same numbers.  z (unit 2) is not needed
+    // before the gated norm.
     MX_TL(4);
-    grid_sync(base + kMixGrid);
+    publish_wait(m.staged + kDeltaWsStride * b, 16, [&](int i) {
+        return m.staged + kDeltaWsStride * ((i < 8 ? 0 : 128) + 8 * kh + (i & 7));
+    });
     MX_TL(5);
 
     // ---- phase B: the rule for head rh, columns rc0 .. rc0 + 15 ----
     {
-        const int kh = rh >> 1;  // value head h reads key head h / 2
         // The rule's inputs, loaded by every thread (clamped to token 0: no
         // branch around loads, so that the waits below cover only them).
         const bool is_qk = tid < 16 * T;
@@ -695,7 +710,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         __syncthreads();
         if (tid == 0) {
             const unsigned long long before =
-                __hip_atomic_fetch_add(m.heads + rh, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(m.heads + kDeltaWsStride * rh, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_s = (before + 1) % kMixHeadGroups == 0;
         }
         __syncthreads();
@@ -734,7 +749,9 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     }
     MX_TL(8);
     MX_WORD(12, static_cast<unsigned long long>(last_s));
-    grid_sync(base + 2 * kMixGrid);
+    // Phase D reads every head's normed rows.
+    publish_wait(last_s ? m.normed + kDeltaWsStride * rh : nullptr, kDnValueHeads,
+                 [&](int i) { return m.normed + kDeltaWsStride * i; });
     MX_TL(9);
 
     // ---- phase D: out_proj rows 8b .. 8b + 7 ----
@@ -790,9 +807,9 @@ DeltaWorkspace carve_delta(void* base, int tokens) {
     uint8_t* p = static_cast<uint8_t*>(base);
     // control block (fixed offsets whatever the token count; zero at allocation)
     w.status = reinterpret_cast<int32_t*>(p + kDeltaWsStatus);
-    w.arrive = reinterpret_cast<unsigned long long*>(p + kDeltaWsArrive);
-    w.release = reinterpret_cast<unsigned long long*>(p + kDeltaWsRelease);
     w.heads = reinterpret_cast<unsigned long long*>(p + kDeltaWsHeads);
+    w.normed = reinterpret_cast<unsigned long long*>(p + kDeltaWsNormed);
+    w.staged = reinterpret_cast<unsigned long long*>(p + kDeltaWsStaged);
     size_t off = kDeltaWsControl;
     auto take = [&](size_t bytes) {
         const size_t at = off;
@@ -834,9 +851,9 @@ hipError_t launch_delta_mixer(DnProjectArgs p, void* state, bool state_bf16, voi
     m.o = w.o;
     m.core = w.core;
     m.status = w.status;
-    m.arrive = w.arrive;
-    m.release = w.release;
     m.heads = w.heads;
+    m.normed = w.normed;
+    m.staged = w.staged;
     const StageEvents ev = timing_events(kStageDeltaMixer);
     if (state_bf16) {
         LRMOE_LAUNCH(dn_mixer<true>, dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);

@@ -391,9 +391,9 @@ struct DnRuleArgs {
 
 struct DeltaWorkspace {
     int32_t* status;               // LRMOE_STATUS_TIMEOUT when a wait expired
-    unsigned long long* arrive;    // grid-barrier arrivals (2 x 256 per call, never reset)
-    unsigned long long* release;   // the arrival count the last completed barrier reached
     unsigned long long* heads;     // [32] rule workgroups done per head (8 per call, never reset)
+    unsigned long long* normed;    // [32] per head: number of the last call whose normed rows are stored
+    unsigned long long* staged;    // [256] per workgroup: number of the last call whose q, k, v rows are stored
     uint16_t* act;
     uint16_t* z;
     uint16_t* beta;
@@ -403,13 +403,16 @@ struct DeltaWorkspace {
     size_t bytes;
 };
 
-// Offsets of the mixer workspace's control block (each counter in its own
-// 256-byte block).
+// Offsets of the mixer workspace's control block: the status word, the 32
+// per-head counters, the 32 per-head "normed rows stored" flags and the 256
+// per-workgroup "q, k and v rows stored" flags, each counter or flag in its
+// own 128-byte line.
 constexpr size_t kDeltaWsStatus = 0;
-constexpr size_t kDeltaWsArrive = 256;
-constexpr size_t kDeltaWsRelease = 512;
-constexpr size_t kDeltaWsHeads = 768;
-constexpr size_t kDeltaWsControl = 1024;
+constexpr size_t kDeltaWsHeads = 1024;
+constexpr size_t kDeltaWsNormed = 5120;
+constexpr size_t kDeltaWsStaged = 9216;
+constexpr size_t kDeltaWsStride = 16;  // u64 words between counters or flags
+constexpr size_t kDeltaWsControl = 41984;
 
 struct DnMixerArgs {
     DnProjectArgs p;
@@ -418,9 +421,9 @@ struct DnMixerArgs {
     uint16_t* o;
     uint16_t* core;
     int32_t* status;
-    unsigned long long* arrive;
-    unsigned long long* release;
     unsigned long long* heads;
+    unsigned long long* normed;
+    unsigned long long* staged;
 };
 
 constexpr int kDeltaMaxTokens = 16;
