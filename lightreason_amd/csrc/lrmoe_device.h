@@ -382,37 +382,6 @@ __device__ __forceinline__ uint32_t ld_agent32(const void* p) {
     return __hip_atomic_load(as_g32(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Grid barriers in two levels.  Workgroup b counts itself in on group
-// counter b % 32 (its members b, b + 32, ... all run on one XCD); the
-// arrival that completes a group counts the group in on the global counter;
-// the arrival that completes that stores the barrier's number in the release
-// word, which every workgroup polls.  Atomics on one address serialise: 256
-// of them on one counter make a barrier cost ~4 us back to back on MI355X,
-// 32 counters of 8 plus one of 32 ~1.6 us.  Nothing is ever reset: barrier
-// number e (counted from 1 over every launch on the same control words) is
-// complete when the release word reads e, and a launch takes its first
-// number from the release word at its start (no barrier of its own can
-// complete before every one of its workgroups has arrived).
-constexpr int kBarrierGroups = 32;
-constexpr int kBarrierStride = 16;  // u64 words between group counters (128 bytes)
-
-// Workgroup `b` of a grid of `grid` arrives at barrier number `e`.
-// `groups` holds kBarrierGroups counters kBarrierStride words apart.
-__device__ __forceinline__ void barrier_arrive(unsigned long long* groups, unsigned long long* global,
-                                               unsigned long long* release, int b, int grid,
-                                               unsigned long long e) {
-    const int g = b % kBarrierGroups;
-    const unsigned long long members = static_cast<unsigned long long>(
-        grid / kBarrierGroups + (g < grid % kBarrierGroups ? 1 : 0));
-    const unsigned long long groups_live = static_cast<unsigned long long>(grid < kBarrierGroups ? grid : kBarrierGroups);
-    const unsigned long long before =
-        __hip_atomic_fetch_add(as_g64(groups + kBarrierStride * g), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before + 1 == members * e) {
-        const unsigned long long done =
-            __hip_atomic_fetch_add(as_g64(global), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done + 1 == groups_live * e) st_agent64(release, e);
-    }
-}
 // 16 bytes at base + byte_offset with an agent-scope (sc1) buffer load from a
 // raw buffer of `bytes` bytes at base: a load at or past the end reads zeros
 // and touches no memory (the buffer's range check), so callers need no
