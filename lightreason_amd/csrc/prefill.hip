@@ -386,11 +386,8 @@ __global__ __launch_bounds__(kDnThreads, 1) void pf_experts(ExpertArgs a) {
     while (cur < n_gu) {
         uint32_t claimed = 0u;
         if (tid == 0) claimed = take();
-        // tile-major: the list's units take tile 0 in turn, then tile 1, ...,
-        // so the units of one expert (the shared expert's 16, a hot expert's
-        // several) stream the same weight rows at once, through one L2
-        const int u = first + cur % units;
-        const int tile = cur / units;
+        const int u = first + cur / kGuTiles;
+        const int tile = cur % kGuTiles;
         // The item's code is written out here rather than called as an
         // inlined function: that form spills registers.
         Unit w;
