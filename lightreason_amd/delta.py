@@ -96,7 +96,7 @@ def _workspace(device: torch.device) -> torch.Tensor:
     """Scratch for lrmoe_delta_mixer on the current stream of `device`
     (sized for 16 tokens, so its address never changes; one per stream, as
     calls sharing a workspace must not overlap; zeroed once, as its
-    barrier counters and status word require)."""
+    counters, flags and status word require)."""
     key = (device, _stream(device))
     ws = _WORKSPACES.get(key)
     if ws is None:
