@@ -18,14 +18,22 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm_kernel(const uint16_t* x, c
     const int t = blockIdx.x;
     const int lane = threadIdx.x;
     const size_t at = static_cast<size_t>(t) * kHidden + 32 * lane;
-    uint4 v[4], w[4];
+    // every load at once: the row, the addend and the norm weights (one
+    // round trip; dummy addresses where a pointer is null)
+    uint4 v[4], bv[4], w[4];
+    const uint16_t* add_row = add != nullptr ? add + at : x + at;
+    const uint16_t* w_row = (norm != nullptr ? norm : x) + 32 * lane;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = ldg16(x + at + 8 * i);
+    for (int i = 0; i < 4; ++i) {
+        v[i] = ldg16(x + at + 8 * i);
+        bv[i] = ldg16(add_row + 8 * i);
+        w[i] = ldg16(w_row + 8 * i);
+    }
     if (add != nullptr) {
         // bf16(x + add) elementwise, the bf16 tensor add of the residual
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint4 b = ldg16(add + at + 8 * i);
+            const uint4 b = bv[i];
             float xf[8], bf[8];
             unpack8(v[i], xf);
             unpack8(b, bf);
@@ -40,8 +48,6 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm_kernel(const uint16_t* x, c
         for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sum_out + at + 8 * i) = v[i];
     }
     if (norm == nullptr) return;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = ldg16(norm + 32 * lane + 8 * i);
     float f[32];
 #pragma unroll
     for (int i = 0; i < 4; ++i) unpack8(v[i], f + 8 * i);
