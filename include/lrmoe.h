@@ -417,6 +417,25 @@ int lrmoe_delta_mixer(const uint16_t *hidden, int tokens, const uint16_t *in_pro
                       uint16_t *conv_record, void *state_record, uint16_t *out, void *workspace,
                       size_t workspace_bytes, void *stream);
 
+/* The linear-attention half of a decoder layer in one call: [HF]
+ * Qwen3_5MoeDecoderLayer.forward 834-875 runs residual -> input_layernorm
+ * (Qwen3_5MoeRMSNorm 801-818) -> the mixer -> residual + mixer output as
+ * three torch steps; here `residual` [tokens][2048] bf16 is the layer's
+ * input, normed inside the mixer launch with input_norm [2048] (applied as
+ * 1 + w) and input_eps, bit for bit as lrmoe_add_rmsnorm would write it;
+ * out receives the mixer output as from lrmoe_delta_mixer on those normed
+ * rows, and sum_out [tokens][2048] bf16(residual + out).  norm_out, when
+ * not NULL, receives the normed rows.  sum_out may be residual itself.  No
+ * reference counterpart as one call: it saves the two glue launches per
+ * layer.  Other arguments, workspace and status as lrmoe_delta_mixer's. */
+int lrmoe_delta_mixer_step(const uint16_t *residual, int tokens, const uint16_t *input_norm, float input_eps,
+                           const uint16_t *in_proj_qkv, const uint16_t *in_proj_z, const uint16_t *in_proj_b,
+                           const uint16_t *in_proj_a, const uint16_t *conv_weight, const uint16_t *A_log,
+                           const uint16_t *dt_bias, const uint16_t *norm_weight, float eps, const uint16_t *out_proj,
+                           uint16_t *conv_state, void *state, int state_bf16, uint16_t *conv_record,
+                           void *state_record, uint16_t *out, uint16_t *sum_out, uint16_t *norm_out,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- full-attention decode (the attention before each of the 10
  * full-attention layers' MoE) ----------------------------------------------- */
 
@@ -464,6 +483,21 @@ int lrmoe_attn_decode_at(const uint16_t *hidden, int tokens, const uint16_t *q_p
                          const uint16_t *k_norm, float eps, const uint16_t *cos, const uint16_t *sin,
                          uint16_t *k_cache, uint16_t *v_cache, int capacity, const int32_t *length, uint16_t *out,
                          void *workspace, size_t workspace_bytes, void *stream);
+
+/* The full-attention half of a decoder layer in one call, as
+ * lrmoe_delta_mixer_step for the mixer: `residual` is the layer's input,
+ * normed inside the projection launch with input_norm / input_eps; out is
+ * the attention output and sum_out bf16(residual + out); norm_out, when not
+ * NULL, the normed rows.  The cache length is `length`, or *length_dev read
+ * on the device when length_dev is not NULL (lrmoe_attn_decode_at).  No
+ * reference counterpart as one call.  Other arguments and workspace as
+ * lrmoe_attn_decode's. */
+int lrmoe_attn_decode_step(const uint16_t *residual, int tokens, const uint16_t *input_norm, float input_eps,
+                           const uint16_t *q_proj, const uint16_t *k_proj, const uint16_t *v_proj,
+                           const uint16_t *o_proj, const uint16_t *q_norm, const uint16_t *k_norm, float eps,
+                           const uint16_t *cos, const uint16_t *sin, uint16_t *k_cache, uint16_t *v_cache,
+                           int capacity, int length, const int32_t *length_dev, uint16_t *out, uint16_t *sum_out,
+                           uint16_t *norm_out, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

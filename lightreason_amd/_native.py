@@ -59,11 +59,15 @@ _SIGNATURES = {
     "lrmoe_delta_rule": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "lrmoe_delta_mixer": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _I, _P, _P, _P, _P,
                            C.c_size_t, _P], _I),
+    "lrmoe_delta_mixer_step": ([_P, _I, _P, C.c_float, _P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _I,
+                                _P, _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
     "lrmoe_attn_workspace_bytes": ([_I], C.c_size_t),
     "lrmoe_attn_decode": ([_P, _I, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _I, _I, _P, _P, C.c_size_t,
                            _P], _I),
     "lrmoe_attn_decode_at": ([_P, _I, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _I, _P, _P, _P,
                               C.c_size_t, _P], _I),
+    "lrmoe_attn_decode_step": ([_P, _I, _P, C.c_float, _P, _P, _P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _I, _I,
+                                _P, _P, _P, _P, _P, C.c_size_t, _P], _I),
 }
 
 STAGE_ROUTE = 1

@@ -140,6 +140,45 @@ class AttentionDecode:
                      _stream(dev))
         return out
 
+    def layer_step(self, residual: torch.Tensor, input_norm: torch.Tensor, input_eps: float, cos: torch.Tensor,
+                   sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, length, *, out: torch.Tensor,
+                   sum_out: torch.Tensor, norm_out: torch.Tensor | None = None) -> torch.Tensor:
+        """The decoder layer's full-attention half in one call
+        (``lrmoe_attn_decode_step``): residual [T, 2048] bf16 is normed with
+        input_norm [2048] (applied as 1 + w) in the projection launch,
+        ``out`` receives the attention output and ``sum_out``
+        bf16(residual + out); ``norm_out`` (optional) the normed rows.
+        Caches and ``length`` (int or int32 [1] device tensor) as ``step``.
+        Returns sum_out."""
+        dev = self.device
+        T = residual.shape[0] if residual.dim() == 2 else -1
+        if not 1 <= T <= MAX_TOKENS:
+            raise ValueError(f"residual must be [T, {HIDDEN}] with 1 <= T <= {MAX_TOKENS}, got {tuple(residual.shape)}")
+        _require(residual, "residual", (torch.bfloat16,), (T, HIDDEN), dev)
+        _require(input_norm, "input_norm", (torch.bfloat16,), (HIDDEN,), dev)
+        _require(cos, "cos", (torch.bfloat16,), (T, ROTARY), dev)
+        _require(sin, "sin", (torch.bfloat16,), (T, ROTARY), dev)
+        capacity = k_cache.shape[1] if k_cache.dim() == 3 else -1
+        _require(k_cache, "k_cache", (torch.bfloat16,), (KV_HEADS, capacity, HEAD_DIM), dev)
+        _require(v_cache, "v_cache", (torch.bfloat16,), (KV_HEADS, capacity, HEAD_DIM), dev)
+        on_device = isinstance(length, torch.Tensor)
+        if on_device:
+            _require(length, "length", (torch.int32,), (1,), dev)
+            if capacity < T:
+                raise ValueError(f"{T} tokens exceed the cache capacity {capacity}")
+        elif not 0 <= length <= capacity - T:
+            raise ValueError(f"length {length} + {T} tokens exceeds the cache capacity {capacity}")
+        for name, t in (("out", out), ("sum_out", sum_out)) + ((("norm_out", norm_out),) if norm_out is not None else ()):
+            _require(t, name, (torch.bfloat16,), (T, HIDDEN), dev)
+        ws = _workspace(dev)
+        _native.call("lrmoe_attn_decode_step", residual.data_ptr(), T, input_norm.data_ptr(), float(input_eps),
+                     self.q_proj.data_ptr(), self.k_proj.data_ptr(), self.v_proj.data_ptr(), self.o_proj.data_ptr(),
+                     self.q_norm.data_ptr(), self.k_norm.data_ptr(), self.eps, cos.data_ptr(), sin.data_ptr(),
+                     k_cache.data_ptr(), v_cache.data_ptr(), capacity, 0 if on_device else int(length),
+                     length.data_ptr() if on_device else None, out.data_ptr(), sum_out.data_ptr(),
+                     None if norm_out is None else norm_out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+        return sum_out
+
 
 class _LayerBuffer:
     """Capacity-backed key and value rows of one cache layer: the layer's

@@ -523,12 +523,14 @@ int lrmoe_delta_rule(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
     return status_of(lrmoe::launch_delta_rule(a, key_width, state_bf16 != 0, as_stream(stream)));
 }
 
-int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_proj_qkv, const uint16_t* in_proj_z,
-                      const uint16_t* in_proj_b, const uint16_t* in_proj_a, const uint16_t* conv_weight,
-                      const uint16_t* A_log, const uint16_t* dt_bias, const uint16_t* norm_weight, float eps,
-                      const uint16_t* out_proj, uint16_t* conv_state, void* state, int state_bf16,
-                      uint16_t* conv_record, void* state_record, uint16_t* out, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+// Both mixer entry points; `glue` (the decoder layer's input norm and
+// residual add) is all null for lrmoe_delta_mixer.
+static int delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_proj_qkv, const uint16_t* in_proj_z,
+                       const uint16_t* in_proj_b, const uint16_t* in_proj_a, const uint16_t* conv_weight,
+                       const uint16_t* A_log, const uint16_t* dt_bias, const uint16_t* norm_weight, float eps,
+                       const uint16_t* out_proj, uint16_t* conv_state, void* state, int state_bf16,
+                       uint16_t* conv_record, void* state_record, uint16_t* out, const lrmoe::AttnGlue& glue,
+                       void* workspace, size_t workspace_bytes, void* stream) {
     if (tokens < 0 || tokens > lrmoe::kDeltaMaxTokens) return LRMOE_E_ARG;
     if (tokens == 0) return LRMOE_OK;
     if (!hidden || !in_proj_qkv || !in_proj_z || !in_proj_b || !in_proj_a || !conv_weight || !A_log || !dt_bias ||
@@ -558,8 +560,38 @@ int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_pro
     p.conv_record = conv_record;
     p.out = out;
     p.tokens = tokens;
+    p.in_norm = glue.in_norm;
+    p.in_eps = glue.in_eps;
+    p.norm_out = glue.norm_out;
+    p.sum_out = glue.sum_out;
     const lrmoe::DeltaWorkspace w = lrmoe::carve_delta(workspace, tokens);
     return status_of(lrmoe::launch_delta_mixer(p, state, state_bf16 != 0, state_record, w, as_stream(stream)));
+}
+
+int lrmoe_delta_mixer(const uint16_t* hidden, int tokens, const uint16_t* in_proj_qkv, const uint16_t* in_proj_z,
+                      const uint16_t* in_proj_b, const uint16_t* in_proj_a, const uint16_t* conv_weight,
+                      const uint16_t* A_log, const uint16_t* dt_bias, const uint16_t* norm_weight, float eps,
+                      const uint16_t* out_proj, uint16_t* conv_state, void* state, int state_bf16,
+                      uint16_t* conv_record, void* state_record, uint16_t* out, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    return delta_mixer(hidden, tokens, in_proj_qkv, in_proj_z, in_proj_b, in_proj_a, conv_weight, A_log, dt_bias,
+                       norm_weight, eps, out_proj, conv_state, state, state_bf16, conv_record, state_record, out,
+                       lrmoe::AttnGlue{}, workspace, workspace_bytes, stream);
+}
+
+int lrmoe_delta_mixer_step(const uint16_t* residual, int tokens, const uint16_t* input_norm, float input_eps,
+                           const uint16_t* in_proj_qkv, const uint16_t* in_proj_z, const uint16_t* in_proj_b,
+                           const uint16_t* in_proj_a, const uint16_t* conv_weight, const uint16_t* A_log,
+                           const uint16_t* dt_bias, const uint16_t* norm_weight, float eps, const uint16_t* out_proj,
+                           uint16_t* conv_state, void* state, int state_bf16, uint16_t* conv_record,
+                           void* state_record, uint16_t* out, uint16_t* sum_out, uint16_t* norm_out,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    if (tokens > 0 && (!input_norm || !sum_out)) return LRMOE_E_ARG;
+    if (misaligned(input_norm, 16) || misaligned(sum_out, 2) || misaligned(norm_out, 16)) return LRMOE_E_ARG;
+    return delta_mixer(residual, tokens, in_proj_qkv, in_proj_z, in_proj_b, in_proj_a, conv_weight, A_log, dt_bias,
+                       norm_weight, eps, out_proj, conv_state, state, state_bf16, conv_record, state_record, out,
+                       lrmoe::AttnGlue{input_norm, input_eps, norm_out, sum_out}, workspace, workspace_bytes,
+                       stream);
 }
 
 size_t lrmoe_attn_workspace_bytes(int tokens) {
@@ -573,8 +605,8 @@ size_t lrmoe_attn_workspace_bytes(int tokens) {
 static int attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
                 const uint16_t* v_proj, const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm,
                 float eps, const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
-                int capacity, int length, const int32_t* length_dev, uint16_t* out, void* workspace,
-                size_t workspace_bytes, void* stream) {
+                int capacity, int length, const int32_t* length_dev, uint16_t* out,
+                const lrmoe::AttnGlue& glue, void* workspace, size_t workspace_bytes, void* stream) {
     if (tokens < 0 || tokens > lrmoe::kAttnMaxTokens || length < 0 || capacity < 1 || capacity > (1 << 22) ||
         length > capacity - tokens)
         return LRMOE_E_ARG;
@@ -610,7 +642,8 @@ static int attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_pro
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.att = w.att;
-    return status_of(lrmoe::launch_attn_decode(a, hidden, q_proj, k_proj, v_proj, o_proj, out, as_stream(stream)));
+    return status_of(
+        lrmoe::launch_attn_decode(a, hidden, q_proj, k_proj, v_proj, o_proj, out, glue, as_stream(stream)));
 }
 
 int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
@@ -619,7 +652,7 @@ int lrmoe_attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_proj
                       int capacity, int length, uint16_t* out, void* workspace, size_t workspace_bytes,
                       void* stream) {
     return attn_decode(hidden, tokens, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, eps, cos, sin, k_cache,
-                       v_cache, capacity, length, nullptr, out, workspace, workspace_bytes, stream);
+                       v_cache, capacity, length, nullptr, out, lrmoe::AttnGlue{}, workspace, workspace_bytes, stream);
 }
 
 int lrmoe_attn_decode_at(const uint16_t* hidden, int tokens, const uint16_t* q_proj, const uint16_t* k_proj,
@@ -629,7 +662,20 @@ int lrmoe_attn_decode_at(const uint16_t* hidden, int tokens, const uint16_t* q_p
                          void* workspace, size_t workspace_bytes, void* stream) {
     if (length == nullptr) return LRMOE_E_ARG;
     return attn_decode(hidden, tokens, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, eps, cos, sin, k_cache,
-                       v_cache, capacity, 0, length, out, workspace, workspace_bytes, stream);
+                       v_cache, capacity, 0, length, out, lrmoe::AttnGlue{}, workspace, workspace_bytes, stream);
+}
+
+int lrmoe_attn_decode_step(const uint16_t* residual, int tokens, const uint16_t* input_norm, float input_eps,
+                           const uint16_t* q_proj, const uint16_t* k_proj, const uint16_t* v_proj,
+                           const uint16_t* o_proj, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                           const uint16_t* cos, const uint16_t* sin, uint16_t* k_cache, uint16_t* v_cache,
+                           int capacity, int length, const int32_t* length_dev, uint16_t* out, uint16_t* sum_out,
+                           uint16_t* norm_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (tokens > 0 && (!input_norm || !sum_out)) return LRMOE_E_ARG;
+    if (misaligned(input_norm, 16) || misaligned(sum_out, 2) || misaligned(norm_out, 16)) return LRMOE_E_ARG;
+    return attn_decode(residual, tokens, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, eps, cos, sin, k_cache,
+                       v_cache, capacity, length_dev != nullptr ? 0 : length, length_dev, out,
+                       lrmoe::AttnGlue{input_norm, input_eps, norm_out, sum_out}, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

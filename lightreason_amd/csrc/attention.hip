@@ -59,11 +59,24 @@ constexpr float kAtScale = 0.0625f;                 // 256^-0.5, exact
 
 // Rows [0, split1) come from w0, [split1, split2) from w1 (row - split1),
 // the rest from w2 (row - split2): the q/gate, k and v matrices in one grid.
-template <int kRows, int kK>
+// Fused decoder glue: with kNorm, x is the raw residual stream and its rows
+// are put through the input RMSNorm (weights `norm`, `eps`) on the way into
+// the MFMA operands, bit for bit as a separate norm would write them
+// (workgroup 0 stores them in norm_out when it is not null); with
+// kResidual, sum_out also receives bf16(residual + y).
+struct ProjectGlue {
+    const uint16_t* norm;
+    float eps;
+    uint16_t* norm_out;
+    const uint16_t* residual;
+    uint16_t* sum_out;
+};
+
+template <int kRows, int kK, bool kNorm = false, bool kResidual = false>
 __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restrict__ w0, const uint16_t* __restrict__ w1,
                                                          const uint16_t* __restrict__ w2, int split1, int split2,
                                                          const uint16_t* __restrict__ x, int tokens,
-                                                         uint16_t* __restrict__ y, int y_stride) {
+                                                         uint16_t* __restrict__ y, int y_stride, ProjectGlue glue) {
     constexpr int kRowsPerWave = kRows / kAtWaves;        // 2 or 1
     constexpr int kLoadsPerRow = 8 / kRowsPerWave;        // 4 or 8 loads of 1 KiB per wave and row
     static_assert(kK == 512 * kLoadsPerRow, "a wave streams its rows in 8 loads of 1 KiB");
@@ -89,9 +102,48 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
     const uint16_t* xrow = x + static_cast<int64_t>(t < tokens ? t : 0) * kK + kKw * wave + 8 * g;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) xb[s] = ldg16(xrow + 32 * s);
+    // the fused input norm: wave w's rows w and w + 8 in the norm's layout
+    // (lane l: elements 32 l ..), the weights of the lane's xb pieces
+    [[maybe_unused]] uint4 nrow[2][4], wn[kSteps];
+    [[maybe_unused]] uint32_t res = 0u;
+    static_assert(!kNorm || kK == kHidden, "the input norm runs over hidden rows");
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = wave + 8 * h;
+            const uint16_t* src = x + static_cast<int64_t>(r < tokens ? r : 0) * kK + 32 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nrow[h][i] = ldg16(src + 8 * i);
+        }
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) wn[s] = ldg16(glue.norm + kKw * wave + 32 * s + 8 * g);
+    }
+    if constexpr (kResidual) {
+        // output row row0 + tid / 16, token tid % 16 (clamped where none is stored)
+        const int rr = (tid >> 4) % kRows;
+        const int rt = (tid & 15) < tokens ? (tid & 15) : 0;
+        res = ldg_u16(glue.residual + static_cast<int64_t>(rt) * y_stride + row0 + rr);
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         *reinterpret_cast<uint4*>(&tile[kRowsPerWave * wave + i / kLoadsPerRow][512 * (i % kLoadsPerRow) + 8 * lane]) = wv[i];
+    if constexpr (kNorm) {
+        __shared__ float rscale[16];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float r = row_rms_scale(nrow[h], glue.eps);
+            if (lane == 0) rscale[wave + 8 * h] = r;
+        }
+        __syncthreads();
+        const float r = rscale[t < tokens ? t : 0];
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) xb[s] = rms_apply8(xb[s], wn[s], r);
+        if (blockIdx.x == 0 && glue.norm_out != nullptr && t < tokens) {
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s)
+                *reinterpret_cast<uint4*>(glue.norm_out + static_cast<int64_t>(t) * kK + kKw * wave + 32 * s + 8 * g) = xb[s];
+        }
+    }
     __syncthreads();
     // MFMA row m (rows m >= kRows repeat row m - kRows; their outputs are dropped)
     const int m = t % kRows;
@@ -108,7 +160,12 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
         float p = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kAtWaves; ++ww) p += red[ww][r][tt];
-        if (tt < tokens) y[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(f2bf(p));
+        const uint32_t o = f2bf(p);
+        if (tt < tokens) {
+            y[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(o);
+            if constexpr (kResidual)
+                glue.sum_out[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(f2bf(bf2f(res) + bf2f(o)));
+        }
     }
 }
 
@@ -817,13 +874,21 @@ AttnWorkspace carve_attn(void* base, int tokens) {
 }
 
 hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q, const uint16_t* w_k,
-                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, hipStream_t stream) {
+                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, const AttnGlue& fused,
+                              hipStream_t stream) {
     static_assert(kAtProj % 16 == 0 && kHidden % 8 == 0, "projection grids");
     const int T = a.tokens;
     const StageEvents ev = timing_events(kStageAttention);
     // q/gate, k and v rows: the three weight matrices in one grid
-    LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr, w_q, w_k,
-                 w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj);
+    const ProjectGlue in_glue{fused.in_norm, fused.in_eps, fused.norm_out, nullptr, nullptr};
+    const ProjectGlue out_glue{nullptr, 0.0f, nullptr, x, fused.sum_out};
+    if (fused.in_norm != nullptr) {
+        LRMOE_LAUNCH((at_project<16, kHidden, true, false>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start,
+                     nullptr, w_q, w_k, w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj, in_glue);
+    } else {
+        LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr,
+                     w_q, w_k, w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj, in_glue);
+    }
     if (T <= 4) {
         LRMOE_LAUNCH(at_attend<32>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
     } else {
@@ -834,8 +899,13 @@ hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q
     } else {
         LRMOE_LAUNCH(at_combine<4>, dim3(T * kAtHeads * 4), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);
     }
-    LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, w_o, w_o,
-                 kHidden, kHidden, a.att, T, out, kHidden);
+    if (fused.sum_out != nullptr) {
+        LRMOE_LAUNCH((at_project<8, kAtO, false, true>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr,
+                     ev.stop, w_o, w_o, w_o, kHidden, kHidden, a.att, T, out, kHidden, out_glue);
+    } else {
+        LRMOE_LAUNCH((at_project<8, kAtO>), dim3(kHidden / 8), dim3(kAtThreads), 0, stream, nullptr, ev.stop, w_o, w_o,
+                     w_o, kHidden, kHidden, a.att, T, out, kHidden, out_glue);
+    }
     return hipGetLastError();
 }
 

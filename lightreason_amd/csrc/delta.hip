@@ -336,7 +336,7 @@ __device__ __forceinline__ void state_put(void* base, int64_t i, float v) {
     else static_cast<float*>(base)[i] = v;
 }
 
-template <bool BF16>
+template <bool BF16, bool kNorm>
 __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     const DnProjectArgs& a = m.p;
     __shared__ __attribute__((aligned(16))) uint16_t tile[kMixInRows][kHidden + 8];  // one in_proj unit, row-major
@@ -354,6 +354,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     __shared__ unsigned long long base_s;
     __shared__ int timeout_s;
     __shared__ int last_s;
+    __shared__ float rscale[kDeltaMaxTokens];  // the fused input norm's 1 / rms per token row
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -416,6 +417,22 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) xb[4 * s + j] = ldg16(xrow + 128 * s + 32 * j);
     }
+    // The fused input RMSNorm: wave w's rows w and w + 8 in the norm's
+    // layout (lane l: elements 32 l ..), and the weights of the lane's xb
+    // pieces (rows past T load row 0)
+    [[maybe_unused]] uint4 nrow[2][4], wn[8];
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = wave + 8 * h;
+            const uint16_t* src = a.x + static_cast<int64_t>(r < T ? r : 0) * kHidden + 32 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nrow[h][i] = ldg16(src + 8 * i);
+        }
+        const uint16_t* wsrc = a.in_norm + 256 * wave + 8 * g;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wn[i] = ldg16(wsrc + 32 * i);
+    }
     uint4 w0[8], w1[8], w2[8];
     uint2 c0, c1;
     const int v0 = b, v1 = b + kMixGrid, v2 = b + 2 * kMixGrid;
@@ -430,6 +447,27 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     // in the rule's token loop, where the compiler would otherwise wait for
     // every load in flight (the z unit and the out_proj rows) before the loop.
     asm volatile("" ::"v"(S[0]), "v"(S[1]), "v"(S[2]), "v"(S[3]), "v"(S[4]), "v"(S[5]), "v"(S[6]), "v"(S[7]));
+
+    // The fused input RMSNorm (the decoder layer's input_layernorm): each
+    // wave takes rows w and w + 8 in the norm's own layout and order, then
+    // every lane scales its token-row pieces in place, so the operands equal
+    // a separate norm's rows bit for bit; workgroup 0 stores them when asked.
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float r = row_rms_scale(nrow[h], a.in_eps);
+            if (lane == 0) rscale[wave + 8 * h] = r;
+        }
+        __syncthreads();
+        const float r = rscale[t < T ? t : 0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xb[i] = rms_apply8(xb[i], wn[i], r);
+        if (b == 0 && a.norm_out != nullptr && t < T) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                *reinterpret_cast<uint4*>(a.norm_out + static_cast<int64_t>(t) * kHidden + 256 * wave + 32 * i + 8 * g) = xb[i];
+        }
+    }
 
     // ---- phase A: in_proj (wave w multiplies k in [256 w, 256 w + 256)) ----
     // MFMA A rows from row0 (every lane loads: an output row depends on its
@@ -756,6 +794,11 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
 
     // ---- phase D: out_proj rows 8b .. 8b + 7 ----
     {
+        // (the residual for the fused add: output row 8b + tid / 16, token
+        // tid % 16, clamped for the threads that store none)
+        const int res_row = (tid >> 4) & (kMixRows - 1);
+        const int res_t = (tid & 15) < T ? (tid & 15) : 0;
+        const uint32_t res = ldg_u16(a.x + static_cast<int64_t>(res_t) * kHidden + kMixRows * b + res_row);
         // columns t >= T read token 0's row: their output columns are dropped
         uint4 cb[16];
         const int tc = t < T ? t : 0;
@@ -779,7 +822,14 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
             float p = 0.0f;
 #pragma unroll
             for (int ww = 0; ww < kMixWaves; ++ww) p += red[ww][row][tt];
-            if (tt < T) a.out[static_cast<int64_t>(tt) * kHidden + kMixRows * b + row] = static_cast<uint16_t>(f2bf(p));
+            const uint32_t o = f2bf(p);
+            if (tt < T) {
+                a.out[static_cast<int64_t>(tt) * kHidden + kMixRows * b + row] = static_cast<uint16_t>(o);
+                // bf16(x + out), the decoder's residual add
+                if (a.sum_out != nullptr)
+                    a.sum_out[static_cast<int64_t>(tt) * kHidden + kMixRows * b + row] =
+                        static_cast<uint16_t>(f2bf(bf2f(res) + bf2f(o)));
+            }
         }
     }
     MX_TL(10);
@@ -855,10 +905,19 @@ hipError_t launch_delta_mixer(DnProjectArgs p, void* state, bool state_bf16, voi
     m.normed = w.normed;
     m.staged = w.staged;
     const StageEvents ev = timing_events(kStageDeltaMixer);
+    const bool norm = p.in_norm != nullptr;
     if (state_bf16) {
-        LRMOE_LAUNCH(dn_mixer<true>, dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        if (norm) {
+            LRMOE_LAUNCH((dn_mixer<true, true>), dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        } else {
+            LRMOE_LAUNCH((dn_mixer<true, false>), dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        }
     } else {
-        LRMOE_LAUNCH(dn_mixer<false>, dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        if (norm) {
+            LRMOE_LAUNCH((dn_mixer<false, true>), dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        } else {
+            LRMOE_LAUNCH((dn_mixer<false, false>), dim3(kMixGrid), dim3(kMixThreads), 0, stream, ev.start, ev.stop, m);
+        }
     }
     return hipGetLastError();
 }

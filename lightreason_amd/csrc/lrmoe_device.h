@@ -230,6 +230,34 @@ __device__ __forceinline__ void unpack8(uint4 w, float* out) {
     out[6] = lo_bf(w.w); out[7] = hi_bf(w.w);
 }
 
+// The decoder's input RMSNorm ([HF] Qwen3_5MoeRMSNorm 801-818) of one
+// 2048-element bf16 row held by a wave, lane l holding elements
+// 32 l .. 32 l + 31 in v: 1 / sqrt(mean(x^2) + eps), the sum in the
+// canonical order of the router and norm sums (fmaf from +0 in element
+// order, then the xor butterfly over offsets 1..32), so every caller gets the
+// oracle's value bit for bit.
+__device__ __forceinline__ float row_rms_scale(const uint4 (&v)[4], float eps) {
+    float f[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack8(v[i], f + 8 * i);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(f[j], f[j], acc);
+    const float mean = wave_butterfly_sum(acc) / static_cast<float>(kHidden);
+    return 1.0f / __builtin_sqrtf(mean + eps);
+}
+
+// Eight normed elements: bf16((x * r) * (1 + w)) for bf16 x and weights w.
+__device__ __forceinline__ uint4 rms_apply8(uint4 x, uint4 w, float r) {
+    float xf[8], wf[8];
+    unpack8(x, xf);
+    unpack8(w, wf);
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = f2bf((xf[j] * r) * (1.0f + wf[j]));
+    return make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+}
+
 // v_mfma_f32_16x16x32_bf16.  A is 16x32 (lane l holds row l%16, k-group l/16),
 // B is 32x16 (lane l holds column l%16, the same k-group), D is 16x16 with lane
 // l holding rows 4*(l/16)+i, i=0..3, of column l%16.  The k order inside a

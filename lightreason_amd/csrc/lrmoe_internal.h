@@ -366,6 +366,11 @@ struct DnProjectArgs {
     float* G;                 // [T][32] exp(g)
     uint16_t* out;            // [T][2048]
     int tokens;
+    // The decoder layer's glue, fused (all null for a plain mixer call):
+    const uint16_t* in_norm;  // input RMSNorm weight [2048]: x is then the raw residual stream, normed here
+    float in_eps;
+    uint16_t* norm_out;       // [T][2048] the normed rows (written by workgroup 0), or null
+    uint16_t* sum_out;        // [T][2048] bf16(x + out), the residual add, or null
 };
 
 // The delta rule over `tokens` tokens for `heads` value heads of state
@@ -460,8 +465,19 @@ struct AttnWorkspace {
 AttnWorkspace carve_attn(void* base, int tokens);
 size_t attn_workspace_bytes(int tokens);
 int attn_chunk(int tokens, int total);
+// The decoder layer's glue fused into an attention step (all null for a
+// plain call): x is then the raw residual stream, normed in the projection
+// launch with in_norm / in_eps (the normed rows also to norm_out when not
+// null), and sum_out receives bf16(x + out).
+struct AttnGlue {
+    const uint16_t* in_norm;
+    float in_eps;
+    uint16_t* norm_out;
+    uint16_t* sum_out;
+};
 hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q, const uint16_t* w_k,
-                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, hipStream_t stream);
+                              const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, const AttnGlue& fused,
+                              hipStream_t stream);
 DeltaWorkspace carve_delta(void* base, int tokens);
 size_t delta_workspace_bytes(int tokens);
 hipError_t launch_delta_rule(const DnRuleArgs& a, int key_width, bool state_bf16, hipStream_t stream);

@@ -48,24 +48,9 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm_kernel(const uint16_t* x, c
         for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sum_out + at + 8 * i) = v[i];
     }
     if (norm == nullptr) return;
-    float f[32];
+    const float r = row_rms_scale(v, eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) unpack8(v[i], f + 8 * i);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(f[j], f[j], acc);
-    const float mean = wave_butterfly_sum(acc) / static_cast<float>(kHidden);
-    const float r = 1.0f / __builtin_sqrtf(mean + eps);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float wf[8];
-        unpack8(w[i], wf);
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = f2bf((f[8 * i + j] * r) * (1.0f + wf[j]));
-        *reinterpret_cast<uint4*>(norm_out + at + 8 * i) =
-            make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(norm_out + at + 8 * i) = rms_apply8(v[i], w[i], r);
 }
 
 }  // namespace

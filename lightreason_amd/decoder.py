@@ -2,10 +2,12 @@
 positions, every part native.  Per layer ([HF] Qwen3_5MoeDecoderLayer.forward
 855-877):
 
-* the input RMSNorm (``lrmoe_add_rmsnorm``),
-* the Gated DeltaNet mixer (``lrmoe_delta_mixer``, 3 of every 4 layers) or
-  the full attention (``lrmoe_attn_decode``, every 4th layer),
-* the residual add (``lrmoe_add_rmsnorm``),
+* the input RMSNorm, the Gated DeltaNet mixer (3 of every 4 layers) or the
+  full attention (every 4th layer), and the residual add, as one call
+  (``lrmoe_delta_mixer_step`` / ``lrmoe_attn_decode_step``, which norm the
+  rows inside the mixer or projection launch and add the residual in the
+  output launch; ``fused=False`` runs ``lrmoe_add_rmsnorm`` around
+  ``lrmoe_delta_mixer`` / ``lrmoe_attn_decode`` instead, with the same bits),
 * the MoE block with its post-attention RMSNorm and residual
   (``lrmoe_moe_layer``).
 
@@ -21,7 +23,7 @@ hold ``length`` positions before it, the mixers' states are advanced in
 place).  ``VerifyPass(stack, widths, length)`` captures one graph per width
 over static buffers: a replay reads the block from ``hidden``, the rotary
 rows from ``cos``/``sin`` and the cache length from a device word
-(``lrmoe_attn_decode_at``), appends at positions ``length ..`` of every
+(``lrmoe_attn_decode_step`` with ``length_dev``), appends at positions ``length ..`` of every
 attention cache and advances every mixer state.  ``verify(..., length=n)``
 sets that word before the replay, so the same graphs serve a cache that
 grows between verify blocks.
@@ -145,13 +147,19 @@ class DecoderStack:
 
     def step(self, hidden: torch.Tensor, length, cos: torch.Tensor | None = None,
              sin: torch.Tensor | None = None, *, buffers: StepBuffers | None = None,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, fused: bool = True) -> torch.Tensor:
         """One cached forward of T = hidden.shape[0] (1..16) positions after
         ``length`` cached positions (an int, or a one-element int32 device
         tensor read by the attention kernels when they run); cos, sin [T, 64]
         bf16 (the rotary rows of the new positions) are needed when the stack
         has attention layers.  Returns the last layer's output [T, 2048] bf16
-        (``out`` if given)."""
+        (``out`` if given).
+
+        ``fused`` (default) runs each layer's input norm and residual add
+        inside its mixer or attention launches (``layer_step``; the normed
+        rows are stored only for traced buffers); ``fused=False`` runs them as
+        ``lrmoe_add_rmsnorm`` launches around the plain steps, with the same
+        bits."""
         T = hidden.shape[0]
         if not 1 <= T <= DECODE_MAX_TOKENS or hidden.shape != (T, HIDDEN) or hidden.dtype != torch.bfloat16:
             raise ValueError(f"hidden must be bf16 [T, {HIDDEN}] with 1 <= T <= {DECODE_MAX_TOKENS}")
@@ -163,14 +171,23 @@ class DecoderStack:
             n, mix, h2, h_out = buffers.at(l)
             if l == last and out is not None:
                 h_out = out
-            add_rmsnorm(h, norm=layer.input_norm, eps=layer.eps, norm_out=n)
-            if layer.mixer is not None:
-                layer.mixer.step(n, layer.conv_state, layer.state, out=mix)
+            if layer.mixer is None and (cos is None or sin is None):
+                raise ValueError("an attention layer needs the rotary rows cos and sin")
+            if fused:
+                n_out = n if buffers.trace else None
+                if layer.mixer is not None:
+                    layer.mixer.layer_step(h, layer.input_norm, layer.eps, layer.conv_state, layer.state, out=mix,
+                                           sum_out=h2, norm_out=n_out)
+                else:
+                    layer.attention.layer_step(h, layer.input_norm, layer.eps, cos, sin, layer.k_cache,
+                                               layer.v_cache, length, out=mix, sum_out=h2, norm_out=n_out)
             else:
-                if cos is None or sin is None:
-                    raise ValueError("an attention layer needs the rotary rows cos and sin")
-                layer.attention.step(n, cos, sin, layer.k_cache, layer.v_cache, length, out=mix)
-            add_rmsnorm(h, add=mix, sum_out=h2)
+                add_rmsnorm(h, norm=layer.input_norm, eps=layer.eps, norm_out=n)
+                if layer.mixer is not None:
+                    layer.mixer.step(n, layer.conv_state, layer.state, out=mix)
+                else:
+                    layer.attention.step(n, cos, sin, layer.k_cache, layer.v_cache, length, out=mix)
+                add_rmsnorm(h, add=mix, sum_out=h2)
             moe_layer(h2, layer.moe, out=h_out, indices=buffers.indices[l], weights=buffers.weights[l],
                       workspace=self.workspace)
             h = h_out

@@ -210,6 +210,35 @@ class DeltaMixer:
                      out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
         return out
 
+    def layer_step(self, residual: torch.Tensor, input_norm: torch.Tensor, input_eps: float,
+                   conv_state: torch.Tensor, state: torch.Tensor, *, out: torch.Tensor,
+                   sum_out: torch.Tensor, norm_out: torch.Tensor | None = None) -> torch.Tensor:
+        """The decoder layer's linear-attention half in one launch
+        (``lrmoe_delta_mixer_step``): residual [T, 2048] bf16 is normed with
+        input_norm [2048] (the layer's input_layernorm, applied as 1 + w)
+        inside the mixer, ``out`` receives the mixer output and ``sum_out``
+        bf16(residual + out); ``norm_out`` (optional) the normed rows.
+        States as ``step``.  Returns sum_out."""
+        dev = self.device
+        T = residual.shape[0] if residual.dim() == 2 else -1
+        if not 1 <= T <= MAX_TOKENS:
+            raise ValueError(f"residual must be [T, {HIDDEN}] with 1 <= T <= {MAX_TOKENS}, got {tuple(residual.shape)}")
+        _require(residual, "residual", (torch.bfloat16,), (T, HIDDEN), dev)
+        _require(input_norm, "input_norm", (torch.bfloat16,), (HIDDEN,), dev)
+        _require(conv_state, "conv_state", (torch.bfloat16,), (CONV_DIM, CONV_TAPS), dev)
+        _require(state, "state", (torch.float32, torch.bfloat16), (VALUE_HEADS, HEAD_WIDTH, HEAD_WIDTH), dev)
+        for name, t in (("out", out), ("sum_out", sum_out)) + ((("norm_out", norm_out),) if norm_out is not None else ()):
+            _require(t, name, (torch.bfloat16,), (T, HIDDEN), dev)
+        ws = _workspace(dev)
+        _native.call("lrmoe_delta_mixer_step", residual.data_ptr(), T, input_norm.data_ptr(), float(input_eps),
+                     self.in_proj_qkv.data_ptr(), self.in_proj_z.data_ptr(), self.in_proj_b.data_ptr(),
+                     self.in_proj_a.data_ptr(), self.conv1d.data_ptr(), self.A_log.data_ptr(), self.dt_bias.data_ptr(),
+                     self.norm.data_ptr(), self.eps, self.out_proj.data_ptr(), conv_state.data_ptr(),
+                     state.data_ptr(), int(state.dtype == torch.bfloat16), None, None, out.data_ptr(),
+                     sum_out.data_ptr(), None if norm_out is None else norm_out.data_ptr(), ws.data_ptr(),
+                     ws.numel(), _stream(dev))
+        return sum_out
+
 
 def _live(states):
     """The state tensor of a cache layer: Transformers 5.x keeps a dict

@@ -210,6 +210,40 @@ def test_verify_pass_follows_the_cache_length(decoder, oracle, width):
     vp.set_length(CONTEXT)
 
 
+@pytest.mark.parametrize("width", (1, 16))
+def test_fused_glue_equals_separate_launches(decoder, width):
+    """The layer step with the input norm and residual add fused into the
+    mixer and attention launches (the default) against the same step with
+    them as separate lrmoe_add_rmsnorm launches, from the same states: every
+    layer's normed rows, mixer output, post-mixer residual, routes and
+    output, and the final states, bit for bit."""
+    from lightreason_amd.decoder import StepBuffers
+
+    model, _, _, _ = decoder
+    print(f"[case] fused glue width {width}", flush=True)
+    x = model.hidden(width, step=9100 + width)
+    cos, sin = model.rope(width, CONTEXT)
+    before = _snapshot(model)
+    runs = []
+    for fused in (True, False):
+        _restore(model, before)
+        buf = StepBuffers(LAYERS, width, x.device, trace=True)
+        out = model.stack.step(x, CONTEXT, cos, sin, buffers=buf, fused=fused).clone()
+        torch.cuda.synchronize()
+        runs.append((out, buf, _snapshot(model)))
+    (o1, b1, s1), (o2, b2, s2) = runs
+    for name in ("n", "mix", "h2", "h", "weights"):
+        assert torch.equal(getattr(b1, name).view(torch.int16), getattr(b2, name).view(torch.int16)), name
+    assert torch.equal(b1.indices, b2.indices)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    for (a, b), (c, d) in zip(s1, s2):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           c.view(torch.int16) if c.dtype == torch.bfloat16 else c)
+        assert torch.equal(b.view(torch.int16) if b.dtype == torch.bfloat16 else b,
+                           d.view(torch.int16) if d.dtype == torch.bfloat16 else d)
+    _restore(model, before)
+
+
 def test_verify_pass_rejects_unknown_width(decoder):
     model, vp, _, _ = decoder
     with pytest.raises(ValueError, match="no verify graph"):

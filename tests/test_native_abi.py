@@ -115,6 +115,20 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     assert lib.lrmoe_attn_decode_at(*args_at(4, 100, null)) == -1
     assert lib.lrmoe_attn_decode_at(*args_at(4, 100, C.c_void_p(258))) == -1
     assert lib.lrmoe_attn_decode_at(*args_at(17, 100, aligned)) == -1
+    # the fused layer steps: no input norm, or no residual output
+    mix_step = lambda norm, sum_out, tokens=1: lib.lrmoe_delta_mixer_step(
+        aligned, tokens, norm, C.c_float(1e-6), *([aligned] * 8), C.c_float(1e-6), aligned, aligned, aligned, 0, null,
+        null, aligned, sum_out, null, aligned, big, null)
+    assert mix_step(null, aligned) == -1
+    assert mix_step(aligned, null) == -1
+    assert mix_step(C.c_void_p(258), aligned) == -1
+    assert mix_step(null, null, tokens=0) == 0
+    att_step = lambda norm, sum_out, tokens=1: lib.lrmoe_attn_decode_step(
+        aligned, tokens, norm, C.c_float(1e-6), *([aligned] * 6), C.c_float(1e-6), aligned, aligned, aligned, aligned,
+        100, 0, null, aligned, sum_out, null, aligned, big, null)
+    assert att_step(null, aligned) == -1
+    assert att_step(aligned, null) == -1
+    assert att_step(null, null, tokens=0) == 0
     # decoder glue: nothing to write, a sum without an addend, a norm weight
     # without its output (or the reverse), a misaligned row, a negative count
     eps = C.c_float(1e-6)
