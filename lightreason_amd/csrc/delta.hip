@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
         for (int i = 0; i < 8; ++i) w[i] = ldg16(row0 + (i >> 2) * kHidden + 512 * (i & 3));
         cv = load_conv(v);
     };
-    // The small inputs first -- A_log and dt_bias, the barrier release word, the
+    // The small inputs first -- A_log and dt_bias, the head's counter, the
     // rule's state slab, the token rows -- then in_proj units 0 (q, k) and 1
     // (v).  The memory counter retires in order: waiting for a small input
     // then never waits for a unit, and unit 0 is multiplied as soon as it
@@ -437,6 +437,12 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     uint2 c0, c1;
     const int v0 = b, v1 = b + kMixGrid, v2 = b + 2 * kMixGrid;
     load_unit(w0, c0, v0);
+    // Unit 1 is requested once unit 0's rows have landed: with no unit 1
+    // in the memory system, every CU's unit 0 arrives ~0.9 us earlier and is
+    // multiplied while unit 1 streams (requesting it when half of unit 0
+    // had landed gained ~0.3 us).  (s_waitcnt vmcnt(1): unit 0's conv word
+    // may still be in flight.)
+    __builtin_amdgcn_s_waitcnt((1 & 15) | (7 << 4) | (15 << 8));
     load_unit(w1, c1, v1);
     if (tid == 0) {
         base_s = counted / kMixHeadGroups + 1;
