@@ -216,7 +216,8 @@ def test_fused_glue_equals_separate_launches(decoder, width):
     mixer and attention launches (the default) against the same step with
     them as separate lrmoe_add_rmsnorm launches, from the same states: every
     layer's normed rows, mixer output, post-mixer residual, routes and
-    output, and the final states, bit for bit."""
+    output, and the final states, bit for bit; and the fused step's output
+    with untraced buffers (no normed rows stored)."""
     from lightreason_amd.decoder import StepBuffers
 
     model, _, _, _ = decoder
@@ -231,7 +232,12 @@ def test_fused_glue_equals_separate_launches(decoder, width):
         out = model.stack.step(x, CONTEXT, cos, sin, buffers=buf, fused=fused).clone()
         torch.cuda.synchronize()
         runs.append((out, buf, _snapshot(model)))
+    # the fused step with untraced buffers (no normed rows stored)
+    _restore(model, before)
+    o3 = model.stack.step(x, CONTEXT, cos, sin, buffers=StepBuffers(LAYERS, width, x.device), fused=True).clone()
+    torch.cuda.synchronize()
     (o1, b1, s1), (o2, b2, s2) = runs
+    assert torch.equal(o3.view(torch.int16), o1.view(torch.int16))
     for name in ("n", "mix", "h2", "h", "weights"):
         assert torch.equal(getattr(b1, name).view(torch.int16), getattr(b2, name).view(torch.int16)), name
     assert torch.equal(b1.indices, b2.indices)
