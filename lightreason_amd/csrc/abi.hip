@@ -637,8 +637,7 @@ static int attn_decode(const uint16_t* hidden, int tokens, const uint16_t* q_pro
     a.length_dev = length_dev;
     a.tokens = tokens;
     const int span = length_dev != nullptr ? capacity : length + tokens;  // positions the chunks cover
-    a.chunk = lrmoe::attn_chunk(tokens, span);
-    a.chunks = (span + a.chunk - 1) / a.chunk;
+    lrmoe::attn_geometry(a, tokens, span);
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.att = w.att;

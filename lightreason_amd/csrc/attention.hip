@@ -14,7 +14,10 @@
 //        workgroups of 16 rows): each wave streams 1 KiB of one row per load
 //        instruction, the rows pass through LDS into the MFMA layout, the
 //        T <= 16 tokens are the MFMA's 16 columns; bf16 out (proj).
-//   at_attend  one workgroup per (key/value head g, chunk of P positions):
+//   at_attend  one workgroup per (key/value head g, chunk of whole
+//        32-position sub-blocks), and above 8 tokens per token half of it
+//        (up to 64 query rows per workgroup, so that the 130 chunks of 4096
+//        cached positions become 256 workgroups on 256 CUs):
 //        the query rows of heads 8g..8g+7 normalised and rotated into LDS,
 //        the chunk's new positions (those >= length) normalised, rotated
 //        and appended to the caches, then per 32-position sub-block: key
@@ -48,7 +51,6 @@ constexpr int kAtProj = kAtQg + 2 * kAtKv * kAtD;  // 9216 projected rows
 constexpr int kAtO = kAtHeads * kAtD;              // 4096 o_proj inputs
 constexpr int kAtThreads = 512;
 constexpr int kAtWaves = kAtThreads / 64;
-constexpr int kAtMaxRows = kAtGroup * kAttnMaxTokens;  // query rows of one key/value head: 8 T <= 128
 constexpr int kAtSub = 32;                          // positions per sub-block
 constexpr int kAtQStride = kAtD + 8;                // LDS row strides (bf16 / fp32 elements)
 constexpr int kAtVStride = kAtSub + 8;
@@ -198,22 +200,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Sum and maximum over each 16-lane row of the wave (the MFMA output lanes
-// of one row group), returned to every lane of the row.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += dpp_f<0x141>(v);
-    return v + dpp_f<0x140>(v);
-}
-
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    return fmaxf(v, dpp_f<0x140>(v));
-}
-
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));
@@ -274,9 +260,12 @@ __device__ __forceinline__ uint2 norm_rope(uint2 raw, const uint16_t* w, float e
     return make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
 }
 
-template <int kRows>
+// kRows query rows (8 per token), kTok tokens' rotary rows and new-position
+// key/value rows (all of the call's tokens: a workgroup of one token half
+// still appends, and attends over, every new position).
+template <int kRows, int kTok>
 struct AttendLds {
-    static constexpr int kMaxT = kRows / kAtGroup;
+    static constexpr int kMaxT = kTok;
     __attribute__((aligned(16))) uint16_t qs[kRows][kAtQStride];  // normed, rotated query rows
     __attribute__((aligned(16))) uint16_t ks[kAtSub][kAtQStride];  // a sub-block's key rows
     __attribute__((aligned(16))) uint16_t vs[kAtSub][kAtQStride];  // its value rows
@@ -326,10 +315,10 @@ __device__ __forceinline__ bool attn_length_bad(const AttnArgs& a) {
 // new positions appended, then per 32-position sub-block scores, online
 // softmax and P.V; (max, sum, unnormalised rows) to the partial buffers.
 // kb / vb carry the key and value rows of two sub-blocks in flight.
-template <int kRows>
-__device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>& S, int g, int c, uint4 (&kb)[2][2],
-                                             uint4 (&vb)[2][2]) {
-    constexpr int kMaxT = kRows / kAtGroup;
+template <int kRows, int kTok, bool kHalves>
+__device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows, kTok>& S, int g, int c, int half,
+                                             uint4 (&kb)[2][2], uint4 (&vb)[2][2]) {
+    constexpr int kMaxT = kRows / kAtGroup;  // query tokens per workgroup
     constexpr int kRowTiles = kRows / 16;
     auto& qs = S.qs;
     auto& ks = S.ks;
@@ -350,24 +339,30 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
     const int m = lane & 15;
     const int gq = lane >> 4;
     const int T = a.tokens;
-    const int R = kAtGroup * T;  // query rows r = 8 t + local head
+    // this workgroup's query tokens t0 .. t0 + Tq - 1 (its rows r = 8 (t - t0)
+    // + local head; rows 8 t0 .. of the chunk's partials)
+    const int t0 = kHalves ? half * a.t_half : 0;
+    const int Tq = kHalves ? (half == 0 ? a.t_half : T - a.t_half) : T;
+    const int R = kAtGroup * Tq;
     const int RT = (R + 15) / 16;
     const int L = attn_length(a);  // (chunks past L + T read and write nothing: empty partials)
     const int total = L + T;
-    const int p0 = c * a.chunk;
-    const int p1 = min(p0 + a.chunk, total);
+    // chunk c: sub-blocks c per .. (c + 1) per - 1, the last chunk to the end
+    const int p0 = kAtSub * c * a.per;
+    const int last = c + 1 == a.chunks ? 1 : 0;  // (arithmetic, not a branch ahead of the first loads)
+    const int p1 = min(kAtSub * ((c + 1) * a.per + last * (a.sub_blocks - (c + 1) * a.per)), total);
     uint16_t* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
     uint16_t* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
 
     // Every load below is issued by every lane (dummy addresses where a lane
     // needs none), in the order of need, so that the compiler's in-order
     // waits for one cover only what is older.
-    // (1) wave w's query rows: head 8g + w, tokens 0 .. T - 1 (rows w + 8 t)
+    // (1) wave w's query rows: head 8g + w, tokens t0 .. t0 + Tq - 1 (rows w + 8 j)
     uint2 raw[kMaxT];
     const uint16_t* qsrc = a.proj + (kAtGroup * g + wave) * 2 * kAtD + 4 * lane;
 #pragma unroll
     for (int j = 0; j < kMaxT; ++j)
-        raw[j] = *reinterpret_cast<const uint2*>(qsrc + static_cast<int64_t>(j < T ? j : 0) * kAtProj);
+        raw[j] = *reinterpret_cast<const uint2*>(qsrc + static_cast<int64_t>(t0 + (j < Tq ? j : 0)) * kAtProj);
     // (2) norm weights, cos, sin: 8-byte pieces; piece i < 128 a norm
     // weight's, then T x 16 pieces of cos and of sin
     const int pieces = 128 + 32 * T;
@@ -415,13 +410,13 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         norm_scale(nw[0], lane, w1);
 #pragma unroll
         for (int j0 = 0; j0 < kMaxT; j0 += kPass) {
-            if (j0 < T) {
+            if (j0 < Tq) {
                 float n[kPass][4];
 #pragma unroll
                 for (int j = 0; j < kPass; ++j) rms_norm_row(raw[j0 + j], w1, a.eps, n[j]);
 #pragma unroll
                 for (int j = 0; j < kPass; ++j)
-                    if (j0 + j < T)
+                    if (j0 + j < Tq)
                         *reinterpret_cast<uint2*>(&qs[wave + kAtGroup * (j0 + j)][4 * lane]) =
                             make_uint2(pack_bf2(n[j][0], n[j][1]), pack_bf2(n[j][2], n[j][3]));
             }
@@ -432,12 +427,12 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int j = lane >> 2;
         const int qd = lane & 3;
-        if (j < T) {
+        if (j < Tq) {
             uint16_t* row = &qs[wave + kAtGroup * j][0];
             const uint4* own = reinterpret_cast<const uint4*>(row + 16 * qd);
             const uint4* mate = reinterpret_cast<const uint4*>(row + 16 * (qd ^ 2));
-            const uint4* cp = reinterpret_cast<const uint4*>(&cs[0][j][16 * qd]);
-            const uint4* sp = reinterpret_cast<const uint4*>(&cs[1][j][16 * qd]);
+            const uint4* cp = reinterpret_cast<const uint4*>(&cs[0][t0 + j][16 * qd]);
+            const uint4* sp = reinterpret_cast<const uint4*>(&cs[1][t0 + j][16 * qd]);
             const uint4 xv[2] = {own[0], own[1]};
             const uint4 pv[2] = {mate[0], mate[1]};
             const uint4 cv[2] = {cp[0], cp[1]};
@@ -489,24 +484,6 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[rt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // The 128-row variant: wave w owns row tile w, its query operands held in
-    // registers for the chunk and its rows' running max and sum too (lanes
-    // of 16-lane row gq hold rows 16 w + 4 gq + i, i < 4); the 32-row one
-    // keeps them in LDS.
-    constexpr bool kOwn = kRows == kAtMaxRows;
-    uint4 qreg[kOwn ? kAtD / 32 : 1];
-    float mrun[4], lrun[4];
-    if constexpr (kOwn) {
-        const int rq = wave < RT ? 16 * wave + m : 0;
-#pragma unroll
-        for (int s = 0; s < kAtD / 32; ++s) qreg[s] = *reinterpret_cast<const uint4*>(&qs[rq][32 * s + 8 * gq]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            mrun[i] = -__builtin_inff();
-            lrun[i] = 0.0f;
-        }
-    }
-
     // One sub-block: its rows from registers into ks / vs (16-byte stores
     // along a row), the registers refilled with the sub-block two ahead,
     // then scores, softmax, P.V.
@@ -531,99 +508,63 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         }
         attend_issue(kb, vb, parity, kc, vc, q0 + 2 * kAtSub, range, tid);
         __syncthreads();
-        if constexpr (kOwn) {
-            // scores of both column tiles of the wave's row tile, then the
-            // online softmax on the MFMA outputs (row reductions in 16 lanes)
-            if (wave < RT) {
-                f32x4 s4[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
+        {
+            const int ct = wave & 1;
 #pragma unroll
-                for (int s = 0; s < kAtD / 32; ++s)
+            for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
+                const int rt = (wave >> 1) + 4 * k2;
+                if (rt < RT) {
+                    f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct)
-                        s4[ct] = mfma16x16x32(qreg[s], *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]),
-                                              s4[ct]);
-                float f[4];
+                    for (int s = 0; s < kAtD / 32; ++s)
+                        s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
+                                          *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
+                    const int pos = q0 + 16 * ct + m;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * wave + 4 * gq + i;
-                    float sv[2];
-#pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) {
-                        const int pos = q0 + 16 * ct + m;
-                        const bool ok = r < R && pos < p1 && pos <= L + (r >> 3);
-                        sv[ct] = ok ? rbf(s4[ct][i]) * kAtScale : -__builtin_inff();
-                    }
-                    const float m_new = fmaxf(mrun[i], row16_max(fmaxf(sv[0], sv[1])));
-                    const bool none = m_new == -__builtin_inff();
-                    const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(sv[0] - m_new), none ? 0.0f : fast_exp(sv[1] - m_new));
-                    es[r][m] = static_cast<uint16_t>(e);
-                    es[r][16 + m] = static_cast<uint16_t>(e >> 16);
-                    const float sum = row16_sum(lo_bf(e) + hi_bf(e));
-                    f[i] = none ? 1.0f : (mrun[i] == -__builtin_inff() ? 0.0f : fast_exp(mrun[i] - m_new));
-                    lrun[i] = lrun[i] * f[i] + sum;
-                    mrun[i] = m_new;
-                }
-                if (m == 0) *reinterpret_cast<float4*>(&frow[16 * wave + 4 * gq]) = make_float4(f[0], f[1], f[2], f[3]);
-            }
-        } else {
-            // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
-            {
-                const int ct = wave & 1;
-#pragma unroll
-                for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
-                    const int rt = (wave >> 1) + 4 * k2;
-                    if (rt < RT) {
-                        f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                        for (int s = 0; s < kAtD / 32; ++s)
-                            s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
-                                              *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
-                        const int pos = q0 + 16 * ct + m;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int r = 16 * rt + 4 * gq + i;
-                            const bool ok = r < R && pos < p1 && pos <= L + (r >> 3);
-                            sc[r][16 * ct + m] = ok ? rbf(s4[i]) * kAtScale : -__builtin_inff();
-                        }
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 16 * rt + 4 * gq + i;
+                        const bool ok = r < R && pos < p1 && pos <= L + t0 + (r >> 3);
+                        sc[r][16 * ct + m] = ok ? rbf(s4[i]) * kAtScale : -__builtin_inff();
                     }
                 }
             }
-            __syncthreads();
-            // online softmax: four threads per row, eight positions each
-            {
-                const int r = tid >> 2;
-                const int q = tid & 3;
-                if (r < R) {  // (R is a multiple of 8: whole quads take part)
-                    float s8[8];
-                    float mx = -__builtin_inff();
+        }
+        __syncthreads();
+        // online softmax: four threads per row, eight positions each
+        {
+            const int r = tid >> 2;
+            const int q = tid & 3;
+            if (r < R) {  // (R is a multiple of 8: whole quads take part)
+                float s8[8];
+                float mx = -__builtin_inff();
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        s8[j] = sc[r][8 * q + j];
-                        mx = fmaxf(mx, s8[j]);
-                    }
-                    mx = fmaxf(mx, dpp_f<0xB1>(mx));
-                    mx = fmaxf(mx, dpp_f<0x4E>(mx));
-                    const float m_old = mrow[r];
-                    const float m_new = fmaxf(m_old, mx);
-                    const bool none = m_new == -__builtin_inff();
-                    float sum = 0.0f;
-                    uint32_t e2[4];
+                for (int j = 0; j < 8; ++j) {
+                    s8[j] = sc[r][8 * q + j];
+                    mx = fmaxf(mx, s8[j]);
+                }
+                mx = fmaxf(mx, dpp_f<0xB1>(mx));
+                mx = fmaxf(mx, dpp_f<0x4E>(mx));
+                const float m_old = mrow[r];
+                const float m_new = fmaxf(m_old, mx);
+                const bool none = m_new == -__builtin_inff();
+                float sum = 0.0f;
+                uint32_t e2[4];
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(s8[j] - m_new),
-                                                    none ? 0.0f : fast_exp(s8[j + 1] - m_new));
-                        sum += lo_bf(e) + hi_bf(e);
-                        e2[j / 2] = e;
-                    }
-                    *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
-                    sum += dpp_f<0xB1>(sum);
-                    sum += dpp_f<0x4E>(sum);
-                    const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : fast_exp(m_old - m_new));
-                    if (q == 0) {
-                        mrow[r] = m_new;
-                        lrow[r] = lrow[r] * f + sum;
-                        frow[r] = f;
-                    }
+                for (int j = 0; j < 8; j += 2) {
+                    const uint32_t e = pack_bf2(none ? 0.0f : fast_exp(s8[j] - m_new),
+                                                none ? 0.0f : fast_exp(s8[j + 1] - m_new));
+                    sum += lo_bf(e) + hi_bf(e);
+                    e2[j / 2] = e;
+                }
+                *reinterpret_cast<uint4*>(&es[r][8 * q]) = make_uint4(e2[0], e2[1], e2[2], e2[3]);
+                sum += dpp_f<0xB1>(sum);
+                sum += dpp_f<0x4E>(sum);
+                const float f = none ? 1.0f : (m_old == -__builtin_inff() ? 0.0f : fast_exp(m_old - m_new));
+                if (q == 0) {
+                    mrow[r] = m_new;
+                    lrow[r] = lrow[r] * f + sum;
+                    frow[r] = f;
                 }
             }
         }
@@ -661,16 +602,10 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         sub_block(0, q0);
         if (q0 + kAtSub < p1) sub_block(1, q0 + kAtSub);
     }
-    if constexpr (kOwn) {
-        if (wave < RT && m == 0) {
-            *reinterpret_cast<float4*>(&mrow[16 * wave + 4 * gq]) = make_float4(mrun[0], mrun[1], mrun[2], mrun[3]);
-            *reinterpret_cast<float4*>(&lrow[16 * wave + 4 * gq]) = make_float4(lrun[0], lrun[1], lrun[2], lrun[3]);
-        }
-        __syncthreads();
-    }
 
     // the chunk's partials: unnormalised rows, running max and sum per row
-    float* po = a.part_o + (static_cast<int64_t>(g) * a.chunks + c) * R * kAtD;
+    const int Rall = kAtGroup * T;  // the chunk's partial rows
+    float* po = a.part_o + ((static_cast<int64_t>(g) * a.chunks + c) * Rall + kAtGroup * t0) * kAtD;
 #pragma unroll
     for (int rt = 0; rt < kRowTiles; ++rt) {
         if (rt < RT) {
@@ -688,19 +623,29 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows>
         }
     }
     if (tid < R) {
-        float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * R + tid) * 2;
+        float* pm = a.part_ml + ((static_cast<int64_t>(g) * a.chunks + c) * Rall + kAtGroup * t0 + tid) * 2;
         pm[0] = mrow[tid];
         pm[1] = lrow[tid];
     }
 }
 
-// kRows: the query rows the launch supports (8 T for T <= kRows / 8): 32
-// (about 63 KB of LDS, two workgroups per CU) or 128.
-template <int kRows>
+// kRows: the query rows of a workgroup (8 per token): 32 up to 4 tokens
+// (about 63 KB of LDS, two workgroups per CU), 64 above (one).  Above 8
+// tokens a chunk's rows take two workgroups, one per token half, on the
+// same XCD (workgroups b and b + 8 of each group of 16), so they share the
+// chunk's key and value rows through its L2.
+template <int kRows, int kTok, bool kHalves>
 __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(AttnArgs a) {
-    __shared__ AttendLds<kRows> S;
+    __shared__ AttendLds<kRows, kTok> S;
     uint4 kb[2][2], vb[2][2];  // [sub-block parity][piece]
-    attend_chunk<kRows>(a, S, blockIdx.x / a.chunks, blockIdx.x % a.chunks, kb, vb);
+    if constexpr (kHalves) {
+        const int b = blockIdx.x;
+        const int i = (b >> 4) * 8 + (b & 7);  // (key/value head, chunk) index
+        if (i >= kAtKv * a.chunks) return;     // (the grid is rounded up to whole groups of 16)
+        attend_chunk<kRows, kTok, true>(a, S, i / a.chunks, i % a.chunks, (b >> 3) & 1, kb, vb);
+    } else {
+        attend_chunk<kRows, kTok, false>(a, S, blockIdx.x / a.chunks, blockIdx.x % a.chunks, 0, kb, vb);
+    }
 }
 
 // ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
@@ -839,15 +784,27 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
 
 }  // namespace
 
-int attn_chunk(int tokens, int total) {
-    // one sub-block per chunk up to 4 tokens, two above (the partials of
-    // 8 T rows per chunk stay near the key/value bytes), and few enough
-    // chunks for both heads' workgroups to be resident at once: 256 per head
-    // up to 4 tokens (two workgroups per CU), 128 above (one)
-    const int floor_p = tokens <= 4 ? kAtSub : 2 * kAtSub;
-    const int cap = tokens <= 4 ? kAttnMaxChunks : kAttnMaxChunks / 2;
-    const int need = (total + cap - 1) / cap;
-    return need > floor_p ? need : floor_p;
+void attn_geometry(AttnArgs& a, int tokens, int span) {
+    // Chunks of `per` whole 32-position sub-blocks: one per chunk up to 4
+    // tokens (the partials of 8 T rows per chunk stay small), two above,
+    // more only when the chunks would exceed the cap: 256 per head up to 4
+    // tokens (two workgroups per CU), 128 above, 64 above 8 tokens (two
+    // workgroups per chunk), so that every workgroup is resident at once.
+    // The last chunk takes what the cap leaves (at most 2 per): 4096 cached
+    // positions and 16 new ones make 64 chunks of 2 sub-blocks and one of 3,
+    // not 43 of 3.  A chunk's bounds depend on the span only through `per`,
+    // so a call sized for a cache's capacity and one sized for its length
+    // split the valid positions alike while `per` is the same.
+    const int S = (span + kAtSub - 1) / kAtSub;
+    const int halves = tokens > 8 ? 2 : 1;
+    const int floor_per = tokens <= 4 ? 1 : 2;
+    const int cap = tokens <= 4 ? kAttnMaxChunks : kAttnMaxChunks / 2 / halves;
+    const int per = max(floor_per, (S + cap) / (cap + 1));
+    a.sub_blocks = S;
+    a.per = per;
+    a.chunks = min((S + per - 1) / per, cap);
+    a.halves = halves;
+    a.t_half = (tokens + 1) / 2;
 }
 
 size_t attn_workspace_bytes(int tokens) {
@@ -890,9 +847,14 @@ hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q
                      w_q, w_k, w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj, in_glue);
     }
     if (T <= 4) {
-        LRMOE_LAUNCH(at_attend<32>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
+        LRMOE_LAUNCH((at_attend<32, 4, false>), dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr,
+                     a);
+    } else if (a.halves == 1) {
+        LRMOE_LAUNCH((at_attend<64, 8, false>), dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr,
+                     a);
     } else {
-        LRMOE_LAUNCH(at_attend<kAtMaxRows>, dim3(kAtKv * a.chunks), dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
+        LRMOE_LAUNCH((at_attend<64, kAttnMaxTokens, true>), dim3((2 * kAtKv * a.chunks + 15) / 16 * 16),
+                     dim3(kAtThreads), 0, stream, nullptr, nullptr, a);
     }
     if (T <= 4) {
         LRMOE_LAUNCH(at_combine<8>, dim3(T * kAtHeads * 8), dim3(kAtCombineThreads), 0, stream, nullptr, nullptr, a);

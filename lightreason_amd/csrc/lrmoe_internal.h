@@ -449,8 +449,11 @@ struct AttnArgs {
     int length;             // cached positions before the call
     const int32_t* length_dev;  // or, when set, read on the device (a graph replayed as the cache grows)
     int tokens;
-    int chunk;              // positions per chunk
-    int chunks;             // chunks per key/value head (<= kAttnMaxChunks)
+    int sub_blocks;         // 32-position sub-blocks the chunks cover (ceil(span / 32))
+    int per;                // sub-blocks per chunk: chunk c covers sub-blocks c per .. (c + 1) per - 1,
+    int chunks;             // the last one the rest; chunks per key/value head (<= kAttnMaxChunks)
+    int halves;             // 1, or 2: a chunk's query rows in two workgroups, tokens split at t_half
+    int t_half;
     float* part_o;          // [2][chunks][8 T][256] unnormalised rows
     float* part_ml;         // [2][chunks][8 T][2] running max and sum
     uint16_t* att;          // [T][4096] gated attention rows, bf16
@@ -464,7 +467,9 @@ struct AttnWorkspace {
 };
 AttnWorkspace carve_attn(void* base, int tokens);
 size_t attn_workspace_bytes(int tokens);
-int attn_chunk(int tokens, int total);
+// The chunking of `span` positions for `tokens` tokens: sets sub_blocks,
+// chunks, halves and t_half of a.
+void attn_geometry(AttnArgs& a, int tokens, int span);
 // The decoder layer's glue fused into an attention step (all null for a
 // plain call): x is then the raw residual stream, normed in the projection
 // launch with in_norm / in_eps (the normed rows also to norm_out when not
