@@ -10,10 +10,11 @@
 //
 // Four launches on the caller's stream:
 //
-//   at_project<16, 2048>  q/gate, k and v rows of x (9216 rows in 576
-//        workgroups of 16 rows): each wave streams 1 KiB of one row per load
-//        instruction, the rows pass through LDS into the MFMA layout, the
-//        T <= 16 tokens are the MFMA's 16 columns; bf16 out (proj).
+//   at_project<36, 2048>  q/gate, k and v rows of x (9216 rows in 256
+//        workgroups of 36 rows, one per CU): each wave streams
+//        its k range of every row, 4 rows x 256 B per load instruction,
+//        through its own LDS stage into the MFMA layout; the T <= 16 tokens
+//        are the MFMA's 16 columns; bf16 out (proj).
 //   at_attend  one workgroup per (key/value head g, chunk of whole
 //        32-position sub-blocks), and above 8 tokens per token half of it
 //        (up to 64 query rows per workgroup, so that the 130 chunks of 4096
@@ -24,7 +25,9 @@
 //        and value rows into LDS, scores by MFMA
 //        (bf16-rounded, / 16), an online softmax per query row, P.V by MFMA
 //        into per-wave accumulators; the chunk's (max, sum, unnormalised
-//        rows) go to the partial buffers.
+//        rows) go to the partial buffers, the rows as bf16 (half the bytes
+//        of fp32: at 16 tokens the partials outweigh the 8 MB of cached
+//        keys and values read).
 //   at_combine  per (token, head, eighth or quarter of the dims): the
 //        chunks' partials merged, the sigmoid gate applied (att, bf16).
 //   at_project<8, 4096>  o_proj rows of att (2048 rows in 256 workgroups).
@@ -32,7 +35,10 @@
 // Rounding points follow the Transformers forward in bf16: projections,
 // normed and rotated q/k, scores (then / 16, exact) and the attention
 // output are bf16; the softmax is fp32 (its probabilities enter P.V as
-// bf16 values relative to the chunk's running maximum).
+// bf16 values relative to the chunk's running maximum), and so are the
+// chunks' maxima, sums and the merge; the unnormalised chunk rows are
+// rounded to bf16 once (2^-9 of each chunk's row, the size of the output's
+// own rounding).
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
@@ -74,41 +80,55 @@ struct ProjectGlue {
     uint16_t* sum_out;
 };
 
+// A workgroup projects kRows rows (8 waves, one workgroup per CU, every CU
+// the same rows: 36 of q/gate/k/v, 8 of o_proj): wave w takes the k range
+// [kKw w, kKw (w + 1)) of every row.  Its weight loads, all issued at once
+// (non-temporal), cover 4 rows x 256 B each (lanes 16 j .. 16 j + 15: one
+// row's 256 contiguous bytes, so an instruction reads whole 128-byte
+// lines) and pass per 16-row MFMA tile through the wave's own LDS stage
+// into the MFMA layout (lane (m, g) of step s: row m, elements 32 s + 8 g
+// ..; stage rows past a short tile hold stale values, their outputs are
+// dropped); the T <= 16 tokens are the MFMA's 16 columns, and the waves'
+// sums meet in LDS in wave order.  A row's matrix is chosen per row: rows
+// [0, split1) from w0, [split1, split2) from w1 (row - split1), the rest
+// from w2 (row - split2), splits and row0 multiples of 4.
+template <int kRows>
+__device__ constexpr int at_tile_parts(int a) {  // 4-row loads of tile a per span
+    return (kRows - 16 * a) >= 16 ? 4 : (kRows - 16 * a) / 4;
+}
+
 template <int kRows, int kK, bool kNorm = false, bool kResidual = false>
-__global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restrict__ w0, const uint16_t* __restrict__ w1,
-                                                         const uint16_t* __restrict__ w2, int split1, int split2,
-                                                         const uint16_t* __restrict__ x, int tokens,
-                                                         uint16_t* __restrict__ y, int y_stride, ProjectGlue glue) {
-    constexpr int kRowsPerWave = kRows / kAtWaves;        // 2 or 1
-    constexpr int kLoadsPerRow = 8 / kRowsPerWave;        // 4 or 8 loads of 1 KiB per wave and row
-    static_assert(kK == 512 * kLoadsPerRow, "a wave streams its rows in 8 loads of 1 KiB");
-    constexpr int kKw = kK / kAtWaves;                    // k range of a wave in the MFMA
+__global__ __launch_bounds__(kAtThreads, 2) void at_project(
+    const uint16_t* __restrict__ w0, const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w2, int split1,
+    int split2, const uint16_t* __restrict__ x, int tokens, uint16_t* __restrict__ y, int y_stride, ProjectGlue glue) {
+    constexpr int kTiles = (kRows + 15) / 16;
+    constexpr int kKw = kK / kAtWaves;              // k range of a wave
+    constexpr int kSpans = kKw / 128;               // 128-element spans per row
+    constexpr int kLoads = kSpans * kRows / 4;      // 16-byte weight loads per lane
     constexpr int kSteps = kKw / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t tile[kRows][kK + 8];
-    __shared__ float red[kAtWaves][16][17];
+    constexpr int kStageRow = 256 + 16;             // bytes per staged row (+16: conflict-free both ways)
+    static_assert(kKw % 128 == 0 && kRows % 4 == 0 && kLoads <= 24, "whole spans and 4-row loads");
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kAtWaves][16 * kStageRow];
+    __shared__ float red[kAtWaves][16 * kTiles][17];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int t = lane & 15;
     const int g = lane >> 4;
     const int row0 = blockIdx.x * kRows;
-    const uint16_t* w = row0 < split1 ? w0 : (row0 < split2 ? w1 : w2);
-    const int wrow0 = row0 < split1 ? row0 : (row0 < split2 ? row0 - split1 : row0 - split2);
-    // the rows first (every lane loads: the tile is always full)
-    uint4 wv[8];
-    const uint16_t* wrow = w + static_cast<int64_t>(wrow0 + kRowsPerWave * wave) * kK + 8 * lane;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) wv[i] = ldg16(wrow + (i / kLoadsPerRow) * kK + 512 * (i % kLoadsPerRow));
-    // token rows (columns t >= T read token 0: their outputs are dropped)
+    // token rows first (columns t >= T read token 0: their outputs are
+    // dropped) and what the fused norm needs, then the weights, tile by
+    // tile: load (tile a, span j, part p) is row 16 a + 4 p + lane / 16,
+    // bytes 256 j + 16 (lane % 16) of the wave's range
     uint4 xb[kSteps];
     const uint16_t* xrow = x + static_cast<int64_t>(t < tokens ? t : 0) * kK + kKw * wave + 8 * g;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) xb[s] = ldg16(xrow + 32 * s);
     // the fused input norm: wave w's rows w and w + 8 in the norm's layout
-    // (lane l: elements 32 l ..), the weights of the lane's xb pieces
-    [[maybe_unused]] uint4 nrow[2][4], wn[kSteps];
-    [[maybe_unused]] uint32_t res = 0u;
-    static_assert(!kNorm || kK == kHidden, "the input norm runs over hidden rows");
+    // (lane l: elements 32 l ..); its weights (4 KiB) pass through LDS
+    [[maybe_unused]] uint4 nrow[2][4], wn = make_uint4(0, 0, 0, 0);
+    [[maybe_unused]] uint32_t res[(16 * kRows + kAtThreads - 1) / kAtThreads] = {};
+    static_assert(!kNorm || (kK == kHidden && kHidden == 8 * 256), "the input norm runs over hidden rows");
     if constexpr (kNorm) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -117,20 +137,40 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
 #pragma unroll
             for (int i = 0; i < 4; ++i) nrow[h][i] = ldg16(src + 8 * i);
         }
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) wn[s] = ldg16(glue.norm + kKw * wave + 32 * s + 8 * g);
+        wn = ldg16(glue.norm + 8 * (tid & 255));
     }
+    const uint16_t* wsrc[kRows / 4];  // the lane's row of each 4-row group, at the wave's range
+#pragma unroll
+    for (int q = 0; q < kRows / 4; ++q) {
+        const int r = row0 + 4 * q + (lane >> 4);
+        wsrc[q] = (r < split1   ? w0 + static_cast<int64_t>(r) * kK
+                   : r < split2 ? w1 + static_cast<int64_t>(r - split1) * kK
+                                : w2 + static_cast<int64_t>(r - split2) * kK) +
+                  kKw * wave + 8 * (lane & 15);
+    }
+    uint4 wv[kLoads];
+#pragma unroll
+    for (int a = 0; a < kTiles; ++a)
+#pragma unroll
+        for (int j = 0; j < kSpans; ++j)
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                if (p < at_tile_parts<kRows>(a))
+                    wv[4 * kSpans * a + at_tile_parts<kRows>(a) * j + p] = ldg16_nt(wsrc[4 * a + p] + 128 * j);
     if constexpr (kResidual) {
-        // output row row0 + tid / 16, token tid % 16 (clamped where none is stored)
-        const int rr = (tid >> 4) % kRows;
-        const int rt = (tid & 15) < tokens ? (tid & 15) : 0;
-        res = ldg_u16(glue.residual + static_cast<int64_t>(rt) * y_stride + row0 + rr);
-    }
+        // output (row row0 + i / 16, token i % 16) for i = tid, tid + 512, ..
+        // (tokens clamped where none is stored)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(&tile[kRowsPerWave * wave + i / kLoadsPerRow][512 * (i % kLoadsPerRow) + 8 * lane]) = wv[i];
+        for (int k = 0; k < (16 * kRows + kAtThreads - 1) / kAtThreads; ++k) {
+            const int i = tid + kAtThreads * k < 16 * kRows ? tid + kAtThreads * k : 0;
+            const int rt = (i & 15) < tokens ? (i & 15) : 0;
+            res[k] = ldg_u16(glue.residual + static_cast<int64_t>(rt) * y_stride + row0 + (i >> 4));
+        }
+    }
     if constexpr (kNorm) {
         __shared__ float rscale[16];
+        __shared__ __attribute__((aligned(16))) uint16_t nw[kHidden];
+        if (tid < 256) *reinterpret_cast<uint4*>(&nw[8 * tid]) = wn;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const float r = row_rms_scale(nrow[h], glue.eps);
@@ -139,34 +179,61 @@ __global__ __launch_bounds__(kAtThreads) void at_project(const uint16_t* __restr
         __syncthreads();
         const float r = rscale[t < tokens ? t : 0];
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) xb[s] = rms_apply8(xb[s], wn[s], r);
+        for (int s = 0; s < kSteps; ++s)
+            xb[s] = rms_apply8(xb[s], *reinterpret_cast<const uint4*>(&nw[kKw * wave + 32 * s + 8 * g]), r);
         if (blockIdx.x == 0 && glue.norm_out != nullptr && t < tokens) {
 #pragma unroll
             for (int s = 0; s < kSteps; ++s)
                 *reinterpret_cast<uint4*>(glue.norm_out + static_cast<int64_t>(t) * kK + kKw * wave + 32 * s + 8 * g) = xb[s];
         }
     }
+    // per tile: the steps in order into one accumulator (per span: the
+    // tile's loads into the stage, four operands back out in the MFMA layout)
+    uint8_t* st = stage[wave];
+#pragma unroll
+    for (int a = 0; a < kTiles; ++a) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kSpans; ++j) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                if (p < at_tile_parts<kRows>(a))
+                    *reinterpret_cast<uint4*>(st + (4 * p + (lane >> 4)) * kStageRow + 16 * (lane & 15)) =
+                        wv[4 * kSpans * a + at_tile_parts<kRows>(a) * j + p];
+            // (the stage is the wave's own: in-order LDS access within the
+            // wave, and no reordering by the compiler across these fences)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint4 op[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) op[s] = *reinterpret_cast<const uint4*>(st + t * kStageRow + 16 * (4 * s + g));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc = mfma16x16x32(op[s], xb[4 * j + s], acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][16 * a + 4 * g + i][t] = acc[i];
+    }
     __syncthreads();
-    // MFMA row m (rows m >= kRows repeat row m - kRows; their outputs are dropped)
-    const int m = t % kRows;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s)
-        acc = mfma16x16x32(*reinterpret_cast<const uint4*>(&tile[m][kKw * wave + 32 * s + 8 * g]), xb[s], acc);
+    for (int k = 0; k < (16 * kRows + kAtThreads - 1) / kAtThreads; ++k) {
+        const int i = tid + kAtThreads * k;
+        if (i < 16 * kRows) {
+            const int r = i >> 4;
+            const int tt = i & 15;
+            float p = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][4 * g + i][t] = acc[i];
-    __syncthreads();
-    if (tid < kRows * 16) {
-        const int r = tid >> 4;
-        const int tt = tid & 15;
-        float p = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < kAtWaves; ++ww) p += red[ww][r][tt];
-        const uint32_t o = f2bf(p);
-        if (tt < tokens) {
-            y[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(o);
-            if constexpr (kResidual)
-                glue.sum_out[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(f2bf(bf2f(res) + bf2f(o)));
+            for (int ww = 0; ww < kAtWaves; ++ww) p += red[ww][r][tt];
+            const uint32_t o = f2bf(p);
+            if (tt < tokens) {
+                y[static_cast<int64_t>(tt) * y_stride + row0 + r] = static_cast<uint16_t>(o);
+                if constexpr (kResidual)
+                    glue.sum_out[static_cast<int64_t>(tt) * y_stride + row0 + r] =
+                        static_cast<uint16_t>(f2bf(bf2f(res[k]) + bf2f(o)));
+            }
         }
     }
 }
@@ -603,21 +670,29 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         if (q0 + kAtSub < p1) sub_block(1, q0 + kAtSub);
     }
 
-    // the chunk's partials: unnormalised rows, running max and sum per row
+    // the chunk's partials: unnormalised rows (bf16), running max and sum
+    // per row (fp32).  Lanes m and m ^ 1 hold columns m and m ^ 1 of rows
+    // 4 gq .. 4 gq + 3: one exchange, then the even lane stores rows 4 gq and
+    // 4 gq + 1, the odd lane rows 4 gq + 2 and 4 gq + 3, as column pairs.
     const int Rall = kAtGroup * T;  // the chunk's partial rows
-    float* po = a.part_o + ((static_cast<int64_t>(g) * a.chunks + c) * Rall + kAtGroup * t0) * kAtD;
+    uint16_t* po = a.part_o + ((static_cast<int64_t>(g) * a.chunks + c) * Rall + kAtGroup * t0) * kAtD;
+    const bool odd = (m & 1) != 0;
 #pragma unroll
     for (int rt = 0; rt < kRowTiles; ++rt) {
         if (rt < RT) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * rt + 4 * gq + i;
-                    if (r < R) {
-                        float* dst = po + r * kAtD + 16 * (2 * wave + j) + m;
-                        *dst = acc[rt][j][i];
-                    }
+                const uint32_t w01 = f2bf(acc[rt][j][0]) | (f2bf(acc[rt][j][1]) << 16);
+                const uint32_t w23 = f2bf(acc[rt][j][2]) | (f2bf(acc[rt][j][3]) << 16);
+                const uint32_t x = static_cast<uint32_t>(lane_xor<1>(static_cast<int>(odd ? w01 : w23)));
+                const uint32_t own = odd ? w23 : w01;
+                const uint32_t lo = odd ? (x & 0xffffu) | (own << 16) : (own & 0xffffu) | (x << 16);
+                const uint32_t hi = odd ? (x >> 16) | (own & 0xffff0000u) : (own >> 16) | (x & 0xffff0000u);
+                const int r = 16 * rt + 4 * gq + (odd ? 2 : 0);  // (R is a multiple of 8: r + 1 < R with r)
+                if (r < R) {
+                    uint16_t* dst = po + r * kAtD + 16 * (2 * wave + j) + (m & ~1);
+                    *reinterpret_cast<uint32_t*>(dst) = lo;
+                    *reinterpret_cast<uint32_t*>(dst + kAtD) = hi;
                 }
             }
         }
@@ -651,10 +726,10 @@ __global__ __launch_bounds__(kAtThreads, kRows <= 32 ? 2 : 1) void at_attend(Att
 // ---- merge and gate: att[t][h][d] = bf16(bf16(o) bf16(sigmoid(gate))) -------
 // kSplit workgroups per (token, head), each merging 256 / kSplit dims: the
 // chunks' (max, sum) pairs into LDS, the weights exp(m_c - M) (every
-// workgroup of the row computes them); thread group q (four dims per
+// workgroup of the row computes them); thread group q (eight dims per
 // thread) sums chunks q, q + kGroups, ... (every load issued at once: the
-// gate, the pairs and 8 partial rows per thread); the groups' rows meet in
-// LDS in group order.
+// gate, the pairs and the thread's partial rows); the groups' rows meet in
+// LDS, summed in group order in two steps.
 template <int kGroups, int kDims>
 struct CombineLds {
     float wc[kAttnMaxChunks];
@@ -665,15 +740,18 @@ struct CombineLds {
 };
 
 template <int kThreads, int kSplit>
-using CombineLdsOf = CombineLds<kThreads * kSplit / 64, kAtD / kSplit>;
+using CombineLdsOf = CombineLds<kThreads * kSplit / 32, kAtD / kSplit>;
 
 template <int kThreads, int kSplit>
 __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThreads, kSplit>& S, int t, int h,
                                             int piece) {
-    constexpr int kDims = kAtD / kSplit;             // dims of this workgroup
-    constexpr int kRowThreads = kDims / 4;           // threads per partial row
-    constexpr int kAtCombineGroups = kThreads / kRowThreads;
+    constexpr int kDims = kAtD / kSplit;        // dims of this workgroup
+    constexpr int kRowThreads = kDims / 8;      // threads per partial row
+    constexpr int kGroups = kThreads / kRowThreads;
+    constexpr int kBatch = kAttnMaxChunks / kGroups;  // chunks per thread
+    constexpr int kSets = kThreads / kDims;           // first summing step: kSets sets of kGroups / kSets groups
     static_assert(kThreads >= kAttnMaxChunks && kThreads >= 2 * kDims, "pairs and stores one per thread");
+    static_assert(kBatch * kGroups == kAttnMaxChunks && kBatch <= 8 && kGroups % kSets == 0, "one batch of rows");
     auto& wc = S.wc;
     auto& lc = S.lc;
     auto& part = S.part;
@@ -685,25 +763,22 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
     const int C = a.chunks;
     const int64_t chunk_rows = static_cast<int64_t>(g) * C;  // first chunk of head g
     // every load at once: the gate (threads < 256), the chunks' (max, sum)
-    // pairs, the first batch of partial rows (dummy rows where none)
+    // pairs, the thread's partial rows (chunks q + kGroups k < C)
     const int q = tid / kRowThreads;
     const int dbase = kDims * piece;
-    const int d0 = 4 * (tid % kRowThreads);
-    const float* po = a.part_o + (chunk_rows * R + r) * kAtD + dbase + d0;
+    const int d0 = 8 * (tid % kRowThreads);
+    const uint16_t* po = a.part_o + (chunk_rows * R + r) * kAtD + dbase + d0;
     const int64_t cstride = static_cast<int64_t>(R) * kAtD;
     // (the gate as the 4-byte word holding it)
     const int64_t gi = static_cast<int64_t>(t) * kAtProj + h * 2 * kAtD + kAtD + dbase + (tid % kDims);
     const uint32_t gword = *reinterpret_cast<const uint32_t*>(a.proj + (gi & ~1ll));
     const float* pml = a.part_ml + ((chunk_rows + (tid < C ? tid : 0)) * R + r) * 2;
     const float2 ml = *reinterpret_cast<const float2*>(pml);
-    auto load_row = [&](int c) -> float4 {
-        return *reinterpret_cast<const float4*>(po + static_cast<int64_t>(c) * cstride);
-    };
-    float4 v[8];
+    uint4 v[kBatch];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int c = q + kAtCombineGroups * k;
-        v[k] = load_row(c < C ? c : 0);
+    for (int k = 0; k < kBatch; ++k) {
+        const int c = q + kGroups * k;
+        v[k] = c < C ? *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(c) * cstride) : make_uint4(0, 0, 0, 0);
     }
     if (tid < C) {
         wc[tid] = ml.x;
@@ -732,32 +807,38 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, CombineLdsOf<kThr
         if (tid == 0) den_s = den;
     }
     __syncthreads();
-    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c0 = q; c0 < C; c0 += kAtCombineGroups * 8) {
-        if (c0 != q) {  // chunks past the first batch (more than 128)
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int c = c0 + kAtCombineGroups * k;
-                v[k] = load_row(c < C ? c : 0);
-            }
-        }
+    for (int k = 0; k < kBatch; ++k) {
+        const int c = q + kGroups * k;
+        const float wk = c < C ? wc[c] : 0.0f;
+        const uint32_t u[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int c = c0 + kAtCombineGroups * k;
-            const float wk = c < C ? wc[c] : 0.0f;
-            acc.x += v[k].x * wk;
-            acc.y += v[k].y * wk;
-            acc.z += v[k].z * wk;
-            acc.w += v[k].w * wk;
+        for (int i = 0; i < 4; ++i) {
+            acc[2 * i] += bf2f(u[i] & 0xffffu) * wk;
+            acc[2 * i + 1] += bf2f(u[i] >> 16) * wk;
         }
     }
-    *reinterpret_cast<float4*>(&part[q][d0]) = acc;
+    *reinterpret_cast<float4*>(&part[q][d0]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(&part[q][d0 + 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    __syncthreads();
+    // groups s kGroups / kSets .. into part[s] (each thread one dim of one set)
+    {
+        const int d = tid % kDims;
+        const int s0 = tid / kDims;
+        constexpr int kPer = kGroups / kSets;
+        float num = part[kPer * s0][d];
+#pragma unroll
+        for (int k = 1; k < kPer; ++k) num += part[kPer * s0 + k][d];
+        __syncthreads();
+        part[s0][d] = num;
+    }
     __syncthreads();
     if (tid < kDims) {
         const int d = tid;
         float num = part[0][d];
 #pragma unroll
-        for (int k = 1; k < kAtCombineGroups; ++k) num += part[k][d];
+        for (int k = 1; k < kSets; ++k) num += part[k][d];
         const float o = rbf(num / den_s);
         const float gate = bf2f((gi & 1) ? gword >> 16 : gword & 0xffffu);
         const float sg = rbf(1.0f / (1.0f + lr_exp(-gate)));
@@ -824,7 +905,7 @@ AttnWorkspace carve_attn(void* base, int tokens) {
     w.proj = reinterpret_cast<uint16_t*>(take(T * kAtProj * 2));
     w.att = reinterpret_cast<uint16_t*>(take(T * kAtO * 2));
     const size_t rows = static_cast<size_t>(kAtGroup) * T;
-    w.part_o = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * rows * kAtD * 4));
+    w.part_o = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * rows * kAtD * 2));
     w.part_ml = reinterpret_cast<float*>(take(static_cast<size_t>(kAtKv) * kAttnMaxChunks * rows * 2 * 4));
     w.bytes = off;
     return w;
@@ -833,17 +914,17 @@ AttnWorkspace carve_attn(void* base, int tokens) {
 hipError_t launch_attn_decode(AttnArgs a, const uint16_t* x, const uint16_t* w_q, const uint16_t* w_k,
                               const uint16_t* w_v, const uint16_t* w_o, uint16_t* out, const AttnGlue& fused,
                               hipStream_t stream) {
-    static_assert(kAtProj % 16 == 0 && kHidden % 8 == 0, "projection grids");
+    static_assert(kAtProj % 36 == 0 && kAtQg % 4 == 0 && kAtVRow % 4 == 0 && kHidden % 8 == 0, "projection grids");
     const int T = a.tokens;
     const StageEvents ev = timing_events(kStageAttention);
     // q/gate, k and v rows: the three weight matrices in one grid
     const ProjectGlue in_glue{fused.in_norm, fused.in_eps, fused.norm_out, nullptr, nullptr};
     const ProjectGlue out_glue{nullptr, 0.0f, nullptr, x, fused.sum_out};
     if (fused.in_norm != nullptr) {
-        LRMOE_LAUNCH((at_project<16, kHidden, true, false>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start,
+        LRMOE_LAUNCH((at_project<36, kHidden, true, false>), dim3(kAtProj / 36), dim3(kAtThreads), 0, stream, ev.start,
                      nullptr, w_q, w_k, w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj, in_glue);
     } else {
-        LRMOE_LAUNCH((at_project<16, kHidden>), dim3(kAtProj / 16), dim3(kAtThreads), 0, stream, ev.start, nullptr,
+        LRMOE_LAUNCH((at_project<36, kHidden>), dim3(kAtProj / 36), dim3(kAtThreads), 0, stream, ev.start, nullptr,
                      w_q, w_k, w_v, kAtKRow, kAtVRow, x, T, a.proj, kAtProj, in_glue);
     }
     if (T <= 4) {

@@ -454,14 +454,14 @@ struct AttnArgs {
     int chunks;             // the last one the rest; chunks per key/value head (<= kAttnMaxChunks)
     int halves;             // 1, or 2: a chunk's query rows in two workgroups, tokens split at t_half
     int t_half;
-    float* part_o;          // [2][chunks][8 T][256] unnormalised rows
+    uint16_t* part_o;       // [2][chunks][8 T][256] unnormalised rows, bf16
     float* part_ml;         // [2][chunks][8 T][2] running max and sum
     uint16_t* att;          // [T][4096] gated attention rows, bf16
 };
 struct AttnWorkspace {
     uint16_t* proj;
     uint16_t* att;
-    float* part_o;
+    uint16_t* part_o;
     float* part_ml;
     size_t bytes;
 };

@@ -79,10 +79,11 @@ def _close_rows(got, want, what):
     assert same >= 0.98 and excess <= 1.0, what
 
 
-# Blocks of more than 4 tokens run the 128-row attention variant; beyond 8192
-# cached positions its chunks are longer than 64 and not a multiple of 32
-# (partial sub-blocks, chunk boundaries inside a sub-block, up to 128 chunks
-# to merge): (9000, 8), (16383, 5) and (20000, 16).
+# Blocks of more than 4 tokens run the 64-row attention variants (above 8
+# tokens a chunk's rows in two workgroups, split at the token half); past
+# the chunk cap the chunks hold more than two 32-position sub-blocks and the
+# last one the remainder (up to 128 chunks to merge): (9000, 8), (16383, 5)
+# and (20000, 16).
 CASES = [(0, 1), (1, 1), (37, 1), (63, 1), (300, 1), (2000, 1), (5000, 1), (20000, 1),
          (40, 3), (31, 5), (3000, 8), (130, 16), (600, 16), (4100, 16),
          (9000, 8), (16383, 5), (20000, 16)]
