@@ -442,6 +442,20 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
                             : ((i - 128) < 16 * T ? a.cos : a.sin) + 4 * ((i - 128) % (16 * T));
         pc[k] = *reinterpret_cast<const uint2*>(src);
     }
+    // (2b) the chunk's new positions (p >= length): their projected key and
+    // value rows, wave w taking positions p_new + w + 8 i (token 0's rows
+    // where there is none), loaded here so that the chunk holding them
+    // does not wait for a second round trip below
+    const int p_new = attn_length_bad(a) ? p1 : max(p0, L);  // (no cache row written for a bad length)
+    constexpr int kNew = (kTok + kAtWaves - 1) / kAtWaves;
+    uint2 kraw[kNew], vraw[kNew];
+#pragma unroll
+    for (int i = 0; i < kNew; ++i) {
+        const int p = p_new + wave + kAtWaves * i;
+        const uint16_t* pr = a.proj + static_cast<int64_t>(p < p1 ? p - L : 0) * kAtProj + g * kAtD + 4 * lane;
+        kraw[i] = *reinterpret_cast<const uint2*>(pr + kAtKRow);
+        vraw[i] = *reinterpret_cast<const uint2*>(pr + kAtVRow);
+    }
     // (3) key and value rows of sub-blocks 0 and 1 (16-byte piece j of a
     // sub-block: row j / 32, dims 8 (j % 32) ..; rows past the chunk read
     // zeros: the buffer range ends at p1).  Rows of new positions read
@@ -528,19 +542,19 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
     // (5) new positions of this chunk: keys normed and rotated, values as
     // projected, into fk / fv for this call and appended to the caches for
     // later ones (no other workgroup reads them in this call)
-    const int p_new = attn_length_bad(a) ? p1 : max(p0, L);  // (no cache row written for a bad length)
-    for (int p = p_new + wave; p < p1; p += kAtWaves) {
-        const int t = p - L;
-        const uint16_t* pr = a.proj + static_cast<int64_t>(t) * kAtProj;
-        const uint2 kraw = *reinterpret_cast<const uint2*>(pr + kAtKRow + g * kAtD + 4 * lane);
-        const uint2 vraw = *reinterpret_cast<const uint2*>(pr + kAtVRow + g * kAtD + 4 * lane);
-        const uint2 k = norm_rope(kraw, nw[1], a.eps, cs[0][t], cs[1][t], lane);
-        *reinterpret_cast<uint2*>(&fk[t][4 * lane]) = k;
-        *reinterpret_cast<uint2*>(&fv[t][4 * lane]) = vraw;
-        st_agent64(kc + static_cast<int64_t>(p) * kAtD + 4 * lane,
-                   static_cast<uint64_t>(k.x) | (static_cast<uint64_t>(k.y) << 32));
-        st_agent64(vc + static_cast<int64_t>(p) * kAtD + 4 * lane,
-                   static_cast<uint64_t>(vraw.x) | (static_cast<uint64_t>(vraw.y) << 32));
+#pragma unroll
+    for (int i = 0; i < kNew; ++i) {
+        const int p = p_new + wave + kAtWaves * i;
+        if (p < p1) {
+            const int t = p - L;
+            const uint2 k = norm_rope(kraw[i], nw[1], a.eps, cs[0][t], cs[1][t], lane);
+            *reinterpret_cast<uint2*>(&fk[t][4 * lane]) = k;
+            *reinterpret_cast<uint2*>(&fv[t][4 * lane]) = vraw[i];
+            st_agent64(kc + static_cast<int64_t>(p) * kAtD + 4 * lane,
+                       static_cast<uint64_t>(k.x) | (static_cast<uint64_t>(k.y) << 32));
+            st_agent64(vc + static_cast<int64_t>(p) * kAtD + 4 * lane,
+                       static_cast<uint64_t>(vraw[i].x) | (static_cast<uint64_t>(vraw[i].y) << 32));
+        }
     }
     __syncthreads();
 
