@@ -42,6 +42,28 @@
 #include "lrmoe_device.h"
 #include "lrmoe_internal.h"
 
+// Timeline build (-DLRMOE_TIMELINE, liblrmoe_timeline.so; the product
+// library has none of it): thread 0 of every workgroup stamps the 100 MHz
+// wall clock into the buffer given by lrmoe_attn_timeline_set, 8192 words
+// per launch: at_project (q/gate/k/v) words 8192 + 4 b: 0 entry, 1 end;
+// at_attend words 16 b: 0 entry, 1 first barrier passed (query rows,
+// norm weights, cos, sin landed), 2 query rows normed and rotated, 3 new
+// positions appended, 4 + n sub-block n done (n < 3), 7 partials stored;
+// at_combine words 16384 + 4 b and o_proj words 24576 + 4 b: 0 entry, 1 end.
+#ifdef LRMOE_TIMELINE
+__device__ unsigned long long* g_attn_timeline;
+extern "C" int lrmoe_attn_timeline_set(void* p) {
+    return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(g_attn_timeline), &p, sizeof(p)));
+}
+#define AT_TL(base, stride, k)                                                                   \
+    do {                                                                                         \
+        if (threadIdx.x == 0 && g_attn_timeline != nullptr)                                      \
+            g_attn_timeline[(base) + blockIdx.x * (stride) + (k)] = wall_clock64();               \
+    } while (0)
+#else
+#define AT_TL(base, stride, k)
+#endif
+
 namespace lrmoe {
 namespace {
 
@@ -116,6 +138,8 @@ __global__ __launch_bounds__(kAtThreads, 2) void at_project(
     const int t = lane & 15;
     const int g = lane >> 4;
     const int row0 = blockIdx.x * kRows;
+    [[maybe_unused]] constexpr int kTl = kK == kHidden ? 8192 : 24576;  // (timeline words of this launch)
+    AT_TL(kTl, 4, 0);
     // token rows first (columns t >= T read token 0: their outputs are
     // dropped) and what the fused norm needs, then the weights, tile by
     // tile: load (tile a, span j, part p) is row 16 a + 4 p + lane / 16,
@@ -236,6 +260,7 @@ __global__ __launch_bounds__(kAtThreads, 2) void at_project(
             }
         }
     }
+    AT_TL(kTl, 4, 1);
 }
 
 // ---- attention partials ------------------------------------------------------
@@ -420,6 +445,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
     const int p1 = min(kAtSub * ((c + 1) * a.per + last * (a.sub_blocks - (c + 1) * a.per)), total);
     uint16_t* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
     uint16_t* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * kAtD;
+    AT_TL(0, 16, 0);
 
     // Every load below is issued by every lane (dummy addresses where a lane
     // needs none), in the order of need, so that the compiler's in-order
@@ -478,6 +504,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         frow[tid] = 1.0f;
     }
     __syncthreads();
+    AT_TL(0, 16, 1);
     // (4) the query rows normed and rotated into qs: one row when T = 1;
     // else (a) every row of the wave normalised, up to 8 rows per pass (rows
     // past T repeat token 0 and are not stored) so that their independent
@@ -539,6 +566,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
             reinterpret_cast<uint4*>(row + 16 * qd)[1] = out[1];
         }
     }
+    AT_TL(0, 16, 2);
     // (5) new positions of this chunk: keys normed and rotated, values as
     // projected, into fk / fv for this call and appended to the caches for
     // later ones (no other workgroup reads them in this call)
@@ -557,6 +585,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         }
     }
     __syncthreads();
+    AT_TL(0, 16, 3);
 
     // P.V accumulators: wave w owns dim tiles 2w, 2w + 1 of every row tile
     f32x4 acc[kRowTiles][2];
@@ -679,9 +708,14 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         }
         __syncthreads();
     };
+    [[maybe_unused]] int n_sub = 0;  // (timeline words)
     for (int q0 = p0; q0 < p1; q0 += 2 * kAtSub) {
         sub_block(0, q0);
-        if (q0 + kAtSub < p1) sub_block(1, q0 + kAtSub);
+        AT_TL(0, 16, 4 + min(n_sub++, 2));
+        if (q0 + kAtSub < p1) {
+            sub_block(1, q0 + kAtSub);
+            AT_TL(0, 16, 4 + min(n_sub++, 2));
+        }
     }
 
     // the chunk's partials: unnormalised rows (bf16), running max and sum
@@ -716,6 +750,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         pm[0] = mrow[tid];
         pm[1] = lrow[tid];
     }
+    AT_TL(0, 16, 7);
 }
 
 // kRows: the query rows of a workgroup (8 per token): 32 up to 4 tokens
@@ -873,8 +908,10 @@ constexpr int kAtCombineThreads = 256;
 template <int kSplit>
 __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
     __shared__ CombineLdsOf<kAtCombineThreads, kSplit> S;
+    AT_TL(16384, 4, 0);
     const int row = blockIdx.x / kSplit;
     combine_row<kAtCombineThreads, kSplit>(a, S, row / kAtHeads, row % kAtHeads, blockIdx.x % kSplit);
+    AT_TL(16384, 4, 1);
 }
 
 }  // namespace

@@ -1,8 +1,9 @@
 """Per-workgroup timeline of one decode layer (lrmoe_moe_layer, T <= 16),
-or with --mixer of one Gated DeltaNet mixer step (lrmoe_delta_mixer), from
-the timeline build of the library (`python -m lightreason_amd.build
---timeline`: liblrmoe_timeline.so, whose decode and mixer kernels stamp the
-wall clock at their phases).
+with --mixer of one Gated DeltaNet mixer step (lrmoe_delta_mixer), or with
+--attention of one full-attention step (lrmoe_attn_decode), from the
+timeline build of the library (`python -m lightreason_amd.build
+--timeline`: liblrmoe_timeline.so, whose decode, mixer and attention
+kernels stamp the wall clock at their phases).
 
 Runs the workload the benchmark times -- 40 resident seeded layers (seed
 2026), T tokens, with Zipf(1.1) Gumbel logits (T > 1) or the router (T = 1)
@@ -16,7 +17,14 @@ The mixer run steps 30 resident seeded mixers of the 35B shape (seed 7)
 three times over, stamps every call of the last two passes, and prints per
 phase the median over calls of the per-workgroup median and maximum.
 
-Usage: python -m lightreason_amd.timeline [--tokens T] [--layers L] [--mixer]
+The attention run replays a graph of one step on each of 10 resident
+seeded layers of the 35B shape (4096 cached positions) and reads the
+stamps of its last step after each replay: per launch (q/gate/k/v
+projection, attention partials, merge, o_proj) the entry and end, and the
+partial kernel's phases, as the median over replays of the per-workgroup
+median and maximum, in us from the projection's first entry.
+
+Usage: python -m lightreason_amd.timeline [--tokens T] [--layers L] [--mixer | --attention]
 """
 
 from __future__ import annotations
@@ -82,12 +90,84 @@ def mixer_timeline(lib, tokens: int, layers: int, seed: int) -> int:
     return 0
 
 
+ATTN_PHASES = (("first barrier", 1), ("queries normed", 2), ("new positions", 3), ("sub-block 0", 4),
+               ("sub-block 1", 5), ("sub-block 2", 6), ("partials stored", 7))
+
+
+def attention_timeline(lib, tokens: int, layers: int, seed: int, replays: int = 20) -> int:
+    from .attention import AttentionDecode
+
+    lib.lrmoe_attn_timeline_set.argtypes = [C.c_void_p]
+    lib.lrmoe_attn_timeline_set.restype = C.c_int
+    device = torch.device("cuda:0")
+    g = torch.Generator(device=device).manual_seed(seed)
+    rnd = lambda *shape, s=0.02: (torch.randn(*shape, generator=g, device=device) * s).to(torch.bfloat16)  # noqa: E731
+    hidden, context = 2048, 4096
+    mods = [AttentionDecode(q_proj=rnd(8192, hidden), k_proj=rnd(512, hidden), v_proj=rnd(512, hidden),
+                            o_proj=rnd(hidden, 4096), q_norm=rnd(256, s=0.1), k_norm=rnd(256, s=0.1))
+            for _ in range(layers)]
+    caches = [(rnd(2, context + 16, 256, s=1.0), rnd(2, context + 16, 256, s=1.0)) for _ in range(layers)]
+    pos = torch.arange(context, context + tokens, device=device, dtype=torch.float32)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, device=device, dtype=torch.float32) / 64))
+    ang = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], dim=1)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    xs = [torch.randn(tokens, hidden, generator=g, device=device).to(torch.bfloat16) for _ in range(layers)]
+    outs = [torch.empty(tokens, hidden, dtype=torch.bfloat16, device=device) for _ in range(layers)]
+    stamps = torch.zeros(4 * 8192, dtype=torch.int64, device=device)
+    if lib.lrmoe_attn_timeline_set(C.c_void_p(stamps.data_ptr())) != 0:
+        raise RuntimeError("lrmoe_attn_timeline_set failed")
+
+    def run():
+        for l in range(layers):
+            mods[l].step(xs[l], cos, sin, caches[l][0], caches[l][1], context, out=outs[l])
+
+    run()  # (workspaces allocated before capture)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    calls = []
+    for _ in range(replays):
+        stamps.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        calls.append(stamps.view(4, 8192).cpu().numpy().astype(np.int64))
+    del graph
+    st = np.stack(calls)  # [replay][launch][word]
+    t0 = np.array([c[1][c[1] > 0].min() for c in st])[:, None]  # the projection's first entry
+    rel = lambda a: np.where(a > 0, (a - t0) / 100.0, np.nan)  # noqa: E731
+
+    def row(name, v):
+        med = np.nanmedian(np.nanmedian(v, 1))
+        mx = np.nanmedian(np.nanmax(v, 1))
+        print(f"  {name:28s} {med:6.2f} / {mx:6.2f}")
+
+    print(f"full-attention step T={tokens}, {context} cached positions, {replays} replays of {layers} layers; "
+          "us from the projection's first entry, median over replays of the per-workgroup median / max")
+    for launch, name, stride in ((1, "q/gate/k/v projection", 4), (0, "attention partials", 16),
+                                 (2, "merge", 4), (3, "o_proj", 4)):
+        words = st[:, launch, :].reshape(len(calls), -1, stride)
+        live = (words[:, :, 0] > 0).any(0)
+        words = words[:, live, :]
+        row(f"{name}: entry", rel(words[:, :, 0]))
+        if launch == 0:
+            for pname, i in ATTN_PHASES:
+                v = rel(words[:, :, i])
+                if not np.isnan(v).all():
+                    row(f"  {pname}", v)
+            row(f"{name}: end", rel(words[:, :, 7]))
+        else:
+            row(f"{name}: end", rel(words[:, :, 1]))
+    return 0
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--tokens", type=int, default=8)
     parser.add_argument("--layers", type=int, default=None, help="40 decode layers, 30 mixers")
     parser.add_argument("--seed", type=int, default=None, help="2026 decode, 7 mixers")
     parser.add_argument("--mixer", action="store_true", help="time the Gated DeltaNet mixer step instead")
+    parser.add_argument("--attention", action="store_true", help="time the full-attention step instead")
     args = parser.parse_args(argv)
     from .build import TIMELINE_LIBRARY
     if not TIMELINE_LIBRARY.exists():
@@ -97,6 +177,8 @@ def main(argv=None) -> int:
     lib = _native.library()
     if args.mixer:
         return mixer_timeline(lib, args.tokens, args.layers or 30, 7 if args.seed is None else args.seed)
+    if args.attention:
+        return attention_timeline(lib, args.tokens, args.layers or 10, 8 if args.seed is None else args.seed)
     args.layers = args.layers or 40
     args.seed = 2026 if args.seed is None else args.seed
     lib.lrmoe_timeline_set.argtypes = [C.c_void_p]
