@@ -80,12 +80,13 @@ def _close_rows(got, want, what):
 
 
 # Blocks of more than 4 tokens run the 64-row attention variants (above 8
-# tokens a chunk's rows in two workgroups, split at the token half); past
-# the chunk cap the chunks hold more than two 32-position sub-blocks and the
-# last one the remainder (up to 128 chunks to merge): (9000, 8), (16383, 5)
-# and (20000, 16).
+# tokens a chunk's rows in two workgroups, split at the token half: 9 as
+# 5 + 4, 13 as 7 + 6); past the chunk cap the chunks hold more than two
+# 32-position sub-blocks and the last one the remainder (up to 128 chunks
+# to merge): (9000, 8), (16383, 5) and (20000, 16).
 CASES = [(0, 1), (1, 1), (37, 1), (63, 1), (300, 1), (2000, 1), (5000, 1), (20000, 1),
          (40, 3), (31, 5), (3000, 8), (130, 16), (600, 16), (4100, 16),
+         (450, 9), (1000, 10), (3333, 13),
          (9000, 8), (16383, 5), (20000, 16)]
 
 
