@@ -82,7 +82,7 @@ constexpr int kAtWaves = kAtThreads / 64;
 constexpr int kAtSub = 32;                          // positions per sub-block
 constexpr int kAtQStride = kAtD + 8;                // LDS row strides (bf16 / fp32 elements)
 constexpr int kAtVStride = kAtSub + 8;
-constexpr int kAtSStride = kAtSub + 1;
+constexpr int kAtSStride = kAtSub + 4;  // (rows 4 apart 16 banks apart: the score stores conflict 2-way)
 constexpr float kAtScale = 0.0625f;                 // 256^-0.5, exact
 
 // ---- projections: y[t][row] = bf16(sum_k W[row][k] x[t][k]) ---------------
@@ -587,6 +587,19 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
     __syncthreads();
     AT_TL(0, 16, 3);
 
+    // The 64-row variants keep each wave's query operands (row tile w / 2 of
+    // the scores) in registers for every sub-block: half the LDS reads of
+    // the score phase.
+    static_assert(kRowTiles <= 4, "one score row tile per wave");
+    constexpr bool kQReg = kRows == 64;
+    [[maybe_unused]] uint4 qa[kQReg ? kAtD / 32 : 1];
+    if constexpr (kQReg) {
+        const int rt = wave >> 1;
+#pragma unroll
+        for (int s = 0; s < kAtD / 32; ++s)
+            qa[s] = rt < RT ? *reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]) : make_uint4(0, 0, 0, 0);
+    }
+
     // P.V accumulators: wave w owns dim tiles 2w, 2w + 1 of every row tile
     f32x4 acc[kRowTiles][2];
 #pragma unroll
@@ -618,18 +631,20 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         }
         attend_issue(kb, vb, parity, kc, vc, q0 + 2 * kAtSub, range, tid);
         __syncthreads();
-        // scores: wave w takes column tile w & 1 of row tiles w / 2, w / 2 + 4
+        // scores: wave w takes column tile w & 1 of row tile w / 2
         {
             const int ct = wave & 1;
-#pragma unroll
-            for (int k2 = 0; k2 < (kRowTiles + 3) / 4; ++k2) {
-                const int rt = (wave >> 1) + 4 * k2;
+            {
+                const int rt = wave >> 1;
                 if (rt < RT) {
                     f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int s = 0; s < kAtD / 32; ++s)
-                        s4 = mfma16x16x32(*reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]),
-                                          *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
+                    for (int s = 0; s < kAtD / 32; ++s) {
+                        uint4 qop;
+                        if constexpr (kQReg) qop = qa[s];
+                        else qop = *reinterpret_cast<const uint4*>(&qs[16 * rt + m][32 * s + 8 * gq]);
+                        s4 = mfma16x16x32(qop, *reinterpret_cast<const uint4*>(&ks[16 * ct + m][32 * s + 8 * gq]), s4);
+                    }
                     const int pos = q0 + 16 * ct + m;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -641,7 +656,11 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
             }
         }
         __syncthreads();
-        // online softmax: four threads per row, eight positions each
+        // online softmax: four threads per row, eight positions each.  P.V's
+        // k-slot 8 q + j (the A operand's lane group q) holds position
+        // 2 q + 8 (j / 2) + j % 2, the same in the probabilities (es) and
+        // in the value rows gathered below: the gather's four lane groups
+        // then read rows 2 apart, in disjoint banks.
         {
             const int r = tid >> 2;
             const int q = tid & 3;
@@ -649,9 +668,11 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
                 float s8[8];
                 float mx = -__builtin_inff();
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    s8[j] = sc[r][8 * q + j];
-                    mx = fmaxf(mx, s8[j]);
+                for (int j = 0; j < 8; j += 2) {
+                    const float2 pr = *reinterpret_cast<const float2*>(&sc[r][2 * q + 8 * (j >> 1)]);
+                    s8[j] = pr.x;
+                    s8[j + 1] = pr.y;
+                    mx = fmaxf(mx, fmaxf(pr.x, pr.y));
                 }
                 mx = fmaxf(mx, dpp_f<0xB1>(mx));
                 mx = fmaxf(mx, dpp_f<0x4E>(mx));
@@ -680,8 +701,8 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
         }
         __syncthreads();
         // P.V: rescale, then one k-step of 32 positions per tile; the B
-        // operand (positions 8 gq .. 8 gq + 7 of dim 16 dt + m) gathered
-        // from vs, once per dim tile
+        // operand (k-slots 8 gq .. 8 gq + 7: positions 2 gq + 8 e, 2 gq +
+        // 8 e + 1 of dim 16 dt + m) gathered from vs, once per dim tile
         uint4 vop[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -689,7 +710,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                w[e] = static_cast<uint32_t>(vs[8 * gq + 2 * e][d]) | (static_cast<uint32_t>(vs[8 * gq + 2 * e + 1][d]) << 16);
+                w[e] = static_cast<uint32_t>(vs[2 * gq + 8 * e][d]) | (static_cast<uint32_t>(vs[2 * gq + 8 * e + 1][d]) << 16);
             vop[j] = make_uint4(w[0], w[1], w[2], w[3]);
         }
 #pragma unroll

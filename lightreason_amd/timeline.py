@@ -144,6 +144,13 @@ def attention_timeline(lib, tokens: int, layers: int, seed: int, replays: int = 
 
     print(f"full-attention step T={tokens}, {context} cached positions, {replays} replays of {layers} layers; "
           "us from the projection's first entry, median over replays of the per-workgroup median / max")
+    # the chunk of each at_attend workgroup (the launch geometry of attention.hip)
+    S = (context + tokens + 31) // 32
+    cap, floor_per = (256, 1) if tokens <= 4 else (128, 2) if tokens <= 8 else (64, 2)
+    per = max(floor_per, (S + cap) // (cap + 1))
+    chunks = min((S + per - 1) // per, cap)
+    b = np.arange(512)
+    chunk_of = ((b >> 4) * 8 + (b & 7)) % chunks if tokens > 8 else b % chunks
     for launch, name, stride in ((1, "q/gate/k/v projection", 4), (0, "attention partials", 16),
                                  (2, "merge", 4), (3, "o_proj", 4)):
         words = st[:, launch, :].reshape(len(calls), -1, stride)
@@ -151,10 +158,14 @@ def attention_timeline(lib, tokens: int, layers: int, seed: int, replays: int = 
         words = words[:, live, :]
         row(f"{name}: entry", rel(words[:, :, 0]))
         if launch == 0:
+            last = chunk_of[:live.size][live] == chunks - 1
             for pname, i in ATTN_PHASES:
                 v = rel(words[:, :, i])
                 if not np.isnan(v).all():
                     row(f"  {pname}", v)
+                    if (~np.isnan(v[:, ~last])).any():
+                        row(f"    (all but the last chunk)", v[:, ~last])
+                    row(f"    (the last chunk)", v[:, last])
             row(f"{name}: end", rel(words[:, :, 7]))
         else:
             row(f"{name}: end", rel(words[:, :, 1]))
