@@ -294,9 +294,10 @@ hipError_t launch_rule_d(const DnRuleArgs& a, bool bf16, hipStream_t stream) {
 //            call) forms the head's gated RMSNorm (phase C: o, z and the
 //            norm weights in one round trip) and sets the head's "normed"
 //            flag;
-//   wait     for all 32 normed flags;
+//   wait     per wave, for the normed flags of the 4 heads whose rows it
+//            multiplies (wave w: heads 4w .. 4w + 3);
 //   phase D  out_proj rows 8b .. 8b + 7 from the registers and the normed
-//            rows.
+//            rows, each wave's requested as soon as its heads are normed.
 //
 // Flags hold the number of the last call that set them (the head counter at
 // the start, divided by 8, plus 1), so nothing is ever reset; each sits in a
@@ -793,9 +794,25 @@ __global__ __launch_bounds__(kMixThreads, 1) void dn_mixer(DnMixerArgs m) {
     }
     MX_TL(8);
     MX_WORD(12, static_cast<unsigned long long>(last_s));
-    // Phase D reads every head's normed rows.
-    publish_wait(last_s ? m.normed + kDeltaWsStride * rh : nullptr, kDnValueHeads,
-                 [&](int i) { return m.normed + kDeltaWsStride * i; });
+    // Phase D: wave w multiplies the normed rows of heads 4w .. 4w + 3 (k in
+    // [512 w, 512 w + 512)), so it waits for those four heads' flags only
+    // and requests their rows at once; the waves meet at the reduction.
+    // (The head's flag is published once every wave's stores are complete.)
+    static_assert(kDnValueHeads == 4 * kMixWaves, "four heads per wave in phase D");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0 && last_s) st_agent64(m.normed + kDeltaWsStride * rh, call);
+    if (lane < 4) {
+        const unsigned long long* f = m.normed + kDeltaWsStride * (4 * wave + lane);
+        const uint64_t start = wall_clock64();
+        while (ld_agent64(f) < call) {
+            if (wall_clock64() - start > kMixSpinTicks) {
+                timeout_s = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
     MX_TL(9);
 
     // ---- phase D: out_proj rows 8b .. 8b + 7 ----
