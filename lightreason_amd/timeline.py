@@ -155,6 +155,8 @@ def attention_timeline(lib, tokens: int, layers: int, seed: int, replays: int = 
                                  (2, "merge", 4), (3, "o_proj", 4)):
         words = st[:, launch, :].reshape(len(calls), -1, stride)
         live = (words[:, :, 0] > 0).any(0)
+        if not live.any():  # (one token: the merge and o_proj are one launch, stamped as the merge)
+            continue
         words = words[:, live, :]
         row(f"{name}: entry", rel(words[:, :, 0]))
         if launch == 0:
