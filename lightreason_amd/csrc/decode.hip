@@ -823,12 +823,14 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
             }
             __syncthreads();
             // This workgroup's 8 logits of token t as 4 tagged words (logits
-            // 2k and 2k+1 in word k of the token's row).
+            // 2k and 2k+1 in word k of the token's row), in every copy.
             if (tid < 4 * T) {
                 const int t = tid >> 2;
                 const int q = tid & 3;
                 const uint32_t pair = static_cast<uint32_t>(P.lg[t][2 * q]) | (static_cast<uint32_t>(P.lg[t][2 * q + 1]) << 16);
-                st_agent64(a.logits + static_cast<size_t>(t) * (kExperts / 2) + (kWaves / 2) * block + q, tag_bits | pair);
+                uint64_t* dst = a.logits + static_cast<size_t>(t) * (kExperts / 2) + (kWaves / 2) * block + q;
+#pragma unroll
+                for (int c = 0; c < kDecodeLogitCopies; ++c) st_agent64(dst + c * kDecodeLogitCopyWords, tag_bits | pair);
             }
             TL(123, 0);
         }
@@ -837,15 +839,21 @@ __device__ __forceinline__ int32_t decode_layer(const DecodeArgs& a, Plan<kCodec
     // ---- 4. the route plan ----
     if (a.router != nullptr) {
         // Each wave reloads its tokens' logit rows (bounded) until every word
-        // carries this call's tag; lane l ends with logits 4l..4l+3.
-        const uint64_t* row_lo = a.logits + static_cast<size_t>(has_lo ? t_lo : 0) * (kExperts / 2) + 2 * lane;
-        const uint64_t* row_hi = a.logits + static_cast<size_t>(has_hi ? t_hi : 0) * (kExperts / 2) + 2 * lane;
-        uint64_t lw[4];
+        // carries this call's tag; lane l ends with logits 4l..4l+3.  The
+        // rows come from copy b % 8, and a wave without a token loads none.
+        const uint64_t* copy = a.logits + static_cast<size_t>(blockIdx.x % kDecodeLogitCopies) * kDecodeLogitCopyWords;
+        const uint64_t* row_lo = copy + static_cast<size_t>(has_lo ? t_lo : 0) * (kExperts / 2) + 2 * lane;
+        const uint64_t* row_hi = copy + static_cast<size_t>(has_hi ? t_hi : 0) * (kExperts / 2) + 2 * lane;
+        uint64_t lw[4] = {0ull, 0ull, 0ull, 0ull};
         auto fetch = [&]() {
-            lw[0] = ld_agent64(row_lo);
-            lw[1] = ld_agent64(row_lo + 1);
-            lw[2] = ld_agent64(row_hi);
-            lw[3] = ld_agent64(row_hi + 1);
+            if (has_lo) {
+                lw[0] = ld_agent64(row_lo);
+                lw[1] = ld_agent64(row_lo + 1);
+            }
+            if (has_hi) {
+                lw[2] = ld_agent64(row_hi);
+                lw[3] = ld_agent64(row_hi + 1);
+            }
             return (has_lo && (tag_of(lw[0]) != tag || tag_of(lw[1]) != tag)) ||
                    (has_hi && (tag_of(lw[2]) != tag || tag_of(lw[3]) != tag));
         };

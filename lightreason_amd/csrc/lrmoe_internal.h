@@ -65,6 +65,11 @@ struct DecodeSync {
 // a word has that word's data; an 8-byte store is seen whole or not at all.
 // (A tag repeats only after 2^32 - 1 decode calls on one workspace.)
 constexpr int kDecodeTagShift = 32;
+// The router's tagged logit rows are written in one copy per XCD (copy
+// b % 8 read by workgroup b): every workgroup polls them, and 256 readers
+// of one 1 KiB row crowd the few memory channels that hold it.
+constexpr int kDecodeLogitCopies = 8;
+constexpr int kDecodeLogitCopyWords = kDecodeMaxTokens * 128;  // 16 KiB apart
 
 // Control block at the start of every workspace.  The route counter is reset
 // to zero by the workgroup that consumes it, so a zero-initialised workspace
@@ -141,7 +146,7 @@ inline Workspace carve(void* base, int tokens) {
     // written by that call.
     ws.dact = reinterpret_cast<uint64_t*>(take((9 * kDecodeMaxTokens + 16) * 256 * 8));
     ws.dy = reinterpret_cast<uint64_t*>(take(9 * kDecodeMaxTokens * 1024 * 8));
-    ws.dlogits = reinterpret_cast<uint64_t*>(take(kDecodeMaxTokens * 128 * 8));
+    ws.dlogits = reinterpret_cast<uint64_t*>(take(kDecodeLogitCopies * kDecodeLogitCopyWords * 8));
     ws.logits = reinterpret_cast<uint16_t*>(take(T * 256 * 2));
     ws.normed = reinterpret_cast<uint16_t*>(take(T * 2048 * 2));
     ws.indices = reinterpret_cast<int64_t*>(take(T * 8 * 8));
