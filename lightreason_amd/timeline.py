@@ -243,6 +243,11 @@ def main(argv=None) -> int:
             v = f(t[:, i])
             cells.append(f"{name} {np.nanmedian(v):.2f}/{np.nanmax(v):.2f}" if (~np.isnan(v)).any() else f"{name} -")
         print("  " + " | ".join(cells) + "   (median/max)")
+        for name, i in (("counters", 7), ("logits_seen", 124), ("plan", 3), ("end", 4)):
+            v = f(t[:, i])
+            if (~np.isnan(v)).any():
+                late = np.argsort(np.nan_to_num(v, nan=-1.0))[::-1][:6]
+                print(f"  latest at {name}: " + ", ".join(f"wg {w} {v[w]:.2f}" for w in late))
         for n in range(STEPS):
             b = 8 + 5 * n
             s0, s1, s2, s3 = (f(t[:, b + i]) for i in range(4))
