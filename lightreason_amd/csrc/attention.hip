@@ -775,7 +775,7 @@ __device__ __forceinline__ void attend_chunk(const AttnArgs& a, AttendLds<kRows,
 }
 
 // kRows: the query rows of a workgroup (8 per token): 32 up to 4 tokens
-// (about 63 KB of LDS, two workgroups per CU), 64 above (one).  Above 8
+// (about 63 KB of LDS), 64 above (103 KB).  Above 8
 // tokens a chunk's rows take two workgroups, one per token half, on the
 // same XCD (workgroups b and b + 8 of each group of 16), so they share the
 // chunk's key and value rows through its L2.
@@ -940,9 +940,12 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
 void attn_geometry(AttnArgs& a, int tokens, int span) {
     // Chunks of `per` whole 32-position sub-blocks: one per chunk up to 4
     // tokens (the partials of 8 T rows per chunk stay small), two above,
-    // more only when the chunks would exceed the cap: 256 per head up to 4
-    // tokens (two workgroups per CU), 128 above, 64 above 8 tokens (two
-    // workgroups per chunk), so that every workgroup is resident at once.
+    // more only when the chunks would exceed the cap: 128 per head up to 8
+    // tokens, 64 above (two workgroups per chunk), so that the launch is at
+    // most 256 workgroups, one per CU.  (Up to 4 tokens a cap of 256, two
+    // 32-row workgroups on some or all CUs, was slower at every length past
+    // 128 sub-blocks: 0.8 us at one token and 4096 positions, 5.2 us at four
+    // tokens and 8100.)
     // The last chunk takes what the cap leaves (at most 2 per): 4096 cached
     // positions and 16 new ones make 64 chunks of 2 sub-blocks and one of 3,
     // not 43 of 3.  A chunk's bounds depend on the span only through `per`,
@@ -951,7 +954,7 @@ void attn_geometry(AttnArgs& a, int tokens, int span) {
     const int S = (span + kAtSub - 1) / kAtSub;
     const int halves = tokens > 8 ? 2 : 1;
     const int floor_per = tokens <= 4 ? 1 : 2;
-    const int cap = tokens <= 4 ? kAttnMaxChunks : kAttnMaxChunks / 2 / halves;
+    const int cap = kAttnMaxChunks / halves;
     const int per = max(floor_per, (S + cap) / (cap + 1));
     a.sub_blocks = S;
     a.per = per;

@@ -440,7 +440,7 @@ constexpr int kDeltaMaxTokens = 16;
 
 // ---- full-attention decode step (attention.hip) ----
 constexpr int kAttnMaxTokens = 16;
-constexpr int kAttnMaxChunks = 256;  // position chunks per key/value head (up to 4 tokens; 128 above)
+constexpr int kAttnMaxChunks = 128;  // position chunks per key/value head (up to 8 tokens; 64 above)
 struct AttnArgs {
     uint16_t* proj;         // [T][9216]: per token q/gate (8192), k (512), v (512) rows, bf16
     const uint16_t* q_norm; // [256]
