@@ -939,7 +939,11 @@ __global__ __launch_bounds__(kAtCombineThreads) void at_combine(AttnArgs a) {
 
 void attn_geometry(AttnArgs& a, int tokens, int span) {
     // Chunks of `per` whole 32-position sub-blocks: one per chunk up to 4
-    // tokens (the partials of 8 T rows per chunk stay small), two above,
+    // tokens (the partials of 8 T rows per chunk stay small), two above
+    // unless chunks of one make at most 128 workgroups (short caches: then
+    // the extra workgroups gain more than the extra partials cost, 0.6-1.5
+    // us a step at 300 and 1000 positions; at 1900 positions and 12-16
+    // tokens, 240 workgroups of one sub-block lost 0.5-0.7 us),
     // more only when the chunks would exceed the cap: 128 per head up to 8
     // tokens, 64 above (two workgroups per chunk), so that the launch is at
     // most 256 workgroups, one per CU.  (Up to 4 tokens a cap of 256, two
@@ -953,7 +957,7 @@ void attn_geometry(AttnArgs& a, int tokens, int span) {
     // split the valid positions alike while `per` is the same.
     const int S = (span + kAtSub - 1) / kAtSub;
     const int halves = tokens > 8 ? 2 : 1;
-    const int floor_per = tokens <= 4 ? 1 : 2;
+    const int floor_per = tokens <= 4 || kAtKv * halves * S <= 128 ? 1 : 2;
     const int cap = kAttnMaxChunks / halves;
     const int per = max(floor_per, (S + cap) / (cap + 1));
     a.sub_blocks = S;

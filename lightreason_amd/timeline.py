@@ -146,7 +146,9 @@ def attention_timeline(lib, tokens: int, layers: int, seed: int, replays: int = 
           "us from the projection's first entry, median over replays of the per-workgroup median / max")
     # the chunk of each at_attend workgroup (the launch geometry of attention.hip)
     S = (context + tokens + 31) // 32
-    cap, floor_per = (128, 1) if tokens <= 4 else (128, 2) if tokens <= 8 else (64, 2)
+    halves = 2 if tokens > 8 else 1
+    cap = 128 // halves
+    floor_per = 1 if tokens <= 4 or 2 * halves * S <= 128 else 2
     per = max(floor_per, (S + cap) // (cap + 1))
     chunks = min((S + per - 1) // per, cap)
     b = np.arange(512)
